@@ -1,0 +1,35 @@
+// common.h -- shared host/device definitions of libholo_mi355x.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/cuda_ops.h"
+#include "../../include/holo_mi355x.h"
+
+namespace holo {
+
+// Library stream (null stream unless holo_set_stream was called) and the
+// copy stream of cuda_memcpy_*_async (reference cuda_ops.cu:88-89).
+hipStream_t stream();
+hipStream_t copy_stream();
+
+// Error latch: first error wins until holo_last_error() reads it.
+void latch_error(int code, const char *what, const char *file, int line);
+
+// Number of compute units of device 0, read once at init.
+int num_cus();
+
+}  // namespace holo
+
+#define HOLO_CHECK(call)                                                        \
+    do {                                                                        \
+        hipError_t holo_e_ = (call);                                            \
+        if (holo_e_ != hipSuccess) holo::latch_error((int)holo_e_, #call, __FILE__, __LINE__); \
+    } while (0)
+
+// After a kernel launch: catch launch-configuration errors immediately.
+#define HOLO_LAUNCH_CHECK() HOLO_CHECK(hipGetLastError())
+
+#define HOLO_REJECT(msg) holo::latch_error(HOLO_EINVAL, (msg), __FILE__, __LINE__)

@@ -1,0 +1,87 @@
+/*
+ * holo_mi355x.h -- extensions of libholo_mi355x.so beyond the reference's
+ * cuda_ops.h.  None of these replaces a reference symbol; each says what in
+ * the reference it relates to.  Existing cuda_ops.h signatures are unchanged.
+ */
+#ifndef HOLO_MI355X_EXT_H
+#define HOLO_MI355X_EXT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML type ids of the formats served (reference src/ai/quant.h:19-33). */
+#define HOLO_TYPE_F32  0
+#define HOLO_TYPE_F16  1
+#define HOLO_TYPE_Q4_0 2
+#define HOLO_TYPE_Q8_0 8
+#define HOLO_TYPE_Q4_K 12
+#define HOLO_TYPE_Q6_K 14
+
+/* ---- errors ---------------------------------------------------------------
+ * The reference ops return void and print (cuda_ops.cu:21-37).  This library
+ * prints too, and latches the first error code until it is read:
+ * 0 = ok, otherwise a hipError_t value, or HOLO_EINVAL for a rejected
+ * argument.  holo_last_error() returns and clears the latch.               */
+#define HOLO_EINVAL 100001
+int holo_last_error(void);
+const char *holo_error_string(int code);
+
+/* ---- stream, events, graphs ----------------------------------------------
+ * All ops launch on one library stream (default: the null stream, as the
+ * reference).  Events are recorded on that stream.  A graph captures every
+ * op issued between begin and end on that stream (stream capture), so a
+ * decode step of many GEMVs replays with one launch.                        */
+void holo_set_stream(void *hip_stream);
+void *holo_get_stream(void);
+void *holo_event_create(void);
+void holo_event_record(void *ev);
+float holo_event_elapsed_ms(void *start, void *stop); /* synchronises on stop */
+void holo_event_destroy(void *ev);
+void *holo_stream_create(void);                 /* default priority */
+void holo_stream_destroy(void *s);
+int holo_graph_begin(void);                     /* library stream must not be the null stream */
+void *holo_graph_end(void);                     /* returns an executable graph or NULL */
+int holo_graph_launch(void *graph_exec);
+void holo_graph_destroy(void *graph_exec);
+
+/* ---- generic dispatch -------------------------------------------------------
+ * The reference's gpu_matmul switch (src/ai/llm_cuda.c:140-163) as one call. */
+void holo_matmul(float *dst, const void *M, const float *v, int out_dim, int in_dim, int type);
+
+/* ---- dequantisation ---------------------------------------------------------
+ * dst[n] = the fp32 weights of n/QK blocks, bit-identical to the reference
+ * CPU routines dequantize_row_q8_0 / q4_0 / q4_k / q6_k
+ * (src/ai/quant.c:118-128, 136-153, 277-311, 241-271).                     */
+void holo_dequant(float *dst, const void *src, int64_t n, int type);
+
+/* ---- fused multi-GEMV for every served format --------------------------------
+ * Same contract as cuda_batched_qkv_q8_0 / cuda_batched_ffn_gate_up_q8_0
+ * (reference cuda_ops.h:60-66) for type Q8_0, Q4_0 or Q4_K.                */
+void holo_batched_qkv(float *q_out, float *k_out, float *v_out,
+                      const void *Wq, const void *Wk, const void *Wv,
+                      const float *x, int q_dim, int kv_dim, int in_dim, int type);
+void holo_batched_ffn_gate_up(float *out, const void *W1, const void *W3,
+                              const float *x, int ffn_dim, int in_dim, int type);
+
+/* ---- batched prefill --------------------------------------------------------
+ * The reference has no batched path (one GEMV per prompt token,
+ * src/ai/llm.c:1049).  Activations X[M][K] fp32 are quantised per row and
+ * 32-block to Q8_0: d = f16_rne(amax/127), q = round-half-away(x*127/amax)
+ * (d=0 -> q=0).  Y[M][N] = sum_b f16(dw)*f16(dx)*I_b with the exact
+ * int32 block dot I_b, accumulated in fp32 in block order.                  */
+void holo_quantize_act_q8_0(void *dst_blocks, const float *X, int rows, int k);
+void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, int K);
+/* Y[M][N] = X[M][K] . W[N][K]^T for W in Q4_0: M >= 64 quantises X and runs
+ * the int8 MFMA GEMM above; M < 64 runs M fp32-activation GEMVs.            */
+void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int N, int K,
+                            void *scratch_q8);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HOLO_MI355X_EXT_H */
