@@ -1,50 +1,64 @@
 // gemv.hip -- fused dequant + matrix-vector product over GGUF Q8_0, Q4_0 and
-// Q4_K blocks with fp32 activations and fp32 accumulation (decode path).
+// Q4_K blocks (decode path, batch 1).
 //
 // Replaces cuda_matmul_q8_0 / q4_0 / q4_k and the two fused Q8_0 multi-GEMVs
 // of the reference (src/ai/cuda_ops.cu:1132-1175, 1184-1395).  The reference
 // CPU path (src/ai/llm.c:770-926, src/ai/quant.c:541-633) defines the result.
 //
-// Work mapping (wave64):
+// Work mapping (wave64, workgroup of 8 waves):
 //   * lane <-> one 32-weight unit of a row (Q8_0/Q4_0 block, Q4_K sub-block);
-//     the 64 lanes of a wave read 64 consecutive units of one row, so each
+//     the 64 lanes of a wave read 64 consecutive units of one row, so one
 //     load instruction covers one contiguous run of the row (1152 B for
 //     Q4_0, 2176 B for Q8_0, 8 superblocks for Q4_K);
-//   * a wave owns a task of R rows and walks the row in 64-unit segments;
-//     the lane's 32 activations are read once per segment and reused for
-//     the R rows;
-//   * activations are staged once per workgroup in LDS (16-byte chunks
-//     XOR-swizzled within each unit so a ds_read_b128 of 8 neighbouring lanes
-//     hits distinct banks), together with the per-unit sum of activations;
-//   * the quant offset is folded out of the inner loop:
-//       Q4_0  d * (sum q*x - 8 * sum x)
-//       Q8_0  d * (sum (q+128)*x - 128 * sum x)   (q+128 = byte ^ 0x80)
-//       Q4_K  (d*sc) * sum q*x - (dmin*m) * sum x
-//     so the inner loop is unpack, v_cvt_f32_ubyte and one FMA per weight;
-//   * the R row sums are reduced across the wave with DPP.
+//   * an item is R rows x one 64-unit segment of the row.  A workgroup owns a
+//     tile of G*R rows x all nsegs segments (G*nsegs items) and deals the
+//     items round-robin to its 8 waves (at most P per wave), so long rows
+//     are split across waves and every wave has P independent items;
+//   * tiles are double-buffered in registers: the raw block loads of the
+//     workgroup's next tile are issued before the current tile is decoded,
+//     and the first tile's loads are issued before x is staged;
+//   * x is staged once per workgroup in LDS with coalesced 16-byte loads
+//     (one float4 per lane; per-unit max and sum reduced across the unit's 8
+//     lanes with DPP);
+//   * each item's R row partials are reduced across the wave with DPP and
+//     written to LDS; after the tile's barrier the row sums are finished and
+//     stored (the partial buffers alternate between tiles).
+//
+// Two activation modes (same weights, same decode):
+//   XM_F32   exact fp32 activations: unpack nibbles/bytes, v_cvt_f32_ubyte,
+//            one FMA per weight; quant offsets folded per unit
+//              Q4_0  d*(sum q*x - 8*sum x)      Q8_0  d*(sum (q+128)*x - 128*sum x)
+//              Q4_K  (d*sc)*sum q*x - (dmin*m)*sum x
+//   XM_I24   activations as 24-bit fixed point per 32-block, held as three
+//            int8 planes: xi = rint(x * Q/amax), Q = 127*65536,
+//            xi = 65536*h + 256*m + l with h in [-127,127], m, l in
+//            [-128,127]; the unit's integer dots sum q*h, sum q*m, sum q*l
+//            run on v_dot4_i32_i8 (4 weights per op) and are exact; the
+//            rest is fp32:  S = 65536*Sh + 256*Sm + Sl,
+//              Q4_0  d_w * (d_x*S - 8*sum x)      Q8_0  d_w * d_x * S
+//              Q4_K  (d*sc) * d_x*S - (dmin*m) * sum x
+//            |x - d_x*xi| <= d_x = amax * 2^-23 per activation: the
+//            activation error is at the level of an fp32 rounding of the
+//            block's largest term.
+// Accumulation across units is fp32 in both modes.
+#include "block_window.h"
 #include "common.h"
 #include "quant_blocks.h"
 
+#include <stdlib.h>
+
 namespace holo {
 
-enum Fmt { FMT_Q4_0 = 0, FMT_Q8_0 = 1, FMT_Q4_K = 2 };
 enum Mode { MODE_PLAIN = 0, MODE_GATEUP = 1 };
+enum XMode { XM_F32 = 0, XM_I24 = 1, XM_GF32 = 2 };
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxSeg = 3;
+constexpr int kQmax = 127 * 65536;  // |xi| <= kQmax splits into h, m, l as above
 
-struct GemvArgs {
-    const uint8_t *W[kMaxSeg];
-    float *y[kMaxSeg];
-    int64_t bytes[kMaxSeg];
-    int rows[kMaxSeg];
-    int task_end[kMaxSeg];  // inclusive prefix sums of tasks per segment
-    int nseg;
-    int ntasks;
-    const float *x;
-    int units;  // 32-weight units per row
-};
+
+// ---- wave reduction ----------------------------------------------------------
 
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_shift_add(float v)
@@ -53,26 +67,273 @@ __device__ __forceinline__ float dpp_shift_add(float v)
     return v + __int_as_float(t);
 }
 
-// Sum over the 64 lanes; the result is returned in every lane.
+// Sum over the 64 lanes, returned in every lane.
 __device__ __forceinline__ float wave_sum(float v)
 {
     v = dpp_shift_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
     v = dpp_shift_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
     v = dpp_shift_add<0x141, 0xF>(v);  // row_half_mirror
-    v = dpp_shift_add<0x140, 0xF>(v);  // row_mirror: every lane of a row holds its row sum
+    v = dpp_shift_add<0x140, 0xF>(v);  // row_mirror: each lane holds its row's sum
     v = dpp_shift_add<0x142, 0xA>(v);  // row_bcast:15 -> rows 1, 3
     v = dpp_shift_add<0x143, 0xC>(v);  // row_bcast:31 -> rows 2, 3
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// Hides a value's known bits from the optimiser, so that
-// (float)((v >> 8k) & 0xFF) selects v_cvt_f32_ubyte{k} instead of being
-// narrowed to a 4-bit v_bfe_u32 plus v_cvt_f32_ubyte0 (one op per weight
-// instead of two).  Emits no instruction.
+// Hides a value's known bits from the optimiser, so (float)((v >> 8k) & 0xFF)
+// selects v_cvt_f32_ubyte{k} instead of a 4-bit v_bfe_u32 + v_cvt_f32_ubyte0.
+// Emits no instruction.
 __device__ __forceinline__ void opaque(uint32_t &v) { asm volatile("" : "+v"(v)); }
 
-// Dot of one unit's 32 nibbles with its 32 activations: sum q*x, q in 0..15.
-__device__ __forceinline__ float nib_dot(const uint32_t (&q)[4], const float4 (&x)[8])
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c)
+{
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// ---- raw block loads (issued early) and decode (at compute time) ----------------
+
+template <int FMT>
+struct Raw;
+
+template <>
+struct Raw<FMT_Q4_0> {
+    u32x4 a;
+    uint32_t e, s;
+};
+template <>
+struct Raw<FMT_Q8_0> {
+    u32x4 a, b;
+    uint32_t e, s;
+};
+template <>
+struct Raw<FMT_Q4_K> {
+    u32x4 h, q;
+    uint32_t j;
+};
+
+// Loads the raw dwords of one unit.  `ba` is the row's first byte rounded
+// down to 4 (wave uniform), `mis` the rounding (0 or 2), `off` the unit's
+// byte offset in the row (unit_offset).  Q4_0/Q8_0 load the dword-aligned
+// window of the block (block_window); Q4_K loads the superblock header and
+// the sub-block's 16 quant bytes.
+// Weight loads go through address-space-1 pointers so they compile to
+// global_load (vmcnt only).  A flat load would also count against lgkmcnt,
+// and every LDS wait would then wait for the weight stream as well.
+typedef __attribute__((address_space(1))) const uint8_t gbyte;
+typedef __attribute__((address_space(1))) const u32x4 gu32x4;
+typedef __attribute__((address_space(1))) const uint32_t gu32;
+
+template <int FMT>
+__device__ __forceinline__ void load_raw(Raw<FMT> &r, gbyte *ba, uint32_t mis, uint32_t off, uint32_t u)
+{
+    if constexpr (FMT == FMT_Q4_0 || FMT == FMT_Q8_0) {
+        Window w = block_window(mis, off);
+        gbyte *p = ba + w.start;
+        r.a = *(gu32x4 *)p;
+        if constexpr (FMT == FMT_Q4_0) {
+            r.e = *(gu32 *)(p + 16);
+        } else {
+            r.b = *(gu32x4 *)(p + 16);
+            r.e = *(gu32 *)(p + 32);
+        }
+        r.s = w.s;
+    } else {
+        gbyte *sb = ba + mis + off;
+        r.j = u & 7u;
+        r.h = *(gu32x4 *)sb;
+        r.q = *(gu32x4 *)(sb + 16 + 16 * r.j);
+    }
+}
+
+// ---- activations staged in LDS ------------------------------------------------
+//
+// XM_F32 : float4 lx[units*8] (chunk c of unit u at slot c ^ (u&7)), then
+//          float sx[units] = sum of the unit's 32 activations
+// XM_I24 : uint4 lq[units*6] (chunks 0/1 = h bytes of columns 0-15/16-31,
+//          2/3 = m bytes, 4/5 = l bytes; the 96-byte unit stride already puts
+//          8 neighbouring lanes on distinct banks), then
+//          float2 ls[units] = { d_x, sum x }
+
+template <int XM>
+__host__ __device__ constexpr int lds_bytes_per_unit()
+{
+    return XM == XM_F32 ? 128 + 4 : 96 + 8;
+}
+
+// Reductions over the 8 lanes of an aligned lane octet (all 8 active).
+template <int CTRL>
+__device__ __forceinline__ float dpp_get(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float octet_sum(float v)
+{
+    v += dpp_get<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_get<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_get<0x141>(v);  // row_half_mirror: lane i <- lane 7-i of the octet
+    return v;
+}
+__device__ __forceinline__ float octet_max(float v)
+{
+    v = fmaxf(v, dpp_get<0xB1>(v));
+    v = fmaxf(v, dpp_get<0x4E>(v));
+    v = fmaxf(v, dpp_get<0x141>(v));
+    return v;
+}
+
+// Packs byte 0 of four ints into one dword (little-endian order a, b, c, d).
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d)
+{
+    uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+    uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);
+    return lo | (hi << 16);
+}
+
+// x staging is split in two so that the activation loads are issued before
+// the first tile's weight loads: vector-memory loads complete in issue order
+// (s_waitcnt vmcnt), so loads issued after the weight stream would make the
+// staging arithmetic wait for the whole weight fetch.
+//
+// Every thread takes float4 chunks i = tid + 256*k of x (unit i>>3, chunk
+// i&7), so the 8 chunks of a unit sit in one aligned lane octet.  The
+// kPreX = 8 chunks per thread (in_dim <= 16384) are loaded up front with
+// buffer loads: every instruction issues, so the compiler's wait counts stay
+// exact, and a chunk past the end of x gets an out-of-range offset, which
+// the buffer unit answers with zeros without touching memory.  Longer rows
+// load their remaining chunks in x_stage.
+constexpr int kPreX = 8;
+constexpr uint32_t kBufferWord3 = 0x00020000u;  // gfx9 raw buffer: 32-bit data format
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t x_rsrc(const float *x, int units)
+{
+    return __builtin_amdgcn_make_buffer_rsrc((void *)x, (short)0, units * 128, kBufferWord3);
+}
+
+__device__ __forceinline__ float4 load_x4(__amdgpu_buffer_rsrc_t rs, uint32_t off)
+{
+    v4f v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void x_preload(const float *__restrict__ x, int units, float4 (&pre)[kPreX])
+{
+    const int tid = threadIdx.x;
+    const __amdgpu_buffer_rsrc_t rs = x_rsrc(x, units);
+#pragma unroll
+    for (int k = 0; k < kPreX; k++) {
+        const int i = tid + kThreads * k;
+        pre[k] = load_x4(rs, i < units * 8 ? (uint32_t)i * 16u : kOutOfRange);
+    }
+}
+
+template <int FMT, int XM>
+__device__ __forceinline__ void x_convert(const float4 v, int i, int units, void *lds)
+{
+    const int u = i >> 3, c = i & 7;
+    const float sx = octet_sum((v.x + v.y) + (v.z + v.w));
+    if constexpr (XM == XM_F32) {
+        float4 *lx = (float4 *)lds;
+        lx[u * 8 + (c ^ (u & 7))] = v;
+        if (c == 0) ((float *)(lx + units * 8))[u] = sx;
+    } else {
+        const float amax = octet_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        const float dx = amax * (1.0f / (float)kQmax);
+        const float inv = amax > 0.f ? (float)kQmax / amax : 0.f;
+        int xi[4] = {(int)__builtin_rintf(v.x * inv), (int)__builtin_rintf(v.y * inv),
+                     (int)__builtin_rintf(v.z * inv), (int)__builtin_rintf(v.w * inv)};
+        int x1[4], x2[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            xi[k] = min(max(xi[k], -kQmax), kQmax);
+            x1[k] = (xi[k] + 128) >> 8;  // xi = 256*x1 + l,  l = low byte (signed)
+            x2[k] = (x1[k] + 128) >> 8;  // x1 = 256*h  + m,  m = low byte (signed), h = x2
+        }
+        uint32_t *lq = (uint32_t *)((uint4 *)lds + u * 6);
+        lq[c] = pack4(x2[0], x2[1], x2[2], x2[3]);       // h plane
+        lq[8 + c] = pack4(x1[0], x1[1], x1[2], x1[3]);   // m plane
+        lq[16 + c] = pack4(xi[0], xi[1], xi[2], xi[3]);  // l plane
+        if (c == 0) ((float2 *)((uint4 *)lds + units * 6))[u] = make_float2(dx, sx);
+    }
+}
+
+template <int FMT, int XM>
+__device__ __forceinline__ void x_stage(const float *__restrict__ x, int units, void *lds, const float4 (&pre)[kPreX])
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < kPreX; k++) {
+        const int i = tid + kThreads * k;
+        if (i < units * 8) x_convert<FMT, XM>(pre[k], i, units, lds);
+    }
+    // in_dim > 16384: the remaining chunks are loaded here (after the weight
+    // loads, so their wait includes the first tile's weights)
+    const __amdgpu_buffer_rsrc_t rs = x_rsrc(x, units);
+    for (int i = tid + kThreads * kPreX; i < units * 8; i += kThreads)
+        x_convert<FMT, XM>(load_x4(rs, (uint32_t)i * 16u), i, units, lds);
+}
+
+template <int XM>
+struct XVals;
+
+template <>
+struct XVals<XM_F32> {
+    float4 x[8];
+    float sx;
+    __device__ __forceinline__ void load(const void *lds, int units, int u)
+    {
+        const float4 *lx = (const float4 *)lds;
+        const float4 *p = lx + u * 8;
+        const int sw = u & 7;
+#pragma unroll
+        for (int c = 0; c < 8; c++) x[c] = p[c ^ sw];
+        sx = ((const float *)(lx + units * 8))[u];
+    }
+};
+
+template <>
+struct XVals<XM_I24> {
+    uint32_t h[8], m[8], l[8];
+    float dx, sx;
+    __device__ __forceinline__ void load(const void *lds, int units, int u)
+    {
+        const uint4 *p = (const uint4 *)lds + u * 6;
+        uint4 c0 = p[0], c1 = p[1], c2 = p[2], c3 = p[3], c4 = p[4], c5 = p[5];
+        h[0] = c0.x; h[1] = c0.y; h[2] = c0.z; h[3] = c0.w;
+        h[4] = c1.x; h[5] = c1.y; h[6] = c1.z; h[7] = c1.w;
+        m[0] = c2.x; m[1] = c2.y; m[2] = c2.z; m[3] = c2.w;
+        m[4] = c3.x; m[5] = c3.y; m[6] = c3.z; m[7] = c3.w;
+        l[0] = c4.x; l[1] = c4.y; l[2] = c4.z; l[3] = c4.w;
+        l[4] = c5.x; l[5] = c5.y; l[6] = c5.z; l[7] = c5.w;
+        float2 s = ((const float2 *)((const uint4 *)lds + units * 6))[u];
+        dx = s.x;
+        sx = s.y;
+    }
+};
+
+// Rows too long for LDS staging: each lane reads its unit's 32 activations
+// from global memory (L1/L2 resident) and sums them itself.
+template <>
+struct XVals<XM_GF32> {
+    float4 x[8];
+    float sx;
+    __device__ __forceinline__ void load(const float *__restrict__ gx, int u)
+    {
+        const float *p = gx + (int64_t)u * 32;
+#pragma unroll
+        for (int c = 0; c < 8; c++) x[c] = make_float4(p[4 * c], p[4 * c + 1], p[4 * c + 2], p[4 * c + 3]);
+        float s = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; c++) s += (x[c].x + x[c].y) + (x[c].z + x[c].w);
+        sx = s;
+    }
+};
+
+// ---- per-unit dot products --------------------------------------------------------
+
+// sum q*x over 32 nibbles (q in 0..15), fp32
+__device__ __forceinline__ float nib_dot_f32(const uint32_t (&q)[4], const float4 (&x)[8])
 {
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
@@ -95,8 +356,8 @@ __device__ __forceinline__ float nib_dot(const uint32_t (&q)[4], const float4 (&
     return (a0 + a1) + (a2 + a3);
 }
 
-// sum (q+128)*x over a Q8_0 unit, q int8 stored in bytes.
-__device__ __forceinline__ float byte_dot(const uint32_t (&q)[8], const float4 (&x)[8])
+// sum (q+128)*x over 32 int8 q, fp32
+__device__ __forceinline__ float byte_dot_f32(const uint32_t (&q)[8], const float4 (&x)[8])
 {
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
@@ -112,184 +373,286 @@ __device__ __forceinline__ float byte_dot(const uint32_t (&q)[8], const float4 (
     return (a0 + a1) + (a2 + a3);
 }
 
-template <int FMT>
-__device__ __forceinline__ float unit_dot(const uint8_t *__restrict__ W, int64_t bytes, int64_t gunit,
-                                          const float4 (&x)[8], float sx)
+// S = 65536*sum q*h + 256*sum q*m + sum q*l over 32 nibbles (q in 0..15);
+// the three integer dots are exact, S rounds once per fma.
+__device__ __forceinline__ float nib_dot_i24(const uint32_t (&q)[4], const XVals<XM_I24> &x)
 {
-    if constexpr (FMT == FMT_Q4_0) {
-        Q4_0Unit u = load_q4_0(W, gunit, bytes);
-        return u.d * fmaf(-8.0f, sx, nib_dot(u.q, x));
-    } else if constexpr (FMT == FMT_Q8_0) {
-        Q8_0Unit u = load_q8_0(W, gunit, bytes);
-        return u.d * fmaf(-128.0f, sx, byte_dot(u.q, x));
-    } else {
-        Q4_KUnit u = load_q4_k(W, gunit);
-        return fmaf(u.dsc, nib_dot(u.q, x), -u.dmn * sx);
+    int ah = 0, am = 0, al = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t ln = q[i] & 0x0F0F0F0Fu;
+        uint32_t hn = (q[i] >> 4) & 0x0F0F0F0Fu;
+        ah = sdot4(ln, x.h[i], ah);
+        ah = sdot4(hn, x.h[4 + i], ah);
+        am = sdot4(ln, x.m[i], am);
+        am = sdot4(hn, x.m[4 + i], am);
+        al = sdot4(ln, x.l[i], al);
+        al = sdot4(hn, x.l[4 + i], al);
     }
+    return fmaf(65536.0f, (float)ah, fmaf(256.0f, (float)am, (float)al));
 }
 
-// x staged in LDS: unit u occupies 8 float4 chunks; chunk c sits at slot
-// c ^ (u & 7).  sx[u] = sum of the unit's 32 activations (fixed order).
-template <bool XLDS>
-struct XSource;
-
-template <>
-struct XSource<true> {
-    const float4 *lx;
-    const float *lsx;
-    __device__ __forceinline__ void get(int u, float4 (&x)[8], float &sx) const
-    {
-        const float4 *p = lx + u * 8;
-        int sw = u & 7;
+// The same over 32 int8 q.
+__device__ __forceinline__ float byte_dot_i24(const uint32_t (&q)[8], const XVals<XM_I24> &x)
+{
+    int ah = 0, am = 0, al = 0;
 #pragma unroll
-        for (int c = 0; c < 8; c++) x[c] = p[c ^ sw];
-        sx = lsx[u];
+    for (int i = 0; i < 8; i++) {
+        ah = sdot4(q[i], x.h[i], ah);
+        am = sdot4(q[i], x.m[i], am);
+        al = sdot4(q[i], x.l[i], al);
     }
-};
+    return fmaf(65536.0f, (float)ah, fmaf(256.0f, (float)am, (float)al));
+}
 
-template <>
-struct XSource<false> {
-    const float *gx;
-    __device__ __forceinline__ void get(int u, float4 (&x)[8], float &sx) const
-    {
-        const float *p = gx + (int64_t)u * 32;
-#pragma unroll
-        for (int c = 0; c < 8; c++) x[c] = make_float4(p[4 * c], p[4 * c + 1], p[4 * c + 2], p[4 * c + 3]);
-        float s = 0.f;
-#pragma unroll
-        for (int c = 0; c < 8; c++) s += (x[c].x + x[c].y) + (x[c].z + x[c].w);
-        sx = s;
+template <int FMT, int XM>
+__device__ __forceinline__ float unit_dot(const Raw<FMT> &r, const XVals<XM> &x)
+{
+    if constexpr (FMT == FMT_Q4_0) {
+        uint32_t sel = realign_sel(r.s);
+        uint32_t q[4] = {perm(r.a.y, r.a.x, sel), perm(r.a.z, r.a.y, sel), perm(r.a.w, r.a.z, sel),
+                         perm(r.e, r.a.w, sel)};
+        float d = half_bits_to_float(__builtin_amdgcn_alignbyte(r.a.y, r.a.x, r.s));
+        if constexpr (XM != XM_I24) {
+            return d * fmaf(-8.0f, x.sx, nib_dot_f32(q, x.x));
+        } else {
+            return d * fmaf(-8.0f, x.sx, x.dx * nib_dot_i24(q, x));
+        }
+    } else if constexpr (FMT == FMT_Q8_0) {
+        uint32_t sel = realign_sel(r.s);
+        uint32_t q[8] = {perm(r.a.y, r.a.x, sel), perm(r.a.z, r.a.y, sel), perm(r.a.w, r.a.z, sel),
+                         perm(r.b.x, r.a.w, sel), perm(r.b.y, r.b.x, sel), perm(r.b.z, r.b.y, sel),
+                         perm(r.b.w, r.b.z, sel), perm(r.e, r.b.w, sel)};
+        float d = half_bits_to_float(__builtin_amdgcn_alignbyte(r.a.y, r.a.x, r.s));
+        if constexpr (XM != XM_I24) {
+            return d * fmaf(-128.0f, x.sx, byte_dot_f32(q, x.x));
+        } else {
+            return d * (x.dx * byte_dot_i24(q, x));
+        }
+    } else {
+        uint32_t sc, mn;
+        q4_k_scale_min(r.h.y, r.h.z, r.h.w, r.j, sc, mn);
+        float dsc = half_bits_to_float(r.h.x) * (float)sc;
+        float dmn = half_bits_to_float(r.h.x >> 16) * (float)mn;
+        uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        if constexpr (XM != XM_I24) {
+            return fmaf(dsc, nib_dot_f32(q, x.x), -dmn * x.sx);
+        } else {
+            return fmaf(dsc, x.dx * nib_dot_i24(q, x), -dmn * x.sx);
+        }
     }
-};
+}
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-template <int FMT, int R, int MODE, bool XLDS>
+// ---- the kernel -------------------------------------------------------------------
+
+struct GemvArgs {
+    const uint8_t *W[kMaxSeg];
+    float *y[kMaxSeg];
+    int rows[kMaxSeg];
+    int tile_end[kMaxSeg];  // inclusive prefix sums of tiles per matrix
+    int nseg;               // matrices in this launch (PLAIN) or 2 (GATEUP)
+    int ntiles;
+    const float *x;
+    int units;              // 32-weight units per row
+    int nsegs;              // 64-unit segments per row
+    int groups;             // G: R-row groups per tile
+    int x_lds_bytes;        // staged x, then the partial-sum buffers
+    int64_t row_bytes;
+};
+
+template <int FMT, int XM, int R, int P, int MODE>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args)
 {
-    extern __shared__ float4 lds[];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
+    extern __shared__ uint4 lds[];
+    constexpr int NM = MODE == MODE_GATEUP ? 2 : 1;
+    const int lane = threadIdx.x & 63;
+    // readfirstlane: the wave index is uniform, so tiles, rows and row base
+    // pointers live in SGPRs and the loads use a 32-bit per-lane offset
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int units = args.units;
+    const int nsegs = args.nsegs;
+    const int G = args.groups;
+    const int ipt = G * nsegs;  // items per tile, <= kWaves * P
+    const int TR = G * R;       // rows per tile
+    float *part = (float *)((char *)lds + args.x_lds_bytes);  // [2][NM][TR][nsegs]
 
-    XSource<XLDS> xs;
-    if constexpr (XLDS) {
-        float *lsx = (float *)(lds + units * 8);
-        for (int i = tid; i < units * 8; i += kThreads) {
-            int u = i >> 3, c = i & 7;
-            const float *g = args.x + (int64_t)i * 4;
-            lds[u * 8 + (c ^ (u & 7))] = make_float4(g[0], g[1], g[2], g[3]);
-        }
-        __syncthreads();
-        for (int u = tid; u < units; u += kThreads) {
-            const float4 *p = lds + u * 8;
-            float s = 0.f;
-#pragma unroll
-            for (int c = 0; c < 8; c++) {
-                float4 v = p[c ^ (u & 7)];
-                s += (v.x + v.y) + (v.z + v.w);
-            }
-            lsx[u] = s;
-        }
-        __syncthreads();
-        xs.lx = lds;
-        xs.lsx = lsx;
-    } else {
-        xs.gx = args.x;
-    }
-
-    const int nsegs = (units + 63) >> 6;
-    for (int task = blockIdx.x * kWaves + wave; task < args.ntasks; task += gridDim.x * kWaves) {
-        int seg = 0;
-        int tbase = 0;
+    // tile -> (matrix, first row)
+    auto locate = [&](int t, int &mseg, int &row0) {
+        int s = 0, base = 0;
         if constexpr (MODE == MODE_PLAIN) {
-            while (seg + 1 < args.nseg && task >= args.task_end[seg]) {
-                tbase = args.task_end[seg];
-                seg++;
+            while (s + 1 < args.nseg && t >= args.tile_end[s]) {
+                base = args.tile_end[s];
+                s++;
             }
         }
-        const int rows = args.rows[seg];
-        const int row0 = (task - tbase) * R;
-        constexpr int NM = MODE == MODE_GATEUP ? 2 : 1;
+        mseg = s;
+        row0 = (t - base) * TR;
+    };
 
-        float acc[NM][R];
+    // item slot p of this wave in tile t: item j = wave + 4p -> (group j / nsegs, segment j % nsegs)
+    auto issue_tile = [&](Raw<FMT>(&buf)[P][NM][R], int t) {
+        int mseg, row0;
+        locate(t, mseg, row0);
+        const int rows = args.rows[mseg];
+        // Every slot loads (an idle slot re-reads the tile's last item), so the
+        // number of loads per call is fixed and the wait counts stay exact.
 #pragma unroll
-        for (int m = 0; m < NM; m++)
-#pragma unroll
-            for (int r = 0; r < R; r++) acc[m][r] = 0.f;
-
-        for (int sg = 0; sg < nsegs; sg++) {
-            int u = sg * 64 + lane;
-            bool active = u < units;
-            int uc = active ? u : units - 1;
-            float4 x[8];
-            float sx;
-            xs.get(uc, x, sx);
+        for (int p = 0; p < P; p++) {
+            const int j = min(wave + kWaves * p, ipt - 1);
+            const int g = j / nsegs, sgm = j - g * nsegs;
+            int u = sgm * 64 + lane;
+            u = u < units ? u : units - 1;
+            const uint32_t off = unit_offset(FMT, (uint32_t)u);
 #pragma unroll
             for (int m = 0; m < NM; m++) {
-                const int mi = MODE == MODE_GATEUP ? m : seg;
-                const uint8_t *W = args.W[mi];
-                const int64_t bytes = args.bytes[mi];
+                const int mi = MODE == MODE_GATEUP ? m : mseg;
 #pragma unroll
                 for (int r = 0; r < R; r++) {
-                    int row = min(row0 + r, rows - 1);
-                    float v = unit_dot<FMT>(W, bytes, (int64_t)row * units + uc, x, sx);
-                    acc[m][r] += active ? v : 0.f;
+                    const int row = min(row0 + g * R + r, rows - 1);
+                    gbyte *rowp = (gbyte *)args.W[mi] + (int64_t)row * args.row_bytes;
+                    const uint32_t mis = (uint32_t)((uintptr_t)rowp & 3u);
+                    load_raw<FMT>(buf[p][m][r], rowp - mis, mis, off, (uint32_t)u);
                 }
             }
         }
+    };
 
+    // One tile = the workgroup's work between two barriers.
+    auto process_tile = [&](const Raw<FMT>(&buf)[P][NM][R], int t, int pb) {
+        float *pt = part + pb * (NM * TR * nsegs);
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            float s0 = wave_sum(acc[0][r]);
-            if constexpr (MODE == MODE_GATEUP) {
-                float s1 = wave_sum(acc[1][r]);
-                if (lane == 0 && row0 + r < rows) args.y[0][row0 + r] = silu(s0) * s1;
-            } else {
-                if (lane == 0 && row0 + r < rows) args.y[seg][row0 + r] = s0;
+        for (int p = 0; p < P; p++) {
+            const int j = wave + kWaves * p;
+            if (j < ipt) {
+                const int g = j / nsegs, sgm = j - g * nsegs;
+                const int u = sgm * 64 + lane;
+                const bool active = u < units;
+                XVals<XM> xv;
+                if constexpr (XM == XM_GF32) xv.load(args.x, active ? u : units - 1);
+                else xv.load(lds, units, active ? u : units - 1);
+#pragma unroll
+                for (int m = 0; m < NM; m++)
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        float v = unit_dot<FMT, XM>(buf[p][m][r], xv);
+                        float s0 = wave_sum(active ? v : 0.f);
+                        if (lane == 0) pt[(m * TR + g * R + r) * nsegs + sgm] = s0;
+                    }
             }
         }
+        __syncthreads();
+
+        // finish the tile's rows: sum the nsegs partials in segment order
+        int mseg, row0;
+        locate(t, mseg, row0);
+        const int rows = args.rows[mseg];
+        for (int rr = threadIdx.x; rr < TR; rr += kThreads) {
+            float s0 = 0.f;
+            for (int k = 0; k < nsegs; k++) s0 += pt[rr * nsegs + k];
+            if (row0 + rr < rows) {
+                if constexpr (MODE == MODE_GATEUP) {
+                    float s1 = 0.f;
+                    for (int k = 0; k < nsegs; k++) s1 += pt[(TR + rr) * nsegs + k];
+                    args.y[0][row0 + rr] = silu(s0) * s1;
+                } else {
+                    args.y[mseg][row0 + rr] = s0;
+                }
+            }
+        }
+    };
+
+    // The grid never exceeds the tile count, so every workgroup has a tile.
+    int t = blockIdx.x;
+    const int my_tiles = (args.ntiles - 1 - t) / (int)gridDim.x + 1;
+
+    Raw<FMT> cur[P][NM][R], nxt[P][NM][R];
+    float4 pre[kPreX];
+    if constexpr (XM != XM_GF32) x_preload(args.x, units, pre);
+    issue_tile(cur, t);
+    if constexpr (XM != XM_GF32) x_stage<FMT, XM>(args.x, units, lds, pre);
+    __syncthreads();
+
+    // All tiles but the last: the next tile's loads are issued (always) before
+    // the current one is decoded.  The partial buffers alternate.
+    int pb = 0;
+    for (int k = 1; k < my_tiles; k++) {
+        issue_tile(nxt, t + gridDim.x);
+        process_tile(cur, t, pb);
+        pb ^= 1;
+        t += gridDim.x;
+#pragma unroll
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int r = 0; r < R; r++) cur[p][m][r] = nxt[p][m][r];
     }
+    process_tile(cur, t, pb);
 }
 
-// ---- host side ---------------------------------------------------------------
+// ---- host side ---------------------------------------------------------------------
+
+// Activation mode and launch shape; environment overrides are read once:
+// HOLO_GEMV_XMODE=f32|i24, HOLO_GEMV_WG_PER_CU, HOLO_GEMV_ROWS=1|2|4.
+struct Tuning {
+    int xmode = XM_F32;
+    int wg_per_cu = 0;  // 0 = by grid size
+    int rows = 0;       // 0 = by shape
+    bool read = false;
+};
+static Tuning g_tune;
+
+static const Tuning &tuning()
+{
+    if (!g_tune.read) {
+        if (const char *e = getenv("HOLO_GEMV_XMODE")) g_tune.xmode = (e[0] == 'f') ? XM_F32 : XM_I24;
+        if (const char *e = getenv("HOLO_GEMV_WG_PER_CU")) g_tune.wg_per_cu = atoi(e) > 0 ? atoi(e) : 0;
+        if (const char *e = getenv("HOLO_GEMV_ROWS")) g_tune.rows = atoi(e);
+        g_tune.read = true;
+    }
+    return g_tune;
+}
 
 constexpr int kMaxLdsBytes = 64 * 1024;
 
-struct Tuning {
-    int max_wg_per_cu = 8;
-};
-static Tuning g_tuning;
-
-static int units_per_row(int fmt, int in_dim)
-{
-    if (fmt == FMT_Q4_K) return (in_dim / 256) * 8;
-    return in_dim / 32;
-}
-
-static int64_t row_bytes(int fmt, int in_dim)
-{
-    if (fmt == FMT_Q4_0) return (int64_t)(in_dim / 32) * 18;
-    if (fmt == FMT_Q8_0) return (int64_t)(in_dim / 32) * 34;
-    return (int64_t)(in_dim / 256) * 144;
-}
-
-template <int FMT, int R, int MODE>
+template <int FMT, int XM, int R, int P, int MODE>
 static void launch_t(GemvArgs &a)
 {
-    size_t lds = (size_t)a.units * (128 + 4);
-    int blocks = (a.ntasks + kWaves - 1) / kWaves;
-    int cap = num_cus() * g_tuning.max_wg_per_cu;
+    constexpr int NM = MODE == MODE_GATEUP ? 2 : 1;
+    size_t lds = (size_t)a.x_lds_bytes + sizeof(float) * 2 * NM * a.groups * R * a.nsegs;
+    // One workgroup per CU for small grids (fewer redundant x stagings), two
+    // once there are more than two tiles per CU (measured on MI355X).
+    int wpc = tuning().wg_per_cu;
+    if (wpc <= 0) wpc = a.ntiles <= 2 * num_cus() ? 1 : 2;
+    int blocks = a.ntiles;
+    int cap = num_cus() * wpc;
     if (blocks > cap) blocks = cap;
-    if (lds <= (size_t)kMaxLdsBytes)
-        hipLaunchKernelGGL((gemv_kernel<FMT, R, MODE, true>), dim3(blocks), dim3(kThreads), lds, stream(), a);
-    else
-        hipLaunchKernelGGL((gemv_kernel<FMT, R, MODE, false>), dim3(blocks), dim3(kThreads), 0, stream(), a);
+    hipLaunchKernelGGL((gemv_kernel<FMT, XM, R, P, MODE>), dim3(blocks), dim3(kThreads), lds, stream(), a);
     HOLO_LAUNCH_CHECK();
 }
 
-constexpr int kRows = 4;
+template <int FMT, int XM, int R, int MODE>
+static void launch_p(GemvArgs &a, int P)
+{
+    if (P <= 2) launch_t<FMT, XM, R, 2, MODE>(a);
+    else if (P == 3) launch_t<FMT, XM, R, 3, MODE>(a);
+    else launch_t<FMT, XM, R, 4, MODE>(a);
+}
+
+template <int FMT, int XM, int MODE>
+static void launch_r(GemvArgs &a, int R, int P)
+{
+    if (R <= 1) {
+        launch_p<FMT, XM, 1, MODE>(a, P);
+    } else if constexpr (MODE == MODE_GATEUP) {
+        launch_p<FMT, XM, 2, MODE>(a, P);  // two matrices per item: at most 2 rows
+    } else {
+        if (R == 2) launch_p<FMT, XM, 2, MODE>(a, P);
+        else launch_p<FMT, XM, 4, MODE>(a, P);
+    }
+}
 
 static bool check_ptr(const void *p, const char *what)
 {
@@ -300,43 +663,98 @@ static bool check_ptr(const void *p, const char *what)
     return true;
 }
 
+// Items per wave P and row groups per tile G for nsegs segments per row:
+// the tile holds G*nsegs <= 4P items; pick the fullest P in 2..4.
+static void tile_shape(int nsegs, int &P, int &G)
+{
+    P = 2;
+    G = 1;
+    double best = -1.0;
+    for (int p = 2; p <= 4; p++) {
+        int g = (kWaves * p) / nsegs;
+        if (g < 1) continue;
+        double util = (double)(g * nsegs) / (kWaves * p);
+        if (util > best + 1e-9) {
+            best = util;
+            P = p;
+            G = g;
+        }
+    }
+}
+
 // One launch over up to three matrices sharing x and in_dim.
 static void gemv_multi(int fmt, int mode, int nseg, const void *const *W, float *const *y, const int *rows,
                        const float *x, int in_dim)
 {
+    const Tuning &tn = tuning();
     GemvArgs a = {};
     a.units = units_per_row(fmt, in_dim);
+    a.row_bytes = row_bytes_of(fmt, in_dim);
+    a.nsegs = (a.units + 63) / 64;
     a.x = x;
     a.nseg = nseg;
-    int tasks = 0;
+    if (a.nsegs > 4 * kWaves) {
+        HOLO_REJECT("gemv: in_dim too large (at most 32 segments of 64 units per row)");
+        return;
+    }
+    // x staged in LDS when it fits (F32 needs 132 B per unit, I24 104 B),
+    // otherwise read by each lane from global memory.
+    int xm = tn.xmode;
+    const size_t budget = (size_t)kMaxLdsBytes - 4096;
+    if (xm == XM_F32 && (size_t)a.units * lds_bytes_per_unit<XM_F32>() > budget) xm = XM_I24;
+    if (xm == XM_I24 && (size_t)a.units * lds_bytes_per_unit<XM_I24>() > budget) xm = XM_GF32;
+    a.x_lds_bytes = xm == XM_F32   ? a.units * lds_bytes_per_unit<XM_F32>()
+                    : xm == XM_I24 ? a.units * lds_bytes_per_unit<XM_I24>()
+                                   : 0;
+    a.x_lds_bytes = (a.x_lds_bytes + 15) & ~15;
+    int P, G;
+    tile_shape(a.nsegs, P, G);
+    int total_rows = 0;
+    for (int s = 0; s < nseg; s++) total_rows += rows[s];
+    int R = tn.rows ? tn.rows : 1;
+    R = R <= 1 ? 1 : R <= 2 ? 2 : 4;
+    if (mode == MODE_GATEUP && R > 2) R = 2;
+    a.groups = G;
+    const int TR = G * R;
+    if (!check_ptr(x, "activation vector must be 4-byte aligned")) return;
+    int tiles = 0;
     for (int s = 0; s < nseg; s++) {
         if (!check_ptr(W[s], "weight matrix must be 4-byte aligned")) return;
         a.W[s] = (const uint8_t *)W[s];
         a.y[s] = y[s];
         a.rows[s] = rows[s];
-        a.bytes[s] = row_bytes(fmt, in_dim) * rows[s];
-        if (mode == MODE_PLAIN) tasks += (rows[s] + kRows - 1) / kRows;
-        a.task_end[s] = tasks;
+        if (mode == MODE_PLAIN) tiles += (rows[s] + TR - 1) / TR;
+        a.tile_end[s] = tiles;
     }
-    if (mode == MODE_GATEUP) tasks = (rows[0] + kRows - 1) / kRows;
-    a.ntasks = tasks;
-    if (tasks == 0) return;
+    if (mode == MODE_GATEUP) tiles = (rows[0] + TR - 1) / TR;
+    a.ntiles = tiles;
+    if (tiles == 0) return;
     if (a.units == 0) {
         // No complete block per row: every dot product is empty.
         for (int s = 0; s < (mode == MODE_GATEUP ? 1 : nseg); s++)
             HOLO_CHECK(hipMemsetAsync(y[s], 0, sizeof(float) * rows[s], stream()));
         return;
     }
-    if (fmt == FMT_Q4_0) {
-        if (mode == MODE_PLAIN) launch_t<FMT_Q4_0, kRows, MODE_PLAIN>(a);
-        else launch_t<FMT_Q4_0, kRows, MODE_GATEUP>(a);
-    } else if (fmt == FMT_Q8_0) {
-        if (mode == MODE_PLAIN) launch_t<FMT_Q8_0, kRows, MODE_PLAIN>(a);
-        else launch_t<FMT_Q8_0, kRows, MODE_GATEUP>(a);
-    } else {
-        if (mode == MODE_PLAIN) launch_t<FMT_Q4_K, kRows, MODE_PLAIN>(a);
-        else launch_t<FMT_Q4_K, kRows, MODE_GATEUP>(a);
+#define HOLO_DISPATCH(F)                                                             \
+    if (xm == XM_F32) {                                                              \
+        if (mode == MODE_PLAIN) launch_r<F, XM_F32, MODE_PLAIN>(a, R, P);            \
+        else launch_r<F, XM_F32, MODE_GATEUP>(a, R, P);                              \
+    } else if (xm == XM_GF32) {                                                      \
+        if (mode == MODE_PLAIN) launch_r<F, XM_GF32, MODE_PLAIN>(a, R, P);           \
+        else launch_r<F, XM_GF32, MODE_GATEUP>(a, R, P);                             \
+    } else {                                                                         \
+        if (mode == MODE_PLAIN) launch_r<F, XM_I24, MODE_PLAIN>(a, R, P);            \
+        else launch_r<F, XM_I24, MODE_GATEUP>(a, R, P);                              \
     }
+    if (fmt == FMT_Q4_0) {
+        HOLO_DISPATCH(FMT_Q4_0)
+    } else if (fmt == FMT_Q8_0) {
+        HOLO_DISPATCH(FMT_Q8_0)
+    } else {
+        HOLO_DISPATCH(FMT_Q4_K)
+    }
+#undef HOLO_DISPATCH
+    (void)total_rows;
 }
 
 static void gemv_one(int fmt, float *dst, const void *M, const float *v, int out_dim, int in_dim)
@@ -382,6 +800,19 @@ void cuda_matmul_q4_0(float *dst, const void *M, const float *v, int out_dim, in
 void cuda_matmul_q4_k(float *dst, const void *M, const float *v, int out_dim, int in_dim)
 {
     gemv_one(FMT_Q4_K, dst, M, v, out_dim, in_dim);
+}
+
+void holo_gemv_set_xmode(int xmode)
+{
+    tuning();
+    g_tune.xmode = xmode ? XM_I24 : XM_F32;
+}
+
+void holo_gemv_set_launch(int rows_per_item, int wg_per_cu)
+{
+    tuning();
+    g_tune.rows = rows_per_item > 0 ? rows_per_item : 0;
+    g_tune.wg_per_cu = wg_per_cu > 0 ? wg_per_cu : 0;
 }
 
 void holo_batched_qkv(float *q_out, float *k_out, float *v_out, const void *Wq, const void *Wk, const void *Wv,

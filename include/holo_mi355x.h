@@ -52,6 +52,24 @@ void holo_graph_destroy(void *graph_exec);
  * The reference's gpu_matmul switch (src/ai/llm_cuda.c:140-163) as one call. */
 void holo_matmul(float *dst, const void *M, const float *v, int out_dim, int in_dim, int type);
 
+/* ---- GEMV activation mode ------------------------------------------------------
+ * HOLO_XMODE_F32 (default): every weight is multiplied by the fp32 activation
+ * itself (v_cvt_f32_ubyte + FMA).  HOLO_XMODE_I24: activations are held per
+ * 32-block as 24-bit fixed point, xi = rint(x * 127*65536/amax),
+ * |x - d*xi| <= amax*2^-23, in three int8 planes; each block's integer dots
+ * run on v_dot4_i32_i8 and are exact.  Both accumulate across blocks in
+ * fp32.  Rows longer than the LDS staging holds (in_dim > 14880 for F32)
+ * switch to I24, and beyond 18880 to fp32 read from global memory.  Applies
+ * to every GEMV entry point.                                                */
+#define HOLO_XMODE_F32 0
+#define HOLO_XMODE_I24 1
+void holo_gemv_set_xmode(int xmode);
+/* Launch shape of the GEMV kernels: rows per work item (1, 2 or 4; 0 = the
+ * default, 1) and workgroups per CU (0 = the default: 1 when the grid has at
+ * most 2 tiles per CU, else 2).  A tuning knob; the defaults are the
+ * measured best on MI355X.                                                 */
+void holo_gemv_set_launch(int rows_per_item, int wg_per_cu);
+
 /* ---- dequantisation ---------------------------------------------------------
  * dst[n] = the fp32 weights of n/QK blocks, bit-identical to the reference
  * CPU routines dequantize_row_q8_0 / q4_0 / q4_k / q6_k

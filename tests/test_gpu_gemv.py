@@ -45,11 +45,16 @@ def _run(holo, synth, qtype, out_dim, in_dim, seed):
     return W, x, dy.download(np.float32, out_dim)
 
 
+@pytest.mark.parametrize("xmode", [1, 0], ids=["i24", "f32"])
 @pytest.mark.parametrize("qtype,out_dim,in_dim", CASES,
                          ids=[f"{NAMES[t]}-{o}x{i}" for t, o, i in CASES])
-def test_gemv_parity(holo, synth, oracle, qtype, out_dim, in_dim):
-    print(f"case {NAMES[qtype]} {out_dim}x{in_dim}", flush=True)
-    W, x, got = _run(holo, synth, qtype, out_dim, in_dim, seed=out_dim * 7919 + in_dim)
+def test_gemv_parity(holo, synth, oracle, qtype, out_dim, in_dim, xmode):
+    print(f"case {NAMES[qtype]} {out_dim}x{in_dim} xmode={xmode}", flush=True)
+    holo.lib().holo_gemv_set_xmode(xmode)
+    try:
+        W, x, got = _run(holo, synth, qtype, out_dim, in_dim, seed=out_dim * 7919 + in_dim)
+    finally:
+        holo.lib().holo_gemv_set_xmode(1)
     want = oracle.matmul(qtype, W, x, out_dim, in_dim)
     truth = oracle.truth(qtype, W, x, out_dim, in_dim)
     e_n, e_r = normwise_err(got, want), max_rel_err(got, want)
