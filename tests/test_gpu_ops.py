@@ -1,0 +1,273 @@
+"""GPU parity of the fused multi-GEMVs, the prefill path and the remaining
+boundary ops, through the C ABI.
+
+Bars:
+  * fused GEMVs: as the single GEMVs (relative error 1e-3 normwise and
+    elementwise), against the oracle's per-matrix products;
+  * prefill: the quantiser and the int8 MFMA product are specified bit for
+    bit (oracle_quantize_act_q8_0 / oracle_gemm_q4_0_q8_0): exact equality;
+  * non-matmul ops: fp32 arithmetic against float64 numpy, 1e-5 normwise
+    (transcendentals: 1e-5 absolute on bounded outputs).
+"""
+import numpy as np
+import pytest
+
+from oracle.oracle import max_rel_err, normwise_err
+
+pytestmark = pytest.mark.gpu
+
+Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
+QK = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
+
+
+def up(holo, a):
+    return holo.DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+def down(buf, n, dtype=np.float32):
+    return buf.download(dtype, n)
+
+
+# ---- fused multi-GEMVs ---------------------------------------------------------------
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K], ids=["q8_0", "q4_0", "q4_k"])
+@pytest.mark.parametrize("dims", [(4096, 1024, 4096), (512, 512, 512), (96, 32, 256 * 3)], ids=str)
+def test_batched_qkv(holo, synth, oracle, t, dims):
+    q_dim, kv_dim, in_dim = dims
+    if in_dim % QK[t]:
+        pytest.skip("in_dim not a multiple of the block")
+    print(f"case qkv type {t} {dims}", flush=True)
+    Wq, Wk, Wv = (synth.blocks(t, r, in_dim, seed=s) for r, s in ((q_dim, 1), (kv_dim, 2), (kv_dim, 3)))
+    x = synth.normal(in_dim, seed=4)
+    dW = [up(holo, w) for w in (Wq, Wk, Wv)]
+    dx = up(holo, x)
+    dy = [holo.DeviceBuffer(4 * r) for r in (q_dim, kv_dim, kv_dim)]
+    if t == Q8_0:
+        holo.lib().cuda_batched_qkv_q8_0(dy[0].ptr, dy[1].ptr, dy[2].ptr, dW[0].ptr, dW[1].ptr, dW[2].ptr,
+                                         dx.ptr, q_dim, kv_dim, in_dim)
+    else:
+        holo.lib().holo_batched_qkv(dy[0].ptr, dy[1].ptr, dy[2].ptr, dW[0].ptr, dW[1].ptr, dW[2].ptr,
+                                    dx.ptr, q_dim, kv_dim, in_dim, t)
+    holo.lib().cuda_sync()
+    holo.check("qkv")
+    for W, y, r in zip((Wq, Wk, Wv), dy, (q_dim, kv_dim, kv_dim)):
+        want = oracle.matmul(t, W, x, r, in_dim)
+        got = down(y, r)
+        assert normwise_err(got, want) <= 1e-3 and max_rel_err(got, want) <= 1e-3
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K], ids=["q8_0", "q4_0", "q4_k"])
+@pytest.mark.parametrize("dims", [(11008, 4096), (300, 512)], ids=str)
+def test_batched_gate_up(holo, synth, oracle, t, dims):
+    ffn, in_dim = dims
+    print(f"case gate_up type {t} {dims}", flush=True)
+    W1 = synth.blocks(t, ffn, in_dim, seed=11)
+    W3 = synth.blocks(t, ffn, in_dim, seed=12)
+    x = synth.normal(in_dim, seed=13)
+    d1, d3, dx, dy = up(holo, W1), up(holo, W3), up(holo, x), holo.DeviceBuffer(4 * ffn)
+    if t == Q8_0:
+        holo.lib().cuda_batched_ffn_gate_up_q8_0(dy.ptr, d1.ptr, d3.ptr, dx.ptr, ffn, in_dim)
+    else:
+        holo.lib().holo_batched_ffn_gate_up(dy.ptr, d1.ptr, d3.ptr, dx.ptr, ffn, in_dim, t)
+    holo.lib().cuda_sync()
+    holo.check("gate_up")
+    g = oracle.matmul(t, W1, x, ffn, in_dim)
+    u = oracle.matmul(t, W3, x, ffn, in_dim)
+    want = oracle.silu_mul(g, u)
+    got = down(dy, ffn)
+    assert normwise_err(got, want) <= 1e-3
+    assert max_rel_err(got, want) <= 1e-3
+
+
+def test_null_matrix_writes_zeros(holo):
+    """matmul_q with M == NULL writes zeros (llm.c:772-775)."""
+    dy = up(holo, np.full(64, 7.0, np.float32))
+    dx = up(holo, np.ones(128, np.float32))
+    holo.lib().cuda_matmul_q4_0(dy.ptr, None, dx.ptr, 64, 128)
+    holo.lib().cuda_sync()
+    assert np.all(down(dy, 64) == 0)
+
+
+# ---- prefill ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,k", [(3, 64), (64, 4096), (512, 4096), (512, 11008)], ids=str)
+def test_quantize_act_bit_exact(holo, synth, oracle, rows, k):
+    print(f"case quantize {rows}x{k}", flush=True)
+    X = synth.normal(rows * k, seed=rows + k).reshape(rows, k)
+    X[0, :32] = 0.0
+    dX = up(holo, X)
+    dq = holo.DeviceBuffer(rows * (k // 32) * 34)
+    holo.lib().holo_quantize_act_q8_0(dq.ptr, dX.ptr, rows, k)
+    holo.lib().cuda_sync()
+    holo.check("quantize")
+    assert np.array_equal(down(dq, rows * (k // 32) * 34, np.uint8), oracle.quantize_act_q8_0(X))
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 16, 32), (64, 64, 256), (77, 150, 4096), (512, 11008, 4096),
+                                   (512, 4096, 11008)], ids=str)
+def test_gemm_q4_0_q8_0_bit_exact(holo, synth, oracle, M, N, K):
+    print(f"case gemm {M}x{N}x{K}", flush=True)
+    W = synth.blocks(Q4_0, N, K, seed=M + N)
+    Xq = oracle.quantize_act_q8_0(synth.normal(M * K, seed=K).reshape(M, K))
+    dW, dXq, dY = up(holo, W), up(holo, Xq), holo.DeviceBuffer(4 * M * N)
+    holo.lib().holo_gemm_q4_0_q8_0(dY.ptr, dW.ptr, dXq.ptr, M, N, K)
+    holo.lib().cuda_sync()
+    holo.check("gemm")
+    got = down(dY, M * N).reshape(M, N)
+    # the oracle is checked on a row subset at the full sizes (CPU time)
+    rows = slice(0, min(M, 24))
+    want = oracle.gemm_q4_0_q8_0(W, Xq.reshape(M, -1)[rows].copy().reshape(-1), rows.stop, N, K)
+    assert np.array_equal(got[rows].view(np.uint32), want.view(np.uint32))
+
+
+def test_matmul_batch_dispatch(holo, synth, oracle):
+    """M >= 64: quantise + MFMA GEMM; M < 64: one fp32 GEMV per row."""
+    N, K = 256, 512
+    W = synth.blocks(Q4_0, N, K, seed=1)
+    dW = up(holo, W)
+    for M in (8, 64):
+        X = synth.normal(M * K, seed=M).reshape(M, K)
+        dX, dY = up(holo, X), holo.DeviceBuffer(4 * M * N)
+        holo.lib().holo_matmul_batch_q4_0(dY.ptr, dW.ptr, dX.ptr, M, N, K, None)
+        holo.lib().cuda_sync()
+        holo.check("batch")
+        got = down(dY, M * N).reshape(M, N)
+        if M < 64:
+            want = np.stack([oracle.matmul(Q4_0, W, X[m], N, K) for m in range(M)])
+            assert normwise_err(got, want) <= 1e-3
+        else:
+            want = oracle.gemm_q4_0_q8_0(W, oracle.quantize_act_q8_0(X), M, N, K)
+            assert np.array_equal(got, want)
+
+
+# ---- remaining boundary ops --------------------------------------------------------------
+
+def test_vector_and_activation_ops(holo, synth):
+    n = 5000
+    a, b = synth.normal(n, seed=1), synth.normal(n, seed=2)
+    da, db, dd = up(holo, a), up(holo, b), holo.DeviceBuffer(4 * n)
+    L = holo.lib()
+    L.cuda_vec_add(dd.ptr, da.ptr, db.ptr, n); L.cuda_sync()
+    assert np.array_equal(down(dd, n), a + b)
+    L.cuda_vec_mul(dd.ptr, da.ptr, db.ptr, n); L.cuda_sync()
+    assert np.array_equal(down(dd, n), a * b)
+    L.cuda_vec_scale(dd.ptr, da.ptr, 0.5, n); L.cuda_sync()
+    assert np.array_equal(down(dd, n), a * np.float32(0.5))
+    dot = L.cuda_vec_dot(da.ptr, db.ptr, n)
+    assert abs(dot - float(np.dot(a.astype(np.float64), b))) < 1e-3
+    a64 = a.astype(np.float64)
+    silu = a64 / (1 + np.exp(-a64))
+    L.cuda_silu_mul(dd.ptr, da.ptr, db.ptr, n); L.cuda_sync()
+    assert normwise_err(down(dd, n), silu * b) < 1e-5
+    dc = up(holo, a); L.cuda_silu(dc.ptr, n); L.cuda_sync()
+    assert normwise_err(down(dc, n), silu) < 1e-5
+    dc = up(holo, a); L.cuda_gelu(dc.ptr, n); L.cuda_sync()
+    gelu = 0.5 * a64 * (1 + np.tanh(0.7978845608 * (a64 + 0.044715 * a64 ** 3)))
+    assert normwise_err(down(dc, n), gelu) < 1e-5
+    dc = up(holo, a); L.cuda_relu(dc.ptr, n); L.cuda_sync()
+    assert np.array_equal(down(dc, n), np.maximum(a, 0))
+    holo.check("vector ops")
+
+
+def test_norm_softmax_argmax(holo, synth):
+    n = 4096
+    x, w = synth.normal(n, seed=3), synth.normal(n, seed=4)
+    dx, dw, dd = up(holo, x), up(holo, w), holo.DeviceBuffer(4 * n)
+    L = holo.lib()
+    L.cuda_rms_norm(dd.ptr, dx.ptr, dw.ptr, n, 1e-5); L.cuda_sync()
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt(np.mean(x64 ** 2) + 1e-5) * w
+    assert normwise_err(down(dd, n), want) < 1e-5
+    L.cuda_layer_norm(dd.ptr, dx.ptr, dw.ptr, None, n, 1e-5); L.cuda_sync()   # the reference's layer norm = RMS norm
+    assert normwise_err(down(dd, n), want) < 1e-5
+    L.cuda_softmax(dd.ptr, dx.ptr, n); L.cuda_sync()
+    e = np.exp(x64 - x64.max())
+    assert normwise_err(down(dd, n), e / e.sum()) < 1e-5
+    v = synth.normal(32000, seed=5)
+    v[12345] = 99.0
+    v[20000] = 99.0
+    dvv = up(holo, v)
+    assert L.cuda_argmax(dvv.ptr, 32000) == 12345              # first index of the maximum
+    holo.check("norm/softmax/argmax")
+
+
+def test_attention_and_rope(holo, synth):
+    L = holo.lib()
+    hd, nh, nkv, kv_len = 128, 8, 2, 37
+    q = synth.normal(nh * hd, seed=6)
+    kc = synth.normal(kv_len * nkv * hd, seed=7)
+    vc = synth.normal(kv_len * nkv * hd, seed=8)
+    dq, dk, dv, dd = up(holo, q), up(holo, kc), up(holo, vc), holo.DeviceBuffer(4 * nh * hd)
+    L.cuda_multi_head_attention(dd.ptr, dq.ptr, dk.ptr, dv.ptr, kv_len, hd, nh, nkv); L.cuda_sync()
+    K = kc.reshape(kv_len, nkv, hd).astype(np.float64)
+    V = vc.reshape(kv_len, nkv, hd).astype(np.float64)
+    want = np.zeros((nh, hd))
+    for h in range(nh):
+        g = h // (nh // nkv)
+        s = K[:, g, :] @ q[h * hd:(h + 1) * hd] / np.sqrt(hd)
+        p = np.exp(s - s.max()); p /= p.sum()
+        want[h] = p @ V[:, g, :]
+    assert normwise_err(down(dd, nh * hd), want.ravel()) < 1e-5
+    datt = holo.DeviceBuffer(4 * kv_len)
+    L.cuda_attention_single(dd.ptr, dq.ptr, dk.ptr, dv.ptr, datt.ptr, kv_len, hd, 1, nkv * hd); L.cuda_sync()
+    s = K[:, 1, :] @ q[:hd] / np.sqrt(hd); p = np.exp(s - s.max()); p /= p.sum()
+    assert normwise_err(down(dd, hd), p @ V[:, 1, :]) < 1e-5
+    # RoPE on pairs (i, i + hd/2)
+    kk = synth.normal(nkv * hd, seed=9)
+    dq2, dk2 = up(holo, q), up(holo, kk)
+    pos, base = 17, 10000.0
+    L.cuda_rope_apply(dq2.ptr, dk2.ptr, pos, hd, nh, nkv, base); L.cuda_sync()
+
+    def rope(a, nheads):
+        a = a.reshape(nheads, hd).astype(np.float64).copy()
+        i = np.arange(hd // 2)
+        th = pos / base ** (2 * i / hd)
+        c, s_ = np.cos(th), np.sin(th)
+        x0, x1 = a[:, :hd // 2].copy(), a[:, hd // 2:].copy()
+        a[:, :hd // 2], a[:, hd // 2:] = x0 * c - x1 * s_, x0 * s_ + x1 * c
+        return a.ravel()
+    assert normwise_err(down(dq2, nh * hd), rope(q, nh)) < 1e-5
+    assert normwise_err(down(dk2, nkv * hd), rope(kk, nkv)) < 1e-5
+    # attention_scores / attention_apply
+    S, T = 3, 5
+    Q = synth.normal(S * hd, seed=10).reshape(S, hd)
+    Kt = synth.normal(T * hd, seed=11).reshape(T, hd)
+    ds = holo.DeviceBuffer(4 * S * T)
+    dQ, dKt = up(holo, Q), up(holo, Kt)   # keep the buffers alive across the calls
+    L.cuda_attention_scores(ds.ptr, dQ.ptr, dKt.ptr, S, T, hd, 0.125); L.cuda_sync()
+    sc = Q.astype(np.float64) @ Kt.T * 0.125
+    assert normwise_err(down(ds, S * T), sc.ravel()) < 1e-5
+    do = holo.DeviceBuffer(4 * S * hd)
+    L.cuda_attention_apply(do.ptr, ds.ptr, dKt.ptr, S, T, hd); L.cuda_sync()
+    assert normwise_err(down(do, S * hd), (down(ds, S * T).reshape(S, T) @ Kt).ravel()) < 1e-5
+    holo.check("attention/rope")
+
+
+@pytest.mark.parametrize("t", [0, 1, Q8_0, Q4_0, Q6_K], ids=["f32", "f16", "q8_0", "q4_0", "q6_k"])
+def test_embeddings_and_dense_gemv(holo, synth, oracle, t):
+    dim, vocab = 512, 40
+    if t == 0:
+        E = synth.normal(vocab * dim, seed=1)
+        rows = E.reshape(vocab, dim)
+    elif t == 1:
+        rows16 = (synth.normal(vocab * dim, seed=1) * np.float32(0.1)).astype(np.float16)
+        E = rows16.view(np.uint16)
+        rows = rows16.astype(np.float32).reshape(vocab, dim)
+    else:
+        E = synth.blocks(t, vocab, dim, seed=2)
+        rows = oracle.dequant(t, E, vocab * dim).reshape(vocab, dim)
+    dE, dd = up(holo, E), holo.DeviceBuffer(4 * dim)
+    fn = {0: "cuda_get_embedding_f32", 1: "cuda_get_embedding_f16", Q8_0: "cuda_get_embedding_q8_0",
+          Q4_0: "cuda_get_embedding_q4_0", Q6_K: "cuda_get_embedding_q6_k"}[t]
+    for tok in (0, 7, vocab - 1):
+        getattr(holo.lib(), fn)(dd.ptr, dE.ptr, tok, dim, vocab)
+        holo.lib().cuda_sync()
+        assert np.array_equal(down(dd, dim), rows[tok]), tok        # bit-exact dequant of one row
+    if t in (0, 1, Q6_K):
+        x = synth.normal(dim, seed=3)
+        dx, dy = up(holo, x), holo.DeviceBuffer(4 * vocab)
+        holo.lib().holo_matmul(dy.ptr, dE.ptr, dx.ptr, vocab, dim, t)
+        holo.lib().cuda_sync()
+        want = rows.astype(np.float64) @ x
+        assert normwise_err(down(dy, vocab), want) < 1e-5
+    holo.check("embedding")
