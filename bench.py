@@ -1,29 +1,35 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized-matmul hot path on one MI355X.
 
-Workload ("Q4_0 GEMV at Llama-2-7B layer shapes,
-batch 1"): one step = the 7 Q4_0 GEMVs of one Llama-2-7B layer
+Headline ("Q4_0 GEMV at Llama-2-7B layer shapes,
+batch 1"): one step = the 7 Q4_0 GEMVs of one Llama-2-7B layer,
     q, k, v, o  4096 x 4096      gate, up  11008 x 4096      down  4096 x 11008
-= 113,836,032 weight bytes, through the drop-in entry point cuda_matmul_q4_0.
-Steps rotate over `--layers` distinct synthetic layers (default 32, 3.64 GB,
-far above the 256 MB MALL) so every step streams its weights from HBM.
-Inputs are resident in HBM before timing starts.
+= 113,836,032 weight bytes, issued as a decode loop on MI355X issues them:
+holo_batched_qkv (q, k, v in one launch), cuda_matmul_q4_0 (o),
+holo_batched_ffn_gate_up (gate and up in one launch, silu(g)*u epilogue) and
+cuda_matmul_q4_0 (down), the four launches of a layer captured in one HIP
+graph.  Steps rotate over --layers distinct synthetic layers (default 32,
+3.64 GB, far above the 256 MB MALL), so each step streams its weights from
+HBM; all inputs are resident in HBM before timing starts.
 
-Printed: ONE JSON line with
-    value        aggregate weight GB/s over the K timed steps (HIP events on the
-                 library stream around the whole timed region)
-    roofline     dominant kernel = the Q4_0 GEMV kernel; achieved = algorithmic
-                 weight bytes per launch / mean launch duration, the durations
-                 measured with HIP events around each launch in a second pass
-    cpu_baseline the reference's own CPU path (matmul_q of src/ai/llm.c,
-                 compiled from the reference sources into oracle/_ref/ with its
-                 release flags), Q4_0 branch = single-threaded scalar code, on a
-                 bounded sample of the same layer shapes
-    extra        config-1/3/5 figures (Q8_0 and Q4_K GEMV GB/s, the full 7B
-                 decode step's matmul time)
+The printed JSON line carries
+  value         aggregate weight GB/s over the K timed steps (HIP events on the
+                library stream around the timed region)
+  roofline      dominant kernel = the fused gate/up Q4_0 GEMV (50,724,864 weight
+                bytes per launch); achieved = those bytes / its mean launch
+                duration, measured with HIP events around each launch in a
+                second, identical pass; traffic = HBM bytes per launch from the
+                committed PMC summary profiles/traffic_q4_0_gateup_<mode>.json
+  cpu_baseline  the reference's own CPU path: matmul_q (src/ai/llm.c:770),
+                compiled from the reference sources into oracle/_ref/ with its
+                release flags; the Q4_0 branch is single-threaded scalar code;
+                a bounded sample of the same layer
+  extra         the unfused drop-in layer (7 cuda_matmul_q4_0 calls), configs
+                1 and 3 (Q8_0 4096x4096; Q4_K Llama-3-8B FFN), config 4 (batched
+                prefill GEMM, int8 MFMA TOP/s), config 5 (full synthetic
+                Llama-2-7B Q4_0 decode step: end-to-end and matmuls-only ms)
 
-Only the CPU-baseline leg touches oracle/ (the reference build under
-oracle/_ref, or the oracle port when that is absent).
+Only the CPU-baseline leg touches oracle/.
 """
 from __future__ import annotations
 
@@ -43,119 +49,251 @@ sys.path.insert(0, str(ROOT / "google-classic_amd"))
 import holo_mi355x as holo  # noqa: E402
 from holo_mi355x import synth  # noqa: E402
 
-HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
 Q4_0, Q8_0, Q4_K = holo.TYPE_Q4_0, holo.TYPE_Q8_0, holo.TYPE_Q4_K
 BASE_SEED = 20251201
+DIM, FFN, VOCAB = 4096, 11008, 32000
 
 # Llama-2-7B layer: (name, out_dim, in_dim)
 LAYER = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
          ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
+CONFIG1 = [("w", 4096, 4096)]                             # Q8_0 GEMV
+CONFIG3 = [("gate", 14336, 4096), ("down", 4096, 14336)]  # Q4_K, Llama-3-8B FFN
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-# BASELINE configs 1 and 3
-CONFIG1 = [("w", 4096, 4096)]                          # Q8_0 GEMV 4096x4096
-CONFIG3 = [("gate", 14336, 4096), ("down", 4096, 14336)]  # Q4_K, Llama-3-8B FFN
+def weight_bytes(qtype, shapes):
+    return sum(holo.row_bytes(qtype, i) * o for _, o, i in shapes)
 
 
-class Layer:
+class Mats:
     """One set of synthetic weight matrices, resident in HBM."""
 
-    def __init__(self, qtype: int, idx: int, config: int, shapes=LAYER):
-        self.shapes = shapes
-        self.qtype = qtype
-        self.mats = []
+    def __init__(self, qtype, idx, config, shapes):
+        self.shapes, self.qtype = shapes, qtype
+        self.buf = {}
         for m, (name, out_dim, in_dim) in enumerate(shapes):
-            seed = synth.tensor_seed(BASE_SEED, config, idx, m)
-            host = synth.blocks(qtype, out_dim, in_dim, seed)
-            self.mats.append((name, out_dim, in_dim, holo.DeviceBuffer.from_array(host)))
-            del host
-
-    @staticmethod
-    def weight_bytes(qtype: int, shapes=LAYER) -> int:
-        return sum(holo.row_bytes(qtype, i) * o for _, o, i in shapes)
+            host = synth.blocks(qtype, out_dim, in_dim, synth.tensor_seed(BASE_SEED, config, idx, m))
+            self.buf[name] = holo.DeviceBuffer.from_array(host)
 
 
-def run_layer(lib, fn, layer: Layer, xs, ys, per_launch_events=None):
-    for j, (name, out_dim, in_dim, W) in enumerate(layer.mats):
-        if per_launch_events is not None:
-            lib.holo_event_record(per_launch_events[j][0])
-        fn(ys[out_dim].ptr, W.ptr, xs[in_dim].ptr, out_dim, in_dim)
-        if per_launch_events is not None:
-            lib.holo_event_record(per_launch_events[j][1])
+class Acts:
+    """Activation vectors in HBM: inputs x<n>, outputs y<n>, q/k/v/h scratch."""
+
+    def __init__(self):
+        self.b = {}
+        for n in (DIM, FFN, 14336):
+            self.b[f"x{n}"] = holo.DeviceBuffer.from_array(synth.normal(n, n))
+        for n in (DIM, FFN, 14336, VOCAB):
+            self.b[f"y{n}"] = holo.DeviceBuffer(4 * n)
+        for n in ("q", "k", "v", "h"):
+            self.b[n] = holo.DeviceBuffer(4 * FFN)
+
+    def __getitem__(self, k):
+        return self.b[k].ptr
 
 
-def gemv_bench(lib, qtype, layers, steps, warmup, xs, ys):
-    """Returns (ms_per_step, GB/s over the timed region, mean per-launch us, bytes/launch)."""
-    fn = {Q4_0: lib.cuda_matmul_q4_0, Q8_0: lib.cuda_matmul_q8_0, Q4_K: lib.cuda_matmul_q4_k}[qtype]
-    nL = len(layers)
+# ---- layer step ------------------------------------------------------------------------
+
+def layer_fused(lib, L, A, ev=None):
+    """The 4 launches of a layer; `ev` = (start, stop) event pairs per launch."""
+    b = L.buf
+    calls = [
+        lambda: lib.holo_batched_qkv(A["q"], A["k"], A["v"], b["q"].ptr, b["k"].ptr, b["v"].ptr, A["x4096"],
+                                     DIM, DIM, DIM, Q4_0),
+        lambda: lib.cuda_matmul_q4_0(A["y4096"], b["o"].ptr, A["v"], DIM, DIM),
+        lambda: lib.holo_batched_ffn_gate_up(A["h"], b["gate"].ptr, b["up"].ptr, A["x4096"], FFN, DIM, Q4_0),
+        lambda: lib.cuda_matmul_q4_0(A["y4096"], b["down"].ptr, A["h"], DIM, FFN),
+    ]
+    for j, c in enumerate(calls):
+        if ev:
+            lib.holo_event_record(ev[j][0])
+        c()
+        if ev:
+            lib.holo_event_record(ev[j][1])
+
+
+def layer_unfused(lib, L, A):
+    """The reference decode loop's pattern: one cuda_matmul_q4_0 per matrix."""
+    for name, o, i in LAYER:
+        lib.cuda_matmul_q4_0(A[f"y{o}"], L.buf[name].ptr, A[f"x{i}"], o, i)
+
+
+def capture(lib, fn):
+    if lib.holo_graph_begin() != 0:
+        raise holo.HoloError("graph capture failed to start")
+    fn()
+    g = lib.holo_graph_end()
+    holo.check("graph capture")
+    if not g:
+        raise holo.HoloError("graph instantiation failed")
+    return g
+
+
+def time_graphs(lib, graphs, steps, warmup):
+    n = len(graphs)
     for i in range(warmup):
-        run_layer(lib, fn, layers[i % nL], xs, ys)
+        lib.holo_graph_launch(graphs[i % n])
     lib.cuda_sync()
     ev = holo.Events()
     ev.start()
     for i in range(steps):
-        run_layer(lib, fn, layers[(warmup + i) % nL], xs, ys)
-    total_ms = ev.stop()
+        lib.holo_graph_launch(graphs[(warmup + i) % n])
+    ms = ev.stop()
     lib.cuda_sync()
-    holo.check("timed region")
-    bytes_step = Layer.weight_bytes(qtype, layers[0].shapes)
-    gbs = steps * bytes_step / (total_ms * 1e-3) / 1e9
+    ev.close()
+    holo.check("timed graphs")
+    return ms
 
-    # Second pass: events around every launch (kernel durations).
-    pairs = [(lib.holo_event_create(), lib.holo_event_create()) for _ in layers[0].shapes]
+
+def mean_launch_us(lib, layers, A, steps, which):
+    """Mean duration (HIP events around each launch) of launch index `which`."""
+    pairs = [(lib.holo_event_create(), lib.holo_event_create()) for _ in range(4)]
     durs = []
     for i in range(steps):
-        run_layer(lib, fn, layers[i % nL], xs, ys, per_launch_events=pairs)
+        layer_fused(lib, layers[i % len(layers)], A, ev=pairs)
         lib.cuda_sync()
-        durs.extend(lib.holo_event_elapsed_ms(a, b) for a, b in pairs)
+        durs.append(lib.holo_event_elapsed_ms(*pairs[which]))
     for a, b in pairs:
         lib.holo_event_destroy(a)
         lib.holo_event_destroy(b)
+    holo.check("per-launch pass")
+    return 1e3 * statistics.mean(durs)
+
+
+def single_gemv_gbs(lib, qtype, sets, steps):
+    """Back-to-back launches of one config's matrices, rotating over copies."""
+    fn = {Q4_0: lib.cuda_matmul_q4_0, Q8_0: lib.cuda_matmul_q8_0, Q4_K: lib.cuda_matmul_q4_k}[qtype]
+    A = sets["acts"]
+
+    def run(k):
+        s = sets["mats"][k % len(sets["mats"])]
+        for name, o, i in s.shapes:
+            fn(A[f"y{o}"], s.buf[name].ptr, A[f"x{i}"], o, i)
+    for k in range(4):
+        run(k)
+    lib.cuda_sync()
+    ev = holo.Events()
+    ev.start()
+    for k in range(steps):
+        run(k)
+    ms = ev.stop()
     ev.close()
-    mean_us = 1e3 * sum(durs) / len(durs)
-    return total_ms / steps, gbs, mean_us, bytes_step / len(layers[0].shapes)
+    holo.check("single gemv")
+    b = weight_bytes(qtype, sets["mats"][0].shapes)
+    return steps * b / (ms * 1e-3) / 1e9, ms * 1e3 / (steps * len(sets["mats"][0].shapes))
 
 
-def cpu_baseline(qtype: int, budget_s: float) -> dict:
-    """The reference CPU path on the same layer shapes (bounded sample)."""
+# ---- config 5: full decode step ----------------------------------------------------------
+
+def decode_step(lib, layers, head, A, ones, matmuls_only):
+    """Synthetic Llama-2-7B decode step at position 0: RoPE is the identity and
+    attention over one cached position returns v, so per layer
+      xb = rms(x); q,k,v = W.xb; x += Wo.v; xb = rms(x); h = silu(W1.xb)*(W3.xb);
+      x += W2.h
+    and after the layers logits = Wout.rms(x).  `matmuls_only` issues the same
+    GEMVs on the same buffers without the norms and residual adds."""
+    x, xb = A["x4096"], A["y4096"]
+    for L in layers:
+        b = L.buf
+        if not matmuls_only:
+            lib.cuda_rms_norm(xb, x, ones.ptr, DIM, 1e-5)
+        lib.holo_batched_qkv(A["q"], A["k"], A["v"], b["q"].ptr, b["k"].ptr, b["v"].ptr, xb, DIM, DIM, DIM, Q4_0)
+        lib.cuda_matmul_q4_0(A["y11008"], b["o"].ptr, A["v"], DIM, DIM)
+        if not matmuls_only:
+            lib.cuda_vec_add(x, x, A["y11008"], DIM)
+            lib.cuda_rms_norm(xb, x, ones.ptr, DIM, 1e-5)
+        lib.holo_batched_ffn_gate_up(A["h"], b["gate"].ptr, b["up"].ptr, xb, FFN, DIM, Q4_0)
+        lib.cuda_matmul_q4_0(A["y11008"], b["down"].ptr, A["h"], DIM, FFN)
+        if not matmuls_only:
+            lib.cuda_vec_add(x, x, A["y11008"], DIM)
+    if not matmuls_only:
+        lib.cuda_rms_norm(xb, x, ones.ptr, DIM, 1e-5)
+    lib.cuda_matmul_q8_0(A["y32000"], head.ptr, xb, VOCAB, DIM)
+
+
+# ---- config 4: prefill ------------------------------------------------------------------
+
+def prefill_tops(lib, reps=10):
+    M = 512
+    out = {}
+    for name, (N, K) in (("11008x4096", (FFN, DIM)), ("4096x11008", (DIM, FFN))):
+        W = holo.DeviceBuffer.from_array(synth.blocks(Q4_0, N, K, seed=N + K))
+        X = holo.DeviceBuffer.from_array(synth.normal(M * K, seed=K))
+        Xq = holo.DeviceBuffer(M * (K // 32) * 34)
+        Y = holo.DeviceBuffer(4 * M * N)
+        lib.holo_quantize_act_q8_0(Xq.ptr, X.ptr, M, K)
+        lib.holo_gemm_q4_0_q8_0(Y.ptr, W.ptr, Xq.ptr, M, N, K)
+        lib.cuda_sync()
+        ev = holo.Events()
+        ev.start()
+        for _ in range(reps):
+            lib.holo_gemm_q4_0_q8_0(Y.ptr, W.ptr, Xq.ptr, M, N, K)
+        ms = ev.stop() / reps
+        ev.start()
+        for _ in range(reps):
+            lib.holo_quantize_act_q8_0(Xq.ptr, X.ptr, M, K)
+        qms = ev.stop() / reps
+        ev.close()
+        tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        out[name] = {"gemm_us": round(ms * 1e3, 2), "int_tops": round(tops, 1),
+                     "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4), "quantize_us": round(qms * 1e3, 2)}
+    holo.check("prefill")
+    return out
+
+
+# ---- CPU baseline -------------------------------------------------------------------------
+
+def measured_traffic(xmode: str):
+    """HBM bytes per gate/up launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the counter
+    reads for a device-to-device copy of known size); None if no summary
+    exists for this activation mode."""
+    p = ROOT / "profiles" / f"traffic_q4_0_gateup_{xmode}.json"
+    if not p.exists():
+        return None
+    return json.loads(p.read_text())["traffic_bytes_per_launch"]
+
+
+def cpu_baseline(budget_s: float) -> dict:
+    """The reference CPU path on one layer's 7 Q4_0 matrices (bounded sample)."""
     sys.path.insert(0, str(ROOT))
-    from oracle import oracle as orc  # test-infrastructure checker / baseline only
+    from oracle import oracle as orc  # checker / baseline only
     if orc.ref_available("release"):
         ref = orc.RefBuild("release")
-        kind, fn = "reference", (lambda M, v, o, i: ref.matmul(qtype, M, v, o, i))
-        what = "oracle/_ref/libholo_ref_release.so matmul_q (reference sources, -O3 -ffast-math -mavx2 -mfma)"
+        kind, fn = "reference", (lambda M, v, o, i: ref.matmul(Q4_0, M, v, o, i))
+        what = ("oracle/_ref/libholo_ref_release.so: matmul_q of the reference sources built with "
+                "-O3 -ffast-math -mavx2 -mfma -fopenmp")
     else:
         o_ = orc.Oracle()
-        kind, fn = "port", (lambda M, v, o, i: o_.matmul(qtype, M, v, o, i))
-        what = "oracle/liboracle.so restatement of matmul_q"
-    mats = []
-    for m, (name, out_dim, in_dim) in enumerate(LAYER):
-        seed = synth.tensor_seed(BASE_SEED, 2, 0, m)
-        mats.append((synth.blocks(qtype, out_dim, in_dim, seed), out_dim, in_dim))
+        kind, fn = "port", (lambda M, v, o, i: o_.matmul(Q4_0, M, v, o, i))
+        what = "oracle/liboracle.so: the oracle's restatement of matmul_q"
+    mats = [(synth.blocks(Q4_0, o, i, synth.tensor_seed(BASE_SEED, 2, 0, m)), o, i)
+            for m, (_, o, i) in enumerate(LAYER)]
     x = {4096: synth.normal(4096, 11), 11008: synth.normal(11008, 12)}
-    bytes_layer = Layer.weight_bytes(qtype)
     for M, o, i in mats:  # warm-up
         fn(M, x[i], o, i)
     times = []
     t_end = time.perf_counter() + budget_s
-    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 2000):
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 5000):
         t0 = time.perf_counter()
         for M, o, i in mats:
             fn(M, x[i], o, i)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    # Q4_0/Q4_K branches have no OpenMP pragma (llm.c:893-915, quant.c:626-633);
-    # Q8_0 runs its AVX2 rows under OpenMP (llm.c:838).
-    cores = 1 if qtype in (Q4_0, Q4_K) else (os.cpu_count() or 1)
-    return {"value": round(bytes_layer / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
-            "sample": f"{len(times)} runs (median) of one Llama-2-7B layer's 7 Q4_0 GEMVs "
-                      f"({bytes_layer} weight bytes) with {what}; host has {os.cpu_count()} logical CPUs",
-            "ms_per_step": round(med * 1e3, 3)}
+    b = weight_bytes(Q4_0, LAYER)
+    return {"value": round(b / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{len(times)} runs (median {med * 1e3:.1f} ms) of one Llama-2-7B layer's 7 Q4_0 GEMVs "
+                      f"({b} weight bytes, {sum(times):.1f} s of CPU work) with {what}; the reference's Q4_0 "
+                      f"branch has no OpenMP pragma (llm.c:893-915), so 1 core; host has {os.cpu_count()} "
+                      f"logical CPUs"}
 
+
+# ---- main ----------------------------------------------------------------------------------
 
 def main():
     ap = argparse.ArgumentParser()
@@ -166,58 +304,101 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--xmode", choices=["i24", "f32"], default="f32",
-                    help="GEMV activation mode (holo_gemv_set_xmode)")
+    ap.add_argument("--xmode", choices=["f32", "i24"], default="f32", help="GEMV activation mode")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run 3 device-to-device copies of BYTES (HBM counter calibration) and exit")
     a = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build runs on one GPU only: the path is a single-GPU decode "
-                                   "GEMV (multi-GPU sharding is a design note, not built)",
-                          "n_gpus": a.gpus}), flush=True)
+        print(json.dumps({"error": "this build runs on one GPU only: the hot path is a single-GPU decode "
+                                   "GEMV (how it would shard is a design note, not built)", "n_gpus": a.gpus}),
+              flush=True)
         sys.exit(2)
 
     lib = holo.load()
     holo.init()
-    log(f"device: {lib.cuda_get_device_name().decode()}")
+    if a.copy_probe:
+        src, dst = holo.DeviceBuffer(a.copy_probe), holo.DeviceBuffer(a.copy_probe)
+        ev = holo.Events()
+        ev.start()
+        for _ in range(3):
+            lib.cuda_memcpy_d2d(dst.ptr, src.ptr, a.copy_probe)
+        ms = ev.stop() / 3
+        holo.check("copy probe")
+        print(json.dumps({"copy_bytes": a.copy_probe, "ms": round(ms, 4),
+                          "gbs": round(2 * a.copy_probe / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return
+    stream = lib.holo_stream_create()
+    lib.holo_set_stream(stream)  # graphs capture a non-null stream
+    lib.holo_gemv_set_xmode(1 if a.xmode == "i24" else 0)
+    log(f"device: {lib.cuda_get_device_name().decode(errors='replace')}")
 
     t0 = time.time()
-    layers = [Layer(Q4_0, i, 2) for i in range(a.layers)]
-    log(f"generated + uploaded {a.layers} Q4_0 layers ({a.layers * Layer.weight_bytes(Q4_0) / 1e9:.2f} GB) "
+    layers = [Mats(Q4_0, i, 2, LAYER) for i in range(a.layers)]
+    A = Acts()
+    log(f"generated + uploaded {a.layers} Q4_0 layers ({a.layers * weight_bytes(Q4_0, LAYER) / 1e9:.2f} GB) "
         f"in {time.time() - t0:.1f}s")
-    xs = {4096: holo.DeviceBuffer.from_array(synth.normal(4096, 1)),
-          11008: holo.DeviceBuffer.from_array(synth.normal(11008, 2))}
-    ys = {4096: holo.DeviceBuffer(4096 * 4), 11008: holo.DeviceBuffer(11008 * 4)}
 
-    lib.holo_gemv_set_xmode(1 if a.xmode == "i24" else 0)
-    ms_step, gbs, mean_us, bytes_launch = gemv_bench(lib, Q4_0, layers, a.steps, a.warmup, xs, ys)
-    achieved = bytes_launch / (mean_us * 1e-6) / 1e9
-    log(f"Q4_0 layer step: {ms_step * 1e3:.1f} us/step, {gbs:.0f} GB/s; mean launch {mean_us:.2f} us "
-        f"-> {achieved:.0f} GB/s per launch")
+    graphs = [capture(lib, lambda L=L: layer_fused(lib, L, A)) for L in layers]
+    total_ms = time_graphs(lib, graphs, a.steps, a.warmup)
+    bytes_step = weight_bytes(Q4_0, LAYER)
+    gbs = a.steps * bytes_step / (total_ms * 1e-3) / 1e9
+    ms_step = total_ms / a.steps
+    gu_us = mean_launch_us(lib, layers, A, a.steps, which=2)
+    gu_bytes = 2 * holo.row_bytes(Q4_0, DIM) * FFN
+    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+    log(f"layer step (fused, graph): {ms_step * 1e3:.1f} us/step, {gbs:.0f} GB/s; gate/up launch {gu_us:.2f} us "
+        f"-> {achieved:.0f} GB/s")
 
     extra = {}
     if not a.no_extra:
-        other = "f32" if a.xmode == "i24" else "i24"
-        lib.holo_gemv_set_xmode(1 if other == "i24" else 0)
-        m2, g2, u2, b2 = gemv_bench(lib, Q4_0, layers, a.steps, a.warmup, xs, ys)
-        extra[f"q4_0_layer_xmode_{other}"] = {"gbs_back_to_back": round(g2, 1),
-                                              "gbs_per_launch": round(b2 / (u2 * 1e-6) / 1e9, 1)}
-        log(f"Q4_0 layer step, xmode {other}: {m2 * 1e3:.1f} us/step, {g2:.0f} GB/s")
-        lib.holo_gemv_set_xmode(1 if a.xmode == "i24" else 0)
+        # the reference decode loop's pattern: 7 cuda_matmul_q4_0 launches per layer
+        ug = [capture(lib, lambda L=L: layer_unfused(lib, L, A)) for L in layers]
+        ums = time_graphs(lib, ug, a.steps, a.warmup)
+        extra["layer_unfused_drop_in"] = {"gbs": round(a.steps * bytes_step / (ums * 1e-3) / 1e9, 1),
+                                          "us_per_step": round(ums * 1e3 / a.steps, 2),
+                                          "launches_per_step": 7}
+        for g in ug:
+            lib.holo_graph_destroy(g)
+        log(f"layer step (7 drop-in launches): {ums * 1e3 / a.steps:.1f} us/step")
+
+        # config 5: full decode step (32 layers + Q8_0 head)
+        if a.layers >= 32:
+            head = holo.DeviceBuffer.from_array(synth.blocks(Q8_0, VOCAB, DIM, synth.tensor_seed(BASE_SEED, 5, 0, 7)))
+            ones = holo.DeviceBuffer.from_array(np.ones(DIM, np.float32))
+            full = capture(lib, lambda: decode_step(lib, layers[:32], head, A, ones, False))
+            mm = capture(lib, lambda: decode_step(lib, layers[:32], head, A, ones, True))
+            reps = max(3, a.steps // 16)
+            full_ms = time_graphs(lib, [full], reps, 2) / reps
+            mm_ms = time_graphs(lib, [mm], reps, 2) / reps
+            step_bytes = 32 * bytes_step + holo.row_bytes(Q8_0, DIM) * VOCAB
+            extra["config5_decode_step"] = {
+                "matmuls_ms": round(mm_ms, 4), "end_to_end_ms": round(full_ms, 4),
+                "weight_bytes": step_bytes, "matmul_weight_gbs": round(step_bytes / (mm_ms * 1e-3) / 1e9, 1),
+                "end_to_end_weight_gbs": round(step_bytes / (full_ms * 1e-3) / 1e9, 1),
+                "launches": {"matmuls": 32 * 4 + 1, "end_to_end": 32 * 8 + 2}}
+            lib.holo_graph_destroy(full)
+            lib.holo_graph_destroy(mm)
+            log(f"config 5 decode step: matmuls {mm_ms:.3f} ms, end-to-end {full_ms:.3f} ms")
+            del head
+
+        for g in graphs:
+            lib.holo_graph_destroy(g)
+        graphs = []
         del layers
-        xs[14336] = holo.DeviceBuffer.from_array(synth.normal(14336, 3))
-        ys[14336] = holo.DeviceBuffer(14336 * 4)
-        # config 1: Q8_0 4096x4096 over 32 copies (570 MB); config 3: Q4_K
-        # Llama-3-8B FFN pair over 10 copies (660 MB).
+
+        # configs 1 and 3 over enough copies to defeat the MALL
         for qt, cfg, name, shapes, copies in ((Q8_0, 1, "config1_q8_0_4096x4096", CONFIG1, 32),
                                               (Q4_K, 3, "config3_q4_k_llama3_ffn", CONFIG3, 10)):
-            ls = [Layer(qt, i, cfg, shapes) for i in range(copies)]
-            m, g, u, b = gemv_bench(lib, qt, ls, 4 * copies, copies, xs, ys)
-            extra[name] = {"gbs_back_to_back": round(g, 1),
-                           "gbs_per_launch": round(b / (u * 1e-6) / 1e9, 1),
-                           "mean_launch_us": round(u, 3), "bytes_per_launch": b}
-            log(f"{name}: {m * 1e3:.1f} us/step, {g:.0f} GB/s back-to-back, {u:.2f} us/launch")
-            del ls
+            sets = {"mats": [Mats(qt, i, cfg, shapes) for i in range(copies)], "acts": A}
+            g, us = single_gemv_gbs(lib, qt, sets, 4 * copies)
+            extra[name] = {"gbs": round(g, 1), "us_per_launch": round(us, 2),
+                           "bytes_per_launch": weight_bytes(qt, shapes) / len(shapes)}
+            log(f"{name}: {g:.0f} GB/s, {us:.2f} us per launch")
+            del sets
+        extra["config4_prefill_m512"] = prefill_tops(lib)
+        log(f"config 4 prefill: {extra['config4_prefill_m512']}")
 
     result = {
         "metric": "Q4_0 GEMV weight GB/s at Llama-2-7B layer shapes (batch 1)",
@@ -230,22 +411,24 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 x f32 -> f32" if a.xmode == "f32" else "q4_0 x (f32 as 24-bit fixed point per 32-block) -> f32",
+        "dtype": "q4_0 x f32 -> f32" if a.xmode == "f32" else "q4_0 x (f32 as 24-bit fixed point) -> f32",
         "data": "synthetic (seeded GGUF Q4_0 blocks, N(0,1) fp32 activations)",
-        "config": {"workload": "Llama-2-7B layer: 7 Q4_0 GEMVs (4x 4096x4096, 2x 11008x4096, 1x 4096x11008), "
-                               f"rotating over {a.layers} distinct layers",
-                   "weight_bytes_per_step": Layer.weight_bytes(Q4_0), "batch": 1,
-                   "entry_point": "cuda_matmul_q4_0"},
-        "roofline": {"bound": "hbm", "kernel": "holo::gemv_kernel<Q4_0>",
+        "config": {"workload": "Llama-2-7B layer: 7 Q4_0 GEMVs (4x 4096x4096, 2x 11008x4096, 1x 4096x11008) "
+                               "as 4 launches (fused q/k/v, o, fused gate/up, down) in a HIP graph, rotating over "
+                               f"{a.layers} distinct layers",
+                   "weight_bytes_per_step": bytes_step, "batch": 1, "activation_mode": a.xmode},
+        "roofline": {"bound": "hbm", "kernel": "holo::gemv_kernel<Q4_0, gate/up>",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": bytes_launch, "mean_launch_us": round(mean_us, 3)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(a.xmode),
+                     "bytes_per_launch": gu_bytes, "mean_launch_us": round(gu_us, 3)},
         "extra": extra,
     }
-    holo.check("bench")
     if not a.no_cpu:
         log("CPU baseline ...")
-        result["cpu_baseline"] = cpu_baseline(Q4_0, a.cpu_budget)
+        result["cpu_baseline"] = cpu_baseline(a.cpu_budget)
+    lib.holo_set_stream(None)
+    lib.holo_stream_destroy(stream)
+    holo.check("bench")
     print(json.dumps(result), flush=True)
 
 

@@ -77,8 +77,6 @@ def main() -> None:
     d["q4_k_qs_sweep_out"] = strict.dequant(Q4_K, qsw.reshape(-1), 128 * 256).view(np.uint32)
 
     for t, name in NAMES.items():
-        if t == Q6_K:
-            continue
         K = QK[t] * 12
         W = synth.blocks(t, 24, K, seed=777 + t)
         x = synth.normal(K, seed=888 + t)

@@ -150,7 +150,7 @@ def test_q4_k_qs_layout_from_reference_vectors(oracle):
 
 # ---- matrix-vector products -----------------------------------------------------------
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q6_K], ids=lambda t: NAMES[t])
 def test_matmul_matches_reference_vectors(oracle, t):
     n = NAMES[t]
     W, x = GOLD[f"mm_{n}_W"], GOLD[f"mm_{n}_x"]
@@ -163,7 +163,7 @@ def test_matmul_matches_reference_vectors(oracle, t):
 
 
 @pytest.mark.skipif(not ref_available("scalar"), reason="oracle/_ref not built (no /root/reference)")
-@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q6_K], ids=lambda t: NAMES[t])
 def test_matmul_matches_reference_build_random(oracle, synth, t):
     K = QK[t] * 16
     W = synth.blocks(t, 33, K, seed=55 + t)
@@ -173,7 +173,7 @@ def test_matmul_matches_reference_build_random(oracle, synth, t):
     assert normwise_err(got, RefBuild("release").matmul(t, W, x, 33, K)) < 1e-5
 
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q6_K], ids=lambda t: NAMES[t])
 def test_matmul_one_hot_and_ones(oracle, synth, t):
     K = QK[t] * 4
     W = synth.blocks(t, 9, K, seed=3 + t)
@@ -186,7 +186,7 @@ def test_matmul_one_hot_and_ones(oracle, synth, t):
     assert normwise_err(oracle.matmul(t, W, ones, 9, K), Wd.astype(np.float64).sum(1)) < 1e-6
 
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q6_K], ids=lambda t: NAMES[t])
 def test_matmul_vs_fp64_truth(oracle, synth, t):
     K = 4096
     W = synth.blocks(t, 64, K, seed=11 + t)
