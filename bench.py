@@ -304,7 +304,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--xmode", choices=["f32", "i24"], default="f32", help="GEMV activation mode")
+    ap.add_argument("--xmode", choices=["mfma", "f32", "i24"], default="mfma", help="GEMV activation mode")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 3 device-to-device copies of BYTES (HBM counter calibration) and exit")
     a = ap.parse_args()
@@ -331,7 +331,7 @@ def main():
         return
     stream = lib.holo_stream_create()
     lib.holo_set_stream(stream)  # graphs capture a non-null stream
-    lib.holo_gemv_set_xmode(1 if a.xmode == "i24" else 0)
+    lib.holo_gemv_set_xmode({"f32": 0, "i24": 1, "mfma": 2}[a.xmode])
     log(f"device: {lib.cuda_get_device_name().decode(errors='replace')}")
 
     t0 = time.time()
@@ -411,13 +411,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 x f32 -> f32" if a.xmode == "f32" else "q4_0 x (f32 as 24-bit fixed point) -> f32",
+        "dtype": "q4_0 x f32 -> f32" if a.xmode == "f32" else "q4_0 x (f32 as 24-bit fixed point) -> f32 (int8 planes, int32 block dots)",
         "data": "synthetic (seeded GGUF Q4_0 blocks, N(0,1) fp32 activations)",
         "config": {"workload": "Llama-2-7B layer: 7 Q4_0 GEMVs (4x 4096x4096, 2x 11008x4096, 1x 4096x11008) "
                                "as 4 launches (fused q/k/v, o, fused gate/up, down) in a HIP graph, rotating over "
                                f"{a.layers} distinct layers",
                    "weight_bytes_per_step": bytes_step, "batch": 1, "activation_mode": a.xmode},
-        "roofline": {"bound": "hbm", "kernel": "holo::gemv_kernel<Q4_0, gate/up>",
+        "roofline": {"bound": "hbm", "kernel": ("holo::gemv_mfma_kernel<Q4_0, gate/up>" if a.xmode == "mfma" else "holo::gemv_kernel<Q4_0, gate/up>"),
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(a.xmode),
                      "bytes_per_launch": gu_bytes, "mean_launch_us": round(gu_us, 3)},

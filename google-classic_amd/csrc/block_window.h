@@ -65,4 +65,35 @@ HOLO_HD Window block_window(uint32_t row_mis, uint32_t off)
 // same memory page as the block and the read cannot fault.
 HOLO_HD uint32_t window_bytes(int fmt) { return fmt == FMT_Q4_0 ? 20u : 36u; }
 
+// ---- coalesced item loads of the MFMA GEMV ------------------------------------
+// An item is 16 rows x one 16-unit segment: seg_bytes(fmt) contiguous bytes
+// of each row, at byte seg * seg_bytes in the row.  A wave loads it as
+// 16-byte pieces: piece p = 64*i + lane (load i) is row p / PR, bytes
+// [16*(p % PR), +16) of the row's segment, PR = seg_bytes / 16 pieces per
+// row (so each load instruction reads whole row runs) and is stored at
+// 16*p in the wave's LDS stage.  Requires units % 8 == 0, so a row's byte
+// count is a multiple of 16 and a row's last segment holds 16 or 8 units;
+// in an 8-unit segment the pieces of the missing half re-read the first
+// half (pieces with column >= PR/2 take column - PR/2).
+HOLO_HD int seg_bytes(int fmt) { return fmt == FMT_Q8_0 ? 544 : 288; }
+
+HOLO_HD int item_pieces(int fmt) { return 16 * (seg_bytes(fmt) / 16); }
+
+struct Piece {
+    int row;   // row within the item (0..15)
+    int col;   // 16-byte column within the row's segment
+};
+
+HOLO_HD Piece item_piece(int fmt, int p, bool half_segment)
+{
+    const int pr = seg_bytes(fmt) / 16;
+    const int np = 16 * pr;
+    if (p > np - 1) p = np - 1;
+    Piece q;
+    q.row = p / pr;
+    q.col = p - q.row * pr;
+    if (half_segment && q.col >= pr / 2) q.col -= pr / 2;
+    return q;
+}
+
 }  // namespace holo

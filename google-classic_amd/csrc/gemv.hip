@@ -45,12 +45,15 @@
 #include "common.h"
 #include "quant_blocks.h"
 
+#include <limits.h>
 #include <stdlib.h>
+
+#include <type_traits>
 
 namespace holo {
 
 enum Mode { MODE_PLAIN = 0, MODE_GATEUP = 1 };
-enum XMode { XM_F32 = 0, XM_I24 = 1, XM_GF32 = 2 };
+enum XMode { XM_F32 = 0, XM_I24 = 1, XM_GF32 = 2, XM_MFMA = 3 };
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
@@ -254,7 +257,9 @@ __device__ __forceinline__ void x_convert(const float4 v, int i, int units, void
         lq[c] = pack4(x2[0], x2[1], x2[2], x2[3]);       // h plane
         lq[8 + c] = pack4(x1[0], x1[1], x1[2], x1[3]);   // m plane
         lq[16 + c] = pack4(xi[0], xi[1], xi[2], xi[3]);  // l plane
-        if (c == 0) ((float2 *)((uint4 *)lds + units * 6))[u] = make_float2(dx, sx);
+        // the MFMA path folds Q4_0's -8 into the stored sum
+        const float s2 = (XM == XM_MFMA && FMT == FMT_Q4_0) ? -8.0f * sx : sx;
+        if (c == 0) ((float2 *)((uint4 *)lds + units * 6))[u] = make_float2(dx, s2);
     }
 }
 
@@ -592,12 +597,431 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args)
     process_tile(cur, t, pb);
 }
 
+// ---- int8 MFMA path -------------------------------------------------------------------
+//
+// The unit dots of the XM_I24 arithmetic (three exact int8 planes of the
+// activations against the unit's weight bytes) run on
+// v_mfma_i32_16x16x64_i8 instead of v_dot4, which takes the per-weight work
+// off the VALU.  That instruction computes D[i][j] = sum_k A[i][k] B[k][j]
+// (16 x 16, k < 64); lane l supplies 16 bytes of A row l%16 and of B column
+// l%16 for the k-chunk l/16 and receives D[i][j], j = l%16, i = 4*(l/16) + r,
+// in register r.
+//
+// Lane l = n + 16*g holds one unit of row n: its weights are B column n in
+// chunk g (first 16 weights in one MFMA, last 16 in a second one).  A row
+// 4*g + p carries activation plane p (h, m, l) of lane group g's unit in
+// chunk g and zeros elsewhere, so D[4g + p][n] is the plane-p dot of exactly
+// that unit and arrives in lane n + 16 g, register p: every lane receives the
+// three integer sums of its own unit.  Only the 12 lanes 20*g + p (p < 3)
+// read plane data from LDS; the others read a zero region, so each A operand
+// is one LDS read with no lane arithmetic.  The MFMA computes 16x more
+// products than are used; on CDNA4 that costs 32 cycles of the matrix core
+// per 1024 weights, far below the time to stream those weights from HBM.
+//
+// Work mapping: an item is 16 rows x one 16-unit segment.  A wave loads it
+// with coalesced 16-byte loads (each load instruction reads whole runs of
+// rows, item_piece), writes it to its own LDS stage, and each lane (n, g)
+// reads back the 4-unit chunk 4g..4g+3 of row n and runs 4 MFMA pairs over
+// it (one per unit).  Loading the chunks directly from HBM would make each
+// load instruction touch 16 rows x 4 scattered pieces; the staged form runs
+// the weight stream at close to the plain-copy rate.  A tile is 16 rows
+// (PLAIN) or 8 gate + 8 up rows (GATEUP: B columns 0-7 gate, 8-15 up)
+// across all G segments; wave w takes items w, w+8, ... (P slots per tile),
+// with two items' loads in flight ahead of the one being computed.
+//
+// Per unit (d = block scale, {dx, c} = the unit's activation scale and sum
+// term staged with the planes, S = 65536*Sh + 256*Sm + Sl):
+//   Q4_0  d * (dx*S + c),  c = -8 * sum x
+//   Q8_0  d * (dx*S)
+//   Q4_K  (d*sc) * (dx*S) - (dmin*m) * c,  c = sum x
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2), aligned(4)));
+typedef __attribute__((address_space(1))) const u32x2 gu32x2;
+
+constexpr int kZeroBytes = 384;  // >= 3*96 + 32: the A reads of non-plane lanes
+
+template <int FMT>
+struct Chunk;
+template <>
+struct Chunk<FMT_Q4_0> {
+    u32x4 q[4];
+    u32x2 e;
+};
+template <>
+struct Chunk<FMT_Q8_0> {
+    u32x4 q[8];
+    u32x2 e;
+};
+template <>
+struct Chunk<FMT_Q4_K> {
+    u32x4 h;
+    u32x4 q[4];
+};
+
+// Dword I of a Q4_0 / Q8_0 chunk (a compile-time index, so the chunk stays in
+// registers).
+template <int I, int FMT>
+__device__ __forceinline__ uint32_t cw(const Chunk<FMT> &c)
+{
+    constexpr int NQ = FMT == FMT_Q4_0 ? 16 : 32;
+    if constexpr (I < NQ) return c.q[I / 4][I % 4];
+    else return c.e[I - NQ];
+}
+
+// ---- coalesced item loads and the per-wave LDS stage ----------------------------
+
+template <int FMT>
+struct Geo {
+    static constexpr int SEGB = FMT == FMT_Q8_0 ? 544 : 288;  // bytes per row per item
+    static constexpr int PR = SEGB / 16;                       // 16-byte pieces per row
+    static constexpr int NP = 16 * PR;                         // pieces per item
+    static constexpr int NL = (NP + 63) / 64;                  // load instructions per item
+    static constexpr int STAGE = 16 * SEGB;                    // LDS stage bytes per wave
+};
+
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4)));   // 16-byte aligned
+typedef uint32_t u32x2a __attribute__((ext_vector_type(2)));   // 8-byte aligned
+typedef __attribute__((address_space(1))) const u32x4a gu32x4a;
+
+template <int FMT>
+struct Raw2 {
+    u32x4a v[Geo<FMT>::NL];
+};
+
+// Lane (n, g)'s chunk from the wave's stage (row n of the item at n * SEGB):
+// Q4_0 / Q8_0 units 4g..4g+3 = bytes [72g, +72) / [136g, +136) of the row
+// (8-byte aligned); Q4_K the header of superblock g/2 and the 64 quant bytes
+// of its half g&1 (16-byte aligned).
+template <int FMT>
+__device__ __forceinline__ void read_chunk(Chunk<FMT> &c, const uint8_t *stage, int n, int g)
+{
+    if constexpr (FMT == FMT_Q4_K) {
+        const uint8_t *b = stage + n * 288 + 144 * (g >> 1);
+        const u32x4a h = *(const u32x4a *)b;
+        c.h = (u32x4){h.x, h.y, h.z, h.w};
+        const uint8_t *q = b + 16 + 64 * (g & 1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const u32x4a v = *(const u32x4a *)(q + 16 * i);
+            c.q[i] = (u32x4){v.x, v.y, v.z, v.w};
+        }
+    } else {
+        constexpr int NQ = FMT == FMT_Q4_0 ? 4 : 8;
+        const uint8_t *b = stage + n * Geo<FMT>::SEGB + (FMT == FMT_Q4_0 ? 72 : 136) * g;
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            const u32x2a lo = *(const u32x2a *)(b + 16 * i);
+            const u32x2a hi = *(const u32x2a *)(b + 16 * i + 8);
+            c.q[i] = (u32x4){lo.x, lo.y, hi.x, hi.y};
+        }
+        const u32x2a e = *(const u32x2a *)(b + 16 * NQ);
+        c.e = (u32x2){e.x, e.y};
+    }
+}
+
+__device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c)
+{
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Unit T (0..3) of the chunk: the weight dwords as two MFMA B operands
+// (weights 0-15, 16-31) and the block scale bits.  Q4_0 block T sits at byte
+// 18T, Q8_0 block T at byte 34T: for even T the scale is the low half of a
+// dword and the quants start 2 bytes into it; for odd T the scale is the
+// high half of a dword and the quants are dword-aligned.
+template <int T, int FMT>
+__device__ __forceinline__ void chunk_unit(const Chunk<FMT> &c, v4i &lo, v4i &hi, uint32_t &dbits)
+{
+    if constexpr (FMT == FMT_Q4_K) {
+        const u32x4 q = c.q[T];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            lo[i] = (int)(q[i] & 0x0F0F0F0Fu);
+            hi[i] = (int)((q[i] >> 4) & 0x0F0F0F0Fu);
+        }
+        dbits = 0;
+    } else {
+        constexpr int W0 = ((FMT == FMT_Q4_0 ? 18 : 34) * T) >> 2;
+        constexpr bool EVEN = (T & 1) == 0;
+        auto qd = [&](auto I) -> uint32_t {
+            constexpr int i = decltype(I)::value;
+            if constexpr (EVEN) return __builtin_amdgcn_alignbyte(cw<W0 + i + 1>(c), cw<W0 + i>(c), 2);
+            else return cw<W0 + 1 + i>(c);
+        };
+        dbits = EVEN ? cw<W0>(c) : (cw<W0>(c) >> 16);
+        uint32_t q[8];
+        q[0] = qd(std::integral_constant<int, 0>{});
+        q[1] = qd(std::integral_constant<int, 1>{});
+        q[2] = qd(std::integral_constant<int, 2>{});
+        q[3] = qd(std::integral_constant<int, 3>{});
+        if constexpr (FMT == FMT_Q8_0) {
+            q[4] = qd(std::integral_constant<int, 4>{});
+            q[5] = qd(std::integral_constant<int, 5>{});
+            q[6] = qd(std::integral_constant<int, 6>{});
+            q[7] = qd(std::integral_constant<int, 7>{});
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                lo[i] = (int)q[i];
+                hi[i] = (int)q[4 + i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                lo[i] = (int)(q[i] & 0x0F0F0F0Fu);
+                hi[i] = (int)((q[i] >> 4) & 0x0F0F0F0Fu);
+            }
+        }
+    }
+}
+
+// The 4 sub-block scales and mins of a Q4_K half superblock, one per byte
+// (quant.c:290-297): half 0 (j < 4)  sc = s[j] & 63, m = s[j+4] & 63;
+// half 1 (j = 4+t)  sc = (s[8+t] & 15) << 2 | s[t] >> 6,
+//                   m  = (s[8+t] >> 4) << 2 | s[4+t] >> 6.
+__device__ __forceinline__ void q4_k_half_scales(const u32x4 h, bool half1, uint32_t &sc, uint32_t &mn)
+{
+    const uint32_t s0 = h.y, s1 = h.z, s2 = h.w;
+    const uint32_t sc1 = ((s2 & 0x0F0F0F0Fu) << 2) | ((s0 >> 6) & 0x03030303u);
+    const uint32_t mn1 = (((s2 >> 4) & 0x0F0F0F0Fu) << 2) | ((s1 >> 6) & 0x03030303u);
+    sc = half1 ? sc1 : (s0 & 0x3F3F3F3Fu);
+    mn = half1 ? mn1 : (s1 & 0x3F3F3F3Fu);
+}
+
+// Unit T of an item: adds its contribution to acc.
+template <int T, int FMT>
+__device__ __forceinline__ void item_unit(float &acc, const Chunk<FMT> &c, const uint8_t *ldsb, uint32_t abase,
+                                          uint32_t sbase, int skip, bool tail, float dk, float mk, uint32_t sc,
+                                          uint32_t mn)
+{
+    const v4i a0 = *(const v4i *)(ldsb + abase + 96 * T);
+    const v4i a1 = *(const v4i *)(ldsb + abase + 96 * T + 16);
+    const float2 xs = *(const float2 *)(ldsb + sbase + 8 * T);
+    v4i lo, hi;
+    uint32_t dbits;
+    chunk_unit<T, FMT>(c, lo, hi, dbits);
+    const v4i zero = {0, 0, 0, 0};
+    const v4i s = mfma_i8(a1, hi, mfma_i8(a0, lo, zero));
+    // |Sh| <= 32*128*127, so 256*Sh + Sm is exact in int32
+    const int t1 = (s[0] << 8) + s[1];
+    const float S = fmaf(256.0f, (float)t1, (float)s[2]);
+    if constexpr (FMT == FMT_Q4_K) {
+        float dsc = dk * (float)((sc >> (8 * T)) & 0xFFu);
+        float dmn = mk * (float)((mn >> (8 * T)) & 0xFFu);
+        if (tail && T < skip) dsc = dmn = 0.f;
+        acc = fmaf(dsc, xs.x * S, fmaf(-dmn, xs.y, acc));
+    } else {
+        float d = half_bits_to_float(dbits);
+        if (tail && T < skip) d = 0.f;
+        if constexpr (FMT == FMT_Q4_0) acc = fmaf(d, fmaf(xs.x, S, xs.y), acc);
+        else acc = fmaf(d, xs.x * S, acc);
+    }
+}
+
+// One item: this lane's 4 units.  abase = LDS byte address of the lane's A
+// operand for unit 0 (plane data or the zero region), sbase = address of the
+// {dx, c} pair of the chunk's first unit.  Slots t < skip repeat units of the
+// previous chunk (clamped tail chunk) and get weight 0; `tail` is wave
+// uniform and true only for the row's last segment.
+template <int FMT>
+__device__ __forceinline__ float item_dot(const Chunk<FMT> &c, const uint8_t *ldsb, uint32_t abase, uint32_t sbase,
+                                          uint32_t cs, int skip, bool tail)
+{
+    float acc = 0.f;
+    float dk = 0.f, mk = 0.f;
+    uint32_t sc = 0, mn = 0;
+    if constexpr (FMT == FMT_Q4_K) {
+        dk = half_bits_to_float(c.h.x);
+        mk = half_bits_to_float(c.h.x >> 16);
+        q4_k_half_scales(c.h, (cs >> 2) & 1u, sc, mn);
+    }
+    item_unit<0, FMT>(acc, c, ldsb, abase, sbase, skip, tail, dk, mk, sc, mn);
+    item_unit<1, FMT>(acc, c, ldsb, abase, sbase, skip, tail, dk, mk, sc, mn);
+    item_unit<2, FMT>(acc, c, ldsb, abase, sbase, skip, tail, dk, mk, sc, mn);
+    item_unit<3, FMT>(acc, c, ldsb, abase, sbase, skip, tail, dk, mk, sc, mn);
+    return acc;
+}
+
+struct MfmaArgs {
+    const uint8_t *W[kMaxSeg];
+    float *y[kMaxSeg];
+    int row_end[kMaxSeg];  // prefix sums of the matrices' rows (PLAIN); unused entries INT_MAX
+    int total_rows;        // rows of all matrices (PLAIN) or of one (GATEUP)
+    int max_tiles;         // tiles of the longest workgroup range
+    const float *x;
+    int units;             // 32-weight units per row
+    int nsegs;             // G: 16-unit segments per row
+    int x_lds_bytes;       // staged activations (planes, then {dx, c} pairs)
+    int64_t row_bytes;
+};
+
+template <int FMT, int P, int MODE>
+__global__ __launch_bounds__(kThreads) void gemv_mfma_kernel(MfmaArgs args)
+{
+    using GE = Geo<FMT>;
+    extern __shared__ uint4 lds[];
+    uint8_t *ldsb = (uint8_t *)lds;
+    constexpr int TR = MODE == MODE_GATEUP ? 8 : 16;  // rows per matrix per tile
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int units = args.units;
+    const int G = args.nsegs;
+    const uint32_t zero_off = (uint32_t)args.x_lds_bytes;
+    uint8_t *stage = ldsb + zero_off + kZeroBytes + wave * GE::STAGE;
+    float *tpart = (float *)(ldsb + zero_off + kZeroBytes + kWaves * GE::STAGE);  // [max_tiles][kWaves][16]
+    uint32_t *tcnt = (uint32_t *)(tpart + args.max_tiles * kWaves * 16);           // [max_tiles]
+    const bool plane_lane = (n >> 2) == g && (n & 3) < 3;
+    const uint32_t plane_off = (uint32_t)(n & 3) * 32u;
+    const uint32_t ls_off = (uint32_t)units * 96u;
+
+    // This workgroup's rows: F full tiles of TR rows dealt round-robin over
+    // the grid (at any moment the grid reads one contiguous stretch of the
+    // matrices), then an even share of the remaining rows as one short tile
+    // (its spare rows re-read the tile's last row and are not stored).
+    const int W = (int)gridDim.x, wg = (int)blockIdx.x;
+    const int F = args.total_rows / (W * TR);
+    const int rem0 = F * W * TR, rem = args.total_rows - rem0;
+    const int ex0 = rem0 + (int)(((int64_t)wg * rem) / W), ex1 = rem0 + (int)(((int64_t)(wg + 1) * rem) / W);
+    const int my_tiles = F + (ex1 > ex0 ? 1 : 0);
+    const int Q = my_tiles * P;  // item slots of this wave: P per tile
+    // rows [row0, rend) of local tile k
+    auto tile_rows = [&](int k, int &row0, int &rend) {
+        if (k < F) {
+            row0 = (k * W + wg) * TR;
+            rend = row0 + TR;
+        } else {
+            row0 = ex0;
+            rend = ex1;
+        }
+    };
+
+    // Kernel-argument arrays are read only with constant indices: a per-lane
+    // index would turn each access into a memory load ahead of every weight
+    // load.  Row v of all matrices -> (matrix, row) by selects.
+    const int re0 = args.row_end[0], re1 = args.row_end[1];
+    const uint64_t w0 = (uint64_t)args.W[0], dw1 = (uint64_t)args.W[1] - w0, dw2 = (uint64_t)args.W[2] - w0;
+    const uint64_t y0 = (uint64_t)args.y[0], dy1 = (uint64_t)args.y[1] - y0, dy2 = (uint64_t)args.y[2] - y0;
+    auto split_row = [&](int v, int &m, int &r) {
+        const int a1 = v >= re0, a2 = v >= re1;
+        m = a1 + a2;
+        r = v - (a2 ? re1 : a1 ? re0 : 0);
+    };
+    auto wbase = [&](int m) -> gbyte * { return (gbyte *)(w0 + (m == 2 ? dw2 : m == 1 ? dw1 : 0)); };
+    auto ybase = [&](int m) -> float * { return (float *)(y0 + (m == 2 ? dy2 : m == 1 ? dy1 : 0)); };
+
+    // Slot q: local tile q / P, item (segment) wave + 8 * (q % P).  Slots
+    // past the end issue nothing (a wave cannot end before its loads return).
+    auto issue = [&](Raw2<FMT> &b, int q) {
+        if (q >= Q) return;
+        const int k = q / P, p = q - k * P;
+        int row0, rend;
+        tile_rows(k, row0, rend);
+        const int seg = min(wave + kWaves * p, G - 1);
+        const bool half = 16 * seg + 16 > units;
+#pragma unroll
+        for (int i = 0; i < GE::NL; i++) {
+            const Piece pc = item_piece(FMT, 64 * i + lane, half);
+            int m, row;
+            if constexpr (MODE == MODE_GATEUP) {
+                m = pc.row >> 3;
+                row = min(row0 + (pc.row & 7), rend - 1);
+            } else {
+                split_row(min(row0 + pc.row, rend - 1), m, row);
+            }
+            gbyte *a = wbase(m) + (int64_t)row * args.row_bytes + seg * GE::SEGB + 16 * pc.col;
+            b.v[i] = *(gu32x4a *)a;
+        }
+    };
+
+    // the item into the wave's stage (16-byte piece p at 16 p)
+    auto stage_write = [&](const Raw2<FMT> &b) {
+#pragma unroll
+        for (int i = 0; i < GE::NL; i++) {
+            const int pc = 64 * i + lane;
+            if (GE::NP % 64 == 0 || pc < GE::NP) *(u32x4a *)(stage + 16 * pc) = b.v[i];
+        }
+    };
+
+    float acc = 0.f;
+    auto process = [&](int q) {
+        const int k = q / P, p = q - k * P;
+        const int j = wave + kWaves * p;
+        if (j < G) {
+            Chunk<FMT> c;
+            read_chunk<FMT>(c, stage, n, g);
+            const int cs0 = 16 * j + 4 * g;
+            const bool valid = cs0 < units;  // false only in an 8-unit last segment
+            const int cs = valid ? cs0 : units - 4;
+            const uint32_t abase = plane_lane ? (uint32_t)cs * 96u + plane_off : zero_off;
+            acc += item_dot<FMT>(c, ldsb, abase, ls_off + (uint32_t)cs * 8u, (uint32_t)cs, valid ? 0 : 4,
+                                 j == G - 1);
+        }
+        if (p == P - 1) {
+            // Tile end without a barrier: the wave's 16 row partials (the four
+            // lane groups summed) go to the tile's own slot, and the wave that
+            // completes the tile's count sums the 8 waves' partials and stores.
+            float r = acc;
+            r += __shfl_xor(r, 16);
+            r += __shfl_xor(r, 32);
+            acc = 0.f;
+            float *pt = tpart + k * (kWaves * 16);
+            if (lane < 16) pt[wave * 16 + lane] = r;
+            uint32_t arrived = 0;
+            if (lane == 0)
+                arrived = __hip_atomic_fetch_add(tcnt + k, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+            arrived = __builtin_amdgcn_readfirstlane(arrived);
+            if (arrived == kWaves - 1 && lane < TR) {
+                int row0, rend;
+                tile_rows(k, row0, rend);
+                const int v = row0 + lane;
+                float s0 = 0.f;
+#pragma unroll
+                for (int w = 0; w < kWaves; w++) s0 += pt[w * 16 + lane];
+                if constexpr (MODE == MODE_GATEUP) {
+                    float s1 = 0.f;
+#pragma unroll
+                    for (int w = 0; w < kWaves; w++) s1 += pt[w * 16 + 8 + lane];
+                    if (v < rend) ybase(0)[v] = silu(s0) * s1;
+                } else if (v < rend) {
+                    int m, row;
+                    split_row(v, m, row);
+                    ybase(m)[row] = s0;
+                }
+            }
+        }
+    };
+
+    Raw2<FMT> b0, b1;
+    float4 pre[kPreX];
+    x_preload(args.x, units, pre);
+    issue(b0, 0);
+    x_stage<FMT, XM_MFMA>(args.x, units, lds, pre);
+    if (threadIdx.x < kZeroBytes / 16) ((uint4 *)(ldsb + zero_off))[threadIdx.x] = make_uint4(0, 0, 0, 0);
+    for (int i = threadIdx.x; i < args.max_tiles; i += kThreads) tcnt[i] = 0;
+    __syncthreads();
+
+    // One item in flight per wave: the next item is issued once the current
+    // one has arrived (more outstanding loads measured slower on MI355X).
+    for (int q = 0; q < Q; q += 2) {
+        stage_write(b0);
+        issue(b1, q + 1);
+        process(q);
+        if (q + 1 < Q) {
+            stage_write(b1);
+            issue(b0, q + 2);
+            process(q + 1);
+        }
+    }
+}
+
 // ---- host side ---------------------------------------------------------------------
 
 // Activation mode and launch shape; environment overrides are read once:
-// HOLO_GEMV_XMODE=f32|i24, HOLO_GEMV_WG_PER_CU, HOLO_GEMV_ROWS=1|2|4.
+// HOLO_GEMV_XMODE=f32|i24|mfma, HOLO_GEMV_WG_PER_CU, HOLO_GEMV_ROWS=1|2|4.
 struct Tuning {
-    int xmode = XM_F32;
+    int xmode = XM_MFMA;
+    bool mfma_q8 = false;  // MFMA path for Q8_0 as well
     int wg_per_cu = 0;  // 0 = by grid size
     int rows = 0;       // 0 = by shape
     bool read = false;
@@ -607,7 +1031,10 @@ static Tuning g_tune;
 static const Tuning &tuning()
 {
     if (!g_tune.read) {
-        if (const char *e = getenv("HOLO_GEMV_XMODE")) g_tune.xmode = (e[0] == 'f') ? XM_F32 : XM_I24;
+        if (const char *e = getenv("HOLO_GEMV_XMODE")) {
+            g_tune.xmode = (e[0] == 'f') ? XM_F32 : (e[0] == 'i') ? XM_I24 : XM_MFMA;
+            g_tune.mfma_q8 = g_tune.xmode == XM_MFMA;
+        }
         if (const char *e = getenv("HOLO_GEMV_WG_PER_CU")) g_tune.wg_per_cu = atoi(e) > 0 ? atoi(e) : 0;
         if (const char *e = getenv("HOLO_GEMV_ROWS")) g_tune.rows = atoi(e);
         g_tune.read = true;
@@ -616,6 +1043,7 @@ static const Tuning &tuning()
 }
 
 constexpr int kMaxLdsBytes = 64 * 1024;
+constexpr size_t kMaxMfmaLds = 160 * 1024;  // MI355X: 160 KB of LDS per workgroup
 
 template <int FMT, int XM, int R, int P, int MODE>
 static void launch_t(GemvArgs &a)
@@ -654,6 +1082,83 @@ static void launch_r(GemvArgs &a, int R, int P)
     }
 }
 
+template <int FMT>
+static size_t mfma_lds_bytes(int units, int max_tiles)
+{
+    const size_t x_lds = ((size_t)units * lds_bytes_per_unit<XM_I24>() + 15) & ~(size_t)15;
+    return x_lds + kZeroBytes + (size_t)kWaves * Geo<FMT>::STAGE + (size_t)max_tiles * (kWaves * 16 * 4 + 4);
+}
+
+static int mfma_max_tiles(int total_rows, int tr, int grid)
+{
+    return total_rows / (grid * tr) + 1;  // full tiles plus the short one
+}
+
+// Workgroups for an MFMA launch: one or two per CU (HOLO_GEMV_WG_PER_CU
+// forces it), at most one per tile of rows.  Two per CU give each CU 16
+// waves; they are used when both fit in LDS and the rows fill the tiles as
+// well as with one per CU (the short last tile costs about a full tile).
+template <int FMT>
+static int mfma_grid(int total_rows, int tr, int units)
+{
+    const int tiles = (total_rows + tr - 1) / tr;
+    auto clamp = [&](int w) { return w < tiles ? w : tiles; };
+    const int forced = tuning().wg_per_cu;
+    if (forced > 0) return clamp(num_cus() * forced);
+    auto fill = [&](int w) {
+        const int t = total_rows / (w * tr) + (total_rows % (w * tr) ? 1 : 0);
+        return (double)total_rows / ((double)w * tr * t);
+    };
+    const int w1 = clamp(num_cus()), w2 = clamp(2 * num_cus());
+    const size_t lds2 = mfma_lds_bytes<FMT>(units, mfma_max_tiles(total_rows, tr, w2));
+    if (w2 > w1 && 2 * lds2 <= kMaxMfmaLds && fill(w2) >= fill(w1) - 0.02) return w2;
+    return w1;
+}
+
+template <int FMT, int MODE>
+static void launch_mfma(MfmaArgs &a, int P)
+{
+    constexpr int TR = MODE == MODE_GATEUP ? 8 : 16;
+    const int blocks = mfma_grid<FMT>(a.total_rows, TR, a.units);
+    a.max_tiles = mfma_max_tiles(a.total_rows, TR, blocks);
+    const size_t lds = mfma_lds_bytes<FMT>(a.units, a.max_tiles);
+    auto go = [&](auto kern) {
+        // more than 64 KB of LDS must be enabled per kernel (once)
+        static bool attr = false;
+        if (!attr) {
+            HOLO_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)kMaxMfmaLds));
+            attr = true;
+        }
+        hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, stream(), a);
+        HOLO_LAUNCH_CHECK();
+    };
+    switch (P) {
+    case 1: go(gemv_mfma_kernel<FMT, 1, MODE>); break;
+    case 2: go(gemv_mfma_kernel<FMT, 2, MODE>); break;
+    case 3: go(gemv_mfma_kernel<FMT, 3, MODE>); break;
+    default: go(gemv_mfma_kernel<FMT, 4, MODE>); break;
+    }
+}
+
+// The MFMA path takes rows whose unit count is a multiple of 8 (row bytes a
+// multiple of 16; in_dim a multiple of 256), at most 4 items per wave per
+// tile, and LDS within kMaxMfmaLds (checked for the largest tile count,
+// every row in its own tile).
+static bool mfma_fits(int fmt, int units, int total_rows, int tr)
+{
+    if (units < 8 || (units & 7) || (units + 15) / 16 > 4 * kWaves) return false;
+    auto lds_for = [&](auto fmtc) {
+        constexpr int F = decltype(fmtc)::value;
+        const int grid = mfma_grid<F>(total_rows, tr, units);
+        return mfma_lds_bytes<F>(units, mfma_max_tiles(total_rows, tr, grid > 0 ? grid : 1));
+    };
+    const size_t lds = fmt == FMT_Q4_0   ? lds_for(std::integral_constant<int, FMT_Q4_0>{})
+                       : fmt == FMT_Q8_0 ? lds_for(std::integral_constant<int, FMT_Q8_0>{})
+                                         : lds_for(std::integral_constant<int, FMT_Q4_K>{});
+    return lds <= kMaxMfmaLds;
+}
+
 static bool check_ptr(const void *p, const char *what)
 {
     if (((uintptr_t)p & 3u) != 0) {
@@ -682,6 +1187,43 @@ static void tile_shape(int nsegs, int &P, int &G)
     }
 }
 
+static void gemv_mfma(int fmt, int mode, int nseg, const void *const *W, float *const *y, const int *rows,
+                      const float *x, int units, int64_t row_bytes)
+{
+    MfmaArgs a = {};
+    a.units = units;
+    a.row_bytes = row_bytes;
+    a.x = x;
+    a.nsegs = (units + 15) / 16;
+    a.x_lds_bytes = (units * lds_bytes_per_unit<XM_I24>() + 15) & ~15;
+    const int P = (a.nsegs + kWaves - 1) / kWaves;
+    int total = 0;
+    for (int s = 0; s < kMaxSeg; s++) {
+        if (s < nseg) {
+            a.W[s] = (const uint8_t *)W[s];
+            a.y[s] = y[s];
+            total += rows[s];
+            a.row_end[s] = total;
+        } else {
+            a.W[s] = a.W[0];
+            a.y[s] = a.y[0];
+            a.row_end[s] = INT_MAX;
+        }
+    }
+    a.total_rows = mode == MODE_GATEUP ? rows[0] : total;
+    if (a.total_rows == 0) return;
+    if (fmt == FMT_Q4_0) {
+        if (mode == MODE_PLAIN) launch_mfma<FMT_Q4_0, MODE_PLAIN>(a, P);
+        else launch_mfma<FMT_Q4_0, MODE_GATEUP>(a, P);
+    } else if (fmt == FMT_Q8_0) {
+        if (mode == MODE_PLAIN) launch_mfma<FMT_Q8_0, MODE_PLAIN>(a, P);
+        else launch_mfma<FMT_Q8_0, MODE_GATEUP>(a, P);
+    } else {
+        if (mode == MODE_PLAIN) launch_mfma<FMT_Q4_K, MODE_PLAIN>(a, P);
+        else launch_mfma<FMT_Q4_K, MODE_GATEUP>(a, P);
+    }
+}
+
 // One launch over up to three matrices sharing x and in_dim.
 static void gemv_multi(int fmt, int mode, int nseg, const void *const *W, float *const *y, const int *rows,
                        const float *x, int in_dim)
@@ -697,9 +1239,25 @@ static void gemv_multi(int fmt, int mode, int nseg, const void *const *W, float 
         HOLO_REJECT("gemv: in_dim too large (at most 32 segments of 64 units per row)");
         return;
     }
+    // Q8_0 rows carry twice the bytes per weight, so the F32 path is already
+    // load-bound on them and measured faster (MI355X); the MFMA path serves
+    // Q4_0 and Q4_K unless HOLO_GEMV_XMODE=mfma asks for it on Q8_0 too.
+    if (tn.xmode == XM_MFMA && (fmt != FMT_Q8_0 || tn.mfma_q8)) {
+        bool aligned16 = ((uintptr_t)x & 3u) == 0;
+        int total = 0;
+        for (int s = 0; s < nseg; s++) {
+            aligned16 = aligned16 && (((uintptr_t)W[s] & 15u) == 0);
+            total += rows[s];
+        }
+        if (mode == MODE_GATEUP) total = rows[0];
+        if (aligned16 && mfma_fits(fmt, a.units, total, mode == MODE_GATEUP ? 8 : 16)) {
+            gemv_mfma(fmt, mode, nseg, W, y, rows, x, a.units, a.row_bytes);
+            return;
+        }
+    }
     // x staged in LDS when it fits (F32 needs 132 B per unit, I24 104 B),
     // otherwise read by each lane from global memory.
-    int xm = tn.xmode;
+    int xm = tn.xmode == XM_MFMA ? XM_F32 : tn.xmode;
     const size_t budget = (size_t)kMaxLdsBytes - 4096;
     if (xm == XM_F32 && (size_t)a.units * lds_bytes_per_unit<XM_F32>() > budget) xm = XM_I24;
     if (xm == XM_I24 && (size_t)a.units * lds_bytes_per_unit<XM_I24>() > budget) xm = XM_GF32;
@@ -805,7 +1363,8 @@ void cuda_matmul_q4_k(float *dst, const void *M, const float *v, int out_dim, in
 void holo_gemv_set_xmode(int xmode)
 {
     tuning();
-    g_tune.xmode = xmode ? XM_I24 : XM_F32;
+    g_tune.xmode = xmode == 1 ? XM_I24 : (xmode == 2 || xmode == 3) ? XM_MFMA : XM_F32;
+    g_tune.mfma_q8 = xmode == 3;
 }
 
 void holo_gemv_set_launch(int rows_per_item, int wg_per_cu)

@@ -53,21 +53,29 @@ void holo_graph_destroy(void *graph_exec);
 void holo_matmul(float *dst, const void *M, const float *v, int out_dim, int in_dim, int type);
 
 /* ---- GEMV activation mode ------------------------------------------------------
- * HOLO_XMODE_F32 (default): every weight is multiplied by the fp32 activation
- * itself (v_cvt_f32_ubyte + FMA).  HOLO_XMODE_I24: activations are held per
- * 32-block as 24-bit fixed point, xi = rint(x * 127*65536/amax),
- * |x - d*xi| <= amax*2^-23, in three int8 planes; each block's integer dots
- * run on v_dot4_i32_i8 and are exact.  Both accumulate across blocks in
- * fp32.  Rows longer than the LDS staging holds (in_dim > 14880 for F32)
- * switch to I24, and beyond 18880 to fp32 read from global memory.  Applies
- * to every GEMV entry point.                                                */
+ * All modes hold the dot products to fp32 accuracy and accumulate across
+ * blocks in fp32.
+ * HOLO_XMODE_MFMA (default): activations are held per 32-block as 24-bit
+ * fixed point, xi = rint(x * 127*65536/amax), |x - d*xi| <= amax*2^-23, in
+ * three int8 planes, and each block's three exact integer dots run on the
+ * int8 matrix cores (v_mfma_i32_16x16x64_i8).  Taken for Q4_0 and Q4_K rows
+ * with in_dim a multiple of 256 up to 16384 and 16-byte aligned matrices;
+ * other shapes run HOLO_XMODE_F32.
+ * HOLO_XMODE_F32: every weight is multiplied by the fp32 activation itself
+ * (v_cvt_f32_ubyte + FMA).
+ * HOLO_XMODE_I24: the MFMA mode's arithmetic on v_dot4_i32_i8.
+ * Rows longer than the LDS staging holds (in_dim > 14880 for F32) switch to
+ * I24, and beyond 18880 to fp32 read from global memory.  Applies to every
+ * GEMV entry point.                                                        */
 #define HOLO_XMODE_F32 0
 #define HOLO_XMODE_I24 1
+#define HOLO_XMODE_MFMA 2      /* default; Q8_0 stays on F32, measured faster */
+#define HOLO_XMODE_MFMA_ALL 3  /* MFMA for Q8_0 as well                      */
 void holo_gemv_set_xmode(int xmode);
 /* Launch shape of the GEMV kernels: rows per work item (1, 2 or 4; 0 = the
- * default, 1) and workgroups per CU (0 = the default: 1 when the grid has at
- * most 2 tiles per CU, else 2).  A tuning knob; the defaults are the
- * measured best on MI355X.                                                 */
+ * default, 1; F32/I24 modes only) and workgroups per CU (0 = the default:
+ * F32/I24 use 1 when the grid has at most 2 tiles per CU, else 2; MFMA
+ * uses 1 or 2 by how evenly the rows fill its tiles).  A tuning knob.      */
 void holo_gemv_set_launch(int rows_per_item, int wg_per_cu);
 
 /* ---- dequantisation ---------------------------------------------------------

@@ -7,6 +7,10 @@
 //   * the window holds the whole block and starts at most 2 bytes before it;
 //   * a dword that reaches past the matrix end starts inside the block and is
 //     4-byte aligned (so it cannot leave the block's memory page).
+// For shapes the MFMA GEMV takes (units per row a multiple of 8), it also
+// rebuilds every 16-byte piece of every item load and checks that it lies
+// inside its row and that the stage bytes the lanes decode as valid units hold
+// exactly those units' bytes.
 // Prints "ok N" (N windows checked) or the first violation, exit status 1.
 #include <stdio.h>
 #include <stdlib.h>
@@ -57,6 +61,30 @@ int main(int argc, char **argv)
                 for (long d = ws; d < we; d += 4) {
                     if (d >= total) return fail("dword starts past the matrix", fmt, row, u, d, d + 4, total);
                     if (d + 4 > total && d < block) return fail("straddling dword not inside block", fmt, row, u, d, block, total);
+                }
+            }
+        }
+        // MFMA item pieces (units a multiple of 8)
+        if (units < 8 || (units & 7)) continue;
+        const long segb = seg_bytes(fmt), pr = segb / 16, np = item_pieces(fmt);
+        if (rb % 16) return fail("row bytes not a multiple of 16", fmt, 0, 0, rb, 16, total);
+        const long nseg = (units + 15) / 16;
+        for (long seg = 0; seg < nseg; seg++) {
+            const bool half = 16 * seg + 16 > units;
+            if (half && units - 16 * seg != 8) return fail("last segment neither 16 nor 8 units", fmt, 0, seg, units, 0, total);
+            // stage bytes that valid lane groups read must hold their own row bytes
+            const long valid_bytes = half ? segb / 2 : segb;
+            for (long p = 0; p < 64 * ((np + 63) / 64); p++) {
+                Piece q = item_piece(fmt, (int)p, half);
+                checked++;
+                if (q.row < 0 || q.row > 15 || q.col < 0 || q.col >= pr) return fail("piece outside the item", fmt, q.row, p, q.col, pr, total);
+                long a = seg * segb + 16 * q.col;  // byte in the row
+                if (a + 16 > rb) return fail("piece past the row end", fmt, q.row, p, a, rb, total);
+                if (p < np) {
+                    long stage_col = p % pr;
+                    if (stage_col * 16 < valid_bytes && q.col != stage_col)
+                        return fail("valid stage bytes not from their own row position", fmt, q.row, p, q.col, stage_col, total);
+                    if (p / pr != q.row) return fail("piece row does not match its stage row", fmt, q.row, p, p / pr, 0, total);
                 }
             }
         }

@@ -24,6 +24,9 @@ CASES = [
     (Q4_0, 1, 32), (Q4_0, 3, 64), (Q4_0, 37, 96), (Q4_0, 65, 2048 + 32), (Q4_0, 130, 4096),
     (Q8_0, 1, 32), (Q8_0, 5, 96), (Q8_0, 33, 2080), (Q8_0, 129, 4096),
     (Q4_K, 1, 256), (Q4_K, 7, 512), (Q4_K, 45, 2304), (Q4_K, 130, 4096),
+    # MFMA path: rows ending in an 8-unit segment (24 and 136 units), a
+    # ragged last tile, and in_dim 16384 (4 items per wave)
+    (Q4_0, 23, 256 * 3), (Q8_0, 19, 256 * 3), (Q4_0, 33, 256 * 17), (Q4_K, 9, 256 * 3), (Q8_0, 40, 16384),
     # BASELINE configs 1-3 and the config-5 head
     (Q8_0, 4096, 4096), (Q4_0, 4096, 4096), (Q4_0, 11008, 4096), (Q4_0, 4096, 11008),
     (Q4_K, 14336, 4096), (Q4_K, 4096, 14336), (Q8_0, 32000, 4096),
@@ -45,7 +48,7 @@ def _run(holo, synth, qtype, out_dim, in_dim, seed):
     return W, x, dy.download(np.float32, out_dim)
 
 
-@pytest.mark.parametrize("xmode", [1, 0], ids=["i24", "f32"])
+@pytest.mark.parametrize("xmode", [3, 1, 0], ids=["mfma", "i24", "f32"])
 @pytest.mark.parametrize("qtype,out_dim,in_dim", CASES,
                          ids=[f"{NAMES[t]}-{o}x{i}" for t, o, i in CASES])
 def test_gemv_parity(holo, synth, oracle, qtype, out_dim, in_dim, xmode):
@@ -54,7 +57,7 @@ def test_gemv_parity(holo, synth, oracle, qtype, out_dim, in_dim, xmode):
     try:
         W, x, got = _run(holo, synth, qtype, out_dim, in_dim, seed=out_dim * 7919 + in_dim)
     finally:
-        holo.lib().holo_gemv_set_xmode(1)
+        holo.lib().holo_gemv_set_xmode(2)
     want = oracle.matmul(qtype, W, x, out_dim, in_dim)
     truth = oracle.truth(qtype, W, x, out_dim, in_dim)
     e_n, e_r = normwise_err(got, want), max_rel_err(got, want)

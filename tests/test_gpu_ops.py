@@ -30,13 +30,21 @@ def down(buf, n, dtype=np.float32):
 
 # ---- fused multi-GEMVs ---------------------------------------------------------------
 
+@pytest.fixture(params=[3, 0], ids=["mfma", "f32"])
+def xmode(request, holo):
+    holo.lib().holo_gemv_set_xmode(request.param)
+    yield request.param
+    holo.lib().holo_gemv_set_xmode(2)
+
+
 @pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K], ids=["q8_0", "q4_0", "q4_k"])
-@pytest.mark.parametrize("dims", [(4096, 1024, 4096), (512, 512, 512), (96, 32, 256 * 3)], ids=str)
-def test_batched_qkv(holo, synth, oracle, t, dims):
+@pytest.mark.parametrize("dims", [(4096, 1024, 4096), (512, 512, 512), (96, 32, 256 * 3), (37, 13, 256 * 3)],
+                         ids=str)
+def test_batched_qkv(holo, synth, oracle, t, dims, xmode):
     q_dim, kv_dim, in_dim = dims
     if in_dim % QK[t]:
         pytest.skip("in_dim not a multiple of the block")
-    print(f"case qkv type {t} {dims}", flush=True)
+    print(f"case qkv type {t} {dims} xmode {xmode}", flush=True)
     Wq, Wk, Wv = (synth.blocks(t, r, in_dim, seed=s) for r, s in ((q_dim, 1), (kv_dim, 2), (kv_dim, 3)))
     x = synth.normal(in_dim, seed=4)
     dW = [up(holo, w) for w in (Wq, Wk, Wv)]
@@ -57,10 +65,10 @@ def test_batched_qkv(holo, synth, oracle, t, dims):
 
 
 @pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K], ids=["q8_0", "q4_0", "q4_k"])
-@pytest.mark.parametrize("dims", [(11008, 4096), (300, 512)], ids=str)
-def test_batched_gate_up(holo, synth, oracle, t, dims):
+@pytest.mark.parametrize("dims", [(11008, 4096), (300, 512), (301, 256 * 3)], ids=str)
+def test_batched_gate_up(holo, synth, oracle, t, dims, xmode):
     ffn, in_dim = dims
-    print(f"case gate_up type {t} {dims}", flush=True)
+    print(f"case gate_up type {t} {dims} xmode {xmode}", flush=True)
     W1 = synth.blocks(t, ffn, in_dim, seed=11)
     W3 = synth.blocks(t, ffn, in_dim, seed=12)
     x = synth.normal(in_dim, seed=13)
