@@ -16,10 +16,14 @@ The printed JSON line carries
   value         aggregate weight GB/s over the K timed steps (HIP events on the
                 library stream around the timed region)
   roofline      dominant kernel = the fused gate/up Q4_0 GEMV (50,724,864 weight
-                bytes per launch); achieved = those bytes / its mean launch
-                duration, measured with HIP events around each launch in a
-                second, identical pass; traffic = HBM bytes per launch from the
-                committed PMC summary profiles/traffic_q4_0_gateup_<mode>.json
+                bytes per launch); achieved = those bytes / its mean kernel
+                duration, measured in a second pass of the same layers issued
+                back to back, with HIP events that the launch itself records
+                at the kernel's start and end
+                (holo_time_next_launch; the span rocprofv3's kernel trace
+                reports), also given with events around the call; traffic =
+                HBM bytes per launch from the committed PMC summary
+                profiles/traffic_q4_0_gateup_<mode>.json
   cpu_baseline  the reference's own CPU path: matmul_q (src/ai/llm.c:770),
                 compiled from the reference sources into oracle/_ref/ with its
                 release flags; the Q4_0 branch is single-threaded scalar code;
@@ -99,8 +103,10 @@ class Acts:
 
 # ---- layer step ------------------------------------------------------------------------
 
-def layer_fused(lib, L, A, ev=None):
-    """The 4 launches of a layer; `ev` = (start, stop) event pairs per launch."""
+def layer_fused(lib, L, A, ev=None, kernel_ev=None):
+    """The 4 launches of a layer; `ev` = (start, stop) event pairs around each
+    launch; `kernel_ev` = (j, start, stop): events on launch j's kernel alone
+    (holo_time_next_launch)."""
     b = L.buf
     calls = [
         lambda: lib.holo_batched_qkv(A["q"], A["k"], A["v"], b["q"].ptr, b["k"].ptr, b["v"].ptr, A["x4096"],
@@ -110,10 +116,12 @@ def layer_fused(lib, L, A, ev=None):
         lambda: lib.cuda_matmul_q4_0(A["y4096"], b["down"].ptr, A["h"], DIM, FFN),
     ]
     for j, c in enumerate(calls):
-        if ev:
+        if ev and ev[j][0]:
             lib.holo_event_record(ev[j][0])
+        if kernel_ev and kernel_ev[0] == j:
+            lib.holo_time_next_launch(kernel_ev[1], kernel_ev[2])
         c()
-        if ev:
+        if ev and ev[j][1]:
             lib.holo_event_record(ev[j][1])
 
 
@@ -150,15 +158,25 @@ def time_graphs(lib, graphs, steps, warmup):
     return ms
 
 
-def mean_launch_us(lib, layers, A, steps, which):
-    """Mean duration (HIP events around each launch) of launch index `which`."""
-    pairs = [(lib.holo_event_create(), lib.holo_event_create()) for _ in range(4)]
-    durs = []
-    for i in range(steps):
-        layer_fused(lib, layers[i % len(layers)], A, ev=pairs)
-        lib.cuda_sync()
-        durs.append(lib.holo_event_elapsed_ms(*pairs[which]))
-    for a, b in pairs:
+def mean_launch_us(lib, layers, A, steps, which, kernel_only):
+    """Mean duration of launch index `which` of the layer step, over `steps`
+    layers issued back to back (one synchronisation at the end, as in the
+    timed graph pass).  kernel_only: HIP events that the launch records at
+    its kernel's start and end (the span rocprofv3's kernel trace measures);
+    otherwise events recorded around the call."""
+    n = min(steps, 64)
+    evs = [(lib.holo_event_create(), lib.holo_event_create()) for _ in range(n)]
+    for i in range(n):
+        e0, e1 = evs[i]
+        if kernel_only:
+            layer_fused(lib, layers[i % len(layers)], A, kernel_ev=(which, e0, e1))
+        else:
+            ev = [(None, None)] * 4
+            ev[which] = (e0, e1)
+            layer_fused(lib, layers[i % len(layers)], A, ev=ev)
+    lib.cuda_sync()
+    durs = [lib.holo_event_elapsed_ms(a, b) for a, b in evs]
+    for a, b in evs:
         lib.holo_event_destroy(a)
         lib.holo_event_destroy(b)
     holo.check("per-launch pass")
@@ -345,11 +363,12 @@ def main():
     bytes_step = weight_bytes(Q4_0, LAYER)
     gbs = a.steps * bytes_step / (total_ms * 1e-3) / 1e9
     ms_step = total_ms / a.steps
-    gu_us = mean_launch_us(lib, layers, A, a.steps, which=2)
+    gu_us = mean_launch_us(lib, layers, A, a.steps, which=2, kernel_only=a.xmode == "mfma")
+    gu_call_us = mean_launch_us(lib, layers, A, a.steps, which=2, kernel_only=False)
     gu_bytes = 2 * holo.row_bytes(Q4_0, DIM) * FFN
     achieved = gu_bytes / (gu_us * 1e-6) / 1e9
-    log(f"layer step (fused, graph): {ms_step * 1e3:.1f} us/step, {gbs:.0f} GB/s; gate/up launch {gu_us:.2f} us "
-        f"-> {achieved:.0f} GB/s")
+    log(f"layer step (fused, graph): {ms_step * 1e3:.1f} us/step, {gbs:.0f} GB/s; gate/up kernel {gu_us:.2f} us "
+        f"-> {achieved:.0f} GB/s (events around the call: {gu_call_us:.2f} us)")
 
     extra = {}
     if not a.no_extra:
@@ -420,7 +439,8 @@ def main():
         "roofline": {"bound": "hbm", "kernel": ("holo::gemv_mfma_kernel<Q4_0, gate/up>" if a.xmode == "mfma" else "holo::gemv_kernel<Q4_0, gate/up>"),
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(a.xmode),
-                     "bytes_per_launch": gu_bytes, "mean_launch_us": round(gu_us, 3)},
+                     "bytes_per_launch": gu_bytes, "mean_launch_us": round(gu_us, 3),
+                     "mean_launch_us_events_around_call": round(gu_call_us, 3)},
         "extra": extra,
     }
     if not a.no_cpu:

@@ -45,6 +45,7 @@
 #include "common.h"
 #include "quant_blocks.h"
 
+#include <hip/hip_ext.h>
 #include <limits.h>
 #include <stdlib.h>
 
@@ -220,12 +221,13 @@ __device__ __forceinline__ float4 load_x4(__amdgpu_buffer_rsrc_t rs, uint32_t of
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
-__device__ __forceinline__ void x_preload(const float *__restrict__ x, int units, float4 (&pre)[kPreX])
+template <int NPX = kPreX>
+__device__ __forceinline__ void x_preload(const float *__restrict__ x, int units, float4 (&pre)[NPX])
 {
     const int tid = threadIdx.x;
     const __amdgpu_buffer_rsrc_t rs = x_rsrc(x, units);
 #pragma unroll
-    for (int k = 0; k < kPreX; k++) {
+    for (int k = 0; k < NPX; k++) {
         const int i = tid + kThreads * k;
         pre[k] = load_x4(rs, i < units * 8 ? (uint32_t)i * 16u : kOutOfRange);
     }
@@ -263,19 +265,19 @@ __device__ __forceinline__ void x_convert(const float4 v, int i, int units, void
     }
 }
 
-template <int FMT, int XM>
-__device__ __forceinline__ void x_stage(const float *__restrict__ x, int units, void *lds, const float4 (&pre)[kPreX])
+template <int FMT, int XM, int NPX = kPreX>
+__device__ __forceinline__ void x_stage(const float *__restrict__ x, int units, void *lds, const float4 (&pre)[NPX])
 {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < kPreX; k++) {
+    for (int k = 0; k < NPX; k++) {
         const int i = tid + kThreads * k;
         if (i < units * 8) x_convert<FMT, XM>(pre[k], i, units, lds);
     }
-    // in_dim > 16384: the remaining chunks are loaded here (after the weight
-    // loads, so their wait includes the first tile's weights)
+    // rows longer than the preload: the remaining chunks are loaded here
+    // (after the weight loads, so their wait includes the first tile's weights)
     const __amdgpu_buffer_rsrc_t rs = x_rsrc(x, units);
-    for (int i = tid + kThreads * kPreX; i < units * 8; i += kThreads)
+    for (int i = tid + kThreads * NPX; i < units * 8; i += kThreads)
         x_convert<FMT, XM>(load_x4(rs, (uint32_t)i * 16u), i, units, lds);
 }
 
@@ -848,6 +850,8 @@ struct MfmaArgs {
     int row_end[kMaxSeg];  // prefix sums of the matrices' rows (PLAIN); unused entries INT_MAX
     int total_rows;        // rows of all matrices (PLAIN) or of one (GATEUP)
     int max_tiles;         // tiles of the longest workgroup range
+    int full_tiles;        // F: full tiles per workgroup (dealt round-robin)
+    int rem_start;         // first row after the full tiles: F * grid * TR
     const float *x;
     int units;             // 32-weight units per row
     int nsegs;             // G: 16-unit segments per row
@@ -879,16 +883,19 @@ __global__ __launch_bounds__(kThreads) void gemv_mfma_kernel(MfmaArgs args)
     // the grid (at any moment the grid reads one contiguous stretch of the
     // matrices), then an even share of the remaining rows as one short tile
     // (its spare rows re-read the tile's last row and are not stored).
-    const int W = (int)gridDim.x, wg = (int)blockIdx.x;
-    const int F = args.total_rows / (W * TR);
-    const int rem0 = F * W * TR, rem = args.total_rows - rem0;
-    const int ex0 = rem0 + (int)(((int64_t)wg * rem) / W), ex1 = rem0 + (int)(((int64_t)(wg + 1) * rem) / W);
+    // (F and the remainder's start come from the host: a division here would
+    // delay every workgroup's first load.)
+    const uint32_t W = gridDim.x, wg = blockIdx.x;
+    const int F = args.full_tiles;
+    const int rem0 = args.rem_start;
+    const uint32_t rem = (uint32_t)(args.total_rows - rem0);  // < W * TR, so wg * rem fits 32 bits
+    const int ex0 = rem0 + (int)((wg * rem) / W), ex1 = rem0 + (int)(((wg + 1) * rem) / W);
     const int my_tiles = F + (ex1 > ex0 ? 1 : 0);
     const int Q = my_tiles * P;  // item slots of this wave: P per tile
     // rows [row0, rend) of local tile k
     auto tile_rows = [&](int k, int &row0, int &rend) {
         if (k < F) {
-            row0 = (k * W + wg) * TR;
+            row0 = (k * (int)W + (int)wg) * TR;
             rend = row0 + TR;
         } else {
             row0 = ex0;
@@ -992,11 +999,15 @@ __global__ __launch_bounds__(kThreads) void gemv_mfma_kernel(MfmaArgs args)
         }
     };
 
+    // x preload: 2P float4 per thread cover rows of up to 128 P units, which
+    // is every row with P items per wave (G = units/16 <= 8 P); each load
+    // instruction costs issue time at kernel start, so no more are issued.
+    constexpr int NPX = 2 * P;
     Raw2<FMT> b0, b1;
-    float4 pre[kPreX];
-    x_preload(args.x, units, pre);
+    float4 pre[NPX];
+    x_preload<NPX>(args.x, units, pre);
     issue(b0, 0);
-    x_stage<FMT, XM_MFMA>(args.x, units, lds, pre);
+    x_stage<FMT, XM_MFMA, NPX>(args.x, units, lds, pre);
     if (threadIdx.x < kZeroBytes / 16) ((uint4 *)(ldsb + zero_off))[threadIdx.x] = make_uint4(0, 0, 0, 0);
     for (int i = threadIdx.x; i < args.max_tiles; i += kThreads) tcnt[i] = 0;
     __syncthreads();
@@ -1082,6 +1093,9 @@ static void launch_r(GemvArgs &a, int R, int P)
     }
 }
 
+// holo_time_next_launch: events for the next MFMA GEMV launch
+static void *g_time_start = nullptr, *g_time_stop = nullptr;
+
 template <int FMT>
 static size_t mfma_lds_bytes(int units, int max_tiles)
 {
@@ -1121,6 +1135,8 @@ static void launch_mfma(MfmaArgs &a, int P)
     constexpr int TR = MODE == MODE_GATEUP ? 8 : 16;
     const int blocks = mfma_grid<FMT>(a.total_rows, TR, a.units);
     a.max_tiles = mfma_max_tiles(a.total_rows, TR, blocks);
+    a.full_tiles = a.total_rows / (blocks * TR);
+    a.rem_start = a.full_tiles * blocks * TR;
     const size_t lds = mfma_lds_bytes<FMT>(a.units, a.max_tiles);
     auto go = [&](auto kern) {
         // more than 64 KB of LDS must be enabled per kernel (once)
@@ -1130,7 +1146,14 @@ static void launch_mfma(MfmaArgs &a, int P)
                                            (int)kMaxMfmaLds));
             attr = true;
         }
-        hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, stream(), a);
+        if (g_time_start) {
+            // events at the kernel's own start and end (holo_time_next_launch)
+            hipExtLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, stream(), (hipEvent_t)g_time_start,
+                                  (hipEvent_t)g_time_stop, 0, a);
+            g_time_start = g_time_stop = nullptr;
+        } else {
+            hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, stream(), a);
+        }
         HOLO_LAUNCH_CHECK();
     };
     switch (P) {
@@ -1365,6 +1388,12 @@ void holo_gemv_set_xmode(int xmode)
     tuning();
     g_tune.xmode = xmode == 1 ? XM_I24 : (xmode == 2 || xmode == 3) ? XM_MFMA : XM_F32;
     g_tune.mfma_q8 = xmode == 3;
+}
+
+void holo_time_next_launch(void *start_event, void *stop_event)
+{
+    g_time_start = start_event;
+    g_time_stop = stop_event;
 }
 
 void holo_gemv_set_launch(int rows_per_item, int wg_per_cu)

@@ -125,6 +125,7 @@ _SIGS = {
     "holo_graph_destroy": (None, [_P]),
     "holo_matmul": (None, [_P, _P, _P, _I, _I, _I]),
     "holo_gemv_set_xmode": (None, [_I]),
+    "holo_time_next_launch": (None, [_P, _P]),
     "holo_gemv_set_launch": (None, [_I, _I]),
     "holo_dequant": (None, [_P, _P, _I64, _I]),
     "holo_batched_qkv": (None, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I]),

@@ -77,6 +77,12 @@ void holo_gemv_set_xmode(int xmode);
  * F32/I24 use 1 when the grid has at most 2 tiles per CU, else 2; MFMA
  * uses 1 or 2 by how evenly the rows fill its tiles).  A tuning knob.      */
 void holo_gemv_set_launch(int rows_per_item, int wg_per_cu);
+/* Times one kernel: the next launch of the MFMA GEMV path records start_event
+ * when its first wave starts and stop_event when its last wave ends
+ * (hipExtLaunchKernelGGL), so the events span the kernel alone, without the
+ * dispatch latency an event pair around the call includes.  One launch only;
+ * a launch that takes another path leaves the request pending.              */
+void holo_time_next_launch(void *start_event, void *stop_event);
 
 /* ---- dequantisation ---------------------------------------------------------
  * dst[n] = the fp32 weights of n/QK blocks, bit-identical to the reference
