@@ -7,10 +7,12 @@ batch 1"): one step = the 7 Q4_0 GEMVs of one Llama-2-7B layer,
 = 113,836,032 weight bytes, issued as a decode loop on MI355X issues them:
 holo_batched_qkv (q, k, v in one launch), cuda_matmul_q4_0 (o),
 holo_batched_ffn_gate_up (gate and up in one launch, silu(g)*u epilogue) and
-cuda_matmul_q4_0 (down), the four launches of a layer captured in one HIP
-graph.  Steps rotate over --layers distinct synthetic layers (default 32,
-3.64 GB, far above the 256 MB MALL), so each step streams its weights from
-HBM; all inputs are resident in HBM before timing starts.
+cuda_matmul_q4_0 (down).  Steps rotate over --layers distinct synthetic
+layers (default 32, 3.64 GB, far above the 256 MB MALL), so each step streams
+its weights from HBM; all inputs are resident in HBM before timing starts.
+Consecutive steps are captured together in HIP graphs (as a decode loop
+captures its layers), so the timed region holds the K steps' kernels and no
+per-step host launch.
 
 The printed JSON line carries
   value         aggregate weight GB/s over the K timed steps (HIP events on the
@@ -28,7 +30,8 @@ The printed JSON line carries
                 compiled from the reference sources into oracle/_ref/ with its
                 release flags; the Q4_0 branch is single-threaded scalar code;
                 a bounded sample of the same layer
-  extra         the unfused drop-in layer (7 cuda_matmul_q4_0 calls), configs
+  extra         the unfused drop-in layer (7 cuda_matmul_q4_0 calls), the layer
+                as one multi-stage launch (holo_gemv_chain), configs
                 1 and 3 (Q8_0 4096x4096; Q4_K Llama-3-8B FFN), config 4 (batched
                 prefill GEMM, int8 MFMA TOP/s), config 5 (full synthetic
                 Llama-2-7B Q4_0 decode step: end-to-end and matmuls-only ms)
@@ -125,6 +128,18 @@ def layer_fused(lib, L, A, ev=None, kernel_ev=None):
             lib.holo_event_record(ev[j][1])
 
 
+def layer_chain(lib, L, A):
+    """The same four GEMVs as one holo_gemv_chain launch (grid-wide barriers
+    between the stages, next stage's first weights issued before each)."""
+    b = L.buf
+    st = [holo.gemv_stage([b["q"].ptr, b["k"].ptr, b["v"].ptr], [A["q"], A["k"], A["v"]], [DIM] * 3, A["x4096"], DIM),
+          holo.gemv_stage([b["o"].ptr], [A["y4096"]], [DIM], A["v"], DIM),
+          holo.gemv_stage([b["gate"].ptr, b["up"].ptr], [A["h"]], [FFN], A["x4096"], DIM, gate_up=True),
+          holo.gemv_stage([b["down"].ptr], [A["y4096"]], [DIM], A["h"], FFN)]
+    if holo.gemv_chain(st, Q4_0) != 0:
+        raise holo.HoloError("holo_gemv_chain rejected the layer")
+
+
 def layer_unfused(lib, L, A):
     """The reference decode loop's pattern: one cuda_matmul_q4_0 per matrix."""
     for name, o, i in LAYER:
@@ -155,6 +170,40 @@ def time_graphs(lib, graphs, steps, warmup):
     lib.cuda_sync()
     ev.close()
     holo.check("timed graphs")
+    return ms
+
+
+MAX_STEPS_PER_GRAPH = 256
+
+
+def time_steps(lib, layers, step_fn, steps, warmup):
+    """Time exactly `steps` layer steps (layer i % len(layers) for step i),
+    issued as a decode loop issues its layers: consecutive steps captured
+    together in HIP graphs (at most MAX_STEPS_PER_GRAPH per graph), so the
+    timed region holds the steps' kernels and no per-step host launch.  The
+    `warmup` steps run first, in graphs of their own."""
+    def build(first, count):
+        out = []
+        for g0 in range(0, count, MAX_STEPS_PER_GRAPH):
+            n = min(MAX_STEPS_PER_GRAPH, count - g0)
+            out.append(capture(lib, lambda g0=g0, n=n: [step_fn(layers[(first + g0 + j) % len(layers)])
+                                                        for j in range(n)]))
+        return out
+    warm = build(0, warmup) if warmup > 0 else []
+    timed = build(warmup, steps)
+    for g in warm:
+        lib.holo_graph_launch(g)
+    lib.cuda_sync()
+    ev = holo.Events()
+    ev.start()
+    for g in timed:
+        lib.holo_graph_launch(g)
+    ms = ev.stop()
+    lib.cuda_sync()
+    ev.close()
+    for g in warm + timed:
+        lib.holo_graph_destroy(g)
+    holo.check("timed steps")
     return ms
 
 
@@ -358,8 +407,7 @@ def main():
     log(f"generated + uploaded {a.layers} Q4_0 layers ({a.layers * weight_bytes(Q4_0, LAYER) / 1e9:.2f} GB) "
         f"in {time.time() - t0:.1f}s")
 
-    graphs = [capture(lib, lambda L=L: layer_fused(lib, L, A)) for L in layers]
-    total_ms = time_graphs(lib, graphs, a.steps, a.warmup)
+    total_ms = time_steps(lib, layers, lambda L: layer_fused(lib, L, A), a.steps, a.warmup)
     bytes_step = weight_bytes(Q4_0, LAYER)
     gbs = a.steps * bytes_step / (total_ms * 1e-3) / 1e9
     ms_step = total_ms / a.steps
@@ -373,14 +421,18 @@ def main():
     extra = {}
     if not a.no_extra:
         # the reference decode loop's pattern: 7 cuda_matmul_q4_0 launches per layer
-        ug = [capture(lib, lambda L=L: layer_unfused(lib, L, A)) for L in layers]
-        ums = time_graphs(lib, ug, a.steps, a.warmup)
+        ums = time_steps(lib, layers, lambda L: layer_unfused(lib, L, A), a.steps, a.warmup)
         extra["layer_unfused_drop_in"] = {"gbs": round(a.steps * bytes_step / (ums * 1e-3) / 1e9, 1),
                                           "us_per_step": round(ums * 1e3 / a.steps, 2),
                                           "launches_per_step": 7}
-        for g in ug:
-            lib.holo_graph_destroy(g)
         log(f"layer step (7 drop-in launches): {ums * 1e3 / a.steps:.1f} us/step")
+        if a.xmode == "mfma":
+            cms = time_steps(lib, layers, lambda L: layer_chain(lib, L, A), a.steps, a.warmup)
+            if lib.holo_gemv_chain_status() != 0:
+                raise holo.HoloError("multi-stage launch could not synchronise")
+            extra["layer_one_launch_chain"] = {"gbs": round(a.steps * bytes_step / (cms * 1e-3) / 1e9, 1),
+                                               "us_per_step": round(cms * 1e3 / a.steps, 2), "launches_per_step": 1}
+            log(f"layer step (one holo_gemv_chain launch): {cms * 1e3 / a.steps:.1f} us/step")
 
         # config 5: full decode step (32 layers + Q8_0 head)
         if a.layers >= 32:
@@ -402,9 +454,6 @@ def main():
             log(f"config 5 decode step: matmuls {mm_ms:.3f} ms, end-to-end {full_ms:.3f} ms")
             del head
 
-        for g in graphs:
-            lib.holo_graph_destroy(g)
-        graphs = []
         del layers
 
         # configs 1 and 3 over enough copies to defeat the MALL

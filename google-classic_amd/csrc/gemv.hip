@@ -215,13 +215,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t x_rsrc(const float *x, int uni
     return __builtin_amdgcn_make_buffer_rsrc((void *)x, (short)0, units * 128, kBufferWord3);
 }
 
+// Cache policy of the activation loads: 0 = default; kDeviceScope (sc1) = a
+// device-coherent read, which never returns a line this XCD's L2 holds from
+// before another XCD wrote it (the multi-stage launch reads earlier stages'
+// outputs this way, without invalidating the cache).
+constexpr int kDeviceScope = 16;
+
+template <int CPOL = 0>
 __device__ __forceinline__ float4 load_x4(__amdgpu_buffer_rsrc_t rs, uint32_t off)
 {
-    v4f v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
+    v4f v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, CPOL));
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
-template <int NPX = kPreX>
+template <int NPX = kPreX, int CPOL = 0>
 __device__ __forceinline__ void x_preload(const float *__restrict__ x, int units, float4 (&pre)[NPX])
 {
     const int tid = threadIdx.x;
@@ -229,7 +236,7 @@ __device__ __forceinline__ void x_preload(const float *__restrict__ x, int units
 #pragma unroll
     for (int k = 0; k < NPX; k++) {
         const int i = tid + kThreads * k;
-        pre[k] = load_x4(rs, i < units * 8 ? (uint32_t)i * 16u : kOutOfRange);
+        pre[k] = load_x4<CPOL>(rs, i < units * 8 ? (uint32_t)i * 16u : kOutOfRange);
     }
 }
 
@@ -265,7 +272,7 @@ __device__ __forceinline__ void x_convert(const float4 v, int i, int units, void
     }
 }
 
-template <int FMT, int XM, int NPX = kPreX>
+template <int FMT, int XM, int NPX = kPreX, int CPOL = 0>
 __device__ __forceinline__ void x_stage(const float *__restrict__ x, int units, void *lds, const float4 (&pre)[NPX])
 {
     const int tid = threadIdx.x;
@@ -278,7 +285,7 @@ __device__ __forceinline__ void x_stage(const float *__restrict__ x, int units, 
     // (after the weight loads, so their wait includes the first tile's weights)
     const __amdgpu_buffer_rsrc_t rs = x_rsrc(x, units);
     for (int i = tid + kThreads * NPX; i < units * 8; i += kThreads)
-        x_convert<FMT, XM>(load_x4(rs, (uint32_t)i * 16u), i, units, lds);
+        x_convert<FMT, XM>(load_x4<CPOL>(rs, (uint32_t)i * 16u), i, units, lds);
 }
 
 template <int XM>
@@ -859,41 +866,74 @@ struct MfmaArgs {
     int64_t row_bytes;
 };
 
-template <int FMT, int P, int MODE>
-__global__ __launch_bounds__(kThreads) void gemv_mfma_kernel(MfmaArgs args)
-{
+// One GEMV launch's work for this workgroup: the per-workgroup constants
+// derived from MfmaArgs and the item pipeline.  Used by gemv_mfma_kernel (one
+// stage) and gemv_chain_kernel (several dependent stages in one launch).
+// XDEV: activations read and outputs written device-coherently (sc1), as the
+// multi-stage launch passes vectors between its stages through memory.
+template <int FMT, int P, int MODE, bool XDEV = false>
+struct MfmaStage {
     using GE = Geo<FMT>;
-    extern __shared__ uint4 lds[];
-    uint8_t *ldsb = (uint8_t *)lds;
-    constexpr int TR = MODE == MODE_GATEUP ? 8 : 16;  // rows per matrix per tile
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n = lane & 15, g = lane >> 4;
-    const int units = args.units;
-    const int G = args.nsegs;
-    const uint32_t zero_off = (uint32_t)args.x_lds_bytes;
-    uint8_t *stage = ldsb + zero_off + kZeroBytes + wave * GE::STAGE;
-    float *tpart = (float *)(ldsb + zero_off + kZeroBytes + kWaves * GE::STAGE);  // [max_tiles][kWaves][16]
-    uint32_t *tcnt = (uint32_t *)(tpart + args.max_tiles * kWaves * 16);           // [max_tiles]
-    const bool plane_lane = (n >> 2) == g && (n & 3) < 3;
-    const uint32_t plane_off = (uint32_t)(n & 3) * 32u;
-    const uint32_t ls_off = (uint32_t)units * 96u;
+    static constexpr int TR = MODE == MODE_GATEUP ? 8 : 16;  // rows per matrix per tile
 
+    const MfmaArgs &args;
+    uint8_t *ldsb;
+    int lane, wave, n, g, units, G;
+    uint32_t zero_off, plane_off, ls_off;
+    bool plane_lane;
+    uint8_t *stage;
+    float *tpart;
+    uint32_t *tcnt;
     // This workgroup's rows: F full tiles of TR rows dealt round-robin over
     // the grid (at any moment the grid reads one contiguous stretch of the
     // matrices), then an even share of the remaining rows as one short tile
-    // (its spare rows re-read the tile's last row and are not stored).
-    // (F and the remainder's start come from the host: a division here would
-    // delay every workgroup's first load.)
-    const uint32_t W = gridDim.x, wg = blockIdx.x;
-    const int F = args.full_tiles;
-    const int rem0 = args.rem_start;
-    const uint32_t rem = (uint32_t)(args.total_rows - rem0);  // < W * TR, so wg * rem fits 32 bits
-    const int ex0 = rem0 + (int)((wg * rem) / W), ex1 = rem0 + (int)(((wg + 1) * rem) / W);
-    const int my_tiles = F + (ex1 > ex0 ? 1 : 0);
-    const int Q = my_tiles * P;  // item slots of this wave: P per tile
+    // (its spare rows re-read the tile's last row and are not stored).  F and
+    // the remainder's start come from the host: a division here would delay
+    // every workgroup's first load.
+    uint32_t W, wg;
+    int F, ex0, ex1, my_tiles, Q;
+    // Kernel-argument arrays are read only with constant indices: a per-lane
+    // index would turn each access into a memory load ahead of every weight
+    // load.  Row v of all matrices -> (matrix, row) by selects.
+    int re0, re1;
+    uint64_t w0, dw1, dw2, y0, dy1, dy2;
+
+    __device__ __forceinline__ MfmaStage(const MfmaArgs &a, uint8_t *l) : args(a), ldsb(l)
+    {
+        lane = threadIdx.x & 63;
+        wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        n = lane & 15;
+        g = lane >> 4;
+        units = a.units;
+        G = a.nsegs;
+        zero_off = (uint32_t)a.x_lds_bytes;
+        stage = ldsb + zero_off + kZeroBytes + wave * GE::STAGE;
+        tpart = (float *)(ldsb + zero_off + kZeroBytes + kWaves * GE::STAGE);  // [max_tiles][kWaves][16]
+        tcnt = (uint32_t *)(tpart + a.max_tiles * kWaves * 16);               // [max_tiles]
+        plane_lane = (n >> 2) == g && (n & 3) < 3;
+        plane_off = (uint32_t)(n & 3) * 32u;
+        ls_off = (uint32_t)units * 96u;
+        W = gridDim.x;
+        wg = blockIdx.x;
+        F = a.full_tiles;
+        const uint32_t rem = (uint32_t)(a.total_rows - a.rem_start);  // < W * TR: wg * rem fits 32 bits
+        ex0 = a.rem_start + (int)((wg * rem) / W);
+        ex1 = a.rem_start + (int)(((wg + 1) * rem) / W);
+        my_tiles = F + (ex1 > ex0 ? 1 : 0);
+        Q = my_tiles * P;  // item slots of this wave: P per tile
+        re0 = a.row_end[0];
+        re1 = a.row_end[1];
+        w0 = (uint64_t)a.W[0];
+        dw1 = (uint64_t)a.W[1] - w0;
+        dw2 = (uint64_t)a.W[2] - w0;
+        y0 = (uint64_t)a.y[0];
+        dy1 = (uint64_t)a.y[1] - y0;
+        dy2 = (uint64_t)a.y[2] - y0;
+    }
+
     // rows [row0, rend) of local tile k
-    auto tile_rows = [&](int k, int &row0, int &rend) {
+    __device__ __forceinline__ void tile_rows(int k, int &row0, int &rend) const
+    {
         if (k < F) {
             row0 = (k * (int)W + (int)wg) * TR;
             rend = row0 + TR;
@@ -901,25 +941,25 @@ __global__ __launch_bounds__(kThreads) void gemv_mfma_kernel(MfmaArgs args)
             row0 = ex0;
             rend = ex1;
         }
-    };
-
-    // Kernel-argument arrays are read only with constant indices: a per-lane
-    // index would turn each access into a memory load ahead of every weight
-    // load.  Row v of all matrices -> (matrix, row) by selects.
-    const int re0 = args.row_end[0], re1 = args.row_end[1];
-    const uint64_t w0 = (uint64_t)args.W[0], dw1 = (uint64_t)args.W[1] - w0, dw2 = (uint64_t)args.W[2] - w0;
-    const uint64_t y0 = (uint64_t)args.y[0], dy1 = (uint64_t)args.y[1] - y0, dy2 = (uint64_t)args.y[2] - y0;
-    auto split_row = [&](int v, int &m, int &r) {
+    }
+    __device__ __forceinline__ void split_row(int v, int &m, int &r) const
+    {
         const int a1 = v >= re0, a2 = v >= re1;
         m = a1 + a2;
         r = v - (a2 ? re1 : a1 ? re0 : 0);
-    };
-    auto wbase = [&](int m) -> gbyte * { return (gbyte *)(w0 + (m == 2 ? dw2 : m == 1 ? dw1 : 0)); };
-    auto ybase = [&](int m) -> float * { return (float *)(y0 + (m == 2 ? dy2 : m == 1 ? dy1 : 0)); };
+    }
+    __device__ __forceinline__ static void store_y(float *p, float v)
+    {
+        if constexpr (XDEV) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else *p = v;
+    }
+    __device__ __forceinline__ gbyte *wbase(int m) const { return (gbyte *)(w0 + (m == 2 ? dw2 : m == 1 ? dw1 : 0)); }
+    __device__ __forceinline__ float *ybase(int m) const { return (float *)(y0 + (m == 2 ? dy2 : m == 1 ? dy1 : 0)); }
 
     // Slot q: local tile q / P, item (segment) wave + 8 * (q % P).  Slots
     // past the end issue nothing (a wave cannot end before its loads return).
-    auto issue = [&](Raw2<FMT> &b, int q) {
+    __device__ __forceinline__ void issue(Raw2<FMT> &b, int q) const
+    {
         if (q >= Q) return;
         const int k = q / P, p = q - k * P;
         int row0, rend;
@@ -936,22 +976,23 @@ __global__ __launch_bounds__(kThreads) void gemv_mfma_kernel(MfmaArgs args)
             } else {
                 split_row(min(row0 + pc.row, rend - 1), m, row);
             }
-            gbyte *a = wbase(m) + (int64_t)row * args.row_bytes + seg * GE::SEGB + 16 * pc.col;
-            b.v[i] = *(gu32x4a *)a;
+            gbyte *ap = wbase(m) + (int64_t)row * args.row_bytes + seg * GE::SEGB + 16 * pc.col;
+            b.v[i] = *(gu32x4a *)ap;
         }
-    };
+    }
 
     // the item into the wave's stage (16-byte piece p at 16 p)
-    auto stage_write = [&](const Raw2<FMT> &b) {
+    __device__ __forceinline__ void stage_write(const Raw2<FMT> &b) const
+    {
 #pragma unroll
         for (int i = 0; i < GE::NL; i++) {
             const int pc = 64 * i + lane;
             if (GE::NP % 64 == 0 || pc < GE::NP) *(u32x4a *)(stage + 16 * pc) = b.v[i];
         }
-    };
+    }
 
-    float acc = 0.f;
-    auto process = [&](int q) {
+    __device__ __forceinline__ void process(int q, float &acc) const
+    {
         const int k = q / P, p = q - k * P;
         const int j = wave + kWaves * p;
         if (j < G) {
@@ -989,39 +1030,179 @@ __global__ __launch_bounds__(kThreads) void gemv_mfma_kernel(MfmaArgs args)
                     float s1 = 0.f;
 #pragma unroll
                     for (int w = 0; w < kWaves; w++) s1 += pt[w * 16 + 8 + lane];
-                    if (v < rend) ybase(0)[v] = silu(s0) * s1;
+                    if (v < rend) store_y(ybase(0) + v, silu(s0) * s1);
                 } else if (v < rend) {
                     int m, row;
                     split_row(v, m, row);
-                    ybase(m)[row] = s0;
+                    store_y(ybase(m) + row, s0);
                 }
             }
         }
-    };
+    }
 
-    // x preload: 2P float4 per thread cover rows of up to 128 P units, which
-    // is every row with P items per wave (G = units/16 <= 8 P); each load
-    // instruction costs issue time at kernel start, so no more are issued.
-    constexpr int NPX = 2 * P;
+    // x into LDS (planes, {dx, c} pairs, the zero region) and the tile
+    // counters cleared; the caller's barrier follows.  x preload: 2P float4
+    // per thread cover rows of up to 128 P units, which is every row with P
+    // items per wave (G = units/16 <= 8 P); each load instruction costs issue
+    // time, so no more are issued.  `first` (loads of slot 0) is issued after
+    // the x loads, so the conversion does not wait for it.
+    __device__ __forceinline__ void stage_x(Raw2<FMT> &first, bool issue_first) const
+    {
+        constexpr int NPX = 2 * P;
+        constexpr int CPOL = XDEV ? kDeviceScope : 0;
+        float4 pre[NPX];
+        x_preload<NPX, CPOL>(args.x, units, pre);
+        if (issue_first) issue(first, 0);
+        x_stage<FMT, XM_MFMA, NPX, CPOL>(args.x, units, (void *)ldsb, pre);
+        if (threadIdx.x < kZeroBytes / 16) ((uint4 *)(ldsb + zero_off))[threadIdx.x] = make_uint4(0, 0, 0, 0);
+        for (int i = threadIdx.x; i < args.max_tiles; i += kThreads) tcnt[i] = 0;
+    }
+
+    // All item slots, slot 0 already issued into b0.  One item in flight per
+    // wave: the next item is issued once the current one has arrived (more
+    // outstanding loads measured slower on MI355X).
+    __device__ __forceinline__ void run(Raw2<FMT> &b0, Raw2<FMT> &b1) const
+    {
+        float acc = 0.f;
+        for (int q = 0; q < Q; q += 2) {
+            stage_write(b0);
+            issue(b1, q + 1);
+            process(q, acc);
+            if (q + 1 < Q) {
+                stage_write(b1);
+                issue(b0, q + 2);
+                process(q + 1, acc);
+            }
+        }
+    }
+};
+
+template <int FMT, int P, int MODE>
+__global__ __launch_bounds__(kThreads) void gemv_mfma_kernel(MfmaArgs args)
+{
+    extern __shared__ uint4 lds[];
+    MfmaStage<FMT, P, MODE> st(args, (uint8_t *)lds);
     Raw2<FMT> b0, b1;
-    float4 pre[NPX];
-    x_preload<NPX>(args.x, units, pre);
-    issue(b0, 0);
-    x_stage<FMT, XM_MFMA, NPX>(args.x, units, lds, pre);
-    if (threadIdx.x < kZeroBytes / 16) ((uint4 *)(ldsb + zero_off))[threadIdx.x] = make_uint4(0, 0, 0, 0);
-    for (int i = threadIdx.x; i < args.max_tiles; i += kThreads) tcnt[i] = 0;
+    st.stage_x(b0, true);
     __syncthreads();
+    st.run(b0, b1);
+}
 
-    // One item in flight per wave: the next item is issued once the current
-    // one has arrived (more outstanding loads measured slower on MI355X).
-    for (int q = 0; q < Q; q += 2) {
-        stage_write(b0);
-        issue(b1, q + 1);
-        process(q);
-        if (q + 1 < Q) {
-            stage_write(b1);
-            issue(b0, q + 2);
-            process(q + 1);
+// ---- several dependent GEMV stages in one launch ----------------------------------
+//
+// A decode layer is a chain of GEMVs whose inputs are earlier outputs.  As
+// separate launches each pays its dispatch, its activation staging and the
+// first HBM round trip of its weights.  gemv_chain_kernel runs the stages in
+// one launch on one workgroup per CU: before the grid-wide barrier that ends
+// a stage, every wave issues the first weight item of the next stage (weights
+// do not depend on the activations), so that item's HBM latency overlaps the
+// barrier and the activation staging.
+//
+// The barrier is a two-level set of counters in device memory that only
+// grow, by a fixed amount per barrier (grid_arrive_wait); every launch leaves
+// them at such a multiple, so the state is valid across launches and graph
+// replays (the grid is the same for every launch).  All
+// workgroups must be resident together: the grid is at most one workgroup per
+// CU and each uses more LDS than half a CU's.  The wait is bounded
+// (kBarrierPolls polls): a workgroup that gives up sets the timeout flag and continues,
+// so no launch can hang; holo_gemv_chain_status() reports and clears it.
+
+constexpr int kMaxStages = 8;
+constexpr uint32_t kBarrierPolls = 1u << 18;  // each poll re-reads and sleeps: ~0.1-0.3 s in all
+
+struct ChainArgs {
+    MfmaArgs st[kMaxStages];
+    int key[kMaxStages];  // 8 * mode + P
+    int nstages;
+    uint32_t *bar;        // barrier words (grid_arrive_wait)
+};
+
+// Barrier words, each on its own 256-byte line: group counters (kBarGroups),
+// the top counter, the timeout flag.
+constexpr int kBarGroups = 8;
+constexpr int kBarStride = 64;  // uint32 words
+constexpr int kBarTop = kBarGroups * kBarStride;
+constexpr int kBarFlag = kBarTop + kBarStride;
+constexpr size_t kBarBytes = (size_t)(kBarFlag + kBarStride) * 4;
+
+// Arrival and wait of one workgroup, by a thread of a wave with no loads
+// outstanding (vmcnt counts loads and stores alike: waiting for the arrival
+// atomic's result also waits for every load the wave issued before it).
+// The caller has made the workgroup's stores complete before.
+__device__ __forceinline__ void grid_arrive_wait(uint32_t *bar)
+{
+    // Two levels, so that no counter takes more than a few dozen atomics:
+    // workgroup b arrives on group counter b % kBarGroups, the last arrival
+    // of a group on the top counter.  Counters only grow, by the group size
+    // (top: by the group count) per barrier, so the barrier number k follows
+    // from the arrival value and the barrier ends when the top counter
+    // reaches k * groups (signed difference: the 32-bit wrap is harmless).
+    const uint32_t G = gridDim.x;
+    const uint32_t ng = G < kBarGroups ? G : kBarGroups;
+    const uint32_t gi = blockIdx.x % ng;
+    const uint32_t size = G / ng + (gi < G % ng ? 1u : 0u);
+    const uint32_t a = __hip_atomic_fetch_add(bar + gi * kBarStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t k = a / size + 1;
+    const uint32_t target = k * ng;
+    if (a + 1 == k * size) {
+        const uint32_t t = __hip_atomic_fetch_add(bar + kBarTop, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t + 1 == target) return;
+    }
+    for (uint32_t polls = 0;; polls++) {
+        const uint32_t c = __hip_atomic_load(bar + kBarTop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((int32_t)(c - target) >= 0) return;
+        if (polls == kBarrierPolls) {
+            __hip_atomic_store(bar + kBarFlag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Calls f with the MfmaStage of (mode, P) = key for stage arguments a.
+template <int FMT, class Fn>
+__device__ __forceinline__ void with_stage(int key, const MfmaArgs &a, uint8_t *ldsb, Fn &&f)
+{
+    switch (key) {
+    case 1: { MfmaStage<FMT, 1, MODE_PLAIN, true> st(a, ldsb); f(st); break; }
+    case 2: { MfmaStage<FMT, 2, MODE_PLAIN, true> st(a, ldsb); f(st); break; }
+    case 3: { MfmaStage<FMT, 3, MODE_PLAIN, true> st(a, ldsb); f(st); break; }
+    case 4: { MfmaStage<FMT, 4, MODE_PLAIN, true> st(a, ldsb); f(st); break; }
+    case 9: { MfmaStage<FMT, 1, MODE_GATEUP, true> st(a, ldsb); f(st); break; }
+    case 10: { MfmaStage<FMT, 2, MODE_GATEUP, true> st(a, ldsb); f(st); break; }
+    case 11: { MfmaStage<FMT, 3, MODE_GATEUP, true> st(a, ldsb); f(st); break; }
+    default: { MfmaStage<FMT, 4, MODE_GATEUP, true> st(a, ldsb); f(st); break; }
+    }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void gemv_chain_kernel(ChainArgs ca)
+{
+    extern __shared__ uint4 lds[];
+    uint8_t *ldsb = (uint8_t *)lds;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    Raw2<FMT> b0, b1;
+    for (int s = 0; s < ca.nstages; s++) {
+        // waves 1-7 issued slot 0 of stage s > 0 before the barrier; wave 0
+        // (which waited at the barrier) issues its slot 0 now
+        with_stage<FMT>(ca.key[s], ca.st[s], ldsb, [&](auto &st) {
+            st.stage_x(b0, s == 0 || wave == 0);
+            __syncthreads();
+            st.run(b0, b1);
+        });
+        if (s + 1 < ca.nstages) {
+            // the stage's outputs are device-coherent stores and the next
+            // stage reads them device-coherently: completing the stores
+            // (workgroup-scope release: no cache maintenance) is all the
+            // ordering the barrier needs
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __syncthreads();
+            if (wave != 0) {
+                with_stage<FMT>(ca.key[s + 1], ca.st[s + 1], ldsb, [&](auto &st) { st.issue(b0, 0); });
+            } else if (threadIdx.x == 0) {
+                grid_arrive_wait(ca.bar);
+            }
+            __syncthreads();
         }
     }
 }
@@ -1247,6 +1428,98 @@ static void gemv_mfma(int fmt, int mode, int nseg, const void *const *W, float *
     }
 }
 
+// ---- multi-stage launch (host) ----
+
+static uint32_t *g_chain_bar = nullptr;  // barrier words (grid_arrive_wait)
+
+bool gemv_chain_init()
+{
+    if (g_chain_bar) return true;
+    if (hipMalloc((void **)&g_chain_bar, kBarBytes) != hipSuccess) {
+        g_chain_bar = nullptr;
+        return false;
+    }
+    return hipMemset(g_chain_bar, 0, kBarBytes) == hipSuccess && hipDeviceSynchronize() == hipSuccess;
+}
+
+void gemv_chain_release()
+{
+    if (g_chain_bar) hipFree(g_chain_bar);
+    g_chain_bar = nullptr;
+}
+
+// Fills the MFMA arguments of one stage for a grid of `grid` workgroups; false
+// if the stage is outside the MFMA path.
+template <int FMT>
+static bool chain_stage_args(const holo_gemv_stage_t &in, int grid, MfmaArgs &a, int &key, size_t &lds)
+{
+    const bool gu = in.gate_up != 0;
+    const int nmat = gu ? 2 : in.nmat;
+    if (nmat < 1 || nmat > kMaxSeg || !in.x || ((uintptr_t)in.x & 3u)) return false;
+    a = MfmaArgs{};
+    a.units = units_per_row(FMT, in.in_dim);
+    a.row_bytes = row_bytes_of(FMT, in.in_dim);
+    if (a.units < 8 || (a.units & 7) || (a.units + 15) / 16 > 4 * kWaves) return false;
+    a.x = in.x;
+    a.nsegs = (a.units + 15) / 16;
+    a.x_lds_bytes = (a.units * lds_bytes_per_unit<XM_I24>() + 15) & ~15;
+    int total = 0;
+    for (int s = 0; s < kMaxSeg; s++) {
+        if (s < nmat) {
+            if (!in.W[s] || ((uintptr_t)in.W[s] & 15u) || in.rows[gu ? 0 : s] <= 0) return false;
+            if (!in.y[gu ? 0 : s]) return false;
+            a.W[s] = (const uint8_t *)in.W[s];
+            a.y[s] = in.y[gu ? 0 : s];
+            total += in.rows[gu ? 0 : s];
+            a.row_end[s] = total;
+        } else {
+            a.W[s] = a.W[0];
+            a.y[s] = a.y[0];
+            a.row_end[s] = INT_MAX;
+        }
+    }
+    const int tr = gu ? 8 : 16;
+    a.total_rows = gu ? in.rows[0] : total;
+    a.max_tiles = mfma_max_tiles(a.total_rows, tr, grid);
+    a.full_tiles = a.total_rows / (grid * tr);
+    a.rem_start = a.full_tiles * grid * tr;
+    const int P = (a.nsegs + kWaves - 1) / kWaves;
+    key = 8 * (gu ? MODE_GATEUP : MODE_PLAIN) + P;
+    lds = mfma_lds_bytes<FMT>(a.units, a.max_tiles);
+    return true;
+}
+
+template <int FMT>
+static int chain_launch(const holo_gemv_stage_t *stages, int nstages)
+{
+    ChainArgs ca = {};
+    const int grid = num_cus();
+    size_t lds = 0;
+    for (int s = 0; s < nstages; s++) {
+        size_t l = 0;
+        if (!chain_stage_args<FMT>(stages[s], grid, ca.st[s], ca.key[s], l)) return HOLO_EINVAL;
+        lds = l > lds ? l : lds;
+    }
+    if (lds > kMaxMfmaLds) return HOLO_EINVAL;
+    ca.nstages = nstages;
+    ca.bar = g_chain_bar;
+    auto kern = gemv_chain_kernel<FMT>;
+    static bool attr = false;
+    if (!attr) {
+        HOLO_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kMaxMfmaLds));
+        attr = true;
+    }
+    // every workgroup must be resident at once (grid barrier)
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)kern, kThreads, lds) != hipSuccess ||
+        per_cu < 1)
+        return HOLO_EINVAL;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream(), ca);
+    HOLO_LAUNCH_CHECK();
+    return 0;
+}
+
 // One launch over up to three matrices sharing x and in_dim.
 static void gemv_multi(int fmt, int mode, int nseg, const void *const *W, float *const *y, const int *rows,
                        const float *x, int in_dim)
@@ -1388,6 +1661,28 @@ void holo_gemv_set_xmode(int xmode)
     tuning();
     g_tune.xmode = xmode == 1 ? XM_I24 : (xmode == 2 || xmode == 3) ? XM_MFMA : XM_F32;
     g_tune.mfma_q8 = xmode == 3;
+}
+
+int holo_gemv_chain(const holo_gemv_stage_t *stages, int nstages, int type)
+{
+    if (!stages || nstages < 1 || nstages > kMaxStages || !g_chain_bar) return HOLO_EINVAL;
+    if (tuning().xmode != XM_MFMA) return HOLO_EINVAL;
+    if (type == HOLO_TYPE_Q4_0) return chain_launch<FMT_Q4_0>(stages, nstages);
+    if (type == HOLO_TYPE_Q4_K) return chain_launch<FMT_Q4_K>(stages, nstages);
+    return HOLO_EINVAL;
+}
+
+int holo_gemv_chain_status(void)
+{
+    if (!g_chain_bar) return 0;
+    uint32_t flag = 0;
+    HOLO_CHECK(hipStreamSynchronize(stream()));
+    HOLO_CHECK(hipMemcpy(&flag, g_chain_bar + kBarFlag, sizeof(flag), hipMemcpyDeviceToHost));
+    if (flag == 0) return 0;
+    // a barrier gave up: the counters may be out of step, so start afresh
+    HOLO_CHECK(hipMemset(g_chain_bar, 0, kBarBytes));
+    HOLO_CHECK(hipDeviceSynchronize());
+    return HOLO_ECHAIN;
 }
 
 void holo_time_next_launch(void *start_event, void *stop_event)

@@ -44,6 +44,7 @@ const char *holo_error_string(int code)
 {
     if (code == 0) return "ok";
     if (code == HOLO_EINVAL) return "invalid argument";
+    if (code == HOLO_ECHAIN) return "multi-stage GEMV launch could not synchronise its workgroups";
     return hipGetErrorString((hipError_t)code);
 }
 
@@ -65,6 +66,10 @@ int cuda_init(void)
         fprintf(stderr, "holo_mi355x: cannot create copy stream\n");
         return -1;
     }
+    if (!holo::gemv_chain_init()) {
+        fprintf(stderr, "holo_mi355x: cannot allocate the GEMV chain barrier\n");
+        return -1;
+    }
     g_initialized = true;
     return 0;
 }
@@ -76,6 +81,7 @@ void cuda_cleanup(void)
     hipDeviceSynchronize();
     if (g_copy_stream) hipStreamDestroy(g_copy_stream);
     g_copy_stream = nullptr;
+    holo::gemv_chain_release();
     g_stream = nullptr;
     g_initialized = false;
 }

@@ -126,6 +126,8 @@ _SIGS = {
     "holo_matmul": (None, [_P, _P, _P, _I, _I, _I]),
     "holo_gemv_set_xmode": (None, [_I]),
     "holo_time_next_launch": (None, [_P, _P]),
+    "holo_gemv_chain": (_I, [_P, _I, _I]),
+    "holo_gemv_chain_status": (_I, []),
     "holo_gemv_set_launch": (None, [_I, _I]),
     "holo_dequant": (None, [_P, _P, _I64, _I]),
     "holo_batched_qkv": (None, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I]),
@@ -136,6 +138,38 @@ _SIGS = {
 }
 
 _lib: C.CDLL | None = None
+
+
+EINVAL, ECHAIN = 100001, 100002
+
+
+class GemvStage(C.Structure):
+    """holo_gemv_stage_t (include/holo_mi355x.h): one stage of holo_gemv_chain."""
+    _fields_ = [("W", C.c_void_p * 3), ("y", C.c_void_p * 3), ("rows", C.c_int * 3), ("nmat", C.c_int),
+                ("gate_up", C.c_int), ("x", C.c_void_p), ("in_dim", C.c_int)]
+
+
+def gemv_stage(W, y, rows, x, in_dim, gate_up=False) -> GemvStage:
+    """A chain stage from device pointers: W, y, rows are sequences (gate/up:
+    W = (gate, up), y = (out,), rows = (ffn_dim,))."""
+    s = GemvStage()
+    for i, w in enumerate(W):
+        s.W[i] = w
+    for i, o in enumerate(y):
+        s.y[i] = o
+    for i, r in enumerate(rows):
+        s.rows[i] = r
+    s.nmat = len(W)
+    s.gate_up = 1 if gate_up else 0
+    s.x = x
+    s.in_dim = in_dim
+    return s
+
+
+def gemv_chain(stages, qtype: int) -> int:
+    """holo_gemv_chain over a list of GemvStage; returns its status code."""
+    arr = (GemvStage * len(stages))(*stages)
+    return lib().holo_gemv_chain(C.cast(arr, C.c_void_p), len(stages), qtype)
 
 
 class HoloError(RuntimeError):
