@@ -33,7 +33,9 @@ The printed JSON line carries
   extra         the unfused drop-in layer (7 cuda_matmul_q4_0 calls), the layer
                 as one multi-stage launch (holo_gemv_chain), configs
                 1 and 3 (Q8_0 4096x4096; Q4_K Llama-3-8B FFN), config 4 (batched
-                prefill GEMM, int8 MFMA TOP/s), config 5 (full synthetic
+                prefill GEMM on the f16 matrix cores: useful TOP/s = 2*M*N*K per
+                kernel time, and its fraction of the dense f16 and int8 peaks),
+                config 5 (full synthetic
                 Llama-2-7B Q4_0 decode step: end-to-end and matmuls-only ms)
 
 Only the CPU-baseline leg touches oracle/.
@@ -58,6 +60,7 @@ from holo_mi355x import synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
+F16_PEAK_TFLOPS = 2500.0   # MI355X dense f16 MFMA
 Q4_0, Q8_0, Q4_K = holo.TYPE_Q4_0, holo.TYPE_Q8_0, holo.TYPE_Q4_K
 BASE_SEED = 20251201
 DIM, FFN, VOCAB = 4096, 11008, 32000
@@ -286,6 +289,10 @@ def decode_step(lib, layers, head, A, ones, matmuls_only):
 # ---- config 4: prefill ------------------------------------------------------------------
 
 def prefill_tops(lib, reps=10):
+    """Config 4: holo_gemm_q4_0_q8_0 at M = 512.  gemm_us is the call (the
+    f16 activation panel pass, the GEMM kernel and the stream-ordered
+    workspace), kernel_us the GEMM kernel alone (holo_time_next_launch).  The
+    block dots run on v_mfma_f32_32x32x16_f16; useful work is 2*M*N*K."""
     M = 512
     out = {}
     for name, (N, K) in (("11008x4096", (FFN, DIM)), ("4096x11008", (DIM, FFN))):
@@ -301,13 +308,22 @@ def prefill_tops(lib, reps=10):
         for _ in range(reps):
             lib.holo_gemm_q4_0_q8_0(Y.ptr, W.ptr, Xq.ptr, M, N, K)
         ms = ev.stop() / reps
+        kernel = []
+        for _ in range(reps):
+            lib.holo_time_next_launch(ev.a, ev.b)
+            lib.holo_gemm_q4_0_q8_0(Y.ptr, W.ptr, Xq.ptr, M, N, K)
+            lib.cuda_sync()
+            kernel.append(float(lib.holo_event_elapsed_ms(ev.a, ev.b)))
+        kms = statistics.median(kernel)
         ev.start()
         for _ in range(reps):
             lib.holo_quantize_act_q8_0(Xq.ptr, X.ptr, M, K)
         qms = ev.stop() / reps
         ev.close()
-        tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-        out[name] = {"gemm_us": round(ms * 1e3, 2), "int_tops": round(tops, 1),
+        ops = 2.0 * M * N * K
+        tops = ops / (kms * 1e-3) / 1e12
+        out[name] = {"gemm_us": round(ms * 1e3, 2), "kernel_us": round(kms * 1e3, 2),
+                     "tops": round(tops, 1), "frac_of_f16_peak": round(tops / F16_PEAK_TFLOPS, 4),
                      "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4), "quantize_us": round(qms * 1e3, 2)}
     holo.check("prefill")
     return out
@@ -374,6 +390,8 @@ def main():
     ap.add_argument("--xmode", choices=["mfma", "f32", "i24"], default="mfma", help="GEMV activation mode")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 3 device-to-device copies of BYTES (HBM counter calibration) and exit")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only run config 4 (prefill GEMM), print its JSON and exit (for profiling)")
     a = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -395,6 +413,9 @@ def main():
         holo.check("copy probe")
         print(json.dumps({"copy_bytes": a.copy_probe, "ms": round(ms, 4),
                           "gbs": round(2 * a.copy_probe / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return
+    if a.prefill_only:
+        print(json.dumps({"config4_prefill_m512": prefill_tops(lib)}), flush=True)
         return
     stream = lib.holo_stream_create()
     lib.holo_set_stream(stream)  # graphs capture a non-null stream

@@ -26,6 +26,10 @@ int num_cus();
 bool gemv_chain_init();
 void gemv_chain_release();
 
+// Events that holo_time_next_launch requested for the next timed kernel
+// launch (MFMA GEMV or prefill GEMM): returns them once and clears them.
+bool take_launch_events(hipEvent_t *start, hipEvent_t *stop);
+
 }  // namespace holo
 
 #define HOLO_CHECK(call)                                                        \

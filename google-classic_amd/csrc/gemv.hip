@@ -1274,8 +1274,18 @@ static void launch_r(GemvArgs &a, int R, int P)
     }
 }
 
-// holo_time_next_launch: events for the next MFMA GEMV launch
+// holo_time_next_launch: events for the next timed launch (MFMA GEMV or
+// prefill GEMM)
 static void *g_time_start = nullptr, *g_time_stop = nullptr;
+
+bool take_launch_events(hipEvent_t *start, hipEvent_t *stop)
+{
+    if (!g_time_start) return false;
+    *start = (hipEvent_t)g_time_start;
+    *stop = (hipEvent_t)g_time_stop;
+    g_time_start = g_time_stop = nullptr;
+    return true;
+}
 
 template <int FMT>
 static size_t mfma_lds_bytes(int units, int max_tiles)
@@ -1327,11 +1337,10 @@ static void launch_mfma(MfmaArgs &a, int P)
                                            (int)kMaxMfmaLds));
             attr = true;
         }
-        if (g_time_start) {
+        hipEvent_t e0, e1;
+        if (take_launch_events(&e0, &e1)) {
             // events at the kernel's own start and end (holo_time_next_launch)
-            hipExtLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, stream(), (hipEvent_t)g_time_start,
-                                  (hipEvent_t)g_time_stop, 0, a);
-            g_time_start = g_time_stop = nullptr;
+            hipExtLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, stream(), e0, e1, 0, a);
         } else {
             hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, stream(), a);
         }

@@ -1,6 +1,7 @@
 // prefill.hip -- batched prefill product over Q4_0 weights: activations are
-// quantised per row and 32-block to Q8_0, and the int8 x int8 block dots run
-// on MFMA (v_mfma_i32_16x16x32_i8, one instruction per 16x16 tile and block).
+// quantised per row and 32-block to Q8_0, and the block dots run on the f16
+// matrix cores (v_mfma_f32_32x32x16_f16), where every operand is a small
+// integer and every block dot is therefore exact.
 //
 // The reference has no batched path (its prompt loop is one GEMV per token,
 // src/ai/llm.c:1049) and no activation quantiser; this is the build's own
@@ -8,19 +9,28 @@
 // (oracle_quantize_act_q8_0, oracle_gemm_q4_0_q8_0):
 //   quantise  d = f16_rne(amax/127), id = 1/(amax/127) (0 if amax = 0),
 //             q = clamp(roundf(x*id), -127, 127)
-//   product   Y[m][n] = sum over blocks b, in order, of
-//             (float)I[m,n,b] * (f16(dw[n,b]) * f16(dx[m,b])),
-//             I = sum_k (qw-8)*qx exact in int32, each step rounded as written
+//   product   Y[m][n]: acc = fmaf((float)I[m,n,b], f16(dw[n,b]) * f16(dx[m,b]), acc)
+//             over blocks b in order, I = sum_k (qw-8)*qx exact
 // Every rounding is specified, so the GPU result is bit-identical to the
-// CPU restatement (no FMA contraction in this file).
+// CPU restatement (no contraction in this file: the one fused multiply-add
+// is written as fmaf).
 #include "common.h"
 #include "quant_blocks.h"
+
+#include <hip/hip_ext.h>
+#include <stdio.h>
+#include <stdlib.h>
 
 #pragma clang fp contract(off)
 
 namespace holo {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 // ---- activation quantiser: one thread per 32-block --------------------------
 
@@ -45,120 +55,308 @@ __global__ __launch_bounds__(256) void quantize_q8_0_k(uint8_t *__restrict__ out
     }
 }
 
-// ---- GEMM ------------------------------------------------------------------------
-// Workgroup: 64 (M) x 64 (N) output tile, 4 waves each owning 32 x 32 (2 x 2
-// MFMA tiles of 16 x 16).  Per 32-block of K the tile's 64 activation blocks
-// and 64 weight blocks are staged in LDS as 32 int8 per row (weights
-// unpacked to q-8) plus the two f16 scales; the next block's raw bytes are
-// loaded into registers while the current one is multiplied.
-//
-// v_mfma_i32_16x16x32_i8 operand layout (wave64): lane l supplies A row
-// l%16, k = 8*(l/16) .. +7 and B column l%16, same k range; it receives
-// D[i][j] for j = l%16, i = 4*(l/16) + 0..3.
+// ---- activation panel: Q8_0 blocks -> f16 values + f16 scale bits ------------
+// P[m][k] = (f16)qx (exact, |qx| <= 127), D[m][b] = the block's d bits.  Block
+// g = m*nb + b lands at P + 32*g, so P is the row-major [M][K] matrix.
 
-constexpr int kTM = 64, kTN = 64;
-
-struct GemmArgs {
-    float *Y;
-    const uint8_t *W;   // Q4_0 [N][K/32]
-    const uint8_t *Xq;  // Q8_0 [M][K/32]
-    int M, N, nb;
-};
-
-// Signed bytes (q - 8) of four nibbles held one per byte.
-__device__ __forceinline__ uint32_t nib_to_s8(uint32_t nib)
+__global__ __launch_bounds__(256) void q8_panel_k(uint4 *__restrict__ P, uint16_t *__restrict__ D,
+                                                  const uint8_t *__restrict__ Xq, int64_t nblocks, int64_t total)
 {
-    uint32_t t = nib ^ 0x08080808u;                      // 4-bit two's complement of q-8
-    uint32_t sign = ((t >> 3) & 0x01010101u) * 0xF0u;    // extend bit 3 into bits 4..7
-    return t | sign;
+    int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= nblocks) return;
+    const Q8_0Unit u = load_q8_0(Xq, g, total);
+    uint32_t w[16];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int8_t lo = (int8_t)(u.q[i] >> (16 * j)), hi = (int8_t)(u.q[i] >> (16 * j + 8));
+            const h2 v = {(_Float16)lo, (_Float16)hi};
+            w[2 * i + j] = __builtin_bit_cast(uint32_t, v);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) P[g * 4 + j] = make_uint4(w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]);
+    D[g] = (uint16_t)u.dh;
 }
 
-__global__ __launch_bounds__(256) void gemm_q4_0_q8_0_k(GemmArgs a)
+// ---- GEMM ------------------------------------------------------------------------
+// Workgroup: 4 waves in a 2 x 2 grid, each wave owning WM x WN tiles of
+// 32 x 32 outputs; the workgroup tile is TM = 64*WM rows (activations) by
+// TN = 64*WN columns (weights).  K advances in stages of S blocks; a stage
+// is staged in LDS as f16 rows (activations copied from the panel, weights
+// unpacked to q-8) plus the f16 scale bits, double-buffered, so one barrier
+// per stage separates the writes of stage s+1 from the reads of stage s-1.
+// The next stage's global loads are issued before the current stage's
+// products and land in registers.
+//
+// v_mfma_f32_32x32x16_f16 (wave64): lane l supplies A[l%32][8*(l/32)+t] and
+// B[8*(l/32)+t][l%32], t = 0..7; D[i][j] lands in lane j + 32*((i/4)%2),
+// register (i%4) + 4*(i/8).  Per block and tile: two instructions give the
+// exact block dot I (k = 0..15, 16..31; integer partial sums < 2^24), and a
+// third, whose only non-zero operands are A[i][0] = dx[i] and B[0][j] = dw[j],
+// gives s[i][j] = dx[i]*dw[j] exactly in the same register layout, leaving
+// one VALU instruction (the fmaf) per output and block.
+
+struct PrefillArgs {
+    float *Y;
+    const uint8_t *W;   // Q4_0 [N][nb]
+    const _Float16 *P;  // f16 [M][K]
+    const uint16_t *D;  // f16 bits [M][nb]
+    int M, N, nb;
+    int ntm, tiles;     // row tiles, all tiles
+    int64_t w_bytes;    // N * nb * 18
+};
+
+template <int WM, int WN, int S>
+struct PGeo {
+    static constexpr int TM = 64 * WM, TN = 64 * WN;
+    static constexpr int ROW = 32 * S + 8;  // f16 per LDS row; the 16-byte pad spreads rows over the banks
+    static constexpr int A_OFF = 0;
+    static constexpr int B_OFF = A_OFF + TM * ROW * 2;
+    static constexpr int AD_OFF = B_OFF + TN * ROW * 2;
+    static constexpr int BD_OFF = AD_OFF + ((TM * S * 2 + 15) & ~15);
+    static constexpr int STAGE = BD_OFF + ((TN * S * 2 + 15) & ~15);
+    static constexpr int LDS = 2 * STAGE;
+    static constexpr int NA = TM * S * 4 / 256;      // 16-byte activation pieces per thread
+    static constexpr int ND = (TM * S + 255) / 256;  // activation scales per thread
+    static constexpr int NB = (TN * S + 255) / 256;  // weight blocks per thread
+    static_assert((TM * S * 4) % 256 == 0, "activation pieces must split evenly over the threads");
+};
+
+// f16 (q - 8) of the eight nibbles of x = qs[4j..4j+3]: lo[0..1] hold k = 4j..4j+3
+// (low nibbles), hi[0..1] k = 16+4j..16+4j+3 (high nibbles).  v_perm pairs a
+// nibble byte with 0x64, giving the f16 value 1024 + q; subtracting 1032 is
+// exact.
+__device__ __forceinline__ void nib_f16(uint32_t x, uint32_t lo[2], uint32_t hi[2])
 {
-    __shared__ uint4 lA[kTM * 2];  // [m][32 bytes]
-    __shared__ uint4 lB[kTN * 2];  // [n][32 bytes]
-    __shared__ float lsa[kTM], lsb[kTN];
+    const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const uint32_t t0 = x & 0x0F0F0F0Fu, t1 = (x >> 4) & 0x0F0F0F0Fu;
+    const uint32_t c64 = 0x64646464u;
+    lo[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(c64, t0, 0x04010400u)) + off);
+    lo[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(c64, t0, 0x04030402u)) + off);
+    hi[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(c64, t1, 0x04010400u)) + off);
+    hi[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(c64, t1, 0x04030402u)) + off);
+}
 
+// Registers of one stage in flight between its global loads and its LDS
+// writes: blocks kb0 .. kb0+S-1 of the workgroup's rows and columns; block
+// indices past the row's last block read the last block again (in bounds,
+// never used).
+template <int WM, int WN, int S>
+struct PStage {
+    using G = PGeo<WM, WN, S>;
+    v4u ra[G::NA];
+    uint32_t rd[G::ND];
+    Q4_0Unit rb[G::NB];
+
+    __device__ __forceinline__ void fetch(const PrefillArgs &a, int tid, int m0, int n0, int kb0)
+    {
+        const int nb = a.nb;
+        const int64_t K = (int64_t)nb * 32;
+#pragma unroll
+        for (int i = 0; i < G::NA; i++) {
+            const int p = tid + 256 * i, r = p / (4 * S), c = p % (4 * S);
+            const int m = min(m0 + r, a.M - 1), b = min(kb0 + c / 4, nb - 1);
+            ra[i] = *(const v4u *)(a.P + (int64_t)m * K + (int64_t)b * 32 + (c % 4) * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < G::ND; i++) {
+            const int v = min(tid + 256 * i, G::TM * S - 1), r = v / S, b = min(kb0 + v % S, nb - 1);
+            rd[i] = a.D[(int64_t)min(m0 + r, a.M - 1) * nb + b];
+        }
+#pragma unroll
+        for (int i = 0; i < G::NB; i++) {
+            const int v = min(tid + 256 * i, G::TN * S - 1), n = v / S, b = min(kb0 + v % S, nb - 1);
+            rb[i] = load_q4_0(a.W, (int64_t)min(n0 + n, a.N - 1) * nb + b, a.w_bytes);
+        }
+    }
+
+    // registers -> one LDS stage buffer (weights unpacked to f16 q-8)
+    __device__ __forceinline__ void stash(uint8_t *base, int tid) const
+    {
+#pragma unroll
+        for (int i = 0; i < G::NA; i++) {
+            const int p = tid + 256 * i, r = p / (4 * S), c = p % (4 * S);
+            *(v4u *)(base + G::A_OFF + (r * G::ROW + c * 8) * 2) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < G::ND; i++) {
+            const int v = tid + 256 * i;
+            if (v < G::TM * S) ((uint16_t *)(base + G::AD_OFF))[v] = (uint16_t)rd[i];
+        }
+#pragma unroll
+        for (int i = 0; i < G::NB; i++) {
+            const int v = tid + 256 * i, n = v / S, s = v % S;
+            if (v < G::TN * S) {
+                uint32_t lo[8], hi[8];
+#pragma unroll
+                for (int j = 0; j < 4; j++) nib_f16(rb[i].q[j], &lo[2 * j], &hi[2 * j]);
+                v4u *dst = (v4u *)(base + G::B_OFF + (n * G::ROW + s * 32) * 2);
+                dst[0] = v4u{lo[0], lo[1], lo[2], lo[3]};  // k = 0..7
+                dst[1] = v4u{lo[4], lo[5], lo[6], lo[7]};  // k = 8..15
+                dst[2] = v4u{hi[0], hi[1], hi[2], hi[3]};  // k = 16..23
+                dst[3] = v4u{hi[4], hi[5], hi[6], hi[7]};  // k = 24..31
+                ((uint16_t *)(base + G::BD_OFF))[v] = (uint16_t)rb[i].dh;
+            }
+        }
+    }
+};
+
+// D: stages of global loads in flight (1 or 2); OCC: workgroups per CU the
+// register allocation is bounded for.
+template <int WM, int WN, int S, int D, int OCC>
+__global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
+{
+    using G = PGeo<WM, WN, S>;
+    extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int m_base = blockIdx.y * kTM, n_base = blockIdx.x * kTN;
-    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+    const int h = lane >> 5, c32 = lane & 31;
 
-    // staging roles: threads 0..63 -> activation row, 64..127 -> weight row
-    const bool stA = tid < 64, stB = tid >= 64 && tid < 128;
-    const int srow = tid & 63;
-    const int am = min(m_base + srow, a.M - 1), bn = min(n_base + srow, a.N - 1);
-    const int64_t a_total = (int64_t)a.M * a.nb * 34, b_total = (int64_t)a.N * a.nb * 18;
+    // Tile of this workgroup.  Workgroups go to the 8 XCDs round-robin; when
+    // the tile count allows, XCD x takes a contiguous run of tiles, so the
+    // row tiles sharing a weight tile share that XCD's L2.
+    const int g = blockIdx.x;
+    const int t = (a.tiles & 7) ? g : (g & 7) * (a.tiles >> 3) + (g >> 3);
+    const int m0 = (t % a.ntm) * G::TM, n0 = (t / a.ntm) * G::TN;
+    const int wm0 = (wave >> 1) * 32 * WM, wn0 = (wave & 1) * 32 * WN;
+    const int nb = a.nb;
+    const int nst = (nb + S - 1) / S;
+    v16f acc[WM][WN];
+#pragma unroll
+    for (int mi = 0; mi < WM; mi++)
+#pragma unroll
+        for (int ni = 0; ni < WN; ni++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[mi][ni][r] = 0.f;
 
-    Q8_0Unit ra;
-    Q4_0Unit rb;
-    auto fetch = [&](int b) {
-        if (stA) ra = load_q8_0(a.Xq, (int64_t)am * a.nb + b, a_total);
-        if (stB) rb = load_q4_0(a.W, (int64_t)bn * a.nb + b, b_total);
+    // Scale operands of v_mfma_f32_32x32x8_f16 (lane l supplies A[l%32][4*(l/32)+t],
+    // B[4*(l/32)+t][l%32], t = 0..3): the f16 scale in element 0 of lanes 0..31,
+    // zero everywhere else, so the product is the single term dx[i]*dw[j].
+    v2u as[WM], bs[WN];
+#pragma unroll
+    for (int mi = 0; mi < WM; mi++) as[mi] = v2u{0u, 0u};
+#pragma unroll
+    for (int ni = 0; ni < WN; ni++) bs[ni] = v2u{0u, 0u};
+
+    auto compute = [&](int buf, int kb0) {
+        const uint8_t *base = lds + buf * G::STAGE;
+        const _Float16 *lA = (const _Float16 *)(base + G::A_OFF);
+        const _Float16 *lB = (const _Float16 *)(base + G::B_OFF);
+        const uint16_t *lAd = (const uint16_t *)(base + G::AD_OFF);
+        const uint16_t *lBd = (const uint16_t *)(base + G::BD_OFF);
+        const v16f zero = {};
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            if (kb0 + s >= nb) break;
+            v8h a0[WM], a1[WM], b0[WN], b1[WN];
+#pragma unroll
+            for (int mi = 0; mi < WM; mi++) {
+                const int r = wm0 + 32 * mi + c32;
+                const _Float16 *pa = lA + r * G::ROW + s * 32 + 8 * h;
+                a0[mi] = *(const v8h *)pa;
+                a1[mi] = *(const v8h *)(pa + 16);
+                as[mi].x = h ? 0u : (uint32_t)lAd[r * S + s];
+            }
+#pragma unroll
+            for (int ni = 0; ni < WN; ni++) {
+                const int n = wn0 + 32 * ni + c32;
+                const _Float16 *pb = lB + n * G::ROW + s * 32 + 8 * h;
+                b0[ni] = *(const v8h *)pb;
+                b1[ni] = *(const v8h *)(pb + 16);
+                bs[ni].x = h ? 0u : (uint32_t)lBd[n * S + s];
+            }
+#pragma unroll
+            for (int mi = 0; mi < WM; mi++)
+#pragma unroll
+                for (int ni = 0; ni < WN; ni++) {
+                    v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0[mi], b0[ni], zero, 0, 0, 0);
+                    I = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[mi], b1[ni], I, 0, 0, 0);
+                    const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, as[mi]),
+                                                                         __builtin_bit_cast(v4h, bs[ni]), zero, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[mi][ni][r] = __builtin_fmaf(I[r], sc[r], acc[mi][ni][r]);
+                }
+        }
     };
 
-    float acc[2][2][4];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) acc[i][j][r] = 0.f;
-
-    fetch(0);
-    for (int b = 0; b < a.nb; b++) {
-        __syncthreads();  // previous block's LDS reads are done
-        if (stA) {
-            lA[srow * 2] = make_uint4(ra.q[0], ra.q[1], ra.q[2], ra.q[3]);
-            lA[srow * 2 + 1] = make_uint4(ra.q[4], ra.q[5], ra.q[6], ra.q[7]);
-            lsa[srow] = ra.d;
-        }
-        if (stB) {
-            uint32_t lo[4], hi[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                lo[i] = nib_to_s8(rb.q[i] & 0x0F0F0F0Fu);         // k = 4i .. 4i+3
-                hi[i] = nib_to_s8((rb.q[i] >> 4) & 0x0F0F0F0Fu);  // k = 16+4i ..
-            }
-            lB[srow * 2] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            lB[srow * 2 + 1] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-            lsb[srow] = rb.d;
-        }
+    PStage<WM, WN, S> pa;
+    pa.fetch(a, tid, m0, n0, 0);
+    pa.stash(lds, tid);
+    if constexpr (D == 1) {
+        // stage st+1 loads while stage st is multiplied
         __syncthreads();
-        if (b + 1 < a.nb) fetch(b + 1);
-
-        const uint8_t *pA = (const uint8_t *)lA, *pB = (const uint8_t *)lB;
-        const int kq = 8 * (lane >> 4);
-#pragma unroll
-        for (int mi = 0; mi < 2; mi++) {
-            const long av = *(const long *)(pA + (wm + mi * 16 + (lane & 15)) * 32 + kq);
-#pragma unroll
-            for (int ni = 0; ni < 2; ni++) {
-                const int n0 = wn + ni * 16;
-                const long bv = *(const long *)(pB + (n0 + (lane & 15)) * 32 + kq);
-                const v4i zero = {0, 0, 0, 0};
-                const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, zero, 0, 0, 0);
-                const float dw = lsb[n0 + (lane & 15)];
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float dx = lsa[wm + mi * 16 + 4 * (lane >> 4) + r];
-                    const float s = dw * dx;
-                    const float t = (float)I[r] * s;
-                    acc[mi][ni][r] = acc[mi][ni][r] + t;
-                }
+        for (int st = 0; st < nst; st++) {
+            if (st + 1 < nst) pa.fetch(a, tid, m0, n0, (st + 1) * S);
+            compute(st & 1, st * S);
+            if (st + 1 < nst) pa.stash(lds + ((st + 1) & 1) * G::STAGE, tid);
+            __syncthreads();
+        }
+    } else {
+        // two register sets carry stages st+1 and st+2 while stage st is
+        // multiplied, so each stage's loads have two stages of products to land
+        PStage<WM, WN, S> pb;
+        if (nst > 1) pa.fetch(a, tid, m0, n0, S);
+        if (nst > 2) pb.fetch(a, tid, m0, n0, 2 * S);
+        __syncthreads();
+        for (int st = 0; st < nst; st += 2) {
+            compute(0, st * S);
+            if (st + 1 < nst) {
+                pa.stash(lds + G::STAGE, tid);
+                if (st + 3 < nst) pa.fetch(a, tid, m0, n0, (st + 3) * S);
             }
+            __syncthreads();
+            if (st + 1 >= nst) break;
+            compute(1, (st + 1) * S);
+            if (st + 2 < nst) {
+                pb.stash(lds, tid);
+                if (st + 4 < nst) pb.fetch(a, tid, m0, n0, (st + 4) * S);
+            }
+            __syncthreads();
         }
     }
 
 #pragma unroll
-    for (int mi = 0; mi < 2; mi++)
+    for (int mi = 0; mi < WM; mi++)
 #pragma unroll
-        for (int ni = 0; ni < 2; ni++)
+        for (int ni = 0; ni < WN; ni++) {
+            const int n = n0 + wn0 + 32 * ni + c32;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m_base + wm + mi * 16 + 4 * (lane >> 4) + r;
-                const int n = n_base + wn + ni * 16 + (lane & 15);
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm0 + 32 * mi + (r & 3) + 4 * h + 8 * (r >> 2);
                 if (m < a.M && n < a.N) a.Y[(int64_t)m * a.N + n] = acc[mi][ni][r];
             }
+        }
+}
+
+// Tile width per problem: the 128 x 128 workgroup tile (64 x 64 per wave)
+// reads the least LDS per product and is used when it yields at least one
+// tile per CU; otherwise the 128 x 64 tile keeps every CU busy.
+static int prefill_tn(int M, int N)
+{
+    const int cus = num_cus() > 0 ? num_cus() : 256;
+    const long tiles128 = (long)((M + 127) / 128) * ((N + 127) / 128);
+    return tiles128 >= cus ? 128 : 64;
+}
+
+template <int WM, int WN, int S, int D, int OCC>
+static void launch_prefill(PrefillArgs a)
+{
+    using G = PGeo<WM, WN, S>;
+    a.ntm = (a.M + G::TM - 1) / G::TM;
+    a.tiles = a.ntm * ((a.N + G::TN - 1) / G::TN);
+    auto kern = gemm_q4_0_f16_k<WM, WN, S, D, OCC>;
+    static bool attr = false;
+    if (!attr) {
+        HOLO_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS));
+        attr = true;
+    }
+    hipEvent_t e0, e1;
+    if (take_launch_events(&e0, &e1))
+        hipExtLaunchKernelGGL(kern, dim3(a.tiles), dim3(256), G::LDS, stream(), e0, e1, 0, a);
+    else
+        hipLaunchKernelGGL(kern, dim3(a.tiles), dim3(256), G::LDS, stream(), a);
+    HOLO_LAUNCH_CHECK();
 }
 
 }  // namespace holo
@@ -195,10 +393,36 @@ void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, 
         HOLO_REJECT("holo_gemm_q4_0_q8_0: W and Xq must be 4-byte aligned");
         return;
     }
-    GemmArgs a = {Y, (const uint8_t *)W, (const uint8_t *)Xq, M, N, K / 32};
-    dim3 grid((N + kTN - 1) / kTN, (M + kTM - 1) / kTM);
-    hipLaunchKernelGGL(gemm_q4_0_q8_0_k, grid, dim3(256), 0, stream(), a);
+    const int nb = K / 32;
+    const int64_t nblk = (int64_t)M * nb;
+    const size_t pbytes = (size_t)nblk * 64, dbytes = ((size_t)nblk * 2 + 255) & ~(size_t)255;
+    void *ws = nullptr;
+    HOLO_CHECK(hipMallocAsync(&ws, pbytes + dbytes, stream()));
+    if (!ws) return;
+    uint4 *P = (uint4 *)ws;
+    uint16_t *D = (uint16_t *)((uint8_t *)ws + pbytes);
+    hipLaunchKernelGGL(q8_panel_k, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, stream(), P, D,
+                       (const uint8_t *)Xq, nblk, nblk * 34);
     HOLO_LAUNCH_CHECK();
+    PrefillArgs a = {Y, (const uint8_t *)W, (const _Float16 *)P, D, M, N, nb, 0, 0, (int64_t)N * nb * 18};
+    // Variant per shape (measured at the config-4 shapes): 128-column tiles,
+    // two workgroups per CU, one stage of loads in flight when there are at
+    // least as many tiles as CUs; otherwise 64-column tiles with two stages in
+    // flight.  HOLO_PREFILL_CFG=<tile>,<stage blocks>,<depth>,<workgroups per CU>
+    // selects one of the compiled variants instead.
+    static int cfg = -1;
+    if (cfg < 0) {
+        const char *e = getenv("HOLO_PREFILL_CFG");
+        int t = 0, st = 0, d = 0, o = 0;
+        cfg = (e && sscanf(e, "%d,%d,%d,%d", &t, &st, &d, &o) == 4) ? t * 1000 + st * 100 + d * 10 + o : 0;
+    }
+    switch (cfg ? cfg : (prefill_tn(M, N) == 128 ? 128212 : 64222)) {
+    case 64112: launch_prefill<2, 1, 1, 1, 2>(a); break;
+    case 64222: launch_prefill<2, 1, 2, 2, 2>(a); break;
+    case 64412: launch_prefill<2, 1, 4, 1, 1>(a); break;
+    default: launch_prefill<2, 2, 2, 1, 2>(a); break;
+    }
+    HOLO_CHECK(hipFreeAsync(ws, stream()));
 }
 
 void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int N, int K, void *scratch_q8)

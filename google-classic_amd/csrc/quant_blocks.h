@@ -60,6 +60,7 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
 struct Q4_0Unit {
     uint32_t q[4];  // 32 nibbles: byte k of q[i] = qs[4i+k]
     float d;
+    uint32_t dh;    // d as raw f16 bits
 };
 
 // W: matrix base (4-byte aligned); g: block index; total: matrix bytes.
@@ -82,7 +83,8 @@ __device__ __forceinline__ Q4_0Unit load_q4_0(const uint8_t *__restrict__ W, int
     u.q[1] = perm(a.z, a.y, sel);
     u.q[2] = perm(a.w, a.z, sel);
     u.q[3] = perm(e, a.w, sel);
-    u.d = half_bits_to_float(__builtin_amdgcn_alignbyte(a.y, a.x, s));
+    u.dh = __builtin_amdgcn_alignbyte(a.y, a.x, s) & 0xFFFFu;
+    u.d = half_bits_to_float(u.dh);
     return u;
 }
 
@@ -90,6 +92,7 @@ __device__ __forceinline__ Q4_0Unit load_q4_0(const uint8_t *__restrict__ W, int
 struct Q8_0Unit {
     uint32_t q[8];  // byte k of q[i] = qs[4i+k] (int8)
     float d;
+    uint32_t dh;    // d as raw f16 bits
 };
 
 __device__ __forceinline__ Q8_0Unit load_q8_0(const uint8_t *__restrict__ W, int64_t g, int64_t total)
@@ -114,7 +117,8 @@ __device__ __forceinline__ Q8_0Unit load_q8_0(const uint8_t *__restrict__ W, int
     u.q[5] = perm(b.z, b.y, sel);
     u.q[6] = perm(b.w, b.z, sel);
     u.q[7] = perm(e, b.w, sel);
-    u.d = half_bits_to_float(__builtin_amdgcn_alignbyte(a.y, a.x, s));
+    u.dh = __builtin_amdgcn_alignbyte(a.y, a.x, s) & 0xFFFFu;
+    u.d = half_bits_to_float(u.dh);
     return u;
 }
 

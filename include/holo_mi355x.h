@@ -107,7 +107,8 @@ int holo_gemv_chain(const holo_gemv_stage_t *stages, int nstages, int type);
  * reset) if a chain launch since the last call gave up waiting.            */
 int holo_gemv_chain_status(void);
 
-/* Times one kernel: the next launch of the MFMA GEMV path records start_event
+/* Times one kernel: the next launch of the MFMA GEMV path or of the prefill
+ * GEMM kernel (holo_gemm_q4_0_q8_0) records start_event
  * when its first wave starts and stop_event when its last wave ends
  * (hipExtLaunchKernelGGL), so the events span the kernel alone, without the
  * dispatch latency an event pair around the call includes.  One launch only;
@@ -133,12 +134,15 @@ void holo_batched_ffn_gate_up(float *out, const void *W1, const void *W3,
  * The reference has no batched path (one GEMV per prompt token,
  * src/ai/llm.c:1049).  Activations X[M][K] fp32 are quantised per row and
  * 32-block to Q8_0: d = f16_rne(amax/127), q = round-half-away(x*127/amax)
- * (d=0 -> q=0).  Y[M][N] = sum_b f16(dw)*f16(dx)*I_b with the exact
- * int32 block dot I_b, accumulated in fp32 in block order.                  */
+ * (d=0 -> q=0).  Y[M][N] accumulates, over blocks b in order,
+ *   acc = fmaf((float)I_b, f16(dw)*f16(dx), acc)
+ * with the exact integer block dot I_b (the scale product is exact in fp32).
+ * holo_gemm_q4_0_q8_0 stages the activations as f16 in a stream-ordered
+ * workspace (hipMallocAsync, M*K*2 + M*(K/32)*2 bytes) for the call.       */
 void holo_quantize_act_q8_0(void *dst_blocks, const float *X, int rows, int k);
 void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, int K);
 /* Y[M][N] = X[M][K] . W[N][K]^T for W in Q4_0: M >= 64 quantises X and runs
- * the int8 MFMA GEMM above; M < 64 runs M fp32-activation GEMVs.            */
+ * the MFMA GEMM above; M < 64 runs M fp32-activation GEMVs.                 */
 void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int N, int K,
                             void *scratch_q8);
 

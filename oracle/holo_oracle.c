@@ -23,8 +23,10 @@
  *                     oracle/_ref matmul_q (release and strict builds)
  *   quantize_act /    build-defined (the reference has no activation
  *   gemm_q4_0_q8_0    quantizer or batched path): pinned by invariants
- *                     |q|<=127, |x-d*q|<=d/2 (+f16 rounding of d) and by an
- *                     independent numpy integer restatement.
+ *                     |q|<=127, |x-d*q|<=d/2 (+f16 rounding of d), by an
+ *                     independent numpy integer restatement and, for the
+ *                     block-order fused rescale, by an exact rational
+ *                     evaluation of each fmaf step.
  */
 #include <math.h>
 #include <stdint.h>
@@ -376,8 +378,10 @@ void oracle_quantize_act_q8_0(const float *x, void *dst, int rows, int k)
 /* Batched product over Q8_0 activations and Q4_0 weights:
  *   Y[m][n] = sum_b f16(dw[n,b]) * f16(dx[m,b]) * I[m,n,b],
  *   I[m,n,b] = sum_{k<32} (qw[n,b,k]-8) * qx[m,b,k]    (exact in int32)
- * The per-block scale is applied as (float)I * (dw*dx) and accumulated in
- * block order in fp32: acc = acc + (float)I * (dw * dx). */
+ * The per-block scale s = dw*dx (a product of two f16 values, exact in fp32)
+ * is applied with one fused multiply-add per block, in block order:
+ *   acc = fmaf((float)I, s, acc)
+ * (I is exact in fp32: |I| <= 32*8*127).  fmaf rounds once (C99 7.12.13). */
 void oracle_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, int K)
 {
     const oq4_0 *w = (const oq4_0 *)W;
@@ -396,7 +400,7 @@ void oracle_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N
                     I += ((wb->qs[j] >> 4) - 8) * xb->qs[j + 16];
                 }
                 float s = oracle_f16_to_f32(wb->d) * oracle_f16_to_f32(xb->d);
-                acc = acc + (float)I * s;
+                acc = fmaf((float)I, s, acc);
             }
             Y[(size_t)m * N + n] = acc;
         }

@@ -259,6 +259,48 @@ def test_gemm_q4_0_q8_0_vs_integer_truth(oracle, synth):
     assert np.array_equal(Y1, want1.astype(np.float32))
 
 
+def _fma_f32(a, b, c):
+    """fmaf(a, b, c) for float32 a, b, c from exact rationals: the float64 sum
+    is used only where it equals the exact value, so the final conversion to
+    float32 is the single rounding fmaf specifies."""
+    from fractions import Fraction
+    exact = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
+    s = float(a) * float(b) + float(c)
+    assert Fraction(s) == exact, "float64 sum inexact for this case"
+    return np.float32(s)
+
+
+def test_gemm_q4_0_q8_0_block_order_fma(oracle, synth):
+    """acc = fmaf((float)I_b, dw_b*dx_b, acc) over blocks b in order, evaluated
+    exactly step by step; a mul-then-add accumulation differs on this input."""
+    M, N, K = 6, 7, 32 * 9
+    W = synth.blocks(Q4_0, N, K, seed=31)
+    Xq = oracle.quantize_act_q8_0(synth.normal(M * K, seed=32).reshape(M, K))
+    Y = oracle.gemm_q4_0_q8_0(W, Xq, M, N, K)
+    wb = W.reshape(N, K // 32, 18)
+    qw = np.concatenate([(wb[:, :, 2:] & 15).astype(np.int64) - 8, (wb[:, :, 2:] >> 4).astype(np.int64) - 8], axis=2)
+    dw = wb[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float32)
+    xb = Xq.reshape(M, K // 32, 34)
+    qx = xb[:, :, 2:].view(np.int8).astype(np.int64)
+    dx = xb[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float32)
+    I = np.einsum("mbk,nbk->mnb", qx, qw)
+    want = np.zeros((M, N), np.float32)
+    muladd = np.zeros((M, N), np.float32)
+    for m in range(M):
+        for n in range(N):
+            acc = np.float32(0)
+            acc2 = np.float32(0)
+            for b in range(K // 32):
+                s = np.float32(dw[n, b] * dx[m, b])
+                assert float(s) == float(dw[n, b]) * float(dx[m, b])  # the scale product is exact
+                acc = _fma_f32(np.float32(I[m, n, b]), s, acc)
+                acc2 = np.float32(acc2 + np.float32(np.float32(I[m, n, b]) * s))
+            want[m, n] = acc
+            muladd[m, n] = acc2
+    assert np.array_equal(Y.view(np.uint32), want.view(np.uint32))
+    assert not np.array_equal(Y.view(np.uint32), muladd.view(np.uint32))
+
+
 def test_silu_mul_vs_numpy(oracle, synth):
     g = synth.normal(1000, seed=1) * np.float32(4)
     u = synth.normal(1000, seed=2)
