@@ -25,7 +25,7 @@ import numpy as np
 PKG_DIR = Path(__file__).resolve().parent.parent
 LIB_PATH = PKG_DIR / "libholo_mi355x.so"
 ROOT = PKG_DIR.parent
-HEADERS = [ROOT / "include" / "cuda_ops.h", ROOT / "include" / "holo_mi355x.h"]
+HEADERS = [ROOT / "include" / "cuda_ops.h", ROOT / "include" / "holo_mi355x.h", ROOT / "include" / "holo_gguf.h"]
 
 # GGML type ids (reference src/ai/quant.h:19-33)
 TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 2, 8, 12, 14
@@ -135,6 +135,27 @@ _SIGS = {
     "holo_quantize_act_q8_0": (None, [_P, _P, _I, _I]),
     "holo_gemm_q4_0_q8_0": (None, [_P, _P, _P, _I, _I, _I]),
     "holo_matmul_batch_q4_0": (None, [_P, _P, _P, _I, _I, _I, _P]),
+    # GGUF files (include/holo_gguf.h)
+    "holo_gguf_open": (_P, [C.c_char_p]),
+    "holo_gguf_close": (None, [_P]),
+    "holo_gguf_version": (C.c_uint32, [_P]),
+    "holo_gguf_n_tensors": (C.c_uint64, [_P]),
+    "holo_gguf_n_kv": (C.c_uint64, [_P]),
+    "holo_gguf_data_offset": (C.c_uint64, [_P]),
+    "holo_gguf_model": (_P, [_P]),
+    "holo_gguf_key": (C.c_char_p, [_P, C.c_uint64]),
+    "holo_gguf_value_type": (_I, [_P, C.c_char_p]),
+    "holo_gguf_get_string": (C.c_char_p, [_P, C.c_char_p]),
+    "holo_gguf_get_int": (_I64, [_P, C.c_char_p, _I64]),
+    "holo_gguf_get_float": (_F, [_P, C.c_char_p, _F]),
+    "holo_gguf_get_array": (_P, [_P, C.c_char_p, C.POINTER(C.c_uint64), C.POINTER(_I)]),
+    "holo_gguf_tensor": (_P, [_P, C.c_uint64]),
+    "holo_gguf_find_tensor": (_P, [_P, C.c_char_p]),
+    "holo_gguf_load_tensor": (_I, [_P, _P, _P, _SZ]),
+    "holo_gguf_upload": (_I, [_P]),
+    "holo_gguf_device_base": (_P, [_P]),
+    "holo_gguf_device_bytes": (_SZ, [_P]),
+    "holo_gguf_device_ptr": (_P, [_P, _P]),
 }
 
 _lib: C.CDLL | None = None
@@ -170,6 +191,21 @@ def gemv_chain(stages, qtype: int) -> int:
     """holo_gemv_chain over a list of GemvStage; returns its status code."""
     arr = (GemvStage * len(stages))(*stages)
     return lib().holo_gemv_chain(C.cast(arr, C.c_void_p), len(stages), qtype)
+
+
+class GgufTensor(C.Structure):
+    """holo_gguf_tensor_t (include/holo_gguf.h), the fields of the reference's
+    gguf_tensor_info_t (src/ai/gguf.h:107-118)."""
+    _fields_ = [("name", C.c_char * 256), ("n_dims", C.c_uint32), ("dims", C.c_uint64 * 4), ("type", C.c_int32),
+                ("offset", C.c_uint64), ("n_elements", C.c_uint64), ("size_bytes", C.c_uint64)]
+
+
+class GgufModel(C.Structure):
+    """holo_gguf_model_t (include/holo_gguf.h), the reference's model fields (src/ai/gguf.h:151-165)."""
+    _fields_ = [("arch", C.c_char * 64)] + [(n, C.c_uint32) for n in (
+        "vocab_size", "context_length", "embedding_length", "block_count", "attention_head_count",
+        "attention_head_count_kv", "attention_key_length", "feed_forward_length")] + [
+        (n, C.c_float) for n in ("rope_freq_base", "rope_freq_scale", "rms_norm_eps")]
 
 
 class HoloError(RuntimeError):
