@@ -1,0 +1,212 @@
+// forward.hip -- the Llama forward over n prompt tokens in one pass (host
+// driver over the row-batched ops), and the model descriptor from a GGUF file.
+//
+// Per layer, with all n rows at once (the reference runs this body once per
+// token: llm.c:1063-1247 on the CPU, llm_cuda.c:598-880 on the GPU):
+//   xb = rms_norm(x); q, k, v = Wq xb, Wk xb, Wv xb; rope(q, k) at pos0 + r;
+//   cache[pos0 + r] = k, v; att = causal attention; x += Wo att;
+//   xb = rms_norm(x); h = silu(W1 xb) * (W3 xb); x += W2 h
+// then the last row: rms_norm, output head -> logits (llm.c:1249-1263).
+#include "common.h"
+
+#include "../../include/holo_forward.h"
+
+#include <string.h>
+
+#include <string>
+
+using namespace holo;
+
+namespace {
+
+bool rows_type_ok(int t)
+{
+    return t == HOLO_TYPE_F32 || t == HOLO_TYPE_F16 || t == HOLO_TYPE_Q4_0 || t == HOLO_TYPE_Q8_0 ||
+           t == HOLO_TYPE_Q4_K || t == HOLO_TYPE_Q6_K;
+}
+
+// Bytes of one row of a block stream of `type` (whole blocks: in_dim / QK).
+int64_t row_bytes(int type, int in_dim)
+{
+    switch (type) {
+    case HOLO_TYPE_F16: return (int64_t)in_dim * 2;
+    case HOLO_TYPE_Q4_0: return (int64_t)(in_dim / 32) * 18;
+    case HOLO_TYPE_Q8_0: return (int64_t)(in_dim / 32) * 34;
+    case HOLO_TYPE_Q4_K: return (int64_t)(in_dim / 256) * 144;
+    case HOLO_TYPE_Q6_K: return (int64_t)(in_dim / 256) * 210;
+    default: return (int64_t)in_dim * 4;
+    }
+}
+
+bool layer_ok(const holo_llama_layer_t &l)
+{
+    return l.wq && l.wk && l.wv && l.wo && l.w1 && l.w2 && l.w3 && rows_type_ok(l.wq_type) && rows_type_ok(l.wk_type) &&
+           rows_type_ok(l.wv_type) && rows_type_ok(l.wo_type) && rows_type_ok(l.w1_type) &&
+           rows_type_ok(l.w2_type) && rows_type_ok(l.w3_type);
+}
+
+// A layer without a norm weight passes x through unchanged (llm.c:1084-1086,
+// 1223-1225, 1251-1254).
+void norm_or_copy(float *dst, const float *x, const float *w, int rows, int n, float eps)
+{
+    if (w)
+        holo_rms_norm_rows(dst, x, w, rows, n, eps);
+    else
+        HOLO_CHECK(hipMemcpyAsync(dst, x, (size_t)rows * n * sizeof(float), hipMemcpyDeviceToDevice, stream()));
+}
+
+}  // namespace
+
+extern "C" {
+
+void holo_matmul_rows(float *Y, const void *W, const float *X, int rows, int out_dim, int in_dim, int type,
+                      int exact)
+{
+    if (rows <= 0 || out_dim <= 0) return;
+    if (type == HOLO_TYPE_Q4_0 && rows >= 64 && !exact && in_dim % 32 == 0) {
+        holo_matmul_batch_q4_0(Y, W, X, rows, out_dim, in_dim, nullptr);
+        return;
+    }
+    for (int r = 0; r < rows; r++)
+        holo_matmul(Y + (int64_t)r * out_dim, W, X + (int64_t)r * in_dim, out_dim, in_dim, type);
+}
+
+int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0, float *logits, int flags)
+{
+    if (!m || !tokens || !logits || n <= 0 || pos0 < 0 || m->n_layers <= 0 || !m->layers || !m->tok_emb ||
+        !m->output || !m->key_cache || !m->value_cache || m->dim <= 0 || m->n_heads <= 0 || m->n_kv_heads <= 0 ||
+        m->n_heads % m->n_kv_heads != 0 || m->head_dim <= 0 || m->head_dim > 128 || m->head_dim % 2 ||
+        m->ffn_dim <= 0 || m->vocab <= 0 || pos0 + n > m->max_seq || !rows_type_ok(m->out_type) ||
+        !(rows_type_ok(m->emb_type) || m->emb_type == HOLO_TYPE_Q4_K)) {
+        HOLO_REJECT("holo_llama_forward: model or shape outside the supported set");
+        return HOLO_EINVAL;
+    }
+    for (int l = 0; l < m->n_layers; l++)
+        if (!layer_ok(m->layers[l])) {
+            HOLO_REJECT("holo_llama_forward: layer with a missing matrix or an unsupported type");
+            return HOLO_EINVAL;
+        }
+    for (int t = 0; t < n; t++)
+        if (tokens[t] < 0 || tokens[t] >= m->vocab) {
+            HOLO_REJECT("holo_llama_forward: token outside the vocabulary");
+            return HOLO_EINVAL;
+        }
+    const int dim = m->dim, hd = m->head_dim, ffn = m->ffn_dim;
+    const int q_dim = m->n_heads * hd, kv_dim = m->n_kv_heads * hd;
+    const int exact = flags & HOLO_FORWARD_EXACT;
+    const int64_t layer_cache = (int64_t)m->max_seq * kv_dim;
+
+    // stream-ordered scratch: token ids, x, xb, q, k, v, att, hb, hb2
+    const size_t rowsz = (size_t)n * sizeof(float);
+    const size_t sz_tok = ((size_t)n * sizeof(int) + 255) & ~(size_t)255;
+    const size_t sizes[] = {sz_tok, rowsz * dim, rowsz * dim, rowsz * q_dim, rowsz * kv_dim, rowsz * kv_dim,
+                            rowsz * q_dim, rowsz * ffn, rowsz * ffn};
+    size_t total = 0;
+    for (size_t s : sizes) total += (s + 255) & ~(size_t)255;
+    void *ws = nullptr;
+    HOLO_CHECK(hipMallocAsync(&ws, total, stream()));
+    if (!ws) return HOLO_EINVAL;
+    uint8_t *p = (uint8_t *)ws;
+    void *bufs[9];
+    for (int i = 0; i < 9; i++) {
+        bufs[i] = p;
+        p += (sizes[i] + 255) & ~(size_t)255;
+    }
+    int *dtok = (int *)bufs[0];
+    float *x = (float *)bufs[1], *xb = (float *)bufs[2], *q = (float *)bufs[3], *k = (float *)bufs[4];
+    float *v = (float *)bufs[5], *att = (float *)bufs[6], *hb = (float *)bufs[7], *hb2 = (float *)bufs[8];
+
+    // embeddings
+    if (m->emb_type == HOLO_TYPE_Q4_K) {
+        // no lookup kernel: exact dequantisation of each token's row
+        for (int t = 0; t < n; t++)
+            holo_dequant(x + (int64_t)t * dim,
+                         (const uint8_t *)m->tok_emb + (int64_t)tokens[t] * row_bytes(HOLO_TYPE_Q4_K, dim),
+                         dim, HOLO_TYPE_Q4_K);
+    } else {
+        HOLO_CHECK(hipMemcpyAsync(dtok, tokens, (size_t)n * sizeof(int), hipMemcpyHostToDevice, stream()));
+        holo_embedding_rows(x, m->tok_emb, dtok, n, dim, m->emb_type);
+    }
+
+    for (int l = 0; l < m->n_layers; l++) {
+        const holo_llama_layer_t &L = m->layers[l];
+        float *kc = m->key_cache + l * layer_cache, *vc = m->value_cache + l * layer_cache;
+        // attention block
+        norm_or_copy(xb, x, L.attn_norm, n, dim, m->rms_eps);
+        holo_matmul_rows(q, L.wq, xb, n, q_dim, dim, L.wq_type, exact);
+        holo_matmul_rows(k, L.wk, xb, n, kv_dim, dim, L.wk_type, exact);
+        holo_matmul_rows(v, L.wv, xb, n, kv_dim, dim, L.wv_type, exact);
+        holo_rope_rows(q, k, n, pos0, hd, m->n_heads, m->n_kv_heads, m->rope_base);
+        HOLO_CHECK(hipMemcpyAsync(kc + (int64_t)pos0 * kv_dim, k, rowsz * kv_dim, hipMemcpyDeviceToDevice, stream()));
+        HOLO_CHECK(hipMemcpyAsync(vc + (int64_t)pos0 * kv_dim, v, rowsz * kv_dim, hipMemcpyDeviceToDevice, stream()));
+        holo_attention_prefill(att, q, kc, vc, n, pos0, hd, m->n_heads, m->n_kv_heads);
+        holo_matmul_rows(xb, L.wo, att, n, dim, q_dim, L.wo_type, exact);
+        cuda_vec_add(x, x, xb, n * dim);
+        // FFN block
+        norm_or_copy(xb, x, L.ffn_norm, n, dim, m->rms_eps);
+        holo_matmul_rows(hb, L.w1, xb, n, ffn, dim, L.w1_type, exact);
+        holo_matmul_rows(hb2, L.w3, xb, n, ffn, dim, L.w3_type, exact);
+        cuda_silu_mul(hb, hb, hb2, n * ffn);
+        holo_matmul_rows(xb, L.w2, hb, n, dim, ffn, L.w2_type, exact);
+        cuda_vec_add(x, x, xb, n * dim);
+    }
+    // the last token: final norm and the output head
+    float *xl = x + (int64_t)(n - 1) * dim;
+    norm_or_copy(xb, xl, m->out_norm, 1, dim, m->rms_eps);
+    holo_matmul(logits, m->output, xb, m->vocab, dim, m->out_type);
+    HOLO_CHECK(hipFreeAsync(ws, stream()));
+    return 0;
+}
+
+int holo_llama_from_gguf(const holo_gguf_t *g, holo_llama_t *m, holo_llama_layer_t *layers, int max_layers)
+{
+    if (!g || !m || !layers || !holo_gguf_device_base(g)) return -1;
+    const holo_gguf_model_t *p = holo_gguf_model(g);
+    const int n_layers = (int)p->block_count;
+    if (n_layers <= 0 || n_layers > max_layers) return -1;
+    memset(m, 0, sizeof(*m));
+    memset(layers, 0, sizeof(*layers) * (size_t)n_layers);
+    auto find = [&](const std::string &name, int *type) -> const void * {
+        const holo_gguf_tensor_t *t = holo_gguf_find_tensor(g, name.c_str());
+        if (!t) return nullptr;
+        if (type) *type = t->type;
+        return holo_gguf_device_ptr(g, t);
+    };
+    m->n_layers = n_layers;
+    m->dim = (int)p->embedding_length;
+    m->n_heads = (int)p->attention_head_count;
+    m->n_kv_heads = (int)p->attention_head_count_kv;
+    m->head_dim = (int)p->attention_key_length;
+    m->ffn_dim = (int)p->feed_forward_length;
+    m->rms_eps = p->rms_norm_eps;
+    m->rope_base = p->rope_freq_base;
+    const holo_gguf_tensor_t *emb = holo_gguf_find_tensor(g, "token_embd.weight");
+    if (!emb) return -1;
+    m->tok_emb = holo_gguf_device_ptr(g, emb);
+    m->emb_type = emb->type;
+    m->vocab = (int)emb->dims[1];  // g_emb_vocab_size (llm.c:368)
+    m->out_norm = (const float *)find("output_norm.weight", nullptr);
+    m->output = find("output.weight", &m->out_type);
+    if (!m->output) {  // tied embeddings (llm.c:387-390)
+        m->output = m->tok_emb;
+        m->out_type = m->emb_type;
+    }
+    for (int l = 0; l < n_layers; l++) {
+        const std::string b = "blk." + std::to_string(l) + ".";
+        holo_llama_layer_t &L = layers[l];
+        L.attn_norm = (const float *)find(b + "attn_norm.weight", nullptr);
+        L.wq = find(b + "attn_q.weight", &L.wq_type);
+        L.wk = find(b + "attn_k.weight", &L.wk_type);
+        L.wv = find(b + "attn_v.weight", &L.wv_type);
+        L.wo = find(b + "attn_output.weight", &L.wo_type);
+        L.ffn_norm = (const float *)find(b + "ffn_norm.weight", nullptr);
+        L.w1 = find(b + "ffn_gate.weight", &L.w1_type);
+        L.w2 = find(b + "ffn_down.weight", &L.w2_type);
+        L.w3 = find(b + "ffn_up.weight", &L.w3_type);
+        if (!L.wq || !L.wk || !L.wv || !L.wo || !L.w1 || !L.w2 || !L.w3) return -1;
+    }
+    m->layers = layers;
+    return 0;
+}
+
+}  // extern "C"

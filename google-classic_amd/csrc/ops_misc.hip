@@ -8,6 +8,8 @@
 #include "common.h"
 #include "quant_blocks.h"
 
+#include "../../include/holo_forward.h"
+
 namespace holo {
 
 constexpr int kBlock = 256;
@@ -211,9 +213,10 @@ __global__ __launch_bounds__(256) void mha_k(float *dst, const float *q, const f
 
 // ---- RoPE (cuda_ops.cu:2102-2140): pairs (i, i + hd/2), theta = pos / base^(2i/hd) ----------
 
-__global__ void rope_k(float *q, float *k, int pos, int hd, int n_heads, int n_kv_heads, float base)
+__device__ __forceinline__ void rope_head(float *q, float *k, int pos, int hd, int n_heads, int n_kv_heads,
+                                          float base, int h, int i)
 {
-    const int h = blockIdx.x, i = threadIdx.x, half = hd / 2;
+    const int half = hd / 2;
     if (i >= half) return;
     const float freq = 1.0f / powf(base, (float)(2 * i) / (float)hd);
     const float th = (float)pos * freq;
@@ -230,6 +233,19 @@ __global__ void rope_k(float *q, float *k, int pos, int hd, int n_heads, int n_k
         p[i] = a * c - b * s;
         p[i + half] = a * s + b * c;
     }
+}
+
+__global__ void rope_k(float *q, float *k, int pos, int hd, int n_heads, int n_kv_heads, float base)
+{
+    rope_head(q, k, pos, hd, n_heads, n_kv_heads, base, blockIdx.x, threadIdx.x);
+}
+
+// Row r of q [rows][n_heads*hd] and k [rows][n_kv_heads*hd] at position pos0 + r.
+__global__ void rope_rows_k(float *q, float *k, int pos0, int hd, int n_heads, int n_kv_heads, float base)
+{
+    const int64_t r = blockIdx.y;
+    rope_head(q + r * n_heads * hd, k + r * n_kv_heads * hd, pos0 + (int)r, hd, n_heads, n_kv_heads, base,
+              blockIdx.x, threadIdx.x);
 }
 
 // ---- embedding lookups (cuda_ops.cu:2147-2300) ---------------------------------------------
@@ -363,6 +379,154 @@ __global__ __launch_bounds__(256) void gemv_q6_k_k(float *dst, const uint8_t *M,
 // Device scalars for the two ops that return a value to the host.
 static float *g_dot = nullptr;
 static int *g_argmax = nullptr;
+
+// ---- row-batched ops of the prefill forward (M activation rows) --------------------------
+
+// RMS norm of each row (the arithmetic of rms_norm_k), one workgroup per row.
+__global__ __launch_bounds__(256) void rms_norm_rows_k(float *dst, const float *x, const float *w, int n, float eps)
+{
+    __shared__ float scratch[16];
+    const int64_t off = (int64_t)blockIdx.x * n;
+    x += off;
+    dst += off;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += x[i] * x[i];
+    ss = block_reduce<false>(ss, scratch);
+    const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = x[i] * scale * (w ? w[i] : 1.0f);
+}
+
+// Embedding rows: row r is token tokens[r] of the table, exact dequantisation
+// (the per-token lookups above, get_embedding of llm.c:941-1008).
+__global__ void emb_rows_k(float *dst, const uint8_t *e, const int *tokens, int dim, int type)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= dim) return;
+    const int64_t r = blockIdx.y, t = tokens[r];
+    float v;
+    switch (type) {
+    case HOLO_TYPE_F16: v = half_bits_to_float_exact(((const uint16_t *)e)[t * dim + i]); break;
+    case HOLO_TYPE_Q8_0: {
+        const uint8_t *b = e + (t * (dim / 32) + i / 32) * 34;
+        v = half_bits_to_float_exact((uint32_t)b[0] | ((uint32_t)b[1] << 8)) * (float)(int8_t)b[2 + i % 32];
+        break;
+    }
+    case HOLO_TYPE_Q4_0: {
+        const uint8_t *b = e + (t * (dim / 32) + i / 32) * 18;
+        const int j = i % 32;
+        const uint8_t q = b[2 + (j & 15)];
+        v = half_bits_to_float_exact((uint32_t)b[0] | ((uint32_t)b[1] << 8)) *
+            (float)((j < 16 ? (q & 15) : (q >> 4)) - 8);
+        break;
+    }
+    case HOLO_TYPE_Q6_K: v = q6_k_value(e + (t * (dim / 256) + i / 256) * 210, i % 256); break;
+    default: v = ((const float *)e)[t * dim + i]; break;
+    }
+    dst[r * dim + i] = v;
+}
+
+// Causal attention over the prompt.  Query row m (position pos0 + m) of head
+// h attends to cached positions 0 .. pos0 + m of KV head h / (n_heads /
+// n_kv_heads): softmax((q . k_p) / sqrt(hd)) . v, as cuda_multi_head_attention
+// computes it for one query (cuda_ops.cu:1813-1952), with the softmax taken
+// online over key tiles (running max and sum, fp32).
+// Workgroup: head h, 32 query rows (8 per wave); keys staged 64 at a time in
+// LDS (key rows padded by one float so the per-lane dot products hit distinct
+// banks).  Lane l scores key l of the tile for each of its wave's 8 queries,
+// then owns output dimensions l and l + 64.
+constexpr int kAttQ = 32, kAttKeys = 64, kAttMaxHd = 128;
+constexpr size_t kAttLds = (size_t)(kAttQ * kAttMaxHd + kAttKeys * (kAttMaxHd + 1) + kAttKeys * kAttMaxHd +
+                                    4 * 8 * kAttKeys) * sizeof(float);
+
+__global__ __launch_bounds__(256) void attention_prefill_k(float *out, const float *q, const float *kc,
+                                                           const float *vc, int rows, int pos0, int hd, int n_heads,
+                                                           int n_kv_heads)
+{
+    extern __shared__ float att_lds[];
+    float *lq = att_lds;                                 // [kAttQ][kAttMaxHd]
+    float *lk = lq + kAttQ * kAttMaxHd;                  // [kAttKeys][kAttMaxHd + 1]
+    float *lv = lk + kAttKeys * (kAttMaxHd + 1);         // [kAttKeys][kAttMaxHd]
+    float *lp = lv + kAttKeys * kAttMaxHd;               // [4 waves][8 queries][kAttKeys]
+    const int h = blockIdx.y, m0 = blockIdx.x * kAttQ;
+    const int kvh = h / (n_heads / n_kv_heads);
+    const int64_t q_dim = (int64_t)n_heads * hd, kv_dim = (int64_t)n_kv_heads * hd;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float scale = 1.0f / sqrtf((float)hd);
+    const int m_end = min(m0 + kAttQ, rows);
+    const int last_key = pos0 + m_end - 1;  // the furthest position any query here attends to
+
+    for (int i = tid; i < kAttQ * hd; i += blockDim.x) {
+        const int r = i / hd, d = i - r * hd;
+        lq[r * kAttMaxHd + d] = m0 + r < rows ? q[(int64_t)(m0 + r) * q_dim + (int64_t)h * hd + d] : 0.f;
+    }
+    float mx[8], sm[8], o0[8], o1[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        mx[j] = -INFINITY;
+        sm[j] = 0.f;
+        o0[j] = 0.f;
+        o1[j] = 0.f;
+    }
+    float *wp = lp + wave * 8 * kAttKeys;
+    for (int p0 = 0; p0 <= last_key; p0 += kAttKeys) {
+        __syncthreads();  // the previous tile is consumed (and lq is written, first time)
+        for (int i = tid; i < kAttKeys * hd; i += blockDim.x) {
+            const int r = i / hd, d = i - r * hd, p = p0 + r;
+            float kv = 0.f, vv = 0.f;
+            if (p <= last_key) {
+                kv = kc[(int64_t)p * kv_dim + (int64_t)kvh * hd + d];
+                vv = vc[(int64_t)p * kv_dim + (int64_t)kvh * hd + d];
+            }
+            lk[r * (kAttMaxHd + 1) + d] = kv;
+            lv[r * kAttMaxHd + d] = vv;
+        }
+        __syncthreads();
+        const int p = p0 + lane;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int r = wave * 8 + j;
+            if (m0 + r >= rows) continue;  // wave-uniform
+            const int qpos = pos0 + m0 + r;
+            float s = -INFINITY;
+            if (p <= qpos) {
+                float dot = 0.f;
+                for (int d = 0; d < hd; d++) dot += lq[r * kAttMaxHd + d] * lk[lane * (kAttMaxHd + 1) + d];
+                s = dot * scale;
+            }
+            // key 0 <= qpos is in the first tile, so the running max is finite from then on
+            const float mnew = fmaxf(mx[j], wave_reduce_max(s));
+            const float pr = p <= qpos ? expf(s - mnew) : 0.f;
+            const float corr = expf(mx[j] - mnew);
+            sm[j] = sm[j] * corr + wave_reduce_sum(pr);
+            o0[j] *= corr;
+            o1[j] *= corr;
+            mx[j] = mnew;
+            wp[j * kAttKeys + lane] = pr;
+        }
+        // wp is written and read by this wave only
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (m0 + wave * 8 + j >= rows) continue;
+            float a0 = 0.f, a1 = 0.f;
+            for (int pp = 0; pp < kAttKeys; pp++) {
+                const float w = wp[j * kAttKeys + pp];
+                a0 += w * lv[pp * kAttMaxHd + lane];
+                a1 += w * lv[pp * kAttMaxHd + ((lane + 64) & (kAttMaxHd - 1))];
+            }
+            o0[j] += a0;
+            o1[j] += a1;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int m = m0 + wave * 8 + j;
+        if (m >= rows) continue;
+        const float inv = 1.0f / sm[j];
+        float *o = out + (int64_t)m * q_dim + (int64_t)h * hd;
+        if (lane < hd) o[lane] = o0[j] * inv;
+        if (lane + 64 < hd) o[lane + 64] = o1[j] * inv;
+    }
+}
 
 }  // namespace holo
 
@@ -589,6 +753,68 @@ void cuda_matmul_q6_k(float *dst, const void *M, const float *v, int out_dim, in
     if (out_dim <= 0) return;
     hipLaunchKernelGGL(gemv_q6_k_k, dim3(blocks_for(out_dim, 4)), dim3(256), 0, stream(), dst, (const uint8_t *)M, v,
                        out_dim, in_dim);
+    HOLO_LAUNCH_CHECK();
+}
+
+void holo_rms_norm_rows(float *dst, const float *x, const float *weight, int rows, int n, float eps)
+{
+    if (rows <= 0 || n <= 0) return;
+    if (!dst || !x) {
+        HOLO_REJECT("holo_rms_norm_rows: null pointer");
+        return;
+    }
+    hipLaunchKernelGGL(rms_norm_rows_k, dim3(rows), dim3(256), 0, stream(), dst, x, weight, n, eps);
+    HOLO_LAUNCH_CHECK();
+}
+
+void holo_rope_rows(float *q, float *k, int rows, int pos0, int head_dim, int n_heads, int n_kv_heads,
+                    float freq_base)
+{
+    const int h = n_heads > n_kv_heads ? n_heads : n_kv_heads;
+    if (rows <= 0 || h <= 0 || head_dim < 2) return;
+    if (head_dim / 2 > 1024 || !q || !k) {
+        HOLO_REJECT("holo_rope_rows: null pointer or head_dim > 2048");
+        return;
+    }
+    hipLaunchKernelGGL(rope_rows_k, dim3(h, rows), dim3(head_dim / 2), 0, stream(), q, k, pos0, head_dim, n_heads,
+                       n_kv_heads, freq_base);
+    HOLO_LAUNCH_CHECK();
+}
+
+void holo_embedding_rows(float *dst, const void *embeddings, const int *tokens, int rows, int dim, int type)
+{
+    if (rows <= 0 || dim <= 0) return;
+    if (!dst || !embeddings || !tokens) {
+        HOLO_REJECT("holo_embedding_rows: null pointer");
+        return;
+    }
+    if (type != HOLO_TYPE_F32 && type != HOLO_TYPE_F16 && type != HOLO_TYPE_Q8_0 && type != HOLO_TYPE_Q4_0 &&
+        type != HOLO_TYPE_Q6_K) {
+        HOLO_REJECT("holo_embedding_rows: type without a lookup kernel");
+        return;
+    }
+    hipLaunchKernelGGL(emb_rows_k, dim3(blocks_for(dim), rows), dim3(kBlock), 0, stream(), dst,
+                       (const uint8_t *)embeddings, tokens, dim, type);
+    HOLO_LAUNCH_CHECK();
+}
+
+void holo_attention_prefill(float *out, const float *q, const float *k_cache, const float *v_cache, int rows,
+                            int pos0, int head_dim, int n_heads, int n_kv_heads)
+{
+    if (rows <= 0 || n_heads <= 0) return;
+    if (!out || !q || !k_cache || !v_cache || pos0 < 0 || head_dim <= 0 || head_dim > kAttMaxHd ||
+        n_kv_heads <= 0 || n_heads % n_kv_heads != 0) {
+        HOLO_REJECT("holo_attention_prefill: null pointer, pos0 < 0, head_dim outside 1..128 or heads not grouped");
+        return;
+    }
+    static bool attr = false;
+    if (!attr) {
+        HOLO_CHECK(hipFuncSetAttribute((const void *)attention_prefill_k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kAttLds));
+        attr = true;
+    }
+    hipLaunchKernelGGL(attention_prefill_k, dim3((rows + kAttQ - 1) / kAttQ, n_heads), dim3(256), kAttLds, stream(),
+                       out, q, k_cache, v_cache, rows, pos0, head_dim, n_heads, n_kv_heads);
     HOLO_LAUNCH_CHECK();
 }
 

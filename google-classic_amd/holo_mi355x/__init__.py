@@ -25,7 +25,8 @@ import numpy as np
 PKG_DIR = Path(__file__).resolve().parent.parent
 LIB_PATH = PKG_DIR / "libholo_mi355x.so"
 ROOT = PKG_DIR.parent
-HEADERS = [ROOT / "include" / "cuda_ops.h", ROOT / "include" / "holo_mi355x.h", ROOT / "include" / "holo_gguf.h"]
+HEADERS = [ROOT / "include" / "cuda_ops.h", ROOT / "include" / "holo_mi355x.h", ROOT / "include" / "holo_gguf.h",
+           ROOT / "include" / "holo_forward.h"]
 
 # GGML type ids (reference src/ai/quant.h:19-33)
 TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 2, 8, 12, 14
@@ -156,6 +157,14 @@ _SIGS = {
     "holo_gguf_device_base": (_P, [_P]),
     "holo_gguf_device_bytes": (_SZ, [_P]),
     "holo_gguf_device_ptr": (_P, [_P, _P]),
+    # prompt forward (include/holo_forward.h)
+    "holo_rms_norm_rows": (None, [_P, _P, _P, _I, _I, _F]),
+    "holo_rope_rows": (None, [_P, _P, _I, _I, _I, _I, _I, _F]),
+    "holo_embedding_rows": (None, [_P, _P, _P, _I, _I, _I]),
+    "holo_attention_prefill": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I]),
+    "holo_matmul_rows": (None, [_P, _P, _P, _I, _I, _I, _I, _I]),
+    "holo_llama_forward": (_I, [_P, _P, _I, _I, _P, _I]),
+    "holo_llama_from_gguf": (_I, [_P, _P, _P, _I]),
 }
 
 _lib: C.CDLL | None = None
@@ -206,6 +215,23 @@ class GgufModel(C.Structure):
         "vocab_size", "context_length", "embedding_length", "block_count", "attention_head_count",
         "attention_head_count_kv", "attention_key_length", "feed_forward_length")] + [
         (n, C.c_float) for n in ("rope_freq_base", "rope_freq_scale", "rms_norm_eps")]
+
+
+class LlamaLayer(C.Structure):
+    """holo_llama_layer_t (include/holo_forward.h)."""
+    _fields_ = [("attn_norm", C.c_void_p), ("wq", C.c_void_p), ("wk", C.c_void_p), ("wv", C.c_void_p),
+                ("wo", C.c_void_p), ("wq_type", C.c_int), ("wk_type", C.c_int), ("wv_type", C.c_int),
+                ("wo_type", C.c_int), ("ffn_norm", C.c_void_p), ("w1", C.c_void_p), ("w2", C.c_void_p),
+                ("w3", C.c_void_p), ("w1_type", C.c_int), ("w2_type", C.c_int), ("w3_type", C.c_int)]
+
+
+class LlamaModel(C.Structure):
+    """holo_llama_t (include/holo_forward.h)."""
+    _fields_ = [(n, C.c_int) for n in ("n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "ffn_dim", "vocab",
+                                       "max_seq")] + [
+        ("rms_eps", C.c_float), ("rope_base", C.c_float), ("tok_emb", C.c_void_p), ("emb_type", C.c_int),
+        ("out_norm", C.c_void_p), ("output", C.c_void_p), ("out_type", C.c_int), ("key_cache", C.c_void_p),
+        ("value_cache", C.c_void_p), ("layers", C.POINTER(LlamaLayer))]
 
 
 class HoloError(RuntimeError):

@@ -11,7 +11,8 @@ import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
 LIB = ROOT / "google-classic_amd" / "libholo_mi355x.so"
-HEADERS = [ROOT / "include" / "cuda_ops.h", ROOT / "include" / "holo_mi355x.h", ROOT / "include" / "holo_gguf.h"]
+HEADERS = [ROOT / "include" / "cuda_ops.h", ROOT / "include" / "holo_mi355x.h", ROOT / "include" / "holo_gguf.h",
+           ROOT / "include" / "holo_forward.h"]
 REF_CALLER = Path("/root/reference/src/ai/llm_cuda.c")
 
 
@@ -46,7 +47,7 @@ def test_binding_covers_the_headers():
 
 def test_headers_compile_as_c():
     cc = shutil.which("gcc")
-    src = "#include \"cuda_ops.h\"\n#include \"holo_mi355x.h\"\n#include \"holo_gguf.h\"\nint main(void){return 0;}\n"
+    src = "#include \"cuda_ops.h\"\n#include \"holo_mi355x.h\"\n#include \"holo_gguf.h\"\n#include \"holo_forward.h\"\nint main(void){return 0;}\n"
     r = subprocess.run([cc, "-std=c99", "-Wall", "-Werror", "-fsyntax-only", f"-I{ROOT / 'include'}", "-x", "c", "-"],
                        input=src, capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
