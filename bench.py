@@ -34,7 +34,8 @@ The printed JSON line carries
                 as one multi-stage launch (holo_gemv_chain), configs
                 1 and 3 (Q8_0 4096x4096; Q4_K Llama-3-8B FFN), config 4 (batched
                 prefill GEMM on the f16 matrix cores: useful TOP/s = 2*M*N*K per
-                kernel time, and its fraction of the dense f16 and int8 peaks),
+                kernel time, and its fraction of the dense f16 and int8 peaks;
+                and a 512-token prompt through the 32 layers in one pass),
                 config 5 (full synthetic
                 Llama-2-7B Q4_0 decode step: end-to-end and matmuls-only ms)
 
@@ -43,6 +44,7 @@ Only the CPU-baseline leg touches oracle/.
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import statistics
@@ -286,6 +288,58 @@ def decode_step(lib, layers, head, A, ones, matmuls_only):
     lib.cuda_matmul_q8_0(A["y32000"], head.ptr, xb, VOCAB, DIM)
 
 
+# ---- config 4 end to end: a prompt through the whole model ------------------------------
+
+def prompt_forward(lib, layers, head, ones, graph_step_ms, n_tokens=512, decode_steps=32):
+    """A 512-token prompt through the 32 synthetic Llama-2-7B layers in one pass
+    (holo_llama_forward): Q4_0 matmuls on the MFMA prefill GEMM, causal prefill
+    attention, KV caches for every position; embeddings tied to the Q8_0 head,
+    unit norm weights, random tokens.  The reference runs a prompt as one
+    decode step per token (llm.c:1049); the comparison is with the fastest
+    decode step here, the graph-captured config-5 step (graph_step_ms), per
+    token of the prompt.  The driver's own n = 1 step (not captured, one
+    launch per op) is reported beside it."""
+    L = (holo.LlamaLayer * 32)()
+    for i, Ls in enumerate(layers[:32]):
+        b = Ls.buf
+        L[i] = holo.LlamaLayer(ones.ptr, b["q"].ptr, b["k"].ptr, b["v"].ptr, b["o"].ptr, Q4_0, Q4_0, Q4_0, Q4_0,
+                               ones.ptr, b["gate"].ptr, b["down"].ptr, b["up"].ptr, Q4_0, Q4_0, Q4_0)
+    max_seq = n_tokens + decode_steps
+    kv_floats = 32 * max_seq * DIM
+    kc, vc = holo.DeviceBuffer(4 * kv_floats), holo.DeviceBuffer(4 * kv_floats)
+    logits = holo.DeviceBuffer(4 * VOCAB)
+    m = holo.LlamaModel(n_layers=32, dim=DIM, n_heads=32, n_kv_heads=32, head_dim=128, ffn_dim=FFN, vocab=VOCAB,
+                        max_seq=max_seq, rms_eps=1e-5, rope_base=10000.0, tok_emb=head.ptr, emb_type=Q8_0,
+                        out_norm=ones.ptr, output=head.ptr, out_type=Q8_0, key_cache=kc.ptr, value_cache=vc.ptr,
+                        layers=L)
+    tokens = np.random.default_rng(5).integers(0, VOCAB, size=max_seq).astype(np.int32)
+    ev = holo.Events()
+
+    def run(t, pos0):
+        rc = lib.holo_llama_forward(C.byref(m), t.ctypes.data, len(t), pos0, logits.ptr, 0)
+        if rc != 0:
+            raise holo.HoloError(f"holo_llama_forward returned {rc}")
+
+    run(tokens[:n_tokens], 0)  # warm-up (also fills the caches for the decode steps)
+    lib.cuda_sync()
+    reps = 3
+    ev.start()
+    for _ in range(reps):
+        run(tokens[:n_tokens], 0)
+    prompt_ms = ev.stop() / reps
+    ev.start()
+    for i in range(decode_steps):
+        run(tokens[n_tokens + i:n_tokens + i + 1], n_tokens + i)
+    step_ms = ev.stop() / decode_steps
+    ev.close()
+    holo.check("prompt forward")
+    return {"prompt_tokens": n_tokens, "prompt_ms": round(prompt_ms, 2),
+            "prompt_tokens_per_s": round(n_tokens / (prompt_ms * 1e-3), 1),
+            "token_by_token_prompt_ms": round(graph_step_ms * n_tokens, 1),
+            "speedup_vs_token_by_token": round(graph_step_ms * n_tokens / prompt_ms, 1),
+            "driver_decode_step_ms_at_end_of_prompt": round(step_ms, 3)}
+
+
 # ---- config 4: prefill ------------------------------------------------------------------
 
 def prefill_tops(lib, reps=10):
@@ -473,6 +527,8 @@ def main():
             lib.holo_graph_destroy(full)
             lib.holo_graph_destroy(mm)
             log(f"config 5 decode step: matmuls {mm_ms:.3f} ms, end-to-end {full_ms:.3f} ms")
+            extra["config4_prompt_forward_512"] = prompt_forward(lib, layers, head, ones, full_ms)
+            log(f"config 4 prompt forward: {extra['config4_prompt_forward_512']}")
             del head
 
         del layers
