@@ -333,11 +333,13 @@ def prompt_forward(lib, layers, head, ones, graph_step_ms, n_tokens=512, decode_
     step_ms = ev.stop() / decode_steps
     ev.close()
     holo.check("prompt forward")
-    return {"prompt_tokens": n_tokens, "prompt_ms": round(prompt_ms, 2),
-            "prompt_tokens_per_s": round(n_tokens / (prompt_ms * 1e-3), 1),
-            "token_by_token_prompt_ms": round(graph_step_ms * n_tokens, 1),
-            "speedup_vs_token_by_token": round(graph_step_ms * n_tokens / prompt_ms, 1),
-            "driver_decode_step_ms_at_end_of_prompt": round(step_ms, 3)}
+    out = {"prompt_tokens": n_tokens, "prompt_ms": round(prompt_ms, 2),
+           "prompt_tokens_per_s": round(n_tokens / (prompt_ms * 1e-3), 1),
+           "driver_decode_step_ms_at_end_of_prompt": round(step_ms, 3)}
+    if graph_step_ms:
+        out["token_by_token_prompt_ms"] = round(graph_step_ms * n_tokens, 1)
+        out["speedup_vs_token_by_token"] = round(graph_step_ms * n_tokens / prompt_ms, 1)
+    return out
 
 
 # ---- config 4: prefill ------------------------------------------------------------------
@@ -446,6 +448,8 @@ def main():
                     help="only run 3 device-to-device copies of BYTES (HBM counter calibration) and exit")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run config 4 (prefill GEMM), print its JSON and exit (for profiling)")
+    ap.add_argument("--prompt-only", action="store_true",
+                    help="only run the 512-token prompt forward over 32 layers, print its JSON and exit")
     a = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -470,6 +474,12 @@ def main():
         return
     if a.prefill_only:
         print(json.dumps({"config4_prefill_m512": prefill_tops(lib)}), flush=True)
+        return
+    if a.prompt_only:
+        layers = [Mats(Q4_0, i, 2, LAYER) for i in range(32)]
+        head = holo.DeviceBuffer.from_array(synth.blocks(Q8_0, VOCAB, DIM, synth.tensor_seed(BASE_SEED, 5, 0, 7)))
+        ones = holo.DeviceBuffer.from_array(np.ones(DIM, np.float32))
+        print(json.dumps({"config4_prompt_forward_512": prompt_forward(lib, layers, head, ones, None)}), flush=True)
         return
     stream = lib.holo_stream_create()
     lib.holo_set_stream(stream)  # graphs capture a non-null stream

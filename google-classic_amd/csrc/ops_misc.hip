@@ -430,35 +430,68 @@ __global__ void emb_rows_k(float *dst, const uint8_t *e, const int *tokens, int 
 // n_kv_heads): softmax((q . k_p) / sqrt(hd)) . v, as cuda_multi_head_attention
 // computes it for one query (cuda_ops.cu:1813-1952), with the softmax taken
 // online over key tiles (running max and sum, fp32).
-// Workgroup: head h, 32 query rows (8 per wave); keys staged 64 at a time in
-// LDS (key rows padded by one float so the per-lane dot products hit distinct
-// banks).  Lane l scores key l of the tile for each of its wave's 8 queries,
-// then owns output dimensions l and l + 64.
-constexpr int kAttQ = 32, kAttKeys = 64, kAttMaxHd = 128;
-constexpr size_t kAttLds = (size_t)(kAttQ * kAttMaxHd + kAttKeys * (kAttMaxHd + 1) + kAttKeys * kAttMaxHd +
-                                    4 * 8 * kAttKeys) * sizeof(float);
+// Workgroup: head h, 32 query rows (8 per wave).  Keys and values are staged
+// 64 positions at a time in LDS (key rows padded to 132 floats, so the 16-byte
+// reads of 16 lanes fall on distinct banks); the next tile's loads are in
+// flight in registers (16-byte loads) while the current tile is used.  Lane l
+// scores key l of the tile against the wave's 8 queries, reading each 16-byte
+// piece of its key once for all 8; the probabilities are then broadcast from
+// the lane that holds them (readlane) while lane l accumulates output
+// dimensions l and l + 64.
+constexpr int kAttQ = 32, kAttKeys = 64, kAttMaxHd = 128, kAttKStride = kAttMaxHd + 4;
+constexpr int kAttPieces = kAttKeys * kAttMaxHd / 4 / 256;  // float4 pieces per thread and tile (8)
+constexpr size_t kAttLds = (size_t)(kAttQ * kAttMaxHd + kAttKeys * kAttKStride + kAttKeys * kAttMaxHd) * sizeof(float);
 
 __global__ __launch_bounds__(256) void attention_prefill_k(float *out, const float *q, const float *kc,
                                                            const float *vc, int rows, int pos0, int hd, int n_heads,
                                                            int n_kv_heads)
 {
     extern __shared__ float att_lds[];
-    float *lq = att_lds;                                 // [kAttQ][kAttMaxHd]
-    float *lk = lq + kAttQ * kAttMaxHd;                  // [kAttKeys][kAttMaxHd + 1]
-    float *lv = lk + kAttKeys * (kAttMaxHd + 1);         // [kAttKeys][kAttMaxHd]
-    float *lp = lv + kAttKeys * kAttMaxHd;               // [4 waves][8 queries][kAttKeys]
-    const int h = blockIdx.y, m0 = blockIdx.x * kAttQ;
+    float *lq = att_lds;                         // [kAttQ][kAttMaxHd]
+    float *lk = lq + kAttQ * kAttMaxHd;          // [kAttKeys][kAttKStride]
+    float *lv = lk + kAttKeys * kAttKStride;     // [kAttKeys][kAttMaxHd]
+    // the causal tiles furthest down the prompt carry the most keys: start them first
+    const int h = blockIdx.y, m0 = (gridDim.x - 1 - blockIdx.x) * kAttQ;
     const int kvh = h / (n_heads / n_kv_heads);
     const int64_t q_dim = (int64_t)n_heads * hd, kv_dim = (int64_t)n_kv_heads * hd;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float scale = 1.0f / sqrtf((float)hd);
     const int m_end = min(m0 + kAttQ, rows);
     const int last_key = pos0 + m_end - 1;  // the furthest position any query here attends to
+    const int hd4 = hd >> 2;                 // hd is a multiple of 4 (checked by the caller)
 
-    for (int i = tid; i < kAttQ * hd; i += blockDim.x) {
-        const int r = i / hd, d = i - r * hd;
-        lq[r * kAttMaxHd + d] = m0 + r < rows ? q[(int64_t)(m0 + r) * q_dim + (int64_t)h * hd + d] : 0.f;
+    for (int i = tid; i < kAttQ * hd4; i += blockDim.x) {
+        const int r = i / hd4, c = i - r * hd4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (m0 + r < rows) v = *(const float4 *)(q + (int64_t)(m0 + r) * q_dim + (int64_t)h * hd + 4 * c);
+        *(float4 *)(lq + r * kAttMaxHd + 4 * c) = v;
     }
+    // the tile at key p0 into registers: piece f = tid + 256 i is key f / hd4,
+    // columns 4 (f % hd4) .. +3; pieces past the tile or the last key load zeros
+    float4 rk[kAttPieces], rv[kAttPieces];
+    auto fetch = [&](int p0) {
+#pragma unroll
+        for (int i = 0; i < kAttPieces; i++) {
+            const int f = tid + 256 * i, r = f / hd4, c = f - r * hd4;
+            rk[i] = rv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < kAttKeys && p0 + r <= last_key) {
+                const int64_t o = (int64_t)(p0 + r) * kv_dim + (int64_t)kvh * hd + 4 * c;
+                rk[i] = *(const float4 *)(kc + o);
+                rv[i] = *(const float4 *)(vc + o);
+            }
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int i = 0; i < kAttPieces; i++) {
+            const int f = tid + 256 * i, r = f / hd4, c = f - r * hd4;
+            if (r < kAttKeys) {
+                *(float4 *)(lk + r * kAttKStride + 4 * c) = rk[i];
+                *(float4 *)(lv + r * kAttMaxHd + 4 * c) = rv[i];
+            }
+        }
+    };
+
     float mx[8], sm[8], o0[8], o1[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
@@ -467,60 +500,66 @@ __global__ __launch_bounds__(256) void attention_prefill_k(float *out, const flo
         o0[j] = 0.f;
         o1[j] = 0.f;
     }
-    float *wp = lp + wave * 8 * kAttKeys;
+    const int r0 = wave * 8;                               // this wave's first query row in the tile
+    const int nq = max(0, min(8, m_end - (m0 + r0)));      // its valid queries (wave-uniform)
+    fetch(0);
     for (int p0 = 0; p0 <= last_key; p0 += kAttKeys) {
         __syncthreads();  // the previous tile is consumed (and lq is written, first time)
-        for (int i = tid; i < kAttKeys * hd; i += blockDim.x) {
-            const int r = i / hd, d = i - r * hd, p = p0 + r;
-            float kv = 0.f, vv = 0.f;
-            if (p <= last_key) {
-                kv = kc[(int64_t)p * kv_dim + (int64_t)kvh * hd + d];
-                vv = vc[(int64_t)p * kv_dim + (int64_t)kvh * hd + d];
-            }
-            lk[r * (kAttMaxHd + 1) + d] = kv;
-            lv[r * kAttMaxHd + d] = vv;
-        }
+        stash();
         __syncthreads();
+        if (p0 + kAttKeys <= last_key) fetch(p0 + kAttKeys);
+        if (nq == 0) continue;
+        // scores of key p0 + lane against the wave's queries
+        float sc[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) sc[j] = 0.f;
+        const float *kr = lk + lane * kAttKStride;
+#pragma unroll 2
+        for (int c = 0; c < hd4; c++) {
+            const float4 k4 = *(const float4 *)(kr + 4 * c);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float4 q4 = *(const float4 *)(lq + (r0 + j) * kAttMaxHd + 4 * c);
+                sc[j] += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+            }
+        }
+        // All 8 queries are scored, also rows past the prompt (their q rows are
+        // zero, their outputs are not written), so the 8 reductions are
+        // independent and interleave.  Sums stay per lane until the end.
         const int p = p0 + lane;
+        float pr[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int r = wave * 8 + j;
-            if (m0 + r >= rows) continue;  // wave-uniform
-            const int qpos = pos0 + m0 + r;
-            float s = -INFINITY;
-            if (p <= qpos) {
-                float dot = 0.f;
-                for (int d = 0; d < hd; d++) dot += lq[r * kAttMaxHd + d] * lk[lane * (kAttMaxHd + 1) + d];
-                s = dot * scale;
-            }
+            const int qpos = pos0 + m0 + r0 + j;
+            const float s = p <= qpos ? sc[j] * scale : -INFINITY;
             // key 0 <= qpos is in the first tile, so the running max is finite from then on
             const float mnew = fmaxf(mx[j], wave_reduce_max(s));
-            const float pr = p <= qpos ? expf(s - mnew) : 0.f;
+            pr[j] = p <= qpos ? expf(s - mnew) : 0.f;
             const float corr = expf(mx[j] - mnew);
-            sm[j] = sm[j] * corr + wave_reduce_sum(pr);
+            sm[j] = sm[j] * corr + pr[j];
             o0[j] *= corr;
             o1[j] *= corr;
             mx[j] = mnew;
-            wp[j * kAttKeys + lane] = pr;
         }
-        // wp is written and read by this wave only
+        // out += sum_p pr[p] v_p: the weight of key pp comes from lane pp
+        const int hi = (lane + 64) & (kAttMaxHd - 1);
+        const int kmax = min(kAttKeys, last_key - p0 + 1);  // keys past last_key have weight 0 everywhere
+        for (int pp = 0; pp < kmax; pp++) {
+            const float va = lv[pp * kAttMaxHd + lane], vb = lv[pp * kAttMaxHd + hi];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if (m0 + wave * 8 + j >= rows) continue;
-            float a0 = 0.f, a1 = 0.f;
-            for (int pp = 0; pp < kAttKeys; pp++) {
-                const float w = wp[j * kAttKeys + pp];
-                a0 += w * lv[pp * kAttMaxHd + lane];
-                a1 += w * lv[pp * kAttMaxHd + ((lane + 64) & (kAttMaxHd - 1))];
+            for (int j = 0; j < 8; j++) {
+                const float w = __builtin_amdgcn_readlane(__float_as_int(pr[j]), pp) ;
+                o0[j] += __int_as_float(w) * va;
+                o1[j] += __int_as_float(w) * vb;
             }
-            o0[j] += a0;
-            o1[j] += a1;
         }
     }
 #pragma unroll
+    for (int j = 0; j < 8; j++) sm[j] = wave_reduce_sum(sm[j]);
+#pragma unroll
     for (int j = 0; j < 8; j++) {
-        const int m = m0 + wave * 8 + j;
-        if (m >= rows) continue;
+        const int m = m0 + r0 + j;
+        if (j >= nq) continue;
         const float inv = 1.0f / sm[j];
         float *o = out + (int64_t)m * q_dim + (int64_t)h * hd;
         if (lane < hd) o[lane] = o0[j] * inv;
@@ -802,9 +841,10 @@ void holo_attention_prefill(float *out, const float *q, const float *k_cache, co
                             int pos0, int head_dim, int n_heads, int n_kv_heads)
 {
     if (rows <= 0 || n_heads <= 0) return;
-    if (!out || !q || !k_cache || !v_cache || pos0 < 0 || head_dim <= 0 || head_dim > kAttMaxHd ||
-        n_kv_heads <= 0 || n_heads % n_kv_heads != 0) {
-        HOLO_REJECT("holo_attention_prefill: null pointer, pos0 < 0, head_dim outside 1..128 or heads not grouped");
+    if (!out || !q || !k_cache || !v_cache || pos0 < 0 || head_dim <= 0 || head_dim > kAttMaxHd || head_dim % 4 ||
+        n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15)) {
+        HOLO_REJECT("holo_attention_prefill: null or misaligned pointer, pos0 < 0, head_dim not a multiple of 4 in "
+                    "4..128, or heads not grouped");
         return;
     }
     static bool attr = false;
