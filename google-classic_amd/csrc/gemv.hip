@@ -220,6 +220,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t x_rsrc(const float *x, int uni
 // before another XCD wrote it (the multi-stage launch reads earlier stages'
 // outputs this way, without invalidating the cache).
 constexpr int kDeviceScope = 16;
+// Cache policy of the weight loads: non-temporal (streamed once per launch).
+constexpr int kNonTemporal = 2;
 
 template <int CPOL = 0>
 __device__ __forceinline__ float4 load_x4(__amdgpu_buffer_rsrc_t rs, uint32_t off)
@@ -252,7 +254,11 @@ __device__ __forceinline__ void x_convert(const float4 v, int i, int units, void
     } else {
         const float amax = octet_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         const float dx = amax * (1.0f / (float)kQmax);
-        const float inv = amax > 0.f ? (float)kQmax / amax : 0.f;
+        // kQmax/amax to within an ulp (v_rcp_f32; a correctly rounded divide is
+        // a dozen dependent instructions on the staging path): the clamp below
+        // keeps |xi| <= kQmax, and |x - dx*xi| stays within dx/2 plus an
+        // fp32 rounding of amax
+        const float inv = amax > 0.f ? (float)kQmax * __builtin_amdgcn_rcpf(amax) : 0.f;
         int xi[4] = {(int)__builtin_rintf(v.x * inv), (int)__builtin_rintf(v.y * inv),
                      (int)__builtin_rintf(v.z * inv), (int)__builtin_rintf(v.w * inv)};
         int x1[4], x2[4];
@@ -897,6 +903,16 @@ struct MfmaStage {
     // load.  Row v of all matrices -> (matrix, row) by selects.
     int re0, re1;
     uint64_t w0, dw1, dw2, y0, dy1, dy2;
+    // Loads of an item of a full tile: the item starts at a wave-uniform
+    // address and piece i of this lane lies loff[i] bytes past it (for GATEUP
+    // the offset also picks the gate or up matrix, counted from the lower of
+    // the two bases, wlo), so an item costs no per-lane address arithmetic.
+    // fast: every such offset fits 32 bits.  The multi-stage launch keeps
+    // the general path (its registers are taken by the stages it holds).
+    static constexpr bool kFastIssue = !XDEV;
+    uint32_t loff[kFastIssue ? GE::NL : 1];
+    uint64_t wlo;
+    bool fast;
 
     __device__ __forceinline__ MfmaStage(const MfmaArgs &a, uint8_t *l) : args(a), ldsb(l)
     {
@@ -929,6 +945,28 @@ struct MfmaStage {
         y0 = (uint64_t)a.y[0];
         dy1 = (uint64_t)a.y[1] - y0;
         dy2 = (uint64_t)a.y[2] - y0;
+        const uint64_t rb = (uint64_t)a.row_bytes;
+        fast = false;
+        wlo = w0;
+        if constexpr (!kFastIssue) {
+        } else if constexpr (MODE == MODE_GATEUP) {
+            const bool up_low = (int64_t)dw1 < 0;
+            wlo = up_low ? w0 + dw1 : w0;
+            const uint64_t dg = up_low ? 0 - dw1 : 0, du = up_low ? 0 : dw1;  // gate and up past wlo
+            fast = (dg > du ? dg : du) + TR * rb < (1ull << 32);
+#pragma unroll
+            for (int i = 0; i < GE::NL; i++) {
+                const Piece pc = item_piece(FMT, 64 * i + lane, false);
+                loff[i] = (uint32_t)((pc.row >> 3 ? du : dg) + (uint64_t)(pc.row & 7) * rb + 16u * pc.col);
+            }
+        } else {
+            fast = TR * rb < (1ull << 32);
+#pragma unroll
+            for (int i = 0; i < GE::NL; i++) {
+                const Piece pc = item_piece(FMT, 64 * i + lane, false);
+                loff[i] = (uint32_t)((uint64_t)pc.row * rb + 16u * pc.col);
+            }
+        }
     }
 
     // rows [row0, rend) of local tile k
@@ -958,6 +996,8 @@ struct MfmaStage {
 
     // Slot q: local tile q / P, item (segment) wave + 8 * (q % P).  Slots
     // past the end issue nothing (a wave cannot end before its loads return).
+    // Weights are read once per launch: the loads are non-temporal, so they
+    // do not push the activations and other reused lines out of the caches.
     __device__ __forceinline__ void issue(Raw2<FMT> &b, int q) const
     {
         if (q >= Q) return;
@@ -966,6 +1006,35 @@ struct MfmaStage {
         tile_rows(k, row0, rend);
         const int seg = min(wave + kWaves * p, G - 1);
         const bool half = 16 * seg + 16 > units;
+        if (kFastIssue && fast && k < F && !half) {
+            // a full tile in one matrix (GATEUP: 8 rows of each): the
+            // uniform item base plus the lane's fixed offsets
+            uint64_t base;
+            bool one = true;
+            if constexpr (MODE == MODE_GATEUP) {
+                base = wlo + (uint64_t)row0 * (uint64_t)args.row_bytes;
+            } else {
+                int m, r, m1, r1;
+                split_row(row0, m, r);
+                split_row(row0 + TR - 1, m1, r1);
+                one = m == m1;
+                base = (uint64_t)wbase(m) + (uint64_t)r * (uint64_t)args.row_bytes;
+            }
+            if (one) {
+                // raw buffer loads: scalar base (uniform by construction),
+                // 32-bit lane offset, no range limit
+                base += (uint64_t)seg * GE::SEGB;
+                const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+                const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+                const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                    (void *)(((uint64_t)hi << 32) | lo), (short)0, -1, kBufferWord3);
+#pragma unroll
+                for (int i = 0; i < GE::NL; i++)
+                    b.v[i] = __builtin_bit_cast(u32x4a, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)loff[i], 0,
+                                                                                              kNonTemporal));
+                return;
+            }
+        }
 #pragma unroll
         for (int i = 0; i < GE::NL; i++) {
             const Piece pc = item_piece(FMT, 64 * i + lane, half);
@@ -977,7 +1046,7 @@ struct MfmaStage {
                 split_row(min(row0 + pc.row, rend - 1), m, row);
             }
             gbyte *ap = wbase(m) + (int64_t)row * args.row_bytes + seg * GE::SEGB + 16 * pc.col;
-            b.v[i] = *(gu32x4a *)ap;
+            b.v[i] = __builtin_nontemporal_load((gu32x4a *)ap);
         }
     }
 
