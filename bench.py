@@ -344,6 +344,35 @@ def prompt_forward(lib, layers, head, ones, graph_step_ms, n_tokens=512, decode_
 
 # ---- config 4: prefill ------------------------------------------------------------------
 
+def decode_attention(lib, kv_lens=(512, 2048, 4096), reps=50):
+    """cuda_multi_head_attention at Llama-2-7B shape (32 heads of 128, no
+    grouping) over caches of kv_len positions: microseconds per call, issued
+    back to back, and the key/value bytes read per second (2 * kv_len * 4096 *
+    4 bytes per call)."""
+    out = {}
+    nh, hd = 32, 128
+    q = holo.DeviceBuffer.from_array(synth.normal(nh * hd, 41))
+    y = holo.DeviceBuffer(4 * nh * hd)
+    for n in kv_lens:
+        kc = holo.DeviceBuffer.from_array(synth.normal(n * nh * hd, 42))
+        vc = holo.DeviceBuffer.from_array(synth.normal(n * nh * hd, 43))
+        for _ in range(5):
+            lib.cuda_multi_head_attention(y.ptr, q.ptr, kc.ptr, vc.ptr, n, hd, nh, nh)
+        lib.cuda_sync()
+        ev = holo.Events()
+        ev.start()
+        for _ in range(reps):
+            lib.cuda_multi_head_attention(y.ptr, q.ptr, kc.ptr, vc.ptr, n, hd, nh, nh)
+        ms = ev.stop()
+        ev.close()
+        holo.check("decode attention")
+        us = ms * 1e3 / reps
+        out[f"kv_len_{n}"] = {"us_per_call": round(us, 2), "kv_gbs": round(2 * n * nh * hd * 4 / (us * 1e-6) / 1e9, 1),
+                              "per_decode_step_32_layers_ms": round(32 * us / 1e3, 3)}
+        del kc, vc
+    return out
+
+
 def prefill_tops(lib, reps=10):
     """Config 4: holo_gemm_q4_0_q8_0 at M = 512.  gemm_us is the call (the
     f16 activation panel pass, the GEMM kernel and the stream-ordered
@@ -554,6 +583,8 @@ def main():
             del sets
         extra["config4_prefill_m512"] = prefill_tops(lib)
         log(f"config 4 prefill: {extra['config4_prefill_m512']}")
+        extra["decode_attention_llama2_7b"] = decode_attention(lib)
+        log(f"decode attention: {extra['decode_attention_llama2_7b']}")
 
     result = {
         "metric": "Q4_0 GEMV weight GB/s at Llama-2-7B layer shapes (batch 1)",

@@ -25,6 +25,10 @@ int num_cus();
 // cuda_init so that no allocation happens inside a graph capture.
 bool gemv_chain_init();
 void gemv_chain_release();
+// The decode-attention range partials (16 MiB), allocated once by cuda_init;
+// without them decode attention runs one range per head.
+bool attention_scratch_init();
+void attention_scratch_release();
 
 // Events that holo_time_next_launch requested for the next timed kernel
 // launch (MFMA GEMV or prefill GEMM): returns them once and clears them.

@@ -211,6 +211,181 @@ __global__ __launch_bounds__(256) void mha_k(float *dst, const float *q, const f
                n_kv_heads * hd, lsc, scratch);
 }
 
+// ---- decode attention: one query row per head, keys split over workgroups ----------
+//
+// softmax((q . k_p) / sqrt(hd)) . v over cached positions p < kv_len, as
+// cuda_multi_head_attention computes it (cuda_ops.cu:1813-1952), for heads of
+// up to 128 dims (a multiple of 4).  The keys are cut into `splits` ranges of
+// `chunk` positions, one workgroup per (range, head), so that a decode step
+// reads the whole cache with the whole chip rather than one workgroup per head.
+// A workgroup takes its range 64 positions at a time: thread (c, g) owns
+// 16-byte column c of the head (32 columns) for keys g, g + 8, ..., g + 56, so
+// all 8 key and 8 value loads of a thread are issued together and each wave
+// instruction reads two whole 512-byte cache rows.  Scores are summed over the
+// 32 column lanes, the softmax runs online over the 64-key passes (running
+// max and sum), and the 8 key groups' partial outputs are summed in a fixed
+// order.  With one range the workgroup writes the output; otherwise it writes
+// (unnormalised output, max, sum) and attn_decode_combine_k merges the ranges
+// of a head in range order, so the result does not depend on timing.
+constexpr int kDecKeys = 64;
+constexpr int kDecMaxSplits = 256;
+constexpr size_t kDecPartFloats = (size_t)4 << 20;  // 16 MiB of range partials, allocated by cuda_init
+static float *g_dec_part = nullptr;
+
+__device__ __forceinline__ float half_wave_sum(float v)
+{
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) v += __shfl_xor(v, off, 32);
+    return v;
+}
+
+__global__ __launch_bounds__(256) void attn_decode_k(float *out, float *part, const float *q, const float *kc,
+                                                     const float *vc, int kv_len, int hd, int n_heads, int n_kv_heads,
+                                                     int chunk)
+{
+    __shared__ float4 lq[32];
+    __shared__ float lsc[kDecKeys];
+    __shared__ float4 lo[8][32];
+    const int h = blockIdx.y, s = blockIdx.x, splits = gridDim.x;
+    const int kvh = h / (n_heads / n_kv_heads);
+    const int64_t kv_dim = (int64_t)n_kv_heads * hd;
+    const int t = threadIdx.x, lane = t & 63, c = t & 31, g = t >> 5;
+    const int hd4 = hd >> 2;
+    const bool col = c < hd4;
+    const float scale = 1.0f / sqrtf((float)hd);
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < hd4) lq[t] = *(const float4 *)(q + (int64_t)h * hd + 4 * t);
+    __syncthreads();
+    const float4 q4 = col ? lq[c] : zero;
+    const float *kb = kc + (int64_t)kvh * hd + 4 * c;
+    const float *vb = vc + (int64_t)kvh * hd + 4 * c;
+    const int p_begin = s * chunk, p_end = min(p_begin + chunk, kv_len);
+    float m = -INFINITY, l = 0.f;
+    float4 o4 = zero;
+    for (int p0 = p_begin; p0 < p_end; p0 += kDecKeys) {
+        float4 k4[8], v4[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int p = p0 + g + 8 * j;
+            k4[j] = zero;
+            v4[j] = zero;
+            if (col && p < p_end) {
+                k4[j] = *(const float4 *)(kb + (int64_t)p * kv_dim);
+                v4[j] = *(const float4 *)(vb + (int64_t)p * kv_dim);
+            }
+        }
+        float sj[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            sj[j] = half_wave_sum(q4.x * k4[j].x + q4.y * k4[j].y + q4.z * k4[j].z + q4.w * k4[j].w);
+        if (c == 0) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) lsc[g + 8 * j] = p0 + g + 8 * j < p_end ? sj[j] * scale : -INFINITY;
+        }
+        __syncthreads();
+        // every wave reduces the same 64 scores in the same order, so m and l
+        // agree across the workgroup; key p0 + i's weight sits in lane i
+        const float sl = lsc[lane];
+        const float mnew = fmaxf(m, wave_reduce_max(sl));  // p0 < p_end: finite from the first pass on
+        const float corr = expf(m - mnew);
+        const float pl = expf(sl - mnew);
+        l = l * corr + wave_reduce_sum(pl);
+        o4 = make_float4(o4.x * corr, o4.y * corr, o4.z * corr, o4.w * corr);
+        m = mnew;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float w = __shfl(pl, g + 8 * j, 64);
+            o4 = make_float4(fmaf(w, v4[j].x, o4.x), fmaf(w, v4[j].y, o4.y), fmaf(w, v4[j].z, o4.z),
+                             fmaf(w, v4[j].w, o4.w));
+        }
+        __syncthreads();  // lsc is rewritten by the next pass
+    }
+    lo[g][c] = o4;
+    __syncthreads();
+    if (t < hd4) {
+        float4 r = lo[0][t];
+#pragma unroll
+        for (int gg = 1; gg < 8; gg++)
+            r = make_float4(r.x + lo[gg][t].x, r.y + lo[gg][t].y, r.z + lo[gg][t].z, r.w + lo[gg][t].w);
+        if (splits == 1) {
+            const float inv = 1.0f / l;
+            *(float4 *)(out + (int64_t)h * hd + 4 * t) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
+        } else {
+            float *pp = part + ((int64_t)h * splits + s) * (hd + 4);
+            *(float4 *)(pp + 4 * t) = r;
+            if (t == 0) {
+                pp[hd] = m;
+                pp[hd + 1] = l;
+            }
+        }
+    }
+}
+
+// Merges a head's ranges: weights e^(m_s - M) in range order.
+__global__ __launch_bounds__(128) void attn_decode_combine_k(float *out, const float *part, int hd, int splits)
+{
+    __shared__ float lw[kDecMaxSplits];
+    __shared__ float scratch[16];
+    const int h = blockIdx.x, t = threadIdx.x;
+    const int stride = hd + 4;
+    const float *ph = part + (int64_t)h * splits * stride;
+    float mx = -INFINITY;
+    for (int s = t; s < splits; s += blockDim.x) mx = fmaxf(mx, ph[(int64_t)s * stride + hd]);
+    const float M = block_reduce<true>(mx, scratch);
+    for (int s = t; s < splits; s += blockDim.x) lw[s] = expf(ph[(int64_t)s * stride + hd] - M);
+    __syncthreads();
+    float L = 0.f;
+    for (int s = 0; s < splits; s++) L = fmaf(lw[s], ph[(int64_t)s * stride + hd + 1], L);
+    const float inv = 1.0f / L;
+    for (int d = t; d < hd; d += blockDim.x) {
+        float o = 0.f;
+        for (int s = 0; s < splits; s++) o = fmaf(lw[s], ph[(int64_t)s * stride + d], o);
+        out[(int64_t)h * hd + d] = o * inv;
+    }
+}
+
+// Shapes the split kernel takes: head_dim a multiple of 4 up to 128, 16-byte
+// aligned rows.
+static bool decode_attention_fits(const float *q, const float *kc, const float *vc, int hd)
+{
+    return hd >= 4 && hd <= 128 && hd % 4 == 0 && !(((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc) & 15);
+}
+
+static void decode_attention(float *dst, const float *q, const float *kc, const float *vc, int kv_len, int hd,
+                             int n_heads, int n_kv_heads)
+{
+    int splits = (kv_len + kDecKeys - 1) / kDecKeys;
+    if (!g_dec_part) splits = 1;
+    splits = min(splits, min(kDecMaxSplits, (int)(kDecPartFloats / ((size_t)n_heads * (hd + 4)))));
+    splits = max(splits, 1);
+    const int chunk = ((kv_len + splits - 1) / splits + kDecKeys - 1) / kDecKeys * kDecKeys;
+    splits = (kv_len + chunk - 1) / chunk;  // every range holds at least one key
+    hipLaunchKernelGGL(attn_decode_k, dim3(splits, n_heads), dim3(256), 0, stream(), dst, g_dec_part, q, kc, vc,
+                       kv_len, hd, n_heads, n_kv_heads, chunk);
+    HOLO_LAUNCH_CHECK();
+    if (splits > 1) {
+        hipLaunchKernelGGL(attn_decode_combine_k, dim3(n_heads), dim3(128), 0, stream(), dst, g_dec_part, hd,
+                           splits);
+        HOLO_LAUNCH_CHECK();
+    }
+}
+
+bool attention_scratch_init()
+{
+    if (g_dec_part) return true;
+    if (hipMalloc((void **)&g_dec_part, kDecPartFloats * sizeof(float)) != hipSuccess) {
+        g_dec_part = nullptr;
+        return false;
+    }
+    return true;
+}
+
+void attention_scratch_release()
+{
+    if (g_dec_part) (void)hipFree(g_dec_part);
+    g_dec_part = nullptr;
+}
+
 // ---- RoPE (cuda_ops.cu:2102-2140): pairs (i, i + hd/2), theta = pos / base^(2i/hd) ----------
 
 __device__ __forceinline__ void rope_head(float *q, float *k, int pos, int hd, int n_heads, int n_kv_heads,
@@ -693,8 +868,16 @@ void cuda_multi_head_attention(float *dst, const float *q, const float *k_cache,
                                int head_dim, int n_heads, int n_kv_heads)
 {
     if (kv_len <= 0 || n_heads <= 0) return;
-    if (kv_len > kMaxLdsScores || n_kv_heads <= 0 || n_heads % n_kv_heads != 0) {
-        HOLO_REJECT("cuda_multi_head_attention: kv_len <= 12288 and n_heads % n_kv_heads == 0 required");
+    if (!dst || !q || !k_cache || !v_cache || n_kv_heads <= 0 || n_heads % n_kv_heads != 0) {
+        HOLO_REJECT("cuda_multi_head_attention: null pointer or n_heads not a multiple of n_kv_heads");
+        return;
+    }
+    if (decode_attention_fits(q, k_cache, v_cache, head_dim)) {
+        decode_attention(dst, q, k_cache, v_cache, kv_len, head_dim, n_heads, n_kv_heads);
+        return;
+    }
+    if (kv_len > kMaxLdsScores) {
+        HOLO_REJECT("cuda_multi_head_attention: kv_len <= 12288 required for this head_dim or alignment");
         return;
     }
     hipLaunchKernelGGL(mha_k, dim3(n_heads), dim3(256), 0, stream(), dst, q, k_cache, v_cache, kv_len, head_dim,
@@ -845,6 +1028,14 @@ void holo_attention_prefill(float *out, const float *q, const float *k_cache, co
         n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15)) {
         HOLO_REJECT("holo_attention_prefill: null or misaligned pointer, pos0 < 0, head_dim not a multiple of 4 in "
                     "4..128, or heads not grouped");
+        return;
+    }
+    if (rows <= 4) {
+        // a decode step (or a few rows): each row on the key-split kernel,
+        // row m attending to positions 0 .. pos0 + m
+        for (int m = 0; m < rows; m++)
+            decode_attention(out + (int64_t)m * n_heads * head_dim, q + (int64_t)m * n_heads * head_dim, k_cache,
+                             v_cache, pos0 + m + 1, head_dim, n_heads, n_kv_heads);
         return;
     }
     static bool attr = false;

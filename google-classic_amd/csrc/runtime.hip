@@ -70,6 +70,10 @@ int cuda_init(void)
         fprintf(stderr, "holo_mi355x: cannot allocate the GEMV chain barrier\n");
         return -1;
     }
+    if (!holo::attention_scratch_init()) {
+        fprintf(stderr, "holo_mi355x: cannot allocate the decode-attention scratch\n");
+        return -1;
+    }
     g_initialized = true;
     return 0;
 }
@@ -82,6 +86,7 @@ void cuda_cleanup(void)
     if (g_copy_stream) hipStreamDestroy(g_copy_stream);
     g_copy_stream = nullptr;
     holo::gemv_chain_release();
+    holo::attention_scratch_release();
     g_stream = nullptr;
     g_initialized = false;
 }
