@@ -55,6 +55,63 @@ void norm_or_copy(float *dst, const float *x, const float *w, int rows, int n, f
         HOLO_CHECK(hipMemcpyAsync(dst, x, (size_t)rows * n * sizeof(float), hipMemcpyDeviceToDevice, stream()));
 }
 
+bool fused_gemv_type(int t) { return t == HOLO_TYPE_Q4_0 || t == HOLO_TYPE_Q8_0 || t == HOLO_TYPE_Q4_K; }
+
+// The prefill GEMM takes the rows: Q4_0, at least 64 rows, not in exact mode.
+bool gemm_rows(int type, int rows, int in_dim, int exact)
+{
+    return type == HOLO_TYPE_Q4_0 && rows >= 64 && !exact && in_dim % 32 == 0;
+}
+
+// q, k, v of n rows of xb.  One GEMM over the three matrices when the rows
+// go to the prefill GEMM (one quantisation, one launch); the fused q/k/v GEMV
+// per row when the three share a GEMV format; otherwise one call per matrix.
+void matmul_qkv(float *q, float *k, float *v, const holo_llama_layer_t &L, const float *xb, int n, int q_dim,
+                int kv_dim, int dim, int exact)
+{
+    const int t = L.wq_type;
+    const bool same = L.wk_type == t && L.wv_type == t;
+    if (same && gemm_rows(t, n, dim, exact) && q_dim % 128 == 0 && kv_dim % 128 == 0) {
+        float *Y[3] = {q, k, v};
+        const void *W[3] = {L.wq, L.wk, L.wv};
+        const int N[3] = {q_dim, kv_dim, kv_dim};
+        holo_matmul_batch_q4_0_multi(Y, W, N, 3, xb, n, dim, nullptr);
+        return;
+    }
+    if (same && fused_gemv_type(t) && !gemm_rows(t, n, dim, exact)) {
+        for (int r = 0; r < n; r++)
+            holo_batched_qkv(q + (int64_t)r * q_dim, k + (int64_t)r * kv_dim, v + (int64_t)r * kv_dim, L.wq, L.wk, L.wv,
+                             xb + (int64_t)r * dim, q_dim, kv_dim, dim, t);
+        return;
+    }
+    holo_matmul_rows(q, L.wq, xb, n, q_dim, dim, L.wq_type, exact);
+    holo_matmul_rows(k, L.wk, xb, n, kv_dim, dim, L.wk_type, exact);
+    holo_matmul_rows(v, L.wv, xb, n, kv_dim, dim, L.wv_type, exact);
+}
+
+// h = silu(W1 xb) * (W3 xb) of n rows (h2: scratch of the same size), by the
+// same three routes; the fused GEMV applies silu * in its epilogue.
+void matmul_gate_up(float *h, float *h2, const holo_llama_layer_t &L, const float *xb, int n, int ffn, int dim,
+                    int exact)
+{
+    const int t = L.w1_type;
+    const bool same = L.w3_type == t;
+    if (same && gemm_rows(t, n, dim, exact) && ffn % 128 == 0) {
+        float *Y[2] = {h, h2};
+        const void *W[2] = {L.w1, L.w3};
+        const int N[2] = {ffn, ffn};
+        holo_matmul_batch_q4_0_multi(Y, W, N, 2, xb, n, dim, nullptr);
+    } else if (same && fused_gemv_type(t) && !gemm_rows(t, n, dim, exact)) {
+        for (int r = 0; r < n; r++)
+            holo_batched_ffn_gate_up(h + (int64_t)r * ffn, L.w1, L.w3, xb + (int64_t)r * dim, ffn, dim, t);
+        return;
+    } else {
+        holo_matmul_rows(h, L.w1, xb, n, ffn, dim, L.w1_type, exact);
+        holo_matmul_rows(h2, L.w3, xb, n, ffn, dim, L.w3_type, exact);
+    }
+    cuda_silu_mul(h, h, h2, n * ffn);
+}
+
 }  // namespace
 
 extern "C" {
@@ -133,9 +190,7 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
         float *kc = m->key_cache + l * layer_cache, *vc = m->value_cache + l * layer_cache;
         // attention block
         norm_or_copy(xb, x, L.attn_norm, n, dim, m->rms_eps);
-        holo_matmul_rows(q, L.wq, xb, n, q_dim, dim, L.wq_type, exact);
-        holo_matmul_rows(k, L.wk, xb, n, kv_dim, dim, L.wk_type, exact);
-        holo_matmul_rows(v, L.wv, xb, n, kv_dim, dim, L.wv_type, exact);
+        matmul_qkv(q, k, v, L, xb, n, q_dim, kv_dim, dim, exact);
         holo_rope_rows(q, k, n, pos0, hd, m->n_heads, m->n_kv_heads, m->rope_base);
         HOLO_CHECK(hipMemcpyAsync(kc + (int64_t)pos0 * kv_dim, k, rowsz * kv_dim, hipMemcpyDeviceToDevice, stream()));
         HOLO_CHECK(hipMemcpyAsync(vc + (int64_t)pos0 * kv_dim, v, rowsz * kv_dim, hipMemcpyDeviceToDevice, stream()));
@@ -144,9 +199,7 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
         cuda_vec_add(x, x, xb, n * dim);
         // FFN block
         norm_or_copy(xb, x, L.ffn_norm, n, dim, m->rms_eps);
-        holo_matmul_rows(hb, L.w1, xb, n, ffn, dim, L.w1_type, exact);
-        holo_matmul_rows(hb2, L.w3, xb, n, ffn, dim, L.w3_type, exact);
-        cuda_silu_mul(hb, hb, hb2, n * ffn);
+        matmul_gate_up(hb, hb2, L, xb, n, ffn, dim, exact);
         holo_matmul_rows(xb, L.w2, hb, n, dim, ffn, L.w2_type, exact);
         cuda_vec_add(x, x, xb, n * dim);
     }

@@ -18,6 +18,7 @@
 #include "quant_blocks.h"
 
 #include <hip/hip_ext.h>
+#include <limits.h>
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -98,14 +99,28 @@ __global__ __launch_bounds__(256) void q8_panel_k(uint4 *__restrict__ P, uint16_
 // gives s[i][j] = dx[i]*dw[j] exactly in the same register layout, leaving
 // one VALU instruction (the fmaf) per output and block.
 
+// Up to three weight matrices share one launch and one activation panel:
+// matrix i holds columns [n_end[i-1], n_end[i]) of the concatenated product
+// and writes its own Y[i] ([M][N_i]).  Every column tile lies in one matrix
+// (the host checks N_i % TN == 0 when there are several).
+constexpr int kPrefillMats = 3;
+
 struct PrefillArgs {
+    float *Y[kPrefillMats];
+    const uint8_t *W[kPrefillMats];  // Q4_0 [N_i][nb]
+    int n_end[kPrefillMats];         // prefix sums of N_i; unused entries INT_MAX
+    const _Float16 *P;               // f16 [M][K]
+    const uint16_t *D;               // f16 bits [M][nb]
+    int M, N, nb;                    // N: all matrices' columns
+    int ntm, tiles;                  // row tiles, all tiles
+};
+
+// The matrix of a column tile, its first column and its width.
+struct PrefillMat {
+    const uint8_t *W;
     float *Y;
-    const uint8_t *W;   // Q4_0 [N][nb]
-    const _Float16 *P;  // f16 [M][K]
-    const uint16_t *D;  // f16 bits [M][nb]
-    int M, N, nb;
-    int ntm, tiles;     // row tiles, all tiles
-    int64_t w_bytes;    // N * nb * 18
+    int nbase, N;
+    int64_t w_bytes;
 };
 
 template <int WM, int WN, int S>
@@ -150,7 +165,7 @@ struct PStage {
     uint32_t rd[G::ND];
     Q4_0Unit rb[G::NB];
 
-    __device__ __forceinline__ void fetch(const PrefillArgs &a, int tid, int m0, int n0, int kb0)
+    __device__ __forceinline__ void fetch(const PrefillArgs &a, const PrefillMat &w, int tid, int m0, int n0, int kb0)
     {
         const int nb = a.nb;
         const int64_t K = (int64_t)nb * 32;
@@ -168,7 +183,7 @@ struct PStage {
 #pragma unroll
         for (int i = 0; i < G::NB; i++) {
             const int v = min(tid + 256 * i, G::TN * S - 1), n = v / S, b = min(kb0 + v % S, nb - 1);
-            rb[i] = load_q4_0(a.W, (int64_t)min(n0 + n, a.N - 1) * nb + b, a.w_bytes);
+            rb[i] = load_q4_0(w.W, (int64_t)min(n0 + n, w.N - 1) * nb + b, w.w_bytes);
         }
     }
 
@@ -218,7 +233,16 @@ __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
     // row tiles sharing a weight tile share that XCD's L2.
     const int g = blockIdx.x;
     const int t = (a.tiles & 7) ? g : (g & 7) * (a.tiles >> 3) + (g >> 3);
-    const int m0 = (t % a.ntm) * G::TM, n0 = (t / a.ntm) * G::TN;
+    const int m0 = (t % a.ntm) * G::TM, ng = (t / a.ntm) * G::TN;
+    // the tile's matrix (constant indices into the argument arrays: selects)
+    const int sel = (ng >= a.n_end[0]) + (ng >= a.n_end[1]);
+    PrefillMat w;
+    w.W = sel == 2 ? a.W[2] : sel == 1 ? a.W[1] : a.W[0];
+    w.Y = sel == 2 ? a.Y[2] : sel == 1 ? a.Y[1] : a.Y[0];
+    w.nbase = sel == 2 ? a.n_end[1] : sel == 1 ? a.n_end[0] : 0;
+    w.N = (sel == 2 ? a.n_end[2] : sel == 1 ? a.n_end[1] : a.n_end[0]) - w.nbase;
+    w.w_bytes = (int64_t)w.N * a.nb * 18;
+    const int n0 = ng - w.nbase;
     const int wm0 = (wave >> 1) * 32 * WM, wn0 = (wave & 1) * 32 * WN;
     const int nb = a.nb;
     const int nst = (nb + S - 1) / S;
@@ -281,13 +305,13 @@ __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
     };
 
     PStage<WM, WN, S> pa;
-    pa.fetch(a, tid, m0, n0, 0);
+    pa.fetch(a, w, tid, m0, n0, 0);
     pa.stash(lds, tid);
     if constexpr (D == 1) {
         // stage st+1 loads while stage st is multiplied
         __syncthreads();
         for (int st = 0; st < nst; st++) {
-            if (st + 1 < nst) pa.fetch(a, tid, m0, n0, (st + 1) * S);
+            if (st + 1 < nst) pa.fetch(a, w, tid, m0, n0, (st + 1) * S);
             compute(st & 1, st * S);
             if (st + 1 < nst) pa.stash(lds + ((st + 1) & 1) * G::STAGE, tid);
             __syncthreads();
@@ -296,21 +320,21 @@ __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
         // two register sets carry stages st+1 and st+2 while stage st is
         // multiplied, so each stage's loads have two stages of products to land
         PStage<WM, WN, S> pb;
-        if (nst > 1) pa.fetch(a, tid, m0, n0, S);
-        if (nst > 2) pb.fetch(a, tid, m0, n0, 2 * S);
+        if (nst > 1) pa.fetch(a, w, tid, m0, n0, S);
+        if (nst > 2) pb.fetch(a, w, tid, m0, n0, 2 * S);
         __syncthreads();
         for (int st = 0; st < nst; st += 2) {
             compute(0, st * S);
             if (st + 1 < nst) {
                 pa.stash(lds + G::STAGE, tid);
-                if (st + 3 < nst) pa.fetch(a, tid, m0, n0, (st + 3) * S);
+                if (st + 3 < nst) pa.fetch(a, w, tid, m0, n0, (st + 3) * S);
             }
             __syncthreads();
             if (st + 1 >= nst) break;
             compute(1, (st + 1) * S);
             if (st + 2 < nst) {
                 pb.stash(lds, tid);
-                if (st + 4 < nst) pb.fetch(a, tid, m0, n0, (st + 4) * S);
+                if (st + 4 < nst) pb.fetch(a, w, tid, m0, n0, (st + 4) * S);
             }
             __syncthreads();
         }
@@ -324,7 +348,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + wm0 + 32 * mi + (r & 3) + 4 * h + 8 * (r >> 2);
-                if (m < a.M && n < a.N) a.Y[(int64_t)m * a.N + n] = acc[mi][ni][r];
+                if (m < a.M && n < w.N) w.Y[(int64_t)m * w.N + n] = acc[mi][ni][r];
             }
         }
 }
@@ -382,19 +406,15 @@ void holo_quantize_act_q8_0(void *dst_blocks, const float *X, int rows, int k)
     HOLO_LAUNCH_CHECK();
 }
 
-void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, int K)
+}  // extern "C"
+
+// One launch over nmat matrices (holo_gemm_q4_0_q8_0 and its multi-matrix form).
+static void gemm_multi(float *const *Y, const void *const *W, const int *N, int nmat, const void *Xq, int M, int K)
 {
-    if (M <= 0 || N <= 0) return;
-    if (!Y || !W || !Xq || K % 32 != 0 || K <= 0) {
-        HOLO_REJECT("holo_gemm_q4_0_q8_0: null pointer or K not a positive multiple of 32");
-        return;
-    }
-    if ((((uintptr_t)W) & 3u) || (((uintptr_t)Xq) & 3u)) {
-        HOLO_REJECT("holo_gemm_q4_0_q8_0: W and Xq must be 4-byte aligned");
-        return;
-    }
     const int nb = K / 32;
     const int64_t nblk = (int64_t)M * nb;
+    int ntot = 0;
+    for (int i = 0; i < nmat; i++) ntot += N[i];
     const size_t pbytes = (size_t)nblk * 64, dbytes = ((size_t)nblk * 2 + 255) & ~(size_t)255;
     void *ws = nullptr;
     HOLO_CHECK(hipMallocAsync(&ws, pbytes + dbytes, stream()));
@@ -404,7 +424,25 @@ void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, 
     hipLaunchKernelGGL(q8_panel_k, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, stream(), P, D,
                        (const uint8_t *)Xq, nblk, nblk * 34);
     HOLO_LAUNCH_CHECK();
-    PrefillArgs a = {Y, (const uint8_t *)W, (const _Float16 *)P, D, M, N, nb, 0, 0, (int64_t)N * nb * 18};
+    PrefillArgs a = {};
+    int acc = 0;
+    for (int i = 0; i < kPrefillMats; i++) {
+        if (i < nmat) {
+            acc += N[i];
+            a.Y[i] = Y[i];
+            a.W[i] = (const uint8_t *)W[i];
+            a.n_end[i] = acc;
+        } else {
+            a.Y[i] = Y[0];
+            a.W[i] = (const uint8_t *)W[0];
+            a.n_end[i] = INT_MAX;
+        }
+    }
+    a.P = (const _Float16 *)P;
+    a.D = D;
+    a.M = M;
+    a.N = ntot;
+    a.nb = nb;
     // Variant per shape (measured at the config-4 shapes): 128-column tiles,
     // two workgroups per CU, one stage of loads in flight when there are at
     // least as many tiles as CUs; otherwise 64-column tiles with two stages in
@@ -416,13 +454,66 @@ void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, 
         int t = 0, st = 0, d = 0, o = 0;
         cfg = (e && sscanf(e, "%d,%d,%d,%d", &t, &st, &d, &o) == 4) ? t * 1000 + st * 100 + d * 10 + o : 0;
     }
-    switch (cfg ? cfg : (prefill_tn(M, N) == 128 ? 128212 : 64222)) {
+    switch (cfg ? cfg : (prefill_tn(M, ntot) == 128 ? 128212 : 64222)) {
     case 64112: launch_prefill<2, 1, 1, 1, 2>(a); break;
     case 64222: launch_prefill<2, 1, 2, 2, 2>(a); break;
     case 64412: launch_prefill<2, 1, 4, 1, 1>(a); break;
     default: launch_prefill<2, 2, 2, 1, 2>(a); break;
     }
     HOLO_CHECK(hipFreeAsync(ws, stream()));
+}
+
+// Several matrices in one launch: each N_i a multiple of 128 (a column tile
+// never straddles two matrices), at most three.
+static bool multi_fits(const int *N, int nmat)
+{
+    if (nmat < 1 || nmat > kPrefillMats) return false;
+    if (nmat == 1) return N[0] > 0;
+    for (int i = 0; i < nmat; i++)
+        if (N[i] <= 0 || N[i] % 128) return false;
+    return true;
+}
+
+static bool gemm_args_ok(const void *Xq, int K)
+{
+    if (!Xq || K % 32 != 0 || K <= 0 || (((uintptr_t)Xq) & 3u)) {
+        HOLO_REJECT("holo_gemm_q4_0_q8_0_multi: Xq null or not 4-byte aligned, or K not a positive multiple of 32");
+        return false;
+    }
+    return true;
+}
+
+extern "C" {
+
+void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, int K)
+{
+    if (M <= 0 || N <= 0) return;
+    if (!Y || !W || !Xq || K % 32 != 0 || K <= 0) {
+        HOLO_REJECT("holo_gemm_q4_0_q8_0: null pointer or K not a positive multiple of 32");
+        return;
+    }
+    if ((((uintptr_t)W) & 3u) || (((uintptr_t)Xq) & 3u)) {
+        HOLO_REJECT("holo_gemm_q4_0_q8_0: W and Xq must be 4-byte aligned");
+        return;
+    }
+    gemm_multi(&Y, &W, &N, 1, Xq, M, K);
+}
+
+void holo_gemm_q4_0_q8_0_multi(float *const *Y, const void *const *W, const int *N, int nmat, const void *Xq, int M,
+                               int K)
+{
+    if (M <= 0) return;
+    if (!Y || !W || !N || !multi_fits(N, nmat)) {
+        HOLO_REJECT("holo_gemm_q4_0_q8_0_multi: null array, or not 1..3 matrices whose N are multiples of 128");
+        return;
+    }
+    for (int i = 0; i < nmat; i++)
+        if (!Y[i] || !W[i] || (((uintptr_t)W[i]) & 3u)) {
+            HOLO_REJECT("holo_gemm_q4_0_q8_0_multi: null or misaligned matrix or output");
+            return;
+        }
+    if (!gemm_args_ok(Xq, K)) return;
+    gemm_multi(Y, W, N, nmat, Xq, M, K);
 }
 
 void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int N, int K, void *scratch_q8)
@@ -437,6 +528,26 @@ void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int 
     if (!q) return;
     holo_quantize_act_q8_0(q, X, M, K);
     holo_gemm_q4_0_q8_0(Y, W, q, M, N, K);
+    if (!scratch_q8) HOLO_CHECK(hipFreeAsync(q, stream()));
+}
+
+void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const int *N, int nmat, const float *X,
+                                  int M, int K, void *scratch_q8)
+{
+    if (M <= 0) return;
+    if (!Y || !W || !N || !X || !multi_fits(N, nmat)) {
+        HOLO_REJECT("holo_matmul_batch_q4_0_multi: null array, or not 1..3 matrices whose N are multiples of 128");
+        return;
+    }
+    if (M < 64) {
+        for (int i = 0; i < nmat; i++) holo_matmul_batch_q4_0(Y[i], W[i], X, M, N[i], K, scratch_q8);
+        return;
+    }
+    void *q = scratch_q8;
+    if (!q) HOLO_CHECK(hipMallocAsync(&q, (size_t)M * (K / 32) * 34, stream()));
+    if (!q) return;
+    holo_quantize_act_q8_0(q, X, M, K);
+    holo_gemm_q4_0_q8_0_multi(Y, W, N, nmat, q, M, K);
     if (!scratch_q8) HOLO_CHECK(hipFreeAsync(q, stream()));
 }
 

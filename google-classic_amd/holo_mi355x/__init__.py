@@ -136,6 +136,8 @@ _SIGS = {
     "holo_quantize_act_q8_0": (None, [_P, _P, _I, _I]),
     "holo_gemm_q4_0_q8_0": (None, [_P, _P, _P, _I, _I, _I]),
     "holo_matmul_batch_q4_0": (None, [_P, _P, _P, _I, _I, _I, _P]),
+    "holo_gemm_q4_0_q8_0_multi": (None, [_P, _P, _P, _I, _P, _I, _I]),
+    "holo_matmul_batch_q4_0_multi": (None, [_P, _P, _P, _I, _P, _I, _I, _P]),
     # GGUF files (include/holo_gguf.h)
     "holo_gguf_open": (_P, [C.c_char_p]),
     "holo_gguf_close": (None, [_P]),

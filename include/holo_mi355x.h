@@ -145,6 +145,17 @@ void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, 
  * the MFMA GEMM above; M < 64 runs M fp32-activation GEMVs.                 */
 void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int N, int K,
                             void *scratch_q8);
+/* The same over nmat = 1..3 Q4_0 matrices that multiply the same X in one
+ * launch, sharing one quantisation and one staged panel (for example q/k/v,
+ * or gate and up): Y[i][M][N[i]] = X . W[i]^T.  With more than one matrix
+ * every N[i] must be a multiple of 128.  Each output is bit-identical to the
+ * single-matrix call.  No reference counterpart (the reference multiplies one
+ * matrix by one token at a time, llm.c:1049); the batched analogue of
+ * holo_batched_qkv / holo_batched_ffn_gate_up.                              */
+void holo_gemm_q4_0_q8_0_multi(float *const *Y, const void *const *W, const int *N, int nmat,
+                               const void *Xq, int M, int K);
+void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const int *N, int nmat,
+                                  const float *X, int M, int K, void *scratch_q8);
 
 #ifdef __cplusplus
 }

@@ -148,6 +148,57 @@ def test_matmul_batch_dispatch(holo, synth, oracle):
             assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("M,Ns,K", [(100, (256, 128, 128), 512), (512, (4096, 1024, 1024), 4096),
+                                    (64, (384, 384), 256), (77, (150,), 1024)], ids=str)
+def test_gemm_multi_matches_single(holo, synth, oracle, M, Ns, K):
+    """Several matrices over the same activations in one launch: every output
+    bit-identical to its single-matrix launch and to the oracle."""
+    import ctypes as C
+    print(f"case gemm multi {M}x{Ns}x{K}", flush=True)
+    lib = holo.lib()
+    Ws = [synth.blocks(Q4_0, n, K, seed=7 + i) for i, n in enumerate(Ns)]
+    X = synth.normal(M * K, seed=3).reshape(M, K)
+    Xq = oracle.quantize_act_q8_0(X)
+    dWs = [up(holo, w) for w in Ws]
+    dXq, dX = up(holo, Xq), up(holo, X)
+    dYs = [holo.DeviceBuffer(4 * M * n) for n in Ns]
+    dYb = [holo.DeviceBuffer(4 * M * n) for n in Ns]
+    k = len(Ns)
+    Yp = (C.c_void_p * k)(*[d.ptr for d in dYs])
+    Wp = (C.c_void_p * k)(*[d.ptr for d in dWs])
+    Np = (C.c_int * k)(*Ns)
+    lib.holo_gemm_q4_0_q8_0_multi(Yp, Wp, Np, k, dXq.ptr, M, K)
+    Yb = (C.c_void_p * k)(*[d.ptr for d in dYb])
+    lib.holo_matmul_batch_q4_0_multi(Yb, Wp, Np, k, dX.ptr, M, K, None)
+    lib.cuda_sync()
+    holo.check("gemm multi")
+    for i, n in enumerate(Ns):
+        dS = holo.DeviceBuffer(4 * M * n)
+        lib.holo_gemm_q4_0_q8_0(dS.ptr, dWs[i].ptr, dXq.ptr, M, n, K)
+        lib.cuda_sync()
+        got = down(dYs[i], M * n)
+        assert np.array_equal(got.view(np.uint32), down(dS, M * n).view(np.uint32)), i
+        assert np.array_equal(down(dYb[i], M * n).view(np.uint32), got.view(np.uint32)), i
+        rows = min(M, 16)
+        want = oracle.gemm_q4_0_q8_0(Ws[i], Xq.reshape(M, -1)[:rows].copy().reshape(-1), rows, n, K)
+        assert np.array_equal(got.reshape(M, n)[:rows].view(np.uint32), want.view(np.uint32)), i
+
+
+def test_gemm_multi_rejects(holo, synth):
+    import ctypes as C
+    lib = holo.lib()
+    d = holo.DeviceBuffer(4 * 64 * 256)
+    w = up(holo, synth.blocks(Q4_0, 200, 256, seed=1))
+    q = holo.DeviceBuffer(64 * 8 * 34)
+    Yp = (C.c_void_p * 2)(d.ptr, d.ptr)
+    Wp = (C.c_void_p * 2)(w.ptr, w.ptr)
+    lib.holo_last_error()
+    lib.holo_gemm_q4_0_q8_0_multi(Yp, Wp, (C.c_int * 2)(200, 200), 2, q.ptr, 64, 256)  # N not a multiple of 128
+    assert lib.holo_last_error() == 100001
+    lib.holo_gemm_q4_0_q8_0_multi(Yp, Wp, (C.c_int * 2)(128, 128), 4, q.ptr, 64, 256)  # too many matrices
+    assert lib.holo_last_error() == 100001
+
+
 # ---- remaining boundary ops --------------------------------------------------------------
 
 def test_vector_and_activation_ops(holo, synth):
