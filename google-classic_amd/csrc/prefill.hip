@@ -353,9 +353,9 @@ __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
         }
 }
 
-// Tile width per problem: the 128 x 128 workgroup tile (64 x 64 per wave)
-// reads the least LDS per product and is used when it yields at least one
-// tile per CU; otherwise the 128 x 64 tile keeps every CU busy.
+// Tile per problem: the 128 x 128 workgroup tile (64 x 64 per wave) reads
+// the least LDS per product and is used when it yields at least one tile per
+// CU; otherwise the 64 x 64 tile gives four times the workgroups.
 static int prefill_tn(int M, int N)
 {
     const int cus = num_cus() > 0 ? num_cus() : 256;
@@ -443,21 +443,26 @@ static void gemm_multi(float *const *Y, const void *const *W, const int *N, int 
     a.M = M;
     a.N = ntot;
     a.nb = nb;
-    // Variant per shape (measured at the config-4 shapes): 128-column tiles,
-    // two workgroups per CU, one stage of loads in flight when there are at
-    // least as many tiles as CUs; otherwise 64-column tiles with two stages in
-    // flight.  HOLO_PREFILL_CFG=<tile>,<stage blocks>,<depth>,<workgroups per CU>
-    // selects one of the compiled variants instead.
+    // Variant per shape (measured at the prompt-forward shapes, M = 512):
+    // 128 x 128 tiles, 2-block stages, one stage of loads in flight, when
+    // there are at least as many such tiles as CUs (q/k/v, gate/up: 137 and
+    // 254 us); otherwise 64 x 64 tiles, 4-block stages, two in flight (o,
+    // down: 58 and 142 us, against 90 and 223 us on 128 x 64 tiles).
+    // HOLO_PREFILL_CFG=<tile rows>,<tile columns>,<stage blocks>,<stages in
+    // flight>,<workgroups per CU> selects one of the compiled variants
+    // (128,128,2,1,2  128,64,2,2,2  64,64,4,1,2  64,64,4,2,2) instead.
     static int cfg = -1;
     if (cfg < 0) {
         const char *e = getenv("HOLO_PREFILL_CFG");
-        int t = 0, st = 0, d = 0, o = 0;
-        cfg = (e && sscanf(e, "%d,%d,%d,%d", &t, &st, &d, &o) == 4) ? t * 1000 + st * 100 + d * 10 + o : 0;
+        int tm = 0, tn = 0, st = 0, d = 0, o = 0;
+        cfg = (e && sscanf(e, "%d,%d,%d,%d,%d", &tm, &tn, &st, &d, &o) == 5)
+                  ? (tm / 64) * 10000 + (tn / 64) * 1000 + st * 100 + d * 10 + o
+                  : 0;
     }
-    switch (cfg ? cfg : (prefill_tn(M, ntot) == 128 ? 128212 : 64222)) {
-    case 64112: launch_prefill<2, 1, 1, 1, 2>(a); break;
-    case 64222: launch_prefill<2, 1, 2, 2, 2>(a); break;
-    case 64412: launch_prefill<2, 1, 4, 1, 1>(a); break;
+    switch (cfg ? cfg : (prefill_tn(M, ntot) == 128 ? 22212 : 11422)) {
+    case 21222: launch_prefill<2, 1, 2, 2, 2>(a); break;
+    case 11412: launch_prefill<1, 1, 4, 1, 2>(a); break;
+    case 11422: launch_prefill<1, 1, 4, 2, 2>(a); break;
     default: launch_prefill<2, 2, 2, 1, 2>(a); break;
     }
     HOLO_CHECK(hipFreeAsync(ws, stream()));
