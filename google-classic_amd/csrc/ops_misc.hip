@@ -211,6 +211,165 @@ __global__ __launch_bounds__(256) void mha_k(float *dst, const float *q, const f
                n_kv_heads * hd, lsc, scratch);
 }
 
+// ---- causal prefill attention on the fp32 matrix cores ------------------------------
+//
+// The same result as attention_prefill_k (softmax((q . k_p) / sqrt(hd)) . v,
+// online over key tiles, fp32), for head sizes 32, 64 and 128, with both
+// products on v_mfma_f32_32x32x2_f32.  A workgroup takes one head and 32
+// query rows; its 4 waves take the 32-key tiles in turn (wave w: tiles w,
+// w + 4, ...) and merge their softmax states through LDS at the end.
+//
+// 32x32x2 f32 (wave64): lane l supplies A[l%32][l/32] and B[l/32][l%32];
+// D[i][j] lands in lane j + 32*((i/4)%2), register (i%4) + 4*(i/8).
+//   scores, transposed: S^T = K Q^T.  Half hh of the wave loads 16-byte chunk
+//     2c + hh of its key row (A) and of its query row (B); the 4 elements of a
+//     chunk feed 4 instructions, so A and B agree on the dimension of every
+//     (step, slot).  Lane j + 32hh then holds query j's scores for keys
+//     (r%4) + 8(r/4) + 4hh, r = 0..15: the row maximum is 15 local steps and
+//     one exchange with lane j ^ 32.
+//   output, transposed: O^T += V^T P^T over 16 steps; step st pairs key
+//     (st%4) + 8(st/4) + 4hh (slot hh) with register st of the probabilities,
+//     which is already the B operand.  A is V: lane i + 32hh reads dims
+//     VB*i .. VB*i + VB - 1 of that key's row, one contiguous row per half;
+//     element b feeds the block of dims VB*i + b.
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_mfma_k(float *out, const float *q, const float *kc,
+                                                           const float *vc, int rows, int pos0, int n_heads,
+                                                           int n_kv_heads)
+{
+    constexpr int NC = HD / 8;   // 16-byte chunk pairs of a row
+    constexpr int VB = HD / 32;  // output blocks: lane i covers dims VB*i .. VB*i + VB - 1
+    extern __shared__ float amf_lds[];
+    float *lo = amf_lds;                       // [4 waves][HD][32]
+    float *lm = lo + 4 * HD * 32;              // [4][32] running max per query
+    float *ll = lm + 4 * 32;                   // [4][64] running sum per lane
+    const int h = blockIdx.y, q0 = (gridDim.x - 1 - blockIdx.x) * 32;  // heaviest query blocks first
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 31, hh = lane >> 5;
+    const int kvh = h / (n_heads / n_kv_heads);
+    const int64_t q_dim = (int64_t)n_heads * HD, kv_dim = (int64_t)n_kv_heads * HD;
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int last_key = pos0 + min(q0 + 32, rows) - 1;  // the furthest position a query here sees
+    const int ntiles = last_key / 32 + 1;
+    const int qpos = pos0 + q0 + j;  // rows past the prompt: computed, not stored
+
+    float4 qr[NC];
+    {
+        const float *qp = q + (int64_t)min(q0 + j, rows - 1) * q_dim + (int64_t)h * HD + 4 * hh;
+#pragma unroll
+        for (int c = 0; c < NC; c++) qr[c] = *(const float4 *)(qp + 8 * c);
+    }
+    const float *kb = kc + (int64_t)kvh * HD + 4 * hh;
+    const float *vb = vc + (int64_t)kvh * HD + VB * j;
+    float m = -INFINITY, l = 0.f;
+    v16f o[VB];
+#pragma unroll
+    for (int b = 0; b < VB; b++) o[b] = v16f{};
+
+    for (int t = wave; t < ntiles; t += 4) {
+        const int key0 = t * 32;
+        float4 kr[NC];
+        {
+            const float *kp = kb + (int64_t)min(key0 + j, last_key) * kv_dim;  // keys past last_key are masked
+#pragma unroll
+            for (int c = 0; c < NC; c++) kr[c] = *(const float4 *)(kp + 8 * c);
+        }
+        v16f s = v16f{};
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].x, qr[c].x, s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].y, qr[c].y, s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].z, qr[c].z, s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].w, qr[c].w, s, 0, 0, 0);
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int key = key0 + (r & 3) + 8 * (r >> 2) + 4 * hh;
+            s[r] = key <= qpos ? s[r] * scale : -INFINITY;
+            tmax = fmaxf(tmax, s[r]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(m, tmax);
+        // a query with no key yet (every key so far past it) keeps m = -inf, l = 0
+        const bool none = mnew == -INFINITY;
+        const float corr = none ? 1.0f : expf(m - mnew);
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            s[r] = none ? 0.f : expf(s[r] - mnew);
+            ps += s[r];
+        }
+        l = l * corr + ps;
+        m = mnew;
+#pragma unroll
+        for (int b = 0; b < VB; b++) o[b] *= corr;
+#pragma unroll
+        for (int st = 0; st < 16; st++) {
+            const int key = key0 + (st & 3) + 8 * (st >> 2) + 4 * hh;
+            const float *vp = vb + (int64_t)min(key, last_key) * kv_dim;  // masked keys: weight 0
+            if constexpr (VB == 4) {
+                const float4 v = *(const float4 *)vp;
+                o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.x, s[st], o[0], 0, 0, 0);
+                o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.y, s[st], o[1], 0, 0, 0);
+                o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.z, s[st], o[2], 0, 0, 0);
+                o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.w, s[st], o[3], 0, 0, 0);
+            } else if constexpr (VB == 2) {
+                const float2 v = *(const float2 *)vp;
+                o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.x, s[st], o[0], 0, 0, 0);
+                o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.y, s[st], o[1], 0, 0, 0);
+            } else {
+                o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(*vp, s[st], o[0], 0, 0, 0);
+            }
+        }
+    }
+
+    // merge the 4 waves: O = sum_w e^(m_w - M) O_w, L = sum_w e^(m_w - M) l_w
+#pragma unroll
+    for (int b = 0; b < VB; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int i = (r & 3) + 8 * (r >> 2) + 4 * hh;
+            lo[(wave * HD + VB * i + b) * 32 + j] = o[b][r];
+        }
+    if (hh == 0) lm[wave * 32 + j] = m;
+    ll[wave * 64 + lane] = l;
+    __syncthreads();
+    for (int e = threadIdx.x; e < 32 * HD; e += 256) {
+        const int qj = e / HD, d = e - qj * HD;  // consecutive threads: consecutive dims of one row
+        if (q0 + qj >= rows) continue;
+        float M = lm[qj];
+#pragma unroll
+        for (int w = 1; w < 4; w++) M = fmaxf(M, lm[w * 32 + qj]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float mw = lm[w * 32 + qj];
+            const float wgt = mw == -INFINITY ? 0.f : expf(mw - M);
+            L += wgt * (ll[w * 64 + qj] + ll[w * 64 + 32 + qj]);
+            O += wgt * lo[(w * HD + d) * 32 + qj];
+        }
+        out[(int64_t)(q0 + qj) * q_dim + (int64_t)h * HD + d] = O / L;
+    }
+}
+
+template <int HD>
+static void launch_attn_prefill_mfma(float *out, const float *q, const float *kc, const float *vc, int rows, int pos0,
+                                     int n_heads, int n_kv_heads)
+{
+    constexpr size_t lds = (size_t)(4 * HD * 32 + 4 * 32 + 4 * 64) * sizeof(float);
+    static bool attr = false;
+    if (!attr) {
+        HOLO_CHECK(hipFuncSetAttribute((const void *)attn_prefill_mfma_k<HD>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    hipLaunchKernelGGL(attn_prefill_mfma_k<HD>, dim3((rows + 31) / 32, n_heads), dim3(256), lds, stream(), out, q, kc,
+                       vc, rows, pos0, n_heads, n_kv_heads);
+    HOLO_LAUNCH_CHECK();
+}
+
 // ---- decode attention: one query row per head, keys split over workgroups ----------
 //
 // softmax((q . k_p) / sqrt(hd)) . v over cached positions p < kv_len, as
@@ -1036,6 +1195,12 @@ void holo_attention_prefill(float *out, const float *q, const float *k_cache, co
         for (int m = 0; m < rows; m++)
             decode_attention(out + (int64_t)m * n_heads * head_dim, q + (int64_t)m * n_heads * head_dim, k_cache,
                              v_cache, pos0 + m + 1, head_dim, n_heads, n_kv_heads);
+        return;
+    }
+    if (head_dim == 128 || head_dim == 64 || head_dim == 32) {
+        if (head_dim == 128) launch_attn_prefill_mfma<128>(out, q, k_cache, v_cache, rows, pos0, n_heads, n_kv_heads);
+        else if (head_dim == 64) launch_attn_prefill_mfma<64>(out, q, k_cache, v_cache, rows, pos0, n_heads, n_kv_heads);
+        else launch_attn_prefill_mfma<32>(out, q, k_cache, v_cache, rows, pos0, n_heads, n_kv_heads);
         return;
     }
     static bool attr = false;

@@ -213,6 +213,12 @@ def test_forward_matches_reference(model, flags):
 
 
 def test_prompt_in_one_pass_equals_decode_loop(model):
+    """Exact mode (fp32-activation matmuls on both sides).  The two sides run
+    attention on different kernels, the prompt on the matrix-core prefill
+    kernel and each decode step on the key-split kernel: two fp32 evaluation
+    orders, each within 1e-5 of float64 per call (test_attention_prefill,
+    test_decode_attention).  Through two layers and the output head the
+    logits then differ by ~1.5e-5 normwise; the bound is 5e-5."""
     print("case prefill vs decode loop", flush=True)
     z = np.load(GOLDEN)
     tokens = z["tokens"][:40]
@@ -223,8 +229,9 @@ def test_prompt_in_one_pass_equals_decode_loop(model):
     for i, t in enumerate(tokens):
         last = model.forward(tokens[i:i + 1], i, 1)
     k2, v2 = model.caches(40)
-    assert normwise_err(one, last) <= 1e-5
-    assert normwise_err(k1, k2) <= 1e-5 and normwise_err(v1, v2) <= 1e-5
+    e, ek, ev = normwise_err(one, last), normwise_err(k1, k2), normwise_err(v1, v2)
+    print(f"  logits {e:.2e}  k {ek:.2e}  v {ev:.2e}", flush=True)
+    assert e <= 5e-5 and ek <= 5e-5 and ev <= 5e-5
 
 
 def test_forward_rejects_bad_input(model):
