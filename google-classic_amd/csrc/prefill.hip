@@ -14,6 +14,16 @@
 // Every rounding is specified, so the GPU result is bit-identical to the
 // CPU restatement (no contraction in this file: the one fused multiply-add
 // is written as fmaf).
+//
+// The f16 product (the default of holo_matmul_batch_q4_0) keeps the
+// activations instead of quantising them, and dequantises the weights as
+// they are staged:
+//   x16 = f16_rne(x),  w16 = f16_rne(f16(dw) * (q - 8)),
+//   Y[m][n] = sum_k x16 * w16, accumulated in fp32 on the matrix cores
+// (restated in float64 by oracle_gemm_q4_0_f16; the GPU is held to the fp32
+// accumulation bound).  No per-block rescale is left, so each 32-block costs
+// two MFMAs per tile and no VALU, and both operands keep 11 significant bits
+// where the Q8_0 activations keep 8.
 #include "common.h"
 #include "quant_blocks.h"
 
@@ -21,6 +31,8 @@
 #include <limits.h>
 #include <stdio.h>
 #include <stdlib.h>
+
+#include <type_traits>
 
 #pragma clang fp contract(off)
 
@@ -79,6 +91,19 @@ __global__ __launch_bounds__(256) void q8_panel_k(uint4 *__restrict__ P, uint16_
 #pragma unroll
     for (int j = 0; j < 4; j++) P[g * 4 + j] = make_uint4(w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]);
     D[g] = (uint16_t)u.dh;
+}
+
+// ---- f16 activation panel: P[m][k] = f16_rne(X[m][k]), 8 values per thread ----
+
+__global__ __launch_bounds__(256) void x16_panel_k(uint4 *__restrict__ P, const float *__restrict__ X, int64_t n8)
+{
+    int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n8) return;
+    const float4 a = ((const float4 *)X)[2 * g], b = ((const float4 *)X)[2 * g + 1];
+    const h2 v0 = {(_Float16)a.x, (_Float16)a.y}, v1 = {(_Float16)a.z, (_Float16)a.w};
+    const h2 v2 = {(_Float16)b.x, (_Float16)b.y}, v3 = {(_Float16)b.z, (_Float16)b.w};
+    P[g] = make_uint4(__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
+                      __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3));
 }
 
 // ---- GEMM ------------------------------------------------------------------------
@@ -158,7 +183,9 @@ __device__ __forceinline__ void nib_f16(uint32_t x, uint32_t lo[2], uint32_t hi[
 // writes: blocks kb0 .. kb0+S-1 of the workgroup's rows and columns; block
 // indices past the row's last block read the last block again (in bounds,
 // never used).
-template <int WM, int WN, int S>
+// XF16: f16 activations without scales, weights dequantised to f16 as they
+// are staged (the f16 product); otherwise the Q8_0 product.
+template <int WM, int WN, int S, bool XF16>
 struct PStage {
     using G = PGeo<WM, WN, S>;
     v4u ra[G::NA];
@@ -175,10 +202,12 @@ struct PStage {
             const int m = min(m0 + r, a.M - 1), b = min(kb0 + c / 4, nb - 1);
             ra[i] = *(const v4u *)(a.P + (int64_t)m * K + (int64_t)b * 32 + (c % 4) * 8);
         }
+        if constexpr (!XF16) {
 #pragma unroll
-        for (int i = 0; i < G::ND; i++) {
-            const int v = min(tid + 256 * i, G::TM * S - 1), r = v / S, b = min(kb0 + v % S, nb - 1);
-            rd[i] = a.D[(int64_t)min(m0 + r, a.M - 1) * nb + b];
+            for (int i = 0; i < G::ND; i++) {
+                const int v = min(tid + 256 * i, G::TM * S - 1), r = v / S, b = min(kb0 + v % S, nb - 1);
+                rd[i] = a.D[(int64_t)min(m0 + r, a.M - 1) * nb + b];
+            }
         }
 #pragma unroll
         for (int i = 0; i < G::NB; i++) {
@@ -195,10 +224,12 @@ struct PStage {
             const int p = tid + 256 * i, r = p / (4 * S), c = p % (4 * S);
             *(v4u *)(base + G::A_OFF + (r * G::ROW + c * 8) * 2) = ra[i];
         }
+        if constexpr (!XF16) {
 #pragma unroll
-        for (int i = 0; i < G::ND; i++) {
-            const int v = tid + 256 * i;
-            if (v < G::TM * S) ((uint16_t *)(base + G::AD_OFF))[v] = (uint16_t)rd[i];
+            for (int i = 0; i < G::ND; i++) {
+                const int v = tid + 256 * i;
+                if (v < G::TM * S) ((uint16_t *)(base + G::AD_OFF))[v] = (uint16_t)rd[i];
+            }
         }
 #pragma unroll
         for (int i = 0; i < G::NB; i++) {
@@ -207,12 +238,22 @@ struct PStage {
                 uint32_t lo[8], hi[8];
 #pragma unroll
                 for (int j = 0; j < 4; j++) nib_f16(rb[i].q[j], &lo[2 * j], &hi[2 * j]);
+                if constexpr (XF16) {
+                    // w16 = f16_rne(dw * (q - 8)): one packed f16 multiply per pair
+                    const _Float16 dw = __builtin_bit_cast(_Float16, (uint16_t)rb[i].dh);
+                    const h2 d2 = {dw, dw};
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        lo[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, lo[j]) * d2);
+                        hi[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, hi[j]) * d2);
+                    }
+                }
                 v4u *dst = (v4u *)(base + G::B_OFF + (n * G::ROW + s * 32) * 2);
                 dst[0] = v4u{lo[0], lo[1], lo[2], lo[3]};  // k = 0..7
                 dst[1] = v4u{lo[4], lo[5], lo[6], lo[7]};  // k = 8..15
                 dst[2] = v4u{hi[0], hi[1], hi[2], hi[3]};  // k = 16..23
                 dst[3] = v4u{hi[4], hi[5], hi[6], hi[7]};  // k = 24..31
-                ((uint16_t *)(base + G::BD_OFF))[v] = (uint16_t)rb[i].dh;
+                if constexpr (!XF16) ((uint16_t *)(base + G::BD_OFF))[v] = (uint16_t)rb[i].dh;
             }
         }
     }
@@ -220,7 +261,7 @@ struct PStage {
 
 // D: stages of global loads in flight (1 or 2); OCC: workgroups per CU the
 // register allocation is bounded for.
-template <int WM, int WN, int S, int D, int OCC>
+template <int WM, int WN, int S, int D, int OCC, bool XF16>
 __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
 {
     using G = PGeo<WM, WN, S>;
@@ -280,7 +321,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
                 const _Float16 *pa = lA + r * G::ROW + s * 32 + 8 * h;
                 a0[mi] = *(const v8h *)pa;
                 a1[mi] = *(const v8h *)(pa + 16);
-                as[mi].x = h ? 0u : (uint32_t)lAd[r * S + s];
+                if constexpr (!XF16) as[mi].x = h ? 0u : (uint32_t)lAd[r * S + s];
             }
 #pragma unroll
             for (int ni = 0; ni < WN; ni++) {
@@ -288,12 +329,17 @@ __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
                 const _Float16 *pb = lB + n * G::ROW + s * 32 + 8 * h;
                 b0[ni] = *(const v8h *)pb;
                 b1[ni] = *(const v8h *)(pb + 16);
-                bs[ni].x = h ? 0u : (uint32_t)lBd[n * S + s];
+                if constexpr (!XF16) bs[ni].x = h ? 0u : (uint32_t)lBd[n * S + s];
             }
 #pragma unroll
             for (int mi = 0; mi < WM; mi++)
 #pragma unroll
                 for (int ni = 0; ni < WN; ni++) {
+                    if constexpr (XF16) {
+                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0[mi], b0[ni], acc[mi][ni], 0, 0, 0);
+                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[mi], b1[ni], acc[mi][ni], 0, 0, 0);
+                        continue;
+                    }
                     v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0[mi], b0[ni], zero, 0, 0, 0);
                     I = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[mi], b1[ni], I, 0, 0, 0);
                     const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, as[mi]),
@@ -304,7 +350,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
         }
     };
 
-    PStage<WM, WN, S> pa;
+    PStage<WM, WN, S, XF16> pa;
     pa.fetch(a, w, tid, m0, n0, 0);
     pa.stash(lds, tid);
     if constexpr (D == 1) {
@@ -319,7 +365,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
     } else {
         // two register sets carry stages st+1 and st+2 while stage st is
         // multiplied, so each stage's loads have two stages of products to land
-        PStage<WM, WN, S> pb;
+        PStage<WM, WN, S, XF16> pb;
         if (nst > 1) pa.fetch(a, w, tid, m0, n0, S);
         if (nst > 2) pb.fetch(a, w, tid, m0, n0, 2 * S);
         __syncthreads();
@@ -363,13 +409,13 @@ static int prefill_tn(int M, int N)
     return tiles128 >= cus ? 128 : 64;
 }
 
-template <int WM, int WN, int S, int D, int OCC>
+template <int WM, int WN, int S, int D, int OCC, bool XF16>
 static void launch_prefill(PrefillArgs a)
 {
     using G = PGeo<WM, WN, S>;
     a.ntm = (a.M + G::TM - 1) / G::TM;
     a.tiles = a.ntm * ((a.N + G::TN - 1) / G::TN);
-    auto kern = gemm_q4_0_f16_k<WM, WN, S, D, OCC>;
+    auto kern = gemm_q4_0_f16_k<WM, WN, S, D, OCC, XF16>;
     static bool attr = false;
     if (!attr) {
         HOLO_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS));
@@ -409,20 +455,29 @@ void holo_quantize_act_q8_0(void *dst_blocks, const float *X, int rows, int k)
 }  // extern "C"
 
 // One launch over nmat matrices (holo_gemm_q4_0_q8_0 and its multi-matrix form).
-static void gemm_multi(float *const *Y, const void *const *W, const int *N, int nmat, const void *Xq, int M, int K)
+// Xq (Q8_0 blocks): the Q8_0 product; otherwise X (fp32, 16-byte aligned):
+// the f16 product.
+static void gemm_multi(float *const *Y, const void *const *W, const int *N, int nmat, const void *Xq, const float *X,
+                       int M, int K)
 {
+    const bool xf16 = Xq == nullptr;
     const int nb = K / 32;
     const int64_t nblk = (int64_t)M * nb;
     int ntot = 0;
     for (int i = 0; i < nmat; i++) ntot += N[i];
-    const size_t pbytes = (size_t)nblk * 64, dbytes = ((size_t)nblk * 2 + 255) & ~(size_t)255;
+    const size_t pbytes = (size_t)nblk * 64, dbytes = xf16 ? 0 : ((size_t)nblk * 2 + 255) & ~(size_t)255;
     void *ws = nullptr;
     HOLO_CHECK(hipMallocAsync(&ws, pbytes + dbytes, stream()));
     if (!ws) return;
     uint4 *P = (uint4 *)ws;
-    uint16_t *D = (uint16_t *)((uint8_t *)ws + pbytes);
-    hipLaunchKernelGGL(q8_panel_k, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, stream(), P, D,
-                       (const uint8_t *)Xq, nblk, nblk * 34);
+    uint16_t *D = xf16 ? nullptr : (uint16_t *)((uint8_t *)ws + pbytes);
+    if (xf16) {
+        const int64_t n8 = nblk * 4;
+        hipLaunchKernelGGL(x16_panel_k, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, stream(), P, X, n8);
+    } else {
+        hipLaunchKernelGGL(q8_panel_k, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, stream(), P, D,
+                           (const uint8_t *)Xq, nblk, nblk * 34);
+    }
     HOLO_LAUNCH_CHECK();
     PrefillArgs a = {};
     int acc = 0;
@@ -459,12 +514,17 @@ static void gemm_multi(float *const *Y, const void *const *W, const int *N, int 
                   ? (tm / 64) * 10000 + (tn / 64) * 1000 + st * 100 + d * 10 + o
                   : 0;
     }
-    switch (cfg ? cfg : (prefill_tn(M, ntot) == 128 ? 22212 : 11422)) {
-    case 21222: launch_prefill<2, 1, 2, 2, 2>(a); break;
-    case 11412: launch_prefill<1, 1, 4, 1, 2>(a); break;
-    case 11422: launch_prefill<1, 1, 4, 2, 2>(a); break;
-    default: launch_prefill<2, 2, 2, 1, 2>(a); break;
-    }
+    auto go = [&](auto xfc) {
+        constexpr bool XF = decltype(xfc)::value;
+        switch (cfg ? cfg : (prefill_tn(M, ntot) == 128 ? 22212 : 11422)) {
+        case 21222: launch_prefill<2, 1, 2, 2, 2, XF>(a); break;
+        case 11412: launch_prefill<1, 1, 4, 1, 2, XF>(a); break;
+        case 11422: launch_prefill<1, 1, 4, 2, 2, XF>(a); break;
+        default: launch_prefill<2, 2, 2, 1, 2, XF>(a); break;
+        }
+    };
+    if (xf16) go(std::true_type{});
+    else go(std::false_type{});
     HOLO_CHECK(hipFreeAsync(ws, stream()));
 }
 
@@ -501,7 +561,7 @@ void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, 
         HOLO_REJECT("holo_gemm_q4_0_q8_0: W and Xq must be 4-byte aligned");
         return;
     }
-    gemm_multi(&Y, &W, &N, 1, Xq, M, K);
+    gemm_multi(&Y, &W, &N, 1, Xq, nullptr, M, K);
 }
 
 void holo_gemm_q4_0_q8_0_multi(float *const *Y, const void *const *W, const int *N, int nmat, const void *Xq, int M,
@@ -518,14 +578,57 @@ void holo_gemm_q4_0_q8_0_multi(float *const *Y, const void *const *W, const int 
             return;
         }
     if (!gemm_args_ok(Xq, K)) return;
-    gemm_multi(Y, W, N, nmat, Xq, M, K);
+    gemm_multi(Y, W, N, nmat, Xq, nullptr, M, K);
 }
+
+void holo_gemm_q4_0_f16_multi(float *const *Y, const void *const *W, const int *N, int nmat, const float *X, int M,
+                              int K)
+{
+    if (M <= 0) return;
+    if (!Y || !W || !N || !multi_fits(N, nmat)) {
+        HOLO_REJECT("holo_gemm_q4_0_f16_multi: null array, or not 1..3 matrices whose N are multiples of 128");
+        return;
+    }
+    for (int i = 0; i < nmat; i++)
+        if (!Y[i] || !W[i] || (((uintptr_t)W[i]) & 3u)) {
+            HOLO_REJECT("holo_gemm_q4_0_f16_multi: null or misaligned matrix or output");
+            return;
+        }
+    if (!X || ((uintptr_t)X & 15u) || K % 32 != 0 || K <= 0) {
+        HOLO_REJECT("holo_gemm_q4_0_f16_multi: X null or not 16-byte aligned, or K not a positive multiple of 32");
+        return;
+    }
+    gemm_multi(Y, W, N, nmat, nullptr, X, M, K);
+}
+
+void holo_gemm_q4_0_f16(float *Y, const void *W, const float *X, int M, int N, int K)
+{
+    if (M <= 0 || N <= 0) return;
+    holo_gemm_q4_0_f16_multi(&Y, &W, &N, 1, X, M, K);
+}
+
+static int g_prefill_mode = HOLO_PREFILL_F16;
+
+void holo_prefill_set_mode(int mode)
+{
+    if (mode != HOLO_PREFILL_F16 && mode != HOLO_PREFILL_Q8_0) {
+        HOLO_REJECT("holo_prefill_set_mode: HOLO_PREFILL_F16 or HOLO_PREFILL_Q8_0");
+        return;
+    }
+    g_prefill_mode = mode;
+}
+
+int holo_prefill_get_mode(void) { return g_prefill_mode; }
 
 void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int N, int K, void *scratch_q8)
 {
     if (M <= 0 || N <= 0) return;
     if (M < 64) {
         for (int m = 0; m < M; m++) cuda_matmul_q4_0(Y + (int64_t)m * N, W, X + (int64_t)m * K, N, K);
+        return;
+    }
+    if (g_prefill_mode == HOLO_PREFILL_F16 && !((uintptr_t)X & 15u) && K % 32 == 0) {
+        holo_gemm_q4_0_f16(Y, W, X, M, N, K);
         return;
     }
     void *q = scratch_q8;
@@ -546,6 +649,10 @@ void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const i
     }
     if (M < 64) {
         for (int i = 0; i < nmat; i++) holo_matmul_batch_q4_0(Y[i], W[i], X, M, N[i], K, scratch_q8);
+        return;
+    }
+    if (g_prefill_mode == HOLO_PREFILL_F16 && !((uintptr_t)X & 15u) && K % 32 == 0) {
+        holo_gemm_q4_0_f16_multi(Y, W, N, nmat, X, M, K);
         return;
     }
     void *q = scratch_q8;

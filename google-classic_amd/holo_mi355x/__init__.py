@@ -138,6 +138,10 @@ _SIGS = {
     "holo_matmul_batch_q4_0": (None, [_P, _P, _P, _I, _I, _I, _P]),
     "holo_gemm_q4_0_q8_0_multi": (None, [_P, _P, _P, _I, _P, _I, _I]),
     "holo_matmul_batch_q4_0_multi": (None, [_P, _P, _P, _I, _P, _I, _I, _P]),
+    "holo_gemm_q4_0_f16": (None, [_P, _P, _P, _I, _I, _I]),
+    "holo_gemm_q4_0_f16_multi": (None, [_P, _P, _P, _I, _P, _I, _I]),
+    "holo_prefill_set_mode": (None, [_I]),
+    "holo_prefill_get_mode": (_I, []),
     # GGUF files (include/holo_gguf.h)
     "holo_gguf_open": (_P, [C.c_char_p]),
     "holo_gguf_close": (None, [_P]),

@@ -141,8 +141,9 @@ void holo_batched_ffn_gate_up(float *out, const void *W1, const void *W3,
  * workspace (hipMallocAsync, M*K*2 + M*(K/32)*2 bytes) for the call.       */
 void holo_quantize_act_q8_0(void *dst_blocks, const float *X, int rows, int k);
 void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, int K);
-/* Y[M][N] = X[M][K] . W[N][K]^T for W in Q4_0: M >= 64 quantises X and runs
- * the MFMA GEMM above; M < 64 runs M fp32-activation GEMVs.                 */
+/* Y[M][N] = X[M][K] . W[N][K]^T for W in Q4_0: M >= 64 runs the f16 product
+ * below (or, in HOLO_PREFILL_Q8_0 mode, quantises X and runs the Q8_0 product
+ * above); M < 64 runs M fp32-activation GEMVs.                               */
 void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int N, int K,
                             void *scratch_q8);
 /* The same over nmat = 1..3 Q4_0 matrices that multiply the same X in one
@@ -154,6 +155,23 @@ void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int 
  * holo_batched_qkv / holo_batched_ffn_gate_up.                              */
 void holo_gemm_q4_0_q8_0_multi(float *const *Y, const void *const *W, const int *N, int nmat,
                                const void *Xq, int M, int K);
+/* The f16 product: no activation quantisation.  x16 = f16_rne(x), w16 =
+ * f16_rne(f16(dw) * (q - 8)), Y = sum_k x16 * w16 accumulated in fp32 on the
+ * matrix cores (order of the hardware: within the fp32 accumulation bound of
+ * the float64 sum of the rounded operands, not bit-reproducible on the CPU).
+ * X[M][K] fp32, 16-byte aligned, K a multiple of 32; a stream-ordered
+ * workspace of M*K*2 bytes.  No reference counterpart (build-defined, like
+ * the Q8_0 product).                                                       */
+void holo_gemm_q4_0_f16(float *Y, const void *W, const float *X, int M, int N, int K);
+void holo_gemm_q4_0_f16_multi(float *const *Y, const void *const *W, const int *N, int nmat,
+                              const float *X, int M, int K);
+/* Which product holo_matmul_batch_q4_0(_multi) runs for M >= 64: the f16
+ * product (default; also taken only when X is 16-byte aligned) or the Q8_0
+ * product above.                                                            */
+#define HOLO_PREFILL_F16 0
+#define HOLO_PREFILL_Q8_0 1
+void holo_prefill_set_mode(int mode);
+int holo_prefill_get_mode(void);
 void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const int *N, int nmat,
                                   const float *X, int M, int K, void *scratch_q8);
 

@@ -27,6 +27,10 @@
  *                     independent numpy integer restatement and, for the
  *                     block-order fused rescale, by an exact rational
  *                     evaluation of each fmaf step.
+ *   gemm_q4_0_f16     build-defined (f16 prefill product): pinned by a closed
+ *                     form on inputs exact in f16, by the reference-pinned
+ *                     oracle_matmul_q4_0 within the f16 rounding bound, and
+ *                     by numpy's own float16 rounding of both operands.
  */
 #include <math.h>
 #include <stdint.h>
@@ -403,6 +407,39 @@ void oracle_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N
                 acc = fmaf((float)I, s, acc);
             }
             Y[(size_t)m * N + n] = acc;
+        }
+    }
+}
+
+/* Batched product over f16 activations and f16-dequantised Q4_0 weights:
+ *   Y[m][n] = sum_k x16[m][k] * w16[n][k]
+ *   x16 = f16_rne(x),  w16 = f16_rne(f16(dw[n,b]) * (q[n][k] - 8))
+ * The products of two f16 values and their sum over k are exact in double up
+ * to its own rounding (at these K far below the fp32 accumulation error the
+ * GPU is held to), so Y is the truth of the rounded operands.  A[m][n] =
+ * sum_k |x16 * w16| scales that error bound.                                */
+void oracle_gemm_q4_0_f16(double *Y, double *A, const float *X, const void *W, int M, int N, int K)
+{
+    const oq4_0 *w = (const oq4_0 *)W;
+    int nb = K / QK32;
+#pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++) {
+        for (int n = 0; n < N; n++) {
+            double acc = 0.0, aa = 0.0;
+            for (int b = 0; b < nb; b++) {
+                const oq4_0 *wb = w + (size_t)n * nb + b;
+                const float dw = oracle_f16_to_f32(wb->d);
+                for (int j = 0; j < 32; j++) {
+                    const int q = j < 16 ? (wb->qs[j] & 0xF) : (wb->qs[j - 16] >> 4);
+                    const float wq = oracle_f16_to_f32(oracle_f32_to_f16_rne(dw * (float)(q - 8)));
+                    const float xq = oracle_f16_to_f32(oracle_f32_to_f16_rne(X[(size_t)m * K + (size_t)b * 32 + j]));
+                    const double p = (double)wq * (double)xq;
+                    acc += p;
+                    aa += fabs(p);
+                }
+            }
+            Y[(size_t)m * N + n] = acc;
+            if (A) A[(size_t)m * N + n] = aa;
         }
     }
 }

@@ -53,6 +53,7 @@ class Oracle:
         l.oracle_silu_mul.argtypes = [_P, _P, _P, _I]
         l.oracle_quantize_act_q8_0.argtypes = [_P, _P, _I, _I]
         l.oracle_gemm_q4_0_q8_0.argtypes = [_P, _P, _P, _I, _I, _I]
+        l.oracle_gemm_q4_0_f16.argtypes = [_P, _P, _P, _P, _I, _I, _I]
         self.l = l
 
     _DQ = {TYPE_Q8_0: "oracle_dequant_q8_0", TYPE_Q4_0: "oracle_dequant_q4_0",
@@ -114,6 +115,15 @@ class Oracle:
         Y = np.empty((M, N), dtype=np.float32)
         self.l.oracle_gemm_q4_0_q8_0(Y.ctypes.data, W.ctypes.data, Xq.ctypes.data, M, N, K)
         return Y
+
+    def gemm_q4_0_f16(self, W: np.ndarray, X: np.ndarray, M: int, N: int, K: int):
+        """(Y, A): the float64 truth of the f16-rounded operands and sum |x16 w16|."""
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        W = np.ascontiguousarray(W)
+        Y = np.empty((M, N), dtype=np.float64)
+        A = np.empty((M, N), dtype=np.float64)
+        self.l.oracle_gemm_q4_0_f16(Y.ctypes.data, A.ctypes.data, X.ctypes.data, W.ctypes.data, M, N, K)
+        return Y, A
 
 
 class RefBuild:

@@ -9,13 +9,14 @@
    KV caches.
    - HOLO_FORWARD_EXACT (fp32-activation GEMVs for every matrix): within the
      1e-3 normwise bar of every dot product of the path.
-   - Default (the Q4_0 matrices of an 80-row prompt on the MFMA GEMM over
-     Q8_0-quantised activations): within 6e-2 normwise.  Quantising an
-     activation block to 8 bits moves each element by up to amax/254 (about
-     0.5% of a Gaussian block's rms); through the 2 layers' 14 matrices the
-     measured effect is 1.6e-2 on the logits and up to 2.9e-2 on the caches,
-     and the bound is twice the largest.  The GEMM itself is bit-exact to its
-     specification (tests/test_gpu_ops.py).
+   - Default (the Q4_0 matrices of an 80-row prompt on the f16 MFMA GEMM:
+     activations and dequantised weights rounded to f16): within 5e-3
+     normwise.  Each f16 rounding moves an operand by up to 2^-11 of itself;
+     through the 2 layers' 14 matrices the measured effect is 1.2e-3 on the
+     logits and up to 1.8e-3 on the caches, and the bound is about 2.7 times
+     the largest.  (The Q8_0-activation product measured 1.6e-2 and 2.9e-2
+     here.)  The GEMM itself is held to its specification in
+     tests/test_gpu_ops.py.
 3. The whole prompt in one pass equals the token-by-token decode loop.
 """
 import ctypes as C
@@ -190,7 +191,7 @@ def model(holo, tmp_path_factory):
 def test_forward_matches_reference(model, flags):
     z = np.load(GOLDEN)
     tokens = z["tokens"]
-    tol = 1e-3 if flags else 6e-2
+    tol = 1e-3 if flags else 5e-3
     for n in (7, 80):
         print(f"case forward prompt {n} flags {flags}", flush=True)
         model.reset()

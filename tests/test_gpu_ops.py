@@ -128,31 +128,67 @@ def test_gemm_q4_0_q8_0_bit_exact(holo, synth, oracle, M, N, K):
     assert np.array_equal(got[rows].view(np.uint32), want.view(np.uint32))
 
 
+def f16_bound(K, A):
+    """fp32 accumulation on the matrix cores: one rounding per 16-product
+    instruction step and per stage, so |y - truth| <= 2 (K/16 + 2) 2^-24 A."""
+    return 2.0 * (K / 16 + 2) * 2.0 ** -24 * A
+
+
 def test_matmul_batch_dispatch(holo, synth, oracle):
-    """M >= 64: quantise + MFMA GEMM; M < 64: one fp32 GEMV per row."""
+    """M >= 64: the f16 product by default, the Q8_0 product in Q8_0 mode; M < 64:
+    one fp32 GEMV per row."""
     N, K = 256, 512
     W = synth.blocks(Q4_0, N, K, seed=1)
     dW = up(holo, W)
-    for M in (8, 64):
+    lib = holo.lib()
+    assert lib.holo_prefill_get_mode() == 0
+    for M, mode in ((8, 0), (64, 0), (64, 1)):
+        lib.holo_prefill_set_mode(mode)
         X = synth.normal(M * K, seed=M).reshape(M, K)
         dX, dY = up(holo, X), holo.DeviceBuffer(4 * M * N)
-        holo.lib().holo_matmul_batch_q4_0(dY.ptr, dW.ptr, dX.ptr, M, N, K, None)
-        holo.lib().cuda_sync()
+        lib.holo_matmul_batch_q4_0(dY.ptr, dW.ptr, dX.ptr, M, N, K, None)
+        lib.cuda_sync()
+        lib.holo_prefill_set_mode(0)
         holo.check("batch")
         got = down(dY, M * N).reshape(M, N)
         if M < 64:
             want = np.stack([oracle.matmul(Q4_0, W, X[m], N, K) for m in range(M)])
             assert normwise_err(got, want) <= 1e-3
+        elif mode == 0:
+            Y, A = oracle.gemm_q4_0_f16(W, X, M, N, K)
+            assert np.all(np.abs(got - Y) <= f16_bound(K, A))
         else:
             want = oracle.gemm_q4_0_q8_0(W, oracle.quantize_act_q8_0(X), M, N, K)
             assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 128, 256), (77, 150, 4096), (512, 4096, 4096), (512, 11008, 4096),
+                                   (512, 4096, 11008)], ids=str)
+def test_gemm_q4_0_f16(holo, synth, oracle, M, N, K):
+    """The f16 product against the float64 truth of the f16-rounded operands
+    (oracle_gemm_q4_0_f16), elementwise within the fp32 accumulation bound, and
+    against the reference's fp32 GEMV of the same rows within 1e-3."""
+    print(f"case gemm f16 {M}x{N}x{K}", flush=True)
+    W = synth.blocks(Q4_0, N, K, seed=M + N + 1)
+    X = synth.normal(M * K, seed=K + 1).reshape(M, K)
+    dW, dX, dY = up(holo, W), up(holo, X), holo.DeviceBuffer(4 * M * N)
+    holo.lib().holo_gemm_q4_0_f16(dY.ptr, dW.ptr, dX.ptr, M, N, K)
+    holo.lib().cuda_sync()
+    holo.check("gemm f16")
+    got = down(dY, M * N).reshape(M, N)
+    rows = min(M, 16)  # the oracle on a row subset at the full sizes (CPU time)
+    Y, A = oracle.gemm_q4_0_f16(W, X[:rows], rows, N, K)
+    assert np.all(np.abs(got[:rows] - Y) <= f16_bound(K, A))
+    ref = np.stack([oracle.matmul(Q4_0, W, X[m], N, K) for m in range(min(rows, 4))])
+    assert normwise_err(got[:len(ref)], ref) <= 1e-3
 
 
 @pytest.mark.parametrize("M,Ns,K", [(100, (256, 128, 128), 512), (512, (4096, 1024, 1024), 4096),
                                     (64, (384, 384), 256), (77, (150,), 1024)], ids=str)
 def test_gemm_multi_matches_single(holo, synth, oracle, M, Ns, K):
     """Several matrices over the same activations in one launch: every output
-    bit-identical to its single-matrix launch and to the oracle."""
+    bit-identical to its single-matrix launch (Q8_0 and f16 products), and the
+    Q8_0 product to the oracle."""
     import ctypes as C
     print(f"case gemm multi {M}x{Ns}x{K}", flush=True)
     lib = holo.lib()
@@ -169,7 +205,9 @@ def test_gemm_multi_matches_single(holo, synth, oracle, M, Ns, K):
     Np = (C.c_int * k)(*Ns)
     lib.holo_gemm_q4_0_q8_0_multi(Yp, Wp, Np, k, dXq.ptr, M, K)
     Yb = (C.c_void_p * k)(*[d.ptr for d in dYb])
-    lib.holo_matmul_batch_q4_0_multi(Yb, Wp, Np, k, dX.ptr, M, K, None)
+    lib.holo_matmul_batch_q4_0_multi(Yb, Wp, Np, k, dX.ptr, M, K, None)  # the f16 product (default mode)
+    dYf = [holo.DeviceBuffer(4 * M * n) for n in Ns]
+    lib.holo_gemm_q4_0_f16_multi((C.c_void_p * k)(*[d.ptr for d in dYf]), Wp, Np, k, dX.ptr, M, K)
     lib.cuda_sync()
     holo.check("gemm multi")
     for i, n in enumerate(Ns):
@@ -178,7 +216,12 @@ def test_gemm_multi_matches_single(holo, synth, oracle, M, Ns, K):
         lib.cuda_sync()
         got = down(dYs[i], M * n)
         assert np.array_equal(got.view(np.uint32), down(dS, M * n).view(np.uint32)), i
-        assert np.array_equal(down(dYb[i], M * n).view(np.uint32), got.view(np.uint32)), i
+        gf = down(dYf[i], M * n)
+        assert np.array_equal(down(dYb[i], M * n).view(np.uint32), gf.view(np.uint32)), i
+        dF = holo.DeviceBuffer(4 * M * n)
+        lib.holo_gemm_q4_0_f16(dF.ptr, dWs[i].ptr, dX.ptr, M, n, K)
+        lib.cuda_sync()
+        assert np.array_equal(down(dF, M * n).view(np.uint32), gf.view(np.uint32)), i
         rows = min(M, 16)
         want = oracle.gemm_q4_0_q8_0(Ws[i], Xq.reshape(M, -1)[:rows].copy().reshape(-1), rows, n, K)
         assert np.array_equal(got.reshape(M, n)[:rows].view(np.uint32), want.view(np.uint32)), i

@@ -306,3 +306,51 @@ def test_silu_mul_vs_numpy(oracle, synth):
     u = synth.normal(1000, seed=2)
     want = (g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))) * u
     assert normwise_err(oracle.silu_mul(g, u), want) < 1e-6
+
+
+# ---- the f16 prefill product ----------------------------------------------------------------
+
+def test_gemm_q4_0_f16_closed_form(oracle):
+    """Inputs exact in f16: scale 1 and nibble 9 make every weight 1, so each
+    output is the row's plain sum; nibble 0 with scale 2 makes every weight -16."""
+    M, N, K = 3, 2, 64
+    W = np.zeros((N, K // 32, 18), np.uint8)
+    W[0, :, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    W[0, :, 2:] = 0x99
+    W[1, :, 0:2] = np.frombuffer(np.float16(2.0).tobytes(), np.uint8)
+    W[1, :, 2:] = 0x00
+    X = (np.arange(M * K, dtype=np.float32).reshape(M, K) % 7 - 3) * 0.25  # exact in f16
+    Y, A = oracle.gemm_q4_0_f16(W.reshape(-1), X, M, N, K)
+    assert np.array_equal(Y[:, 0], X.sum(1).astype(np.float64))
+    assert np.array_equal(Y[:, 1], -16.0 * X.sum(1).astype(np.float64))
+    assert np.array_equal(A[:, 0], np.abs(X).sum(1).astype(np.float64))
+
+
+def test_gemm_q4_0_f16_vs_reference_matmul(oracle, synth):
+    """Against the reference-pinned fp32 GEMV of the same rows: the two differ
+    only by the f16 rounding of each activation and weight (relative 2^-11
+    each) and the fp32 GEMV's own rounding, so |Y - y| <= 2^-10 A (+ fp32)."""
+    M, N, K = 5, 48, 1024
+    W = synth.blocks(Q4_0, N, K, seed=71)
+    X = synth.normal(M * K, seed=72).reshape(M, K)
+    Y, A = oracle.gemm_q4_0_f16(W, X, M, N, K)
+    for m in range(M):
+        y = oracle.matmul(Q4_0, W, X[m], N, K).astype(np.float64)
+        assert np.all(np.abs(Y[m] - y) <= 2.0 ** -10 * A[m] + 1e-6 * A[m])
+
+
+def test_gemm_q4_0_f16_vs_numpy_float16(oracle, synth):
+    """numpy's float16 conversion (its own round-to-nearest-even) of both
+    operands, summed in float64: equal to within float64 rounding."""
+    M, N, K = 4, 16, 256
+    W = synth.blocks(Q4_0, N, K, seed=81)
+    X = synth.normal(M * K, seed=82).reshape(M, K)
+    Y, _ = oracle.gemm_q4_0_f16(W, X, M, N, K)
+    blk = W.reshape(N, K // 32, 18)
+    d = blk[:, :, :2].copy().view(np.float16)[:, :, 0].astype(np.float32)
+    qs = blk[:, :, 2:]
+    q = np.concatenate([qs & 0xF, qs >> 4], axis=2).astype(np.float32) - 8.0   # k = 0..15 low, 16..31 high nibbles
+    w16 = (d[:, :, None] * q).astype(np.float16).astype(np.float64).reshape(N, K)
+    x16 = X.astype(np.float16).astype(np.float64)
+    want = x16 @ w16.T
+    assert np.all(np.abs(Y - want) <= 1e-12 * (np.abs(x16) @ np.abs(w16).T))
