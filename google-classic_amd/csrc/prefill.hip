@@ -499,13 +499,16 @@ static void gemm_multi(float *const *Y, const void *const *W, const int *N, int 
     a.N = ntot;
     a.nb = nb;
     // Variant per shape (measured at the prompt-forward shapes, M = 512):
-    // 128 x 128 tiles, 2-block stages, one stage of loads in flight, when
-    // there are at least as many such tiles as CUs (q/k/v, gate/up: 137 and
-    // 254 us); otherwise 64 x 64 tiles, 4-block stages, two in flight (o,
-    // down: 58 and 142 us, against 90 and 223 us on 128 x 64 tiles).
-    // HOLO_PREFILL_CFG=<tile rows>,<tile columns>,<stage blocks>,<stages in
-    // flight>,<workgroups per CU> selects one of the compiled variants
-    // (128,128,2,1,2  128,64,2,2,2  64,64,4,1,2  64,64,4,2,2) instead.
+    // 128 x 128 tiles with 2-block stages when there are at least as many
+    // such tiles as CUs (q/k/v, gate/up), with two stages of loads in flight
+    // for the f16 product (95 and 181 us) and one for the Q8_0 product, whose
+    // extra scale registers leave no room for a second (137 and 254 us);
+    // otherwise 64 x 64 tiles, 4-block stages, two in flight (o, down: f16
+    // 47 and 113 us, Q8_0 58 and 142 us, against 90 and 223 us on the 128 x 64
+    // tile).  HOLO_PREFILL_CFG=<tile rows>,<tile columns>,<stage blocks>,
+    // <stages in flight>,<workgroups per CU> selects one of the compiled
+    // variants (128,128,2,1,2  128,128,2,2,2 (f16 only)  128,64,2,2,2
+    // 64,64,4,1,2  64,64,4,2,2) instead.
     static int cfg = -1;
     if (cfg < 0) {
         const char *e = getenv("HOLO_PREFILL_CFG");
@@ -516,10 +519,15 @@ static void gemm_multi(float *const *Y, const void *const *W, const int *N, int 
     }
     auto go = [&](auto xfc) {
         constexpr bool XF = decltype(xfc)::value;
-        switch (cfg ? cfg : (prefill_tn(M, ntot) == 128 ? 22212 : 11422)) {
+        const int def = prefill_tn(M, ntot) == 128 ? (XF ? 22222 : 22212) : 11422;
+        switch (cfg ? cfg : def) {
         case 21222: launch_prefill<2, 1, 2, 2, 2, XF>(a); break;
         case 11412: launch_prefill<1, 1, 4, 1, 2, XF>(a); break;
         case 11422: launch_prefill<1, 1, 4, 2, 2, XF>(a); break;
+        case 22222:  // the Q8_0 product has no registers for a second stage: one
+            if constexpr (XF) launch_prefill<2, 2, 2, 2, 2, true>(a);
+            else launch_prefill<2, 2, 2, 1, 2, false>(a);
+            break;
         default: launch_prefill<2, 2, 2, 1, 2, XF>(a); break;
         }
     };
