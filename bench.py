@@ -61,7 +61,6 @@ import holo_mi355x as holo  # noqa: E402
 from holo_mi355x import synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
-INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
 F16_PEAK_TFLOPS = 2500.0   # MI355X dense f16 MFMA
 Q4_0, Q8_0, Q4_K = holo.TYPE_Q4_0, holo.TYPE_Q8_0, holo.TYPE_Q4_K
 BASE_SEED = 20251201
@@ -374,10 +373,14 @@ def decode_attention(lib, kv_lens=(512, 2048, 4096), reps=50):
 
 
 def prefill_tops(lib, reps=10):
-    """Config 4: holo_gemm_q4_0_q8_0 at M = 512.  gemm_us is the call (the
-    f16 activation panel pass, the GEMM kernel and the stream-ordered
-    workspace), kernel_us the GEMM kernel alone (holo_time_next_launch).  The
-    block dots run on v_mfma_f32_32x32x16_f16; useful work is 2*M*N*K."""
+    """Config 4 at M = 512, both batched products:
+      q8_0: holo_gemm_q4_0_q8_0 (Q8_0 activations, bit-exact specification),
+      f16:  holo_gemm_q4_0_f16 (f16 activations and dequantised weights; the
+            default of holo_matmul_batch_q4_0 and the prompt forward).
+    gemm_us is the call (the activation panel pass, the GEMM kernel and the
+    stream-ordered workspace), kernel_us the GEMM kernel alone
+    (holo_time_next_launch).  Both run on v_mfma_f32_32x32x16_f16; useful work
+    is 2*M*N*K."""
     M = 512
     out = {}
     for name, (N, K) in (("11008x4096", (FFN, DIM)), ("4096x11008", (DIM, FFN))):
@@ -386,30 +389,32 @@ def prefill_tops(lib, reps=10):
         Xq = holo.DeviceBuffer(M * (K // 32) * 34)
         Y = holo.DeviceBuffer(4 * M * N)
         lib.holo_quantize_act_q8_0(Xq.ptr, X.ptr, M, K)
-        lib.holo_gemm_q4_0_q8_0(Y.ptr, W.ptr, Xq.ptr, M, N, K)
-        lib.cuda_sync()
         ev = holo.Events()
-        ev.start()
-        for _ in range(reps):
-            lib.holo_gemm_q4_0_q8_0(Y.ptr, W.ptr, Xq.ptr, M, N, K)
-        ms = ev.stop() / reps
-        kernel = []
-        for _ in range(reps):
-            lib.holo_time_next_launch(ev.a, ev.b)
-            lib.holo_gemm_q4_0_q8_0(Y.ptr, W.ptr, Xq.ptr, M, N, K)
+        calls = {"q8_0": lambda: lib.holo_gemm_q4_0_q8_0(Y.ptr, W.ptr, Xq.ptr, M, N, K),
+                 "f16": lambda: lib.holo_gemm_q4_0_f16(Y.ptr, W.ptr, X.ptr, M, N, K)}
+        out[name] = {}
+        for prod, call in calls.items():
+            call()
             lib.cuda_sync()
-            kernel.append(float(lib.holo_event_elapsed_ms(ev.a, ev.b)))
-        kms = statistics.median(kernel)
+            ev.start()
+            for _ in range(reps):
+                call()
+            ms = ev.stop() / reps
+            kernel = []
+            for _ in range(reps):
+                lib.holo_time_next_launch(ev.a, ev.b)
+                call()
+                lib.cuda_sync()
+                kernel.append(float(lib.holo_event_elapsed_ms(ev.a, ev.b)))
+            kms = statistics.median(kernel)
+            tops = 2.0 * M * N * K / (kms * 1e-3) / 1e12
+            out[name][prod] = {"gemm_us": round(ms * 1e3, 2), "kernel_us": round(kms * 1e3, 2),
+                               "tops": round(tops, 1), "frac_of_f16_peak": round(tops / F16_PEAK_TFLOPS, 4)}
         ev.start()
         for _ in range(reps):
             lib.holo_quantize_act_q8_0(Xq.ptr, X.ptr, M, K)
-        qms = ev.stop() / reps
+        out[name]["q8_0"]["quantize_us"] = round(ev.stop() / reps * 1e3, 2)
         ev.close()
-        ops = 2.0 * M * N * K
-        tops = ops / (kms * 1e-3) / 1e12
-        out[name] = {"gemm_us": round(ms * 1e3, 2), "kernel_us": round(kms * 1e3, 2),
-                     "tops": round(tops, 1), "frac_of_f16_peak": round(tops / F16_PEAK_TFLOPS, 4),
-                     "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4), "quantize_us": round(qms * 1e3, 2)}
     holo.check("prefill")
     return out
 
