@@ -261,14 +261,28 @@ def single_gemv_gbs(lib, qtype, sets, steps):
 
 # ---- config 5: full decode step ----------------------------------------------------------
 
-def decode_step(lib, layers, head, A, ones, matmuls_only):
+def decode_step(lib, layers, head, A, ones, matmuls_only, fused=False):
     """Synthetic Llama-2-7B decode step at position 0: RoPE is the identity and
     attention over one cached position returns v, so per layer
       xb = rms(x); q,k,v = W.xb; x += Wo.v; xb = rms(x); h = silu(W1.xb)*(W3.xb);
       x += W2.h
     and after the layers logits = Wout.rms(x).  `matmuls_only` issues the same
-    GEMVs on the same buffers without the norms and residual adds."""
+    GEMVs on the same buffers without the norms and residual adds.  `fused`
+    runs the same step with the norms folded into the q/k/v and gate/up GEMVs
+    and the adds into the o and down GEMVs (4 launches per layer, not 8)."""
     x, xb = A["x4096"], A["y4096"]
+    if fused:
+        for L in layers:
+            b = L.buf
+            lib.holo_batched_qkv_norm(A["q"], A["k"], A["v"], b["q"].ptr, b["k"].ptr, b["v"].ptr, x, ones.ptr, 1e-5,
+                                      xb, DIM, DIM, DIM, Q4_0)
+            lib.holo_matmul_add(x, b["o"].ptr, A["v"], x, DIM, DIM, Q4_0)
+            lib.holo_batched_ffn_gate_up_norm(A["h"], b["gate"].ptr, b["up"].ptr, x, ones.ptr, 1e-5, xb, FFN, DIM,
+                                              Q4_0)
+            lib.holo_matmul_add(x, b["down"].ptr, A["h"], x, DIM, FFN, Q4_0)
+        lib.cuda_rms_norm(xb, x, ones.ptr, DIM, 1e-5)
+        lib.cuda_matmul_q8_0(A["y32000"], head.ptr, xb, VOCAB, DIM)
+        return
     for L in layers:
         b = L.buf
         if not matmuls_only:
@@ -559,18 +573,23 @@ def main():
             ones = holo.DeviceBuffer.from_array(np.ones(DIM, np.float32))
             full = capture(lib, lambda: decode_step(lib, layers[:32], head, A, ones, False))
             mm = capture(lib, lambda: decode_step(lib, layers[:32], head, A, ones, True))
+            fz = capture(lib, lambda: decode_step(lib, layers[:32], head, A, ones, False, True))
             reps = max(3, a.steps // 16)
-            full_ms = time_graphs(lib, [full], reps, 2) / reps
+            unfused_ms = time_graphs(lib, [full], reps, 2) / reps
             mm_ms = time_graphs(lib, [mm], reps, 2) / reps
+            full_ms = time_graphs(lib, [fz], reps, 2) / reps
+            lib.holo_graph_destroy(fz)
             step_bytes = 32 * bytes_step + holo.row_bytes(Q8_0, DIM) * VOCAB
             extra["config5_decode_step"] = {
                 "matmuls_ms": round(mm_ms, 4), "end_to_end_ms": round(full_ms, 4),
+                "end_to_end_unfused_ms": round(unfused_ms, 4),
                 "weight_bytes": step_bytes, "matmul_weight_gbs": round(step_bytes / (mm_ms * 1e-3) / 1e9, 1),
                 "end_to_end_weight_gbs": round(step_bytes / (full_ms * 1e-3) / 1e9, 1),
-                "launches": {"matmuls": 32 * 4 + 1, "end_to_end": 32 * 8 + 2}}
+                "launches": {"matmuls": 32 * 4 + 1, "end_to_end": 32 * 4 + 2, "end_to_end_unfused": 32 * 8 + 2}}
             lib.holo_graph_destroy(full)
             lib.holo_graph_destroy(mm)
-            log(f"config 5 decode step: matmuls {mm_ms:.3f} ms, end-to-end {full_ms:.3f} ms")
+            log(f"config 5 decode step: matmuls {mm_ms:.3f} ms, end-to-end {full_ms:.3f} ms "
+                f"(unfused {unfused_ms:.3f} ms)")
             extra["config4_prompt_forward_512"] = prompt_forward(lib, layers, head, ones, full_ms)
             log(f"config 4 prompt forward: {extra['config4_prompt_forward_512']}")
             del head

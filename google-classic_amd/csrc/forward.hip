@@ -188,20 +188,43 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
     for (int l = 0; l < m->n_layers; l++) {
         const holo_llama_layer_t &L = m->layers[l];
         float *kc = m->key_cache + l * layer_cache, *vc = m->value_cache + l * layer_cache;
+        // One row (a decode step): the norms run inside the q/k/v and gate/up
+        // GEMVs and the residual adds inside the o and down GEMVs.
+        const bool one = n == 1;
+        const bool qkv1 = one && L.attn_norm && fused_gemv_type(L.wq_type) && L.wk_type == L.wq_type &&
+                          L.wv_type == L.wq_type;
+        const bool ffn1 = one && L.ffn_norm && fused_gemv_type(L.w1_type) && L.w3_type == L.w1_type;
         // attention block
-        norm_or_copy(xb, x, L.attn_norm, n, dim, m->rms_eps);
-        matmul_qkv(q, k, v, L, xb, n, q_dim, kv_dim, dim, exact);
+        if (qkv1) {
+            holo_batched_qkv_norm(q, k, v, L.wq, L.wk, L.wv, x, L.attn_norm, m->rms_eps, xb, q_dim, kv_dim, dim,
+                                  L.wq_type);
+        } else {
+            norm_or_copy(xb, x, L.attn_norm, n, dim, m->rms_eps);
+            matmul_qkv(q, k, v, L, xb, n, q_dim, kv_dim, dim, exact);
+        }
         holo_rope_rows(q, k, n, pos0, hd, m->n_heads, m->n_kv_heads, m->rope_base);
         HOLO_CHECK(hipMemcpyAsync(kc + (int64_t)pos0 * kv_dim, k, rowsz * kv_dim, hipMemcpyDeviceToDevice, stream()));
         HOLO_CHECK(hipMemcpyAsync(vc + (int64_t)pos0 * kv_dim, v, rowsz * kv_dim, hipMemcpyDeviceToDevice, stream()));
         holo_attention_prefill(att, q, kc, vc, n, pos0, hd, m->n_heads, m->n_kv_heads);
-        holo_matmul_rows(xb, L.wo, att, n, dim, q_dim, L.wo_type, exact);
-        cuda_vec_add(x, x, xb, n * dim);
+        if (one && fused_gemv_type(L.wo_type)) {
+            holo_matmul_add(x, L.wo, att, x, dim, q_dim, L.wo_type);
+        } else {
+            holo_matmul_rows(xb, L.wo, att, n, dim, q_dim, L.wo_type, exact);
+            cuda_vec_add(x, x, xb, n * dim);
+        }
         // FFN block
-        norm_or_copy(xb, x, L.ffn_norm, n, dim, m->rms_eps);
-        matmul_gate_up(hb, hb2, L, xb, n, ffn, dim, exact);
-        holo_matmul_rows(xb, L.w2, hb, n, dim, ffn, L.w2_type, exact);
-        cuda_vec_add(x, x, xb, n * dim);
+        if (ffn1) {
+            holo_batched_ffn_gate_up_norm(hb, L.w1, L.w3, x, L.ffn_norm, m->rms_eps, xb, ffn, dim, L.w1_type);
+        } else {
+            norm_or_copy(xb, x, L.ffn_norm, n, dim, m->rms_eps);
+            matmul_gate_up(hb, hb2, L, xb, n, ffn, dim, exact);
+        }
+        if (one && fused_gemv_type(L.w2_type)) {
+            holo_matmul_add(x, L.w2, hb, x, dim, ffn, L.w2_type);
+        } else {
+            holo_matmul_rows(xb, L.w2, hb, n, dim, ffn, L.w2_type, exact);
+            cuda_vec_add(x, x, xb, n * dim);
+        }
     }
     // the last token: final norm and the output head
     float *xl = x + (int64_t)(n - 1) * dim;

@@ -480,6 +480,7 @@ struct GemvArgs {
     int groups;             // G: R-row groups per tile
     int x_lds_bytes;        // staged x, then the partial-sum buffers
     int64_t row_bytes;
+    const float *r;         // residual: y = r + W.x (one matrix, PLAIN); may alias y
 };
 
 template <int FMT, int XM, int R, int P, int MODE>
@@ -577,7 +578,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs args)
                     for (int k = 0; k < nsegs; k++) s1 += pt[(TR + rr) * nsegs + k];
                     args.y[0][row0 + rr] = silu(s0) * s1;
                 } else {
-                    args.y[mseg][row0 + rr] = s0;
+                    args.y[mseg][row0 + rr] = args.r ? args.r[row0 + rr] + s0 : s0;
                 }
             }
         }
@@ -870,6 +871,9 @@ struct MfmaArgs {
     int nsegs;             // G: 16-unit segments per row
     int x_lds_bytes;       // staged activations (planes, then {dx, c} pairs)
     int64_t row_bytes;
+    const float *nw;       // RMS-norm weights: x is staged as rms_norm(x) * nw (P <= 2 kernels)
+    float eps;
+    const float *r;        // residual: y = r + W.x (one matrix, PLAIN); may alias y
 };
 
 // One GEMV launch's work for this workgroup: the per-workgroup constants
@@ -1103,6 +1107,7 @@ struct MfmaStage {
                 } else if (v < rend) {
                     int m, row;
                     split_row(v, m, row);
+                    if (!XDEV && args.r) s0 = args.r[row] + s0;
                     store_y(ybase(m) + row, s0);
                 }
             }
@@ -1122,9 +1127,46 @@ struct MfmaStage {
         float4 pre[NPX];
         x_preload<NPX, CPOL>(args.x, units, pre);
         if (issue_first) issue(first, 0);
+        if constexpr (!XDEV && P <= 2) {
+            if (args.nw) rms_norm_pre(pre);
+        }
         x_stage<FMT, XM_MFMA, NPX, CPOL>(args.x, units, (void *)ldsb, pre);
         if (threadIdx.x < kZeroBytes / 16) ((uint4 *)(ldsb + zero_off))[threadIdx.x] = make_uint4(0, 0, 0, 0);
         for (int i = threadIdx.x; i < args.max_tiles; i += kThreads) tcnt[i] = 0;
+    }
+
+    // x <- x * (1/sqrt(mean(x^2) + eps)) * nw, in registers before staging, as
+    // rms_norm_k computes it (cuda_ops.cu:1479-1504): every chunk of x is in
+    // pre[] (the host checks in_dim), so each workgroup reduces the whole
+    // vector itself; the 8 wave sums meet in the first wave's stage, which is
+    // not written before the staging barrier.
+    template <int NPX>
+    __device__ __forceinline__ void rms_norm_pre(float4 (&pre)[NPX]) const
+    {
+        const int tid = threadIdx.x;
+        float4 w4[NPX];
+#pragma unroll
+        for (int k = 0; k < NPX; k++) {
+            const int i = tid + kThreads * k;
+            w4[k] = i < units * 8 ? ((const float4 *)args.nw)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < NPX; k++)  // chunks past the end were loaded as zeros
+            ss += pre[k].x * pre[k].x + pre[k].y * pre[k].y + pre[k].z * pre[k].z + pre[k].w * pre[k].w;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        float *red = (float *)(ldsb + zero_off + kZeroBytes);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) tot += red[w];
+        const float scale = 1.0f / sqrtf(tot / (float)(units * 32) + args.eps);
+#pragma unroll
+        for (int k = 0; k < NPX; k++)
+            pre[k] = make_float4(pre[k].x * scale * w4[k].x, pre[k].y * scale * w4[k].y, pre[k].z * scale * w4[k].z,
+                                 pre[k].w * scale * w4[k].w);
     }
 
     // All item slots, slot 0 already issued into b0.  One item in flight per
@@ -1470,9 +1512,13 @@ static void tile_shape(int nsegs, int &P, int &G)
 }
 
 static void gemv_mfma(int fmt, int mode, int nseg, const void *const *W, float *const *y, const int *rows,
-                      const float *x, int units, int64_t row_bytes)
+                      const float *x, int units, int64_t row_bytes, const float *nw = nullptr, float eps = 0.f,
+                      const float *r = nullptr)
 {
     MfmaArgs a = {};
+    a.nw = nw;
+    a.eps = eps;
+    a.r = r;
     a.units = units;
     a.row_bytes = row_bytes;
     a.x = x;
@@ -1598,9 +1644,12 @@ static int chain_launch(const holo_gemv_stage_t *stages, int nstages)
     return 0;
 }
 
-// One launch over up to three matrices sharing x and in_dim.
-static void gemv_multi(int fmt, int mode, int nseg, const void *const *W, float *const *y, const int *rows,
-                       const float *x, int in_dim)
+// One launch over up to three matrices sharing x and in_dim.  nw: stage
+// rms_norm(x) * nw instead of x (the MFMA path with in_dim <= 8192 only;
+// false, with nothing launched, otherwise).  r: y = r + W.x (one matrix).
+static bool gemv_multi(int fmt, int mode, int nseg, const void *const *W, float *const *y, const int *rows,
+                       const float *x, int in_dim, const float *nw = nullptr, float eps = 0.f,
+                       const float *r = nullptr)
 {
     const Tuning &tn = tuning();
     GemvArgs a = {};
@@ -1609,9 +1658,10 @@ static void gemv_multi(int fmt, int mode, int nseg, const void *const *W, float 
     a.nsegs = (a.units + 63) / 64;
     a.x = x;
     a.nseg = nseg;
+    a.r = r;
     if (a.nsegs > 4 * kWaves) {
         HOLO_REJECT("gemv: in_dim too large (at most 32 segments of 64 units per row)");
-        return;
+        return true;
     }
     // Q8_0 rows carry twice the bytes per weight, so the F32 path is already
     // load-bound on them and measured faster (MI355X); the MFMA path serves
@@ -1624,11 +1674,13 @@ static void gemv_multi(int fmt, int mode, int nseg, const void *const *W, float 
             total += rows[s];
         }
         if (mode == MODE_GATEUP) total = rows[0];
-        if (aligned16 && mfma_fits(fmt, a.units, total, mode == MODE_GATEUP ? 8 : 16)) {
-            gemv_mfma(fmt, mode, nseg, W, y, rows, x, a.units, a.row_bytes);
-            return;
+        const bool norm_ok = !nw || (a.units % 8 == 0 && a.units <= 256 && ((uintptr_t)nw & 15u) == 0);
+        if (aligned16 && norm_ok && mfma_fits(fmt, a.units, total, mode == MODE_GATEUP ? 8 : 16)) {
+            gemv_mfma(fmt, mode, nseg, W, y, rows, x, a.units, a.row_bytes, nw, eps, r);
+            return true;
         }
     }
+    if (nw) return false;
     // x staged in LDS when it fits (F32 needs 132 B per unit, I24 104 B),
     // otherwise read by each lane from global memory.
     int xm = tn.xmode == XM_MFMA ? XM_F32 : tn.xmode;
@@ -1648,10 +1700,10 @@ static void gemv_multi(int fmt, int mode, int nseg, const void *const *W, float 
     if (mode == MODE_GATEUP && R > 2) R = 2;
     a.groups = G;
     const int TR = G * R;
-    if (!check_ptr(x, "activation vector must be 4-byte aligned")) return;
+    if (!check_ptr(x, "activation vector must be 4-byte aligned")) return true;
     int tiles = 0;
     for (int s = 0; s < nseg; s++) {
-        if (!check_ptr(W[s], "weight matrix must be 4-byte aligned")) return;
+        if (!check_ptr(W[s], "weight matrix must be 4-byte aligned")) return true;
         a.W[s] = (const uint8_t *)W[s];
         a.y[s] = y[s];
         a.rows[s] = rows[s];
@@ -1660,12 +1712,17 @@ static void gemv_multi(int fmt, int mode, int nseg, const void *const *W, float 
     }
     if (mode == MODE_GATEUP) tiles = (rows[0] + TR - 1) / TR;
     a.ntiles = tiles;
-    if (tiles == 0) return;
+    if (tiles == 0) return true;
     if (a.units == 0) {
         // No complete block per row: every dot product is empty.
+        if (r) {
+            if (r != y[0])
+                HOLO_CHECK(hipMemcpyAsync(y[0], r, sizeof(float) * rows[0], hipMemcpyDeviceToDevice, stream()));
+            return true;
+        }
         for (int s = 0; s < (mode == MODE_GATEUP ? 1 : nseg); s++)
             HOLO_CHECK(hipMemsetAsync(y[s], 0, sizeof(float) * rows[s], stream()));
-        return;
+        return true;
     }
 #define HOLO_DISPATCH(F)                                                             \
     if (xm == XM_F32) {                                                              \
@@ -1687,6 +1744,7 @@ static void gemv_multi(int fmt, int mode, int nseg, const void *const *W, float 
     }
 #undef HOLO_DISPATCH
     (void)total_rows;
+    return true;
 }
 
 static void gemv_one(int fmt, float *dst, const void *M, const float *v, int out_dim, int in_dim)
@@ -1802,6 +1860,81 @@ void holo_batched_ffn_gate_up(float *out, const void *W1, const void *W3, const 
     float *y[2] = {out, out};
     int rows[2] = {ffn_dim, ffn_dim};
     gemv_multi(fmt, MODE_GATEUP, 2, W, y, rows, x, in_dim);
+}
+
+// ---- fused with the RMS norm before, or the residual add after ---------------------
+// A decode layer is rms_norm -> q/k/v, o -> residual add, rms_norm -> gate/up,
+// down -> residual add (llm_cuda.c:598-880).  These fold the norms into the
+// GEMV's activation staging and the adds into its output stores, halving the
+// launches of a decode step.  No reference counterpart (extensions).
+
+void holo_batched_qkv_norm(float *q_out, float *k_out, float *v_out, const void *Wq, const void *Wk, const void *Wv,
+                           const float *x, const float *norm_w, float eps, float *xb, int q_dim, int kv_dim, int in_dim,
+                           int type)
+{
+    int fmt = fmt_of_type(type);
+    if (fmt < 0 || !Wq || !Wk || !Wv || !x || q_dim < 0 || kv_dim < 0) {
+        HOLO_REJECT("holo_batched_qkv_norm: unsupported type or missing matrix");
+        return;
+    }
+    const void *W[3] = {Wq, Wk, Wv};
+    float *y[3] = {q_out, k_out, v_out};
+    int rows[3] = {q_dim, kv_dim, kv_dim};
+    if (norm_w && gemv_multi(fmt, MODE_PLAIN, 3, W, y, rows, x, in_dim, norm_w, eps)) return;
+    if (!xb) {
+        HOLO_REJECT("holo_batched_qkv_norm: shape outside the fused path and no xb scratch");
+        return;
+    }
+    cuda_rms_norm(xb, x, norm_w, in_dim, eps);
+    gemv_multi(fmt, MODE_PLAIN, 3, W, y, rows, xb, in_dim);
+}
+
+void holo_batched_ffn_gate_up_norm(float *out, const void *W1, const void *W3, const float *x, const float *norm_w,
+                                   float eps, float *xb, int ffn_dim, int in_dim, int type)
+{
+    int fmt = fmt_of_type(type);
+    if (fmt < 0 || !W1 || !W3 || !x || ffn_dim < 0) {
+        HOLO_REJECT("holo_batched_ffn_gate_up_norm: unsupported type or missing matrix");
+        return;
+    }
+    const void *W[2] = {W1, W3};
+    float *y[2] = {out, out};
+    int rows[2] = {ffn_dim, ffn_dim};
+    if (norm_w && gemv_multi(fmt, MODE_GATEUP, 2, W, y, rows, x, in_dim, norm_w, eps)) return;
+    if (!xb) {
+        HOLO_REJECT("holo_batched_ffn_gate_up_norm: shape outside the fused path and no xb scratch");
+        return;
+    }
+    cuda_rms_norm(xb, x, norm_w, in_dim, eps);
+    gemv_multi(fmt, MODE_GATEUP, 2, W, y, rows, xb, in_dim);
+}
+
+void holo_matmul_add(float *y, const void *M, const float *v, const float *r, int out_dim, int in_dim, int type)
+{
+    if (out_dim <= 0) return;
+    if (!y || !r || !v) {
+        HOLO_REJECT("holo_matmul_add: null pointer");
+        return;
+    }
+    const int fmt = fmt_of_type(type);
+    if (!M) {
+        // a NULL matrix multiplies to zeros (llm.c:772-775): y = r
+        if (y != r) HOLO_CHECK(hipMemcpyAsync(y, r, sizeof(float) * out_dim, hipMemcpyDeviceToDevice, stream()));
+        return;
+    }
+    if (fmt >= 0) {
+        const void *W[1] = {M};
+        float *yy[1] = {y};
+        int rows[1] = {out_dim};
+        gemv_multi(fmt, MODE_PLAIN, 1, W, yy, rows, v, in_dim, nullptr, 0.f, r);
+        return;
+    }
+    if (y == r) {
+        HOLO_REJECT("holo_matmul_add: y may alias r only for Q8_0, Q4_0 and Q4_K");
+        return;
+    }
+    holo_matmul(y, M, v, out_dim, in_dim, type);
+    cuda_vec_add(y, y, r, out_dim);
 }
 
 // cuda_ops.cu:1282-1294

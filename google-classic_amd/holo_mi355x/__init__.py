@@ -142,6 +142,9 @@ _SIGS = {
     "holo_gemm_q4_0_f16_multi": (None, [_P, _P, _P, _I, _P, _I, _I]),
     "holo_prefill_set_mode": (None, [_I]),
     "holo_prefill_get_mode": (_I, []),
+    "holo_batched_qkv_norm": (None, [_P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _I, _I, _I, _I]),
+    "holo_batched_ffn_gate_up_norm": (None, [_P, _P, _P, _P, _P, C.c_float, _P, _I, _I, _I]),
+    "holo_matmul_add": (None, [_P, _P, _P, _P, _I, _I, _I]),
     # GGUF files (include/holo_gguf.h)
     "holo_gguf_open": (_P, [C.c_char_p]),
     "holo_gguf_close": (None, [_P]),

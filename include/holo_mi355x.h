@@ -130,6 +130,28 @@ void holo_batched_qkv(float *q_out, float *k_out, float *v_out,
 void holo_batched_ffn_gate_up(float *out, const void *W1, const void *W3,
                               const float *x, int ffn_dim, int in_dim, int type);
 
+/* ---- decode-layer fusions (no reference counterpart) ------------------------
+ * The reference's decode layer runs rms_norm before q/k/v and gate/up and a
+ * residual add after o and down, each its own launch (llm_cuda.c:598-880).
+ * These fold them into the GEMVs:
+ *   holo_batched_qkv_norm / holo_batched_ffn_gate_up_norm: the product of
+ *     rms_norm(x) * norm_w (as cuda_rms_norm with eps) -- the norm is applied
+ *     in the GEMV's activation staging for Q4_0/Q4_K with in_dim <= 8192 and a
+ *     16-byte-aligned norm_w; otherwise cuda_rms_norm writes xb (in_dim
+ *     floats, required then; NULL allowed when the fused path applies) and
+ *     the plain fused GEMV runs on it.
+ *   holo_matmul_add: y = r + W.v, the add in the GEMV's output store; y may
+ *     alias r (in place) for Q8_0, Q4_0 and Q4_K.                          */
+void holo_batched_qkv_norm(float *q_out, float *k_out, float *v_out,
+                           const void *Wq, const void *Wk, const void *Wv,
+                           const float *x, const float *norm_w, float eps, float *xb,
+                           int q_dim, int kv_dim, int in_dim, int type);
+void holo_batched_ffn_gate_up_norm(float *out, const void *W1, const void *W3,
+                                   const float *x, const float *norm_w, float eps, float *xb,
+                                   int ffn_dim, int in_dim, int type);
+void holo_matmul_add(float *y, const void *M, const float *v, const float *r,
+                     int out_dim, int in_dim, int type);
+
 /* ---- batched prefill --------------------------------------------------------
  * The reference has no batched path (one GEMV per prompt token,
  * src/ai/llm.c:1049).  Activations X[M][K] fp32 are quantised per row and

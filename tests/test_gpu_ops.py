@@ -242,6 +242,86 @@ def test_gemm_multi_rejects(holo, synth):
     assert lib.holo_last_error() == 100001
 
 
+# ---- decode-layer fusions -----------------------------------------------------------------
+
+def rms_norm_np(x, w, eps):
+    x64 = x.astype(np.float64)
+    return (x64 / np.sqrt(np.mean(x64 * x64) + eps) * w).astype(np.float32)
+
+
+@pytest.mark.parametrize("t,dim,kv", [(Q4_0, 4096, 1024), (Q4_K, 4096, 4096), (Q4_0, 11008, 512), (Q8_0, 2048, 512)],
+                         ids=["q4_0", "q4_k", "q4_0_long", "q8_0"])
+def test_qkv_and_gate_up_with_norm(holo, synth, oracle, t, dim, kv):
+    """holo_batched_qkv_norm / _gate_up_norm against cuda_rms_norm followed by
+    the plain fused GEMV (1e-5 normwise: only the norm's summation order
+    differs) and against the oracle on numpy's norm (1e-3).  in_dim 11008 and
+    Q8_0 run the unfused route through xb."""
+    print(f"case norm-fused type {t} dim {dim}", flush=True)
+    lib = holo.lib()
+    eps = 1e-5
+    x = synth.normal(dim, seed=5) * 3.0
+    w = (1.0 + 0.1 * synth.normal(dim, seed=6)).astype(np.float32)
+    Ws = [synth.blocks(t, n, dim, seed=10 + i) for i, n in enumerate((dim, kv, kv))]
+    dWs = [up(holo, m) for m in Ws]
+    dx, dw = up(holo, x), up(holo, w)
+    dxb = holo.DeviceBuffer(4 * dim)
+    outs = [holo.DeviceBuffer(4 * n) for n in (dim, kv, kv)]
+    refs = [holo.DeviceBuffer(4 * n) for n in (dim, kv, kv)]
+    lib.holo_batched_qkv_norm(outs[0].ptr, outs[1].ptr, outs[2].ptr, dWs[0].ptr, dWs[1].ptr, dWs[2].ptr, dx.ptr,
+                              dw.ptr, eps, dxb.ptr, dim, kv, dim, t)
+    lib.cuda_rms_norm(dxb.ptr, dx.ptr, dw.ptr, dim, eps)
+    lib.holo_batched_qkv(refs[0].ptr, refs[1].ptr, refs[2].ptr, dWs[0].ptr, dWs[1].ptr, dWs[2].ptr, dxb.ptr,
+                         dim, kv, dim, t)
+    lib.cuda_sync()
+    holo.check("qkv norm")
+    xn = rms_norm_np(x, w, eps)
+    for i, n in enumerate((dim, kv, kv)):
+        got = down(outs[i], n)
+        assert normwise_err(got, down(refs[i], n)) <= 1e-5, i
+        assert normwise_err(got, oracle.matmul(t, Ws[i], xn, n, dim)) <= 1e-3, i
+    # gate/up: silu(W1 xn) * (W3 xn)
+    ffn = kv
+    dg = holo.DeviceBuffer(4 * ffn)
+    lib.holo_batched_ffn_gate_up_norm(dg.ptr, dWs[1].ptr, dWs[2].ptr, dx.ptr, dw.ptr, eps, dxb.ptr, ffn, dim, t)
+    lib.cuda_sync()
+    holo.check("gate_up norm")
+    g = oracle.matmul(t, Ws[1], xn, ffn, dim).astype(np.float64)
+    u = oracle.matmul(t, Ws[2], xn, ffn, dim).astype(np.float64)
+    assert normwise_err(down(dg, ffn), g / (1.0 + np.exp(-g)) * u) <= 1e-3
+
+
+@pytest.mark.parametrize("t,out_dim,in_dim", [(Q4_0, 4096, 4096), (Q4_0, 4096, 11008), (Q8_0, 1024, 4096),
+                                              (Q4_K, 2048, 4096), (0, 256, 512)],
+                         ids=["q4_0", "q4_0_down", "q8_0", "q4_k", "f32"])
+def test_matmul_add(holo, synth, oracle, t, out_dim, in_dim):
+    """y = r + W.v with the add in the GEMV's store: in place (y is r) and out
+    of place, bit-identical to each other, and within 1e-3 of the oracle.  F32
+    runs the unfused route (out of place only)."""
+    print(f"case matmul_add type {t} {out_dim}x{in_dim}", flush=True)
+    lib = holo.lib()
+    W = synth.blocks(t, out_dim, in_dim, seed=21) if t else synth.normal(out_dim * in_dim, seed=21)
+    v = synth.normal(in_dim, seed=22)
+    r = synth.normal(out_dim, seed=23) * 10.0
+    dW, dv, dr = up(holo, W), up(holo, v), up(holo, r)
+    dy = holo.DeviceBuffer(4 * out_dim)
+    lib.holo_matmul_add(dy.ptr, dW.ptr, dv.ptr, dr.ptr, out_dim, in_dim, t)
+    lib.cuda_sync()
+    holo.check("matmul_add")
+    got = down(dy, out_dim)
+    want = r.astype(np.float64) + (oracle.matmul(t, W, v, out_dim, in_dim) if t else
+                                   W.reshape(out_dim, in_dim).astype(np.float64) @ v)
+    assert normwise_err(got, want) <= 1e-3
+    if t:
+        lib.holo_matmul_add(dr.ptr, dW.ptr, dv.ptr, dr.ptr, out_dim, in_dim, t)  # in place
+        lib.cuda_sync()
+        holo.check("matmul_add in place")
+        assert np.array_equal(down(dr, out_dim), got)
+    else:
+        lib.holo_last_error()
+        lib.holo_matmul_add(dr.ptr, dW.ptr, dv.ptr, dr.ptr, out_dim, in_dim, t)
+        assert lib.holo_last_error() == 100001  # in place only for the block formats
+
+
 # ---- remaining boundary ops --------------------------------------------------------------
 
 def test_vector_and_activation_ops(holo, synth):
