@@ -498,6 +498,8 @@ def main():
                     help="only run config 4 (prefill GEMM), print its JSON and exit (for profiling)")
     ap.add_argument("--prompt-only", action="store_true",
                     help="only run the 512-token prompt forward over 32 layers, print its JSON and exit")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="only run the decode-attention measurement, print its JSON and exit")
     a = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -522,6 +524,9 @@ def main():
         return
     if a.prefill_only:
         print(json.dumps({"config4_prefill_m512": prefill_tops(lib)}), flush=True)
+        return
+    if a.attention_only:
+        print(json.dumps({"decode_attention_llama2_7b": decode_attention(lib)}), flush=True)
         return
     if a.prompt_only:
         layers = [Mats(Q4_0, i, 2, LAYER) for i in range(32)]

@@ -480,27 +480,36 @@ __global__ __launch_bounds__(256) void attn_decode_k(float *out, float *part, co
     }
 }
 
-// Merges a head's ranges: weights e^(m_s - M) in range order.
-__global__ __launch_bounds__(128) void attn_decode_combine_k(float *out, const float *part, int hd, int splits)
+// Merges a head's ranges with weights e^(m_s - M).  512 threads: thread
+// (d, g) sums ranges g, g + 4, ... for output dim d, and the 4 groups' sums
+// meet in LDS in group order, so the order is fixed.  (Merging in the split
+// kernel itself, by the last range of a head to arrive, measured slower: the
+// merge becomes a serial tail and every range pays the arrival.)
+__global__ __launch_bounds__(512) void attn_decode_combine_k(float *out, const float *part, int hd, int splits)
 {
     __shared__ float lw[kDecMaxSplits];
+    __shared__ float lg[4][128];
     __shared__ float scratch[16];
-    const int h = blockIdx.x, t = threadIdx.x;
+    const int h = blockIdx.x, t = threadIdx.x, d = t & 127, grp = t >> 7;
     const int stride = hd + 4;
     const float *ph = part + (int64_t)h * splits * stride;
     float mx = -INFINITY;
     for (int s = t; s < splits; s += blockDim.x) mx = fmaxf(mx, ph[(int64_t)s * stride + hd]);
     const float M = block_reduce<true>(mx, scratch);
-    for (int s = t; s < splits; s += blockDim.x) lw[s] = expf(ph[(int64_t)s * stride + hd] - M);
-    __syncthreads();
-    float L = 0.f;
-    for (int s = 0; s < splits; s++) L = fmaf(lw[s], ph[(int64_t)s * stride + hd + 1], L);
-    const float inv = 1.0f / L;
-    for (int d = t; d < hd; d += blockDim.x) {
-        float o = 0.f;
-        for (int s = 0; s < splits; s++) o = fmaf(lw[s], ph[(int64_t)s * stride + d], o);
-        out[(int64_t)h * hd + d] = o * inv;
+    float lsum = 0.f;
+    for (int s = t; s < splits; s += blockDim.x) {
+        const float w = expf(ph[(int64_t)s * stride + hd] - M);
+        lw[s] = w;
+        lsum = fmaf(w, ph[(int64_t)s * stride + hd + 1], lsum);
     }
+    const float L = block_reduce<false>(lsum, scratch);  // its barriers also publish lw
+    if (d < hd) {
+        float o = 0.f;
+        for (int s = grp; s < splits; s += 4) o = fmaf(lw[s], ph[(int64_t)s * stride + d], o);
+        lg[grp][d] = o;
+    }
+    __syncthreads();
+    if (grp == 0 && d < hd) out[(int64_t)h * hd + d] = (((lg[0][d] + lg[1][d]) + lg[2][d]) + lg[3][d]) * (1.0f / L);
 }
 
 // Shapes the split kernel takes: head_dim a multiple of 4 up to 128, 16-byte
@@ -523,7 +532,7 @@ static void decode_attention(float *dst, const float *q, const float *kc, const 
                        kv_len, hd, n_heads, n_kv_heads, chunk);
     HOLO_LAUNCH_CHECK();
     if (splits > 1) {
-        hipLaunchKernelGGL(attn_decode_combine_k, dim3(n_heads), dim3(128), 0, stream(), dst, g_dec_part, hd,
+        hipLaunchKernelGGL(attn_decode_combine_k, dim3(n_heads), dim3(512), 0, stream(), dst, g_dec_part, hd,
                            splits);
         HOLO_LAUNCH_CHECK();
     }
