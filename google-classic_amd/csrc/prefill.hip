@@ -148,9 +148,11 @@ struct PrefillMat {
     int64_t w_bytes;
 };
 
-template <int WM, int WN, int S>
+// WGM x WGN waves per workgroup (4 or 8), each owning WM x WN 32x32 tiles.
+template <int WM, int WN, int S, int WGM = 2, int WGN = 2>
 struct PGeo {
-    static constexpr int TM = 64 * WM, TN = 64 * WN;
+    static constexpr int NT = 64 * WGM * WGN;  // threads
+    static constexpr int TM = 32 * WM * WGM, TN = 32 * WN * WGN;
     static constexpr int ROW = 32 * S + 8;  // f16 per LDS row; the 16-byte pad spreads rows over the banks
     static constexpr int A_OFF = 0;
     static constexpr int B_OFF = A_OFF + TM * ROW * 2;
@@ -158,10 +160,10 @@ struct PGeo {
     static constexpr int BD_OFF = AD_OFF + ((TM * S * 2 + 15) & ~15);
     static constexpr int STAGE = BD_OFF + ((TN * S * 2 + 15) & ~15);
     static constexpr int LDS = 2 * STAGE;
-    static constexpr int NA = TM * S * 4 / 256;      // 16-byte activation pieces per thread
-    static constexpr int ND = (TM * S + 255) / 256;  // activation scales per thread
-    static constexpr int NB = (TN * S + 255) / 256;  // weight blocks per thread
-    static_assert((TM * S * 4) % 256 == 0, "activation pieces must split evenly over the threads");
+    static constexpr int NA = TM * S * 4 / NT;         // 16-byte activation pieces per thread
+    static constexpr int ND = (TM * S + NT - 1) / NT;  // activation scales per thread
+    static constexpr int NB = (TN * S + NT - 1) / NT;  // weight blocks per thread
+    static_assert((TM * S * 4) % NT == 0, "activation pieces must split evenly over the threads");
 };
 
 // f16 (q - 8) of the eight nibbles of x = qs[4j..4j+3]: lo[0..1] hold k = 4j..4j+3
@@ -185,9 +187,9 @@ __device__ __forceinline__ void nib_f16(uint32_t x, uint32_t lo[2], uint32_t hi[
 // never used).
 // XF16: f16 activations without scales, weights dequantised to f16 as they
 // are staged (the f16 product); otherwise the Q8_0 product.
-template <int WM, int WN, int S, bool XF16>
+template <int WM, int WN, int S, bool XF16, int WGM = 2, int WGN = 2>
 struct PStage {
-    using G = PGeo<WM, WN, S>;
+    using G = PGeo<WM, WN, S, WGM, WGN>;
     v4u ra[G::NA];
     uint32_t rd[G::ND];
     Q4_0Unit rb[G::NB];
@@ -198,20 +200,20 @@ struct PStage {
         const int64_t K = (int64_t)nb * 32;
 #pragma unroll
         for (int i = 0; i < G::NA; i++) {
-            const int p = tid + 256 * i, r = p / (4 * S), c = p % (4 * S);
+            const int p = tid + G::NT * i, r = p / (4 * S), c = p % (4 * S);
             const int m = min(m0 + r, a.M - 1), b = min(kb0 + c / 4, nb - 1);
             ra[i] = *(const v4u *)(a.P + (int64_t)m * K + (int64_t)b * 32 + (c % 4) * 8);
         }
         if constexpr (!XF16) {
 #pragma unroll
             for (int i = 0; i < G::ND; i++) {
-                const int v = min(tid + 256 * i, G::TM * S - 1), r = v / S, b = min(kb0 + v % S, nb - 1);
+                const int v = min(tid + G::NT * i, G::TM * S - 1), r = v / S, b = min(kb0 + v % S, nb - 1);
                 rd[i] = a.D[(int64_t)min(m0 + r, a.M - 1) * nb + b];
             }
         }
 #pragma unroll
         for (int i = 0; i < G::NB; i++) {
-            const int v = min(tid + 256 * i, G::TN * S - 1), n = v / S, b = min(kb0 + v % S, nb - 1);
+            const int v = min(tid + G::NT * i, G::TN * S - 1), n = v / S, b = min(kb0 + v % S, nb - 1);
             rb[i] = load_q4_0(w.W, (int64_t)min(n0 + n, w.N - 1) * nb + b, w.w_bytes);
         }
     }
@@ -221,19 +223,19 @@ struct PStage {
     {
 #pragma unroll
         for (int i = 0; i < G::NA; i++) {
-            const int p = tid + 256 * i, r = p / (4 * S), c = p % (4 * S);
+            const int p = tid + G::NT * i, r = p / (4 * S), c = p % (4 * S);
             *(v4u *)(base + G::A_OFF + (r * G::ROW + c * 8) * 2) = ra[i];
         }
         if constexpr (!XF16) {
 #pragma unroll
             for (int i = 0; i < G::ND; i++) {
-                const int v = tid + 256 * i;
+                const int v = tid + G::NT * i;
                 if (v < G::TM * S) ((uint16_t *)(base + G::AD_OFF))[v] = (uint16_t)rd[i];
             }
         }
 #pragma unroll
         for (int i = 0; i < G::NB; i++) {
-            const int v = tid + 256 * i, n = v / S, s = v % S;
+            const int v = tid + G::NT * i, n = v / S, s = v % S;
             if (v < G::TN * S) {
                 uint32_t lo[8], hi[8];
 #pragma unroll
@@ -261,10 +263,10 @@ struct PStage {
 
 // D: stages of global loads in flight (1 or 2); OCC: workgroups per CU the
 // register allocation is bounded for.
-template <int WM, int WN, int S, int D, int OCC, bool XF16>
-__global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
+template <int WM, int WN, int S, int D, int OCC, bool XF16, int WGM = 2, int WGN = 2>
+__global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
 {
-    using G = PGeo<WM, WN, S>;
+    using G = PGeo<WM, WN, S, WGM, WGN>;
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, c32 = lane & 31;
@@ -284,7 +286,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
     w.N = (sel == 2 ? a.n_end[2] : sel == 1 ? a.n_end[1] : a.n_end[0]) - w.nbase;
     w.w_bytes = (int64_t)w.N * a.nb * 18;
     const int n0 = ng - w.nbase;
-    const int wm0 = (wave >> 1) * 32 * WM, wn0 = (wave & 1) * 32 * WN;
+    const int wm0 = (wave / WGN) * 32 * WM, wn0 = (wave % WGN) * 32 * WN;
     const int nb = a.nb;
     const int nst = (nb + S - 1) / S;
     v16f acc[WM][WN];
@@ -350,7 +352,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
         }
     };
 
-    PStage<WM, WN, S, XF16> pa;
+    PStage<WM, WN, S, XF16, WGM, WGN> pa;
     pa.fetch(a, w, tid, m0, n0, 0);
     pa.stash(lds, tid);
     if constexpr (D == 1) {
@@ -365,7 +367,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
     } else {
         // two register sets carry stages st+1 and st+2 while stage st is
         // multiplied, so each stage's loads have two stages of products to land
-        PStage<WM, WN, S, XF16> pb;
+        PStage<WM, WN, S, XF16, WGM, WGN> pb;
         if (nst > 1) pa.fetch(a, w, tid, m0, n0, S);
         if (nst > 2) pb.fetch(a, w, tid, m0, n0, 2 * S);
         __syncthreads();
@@ -409,13 +411,13 @@ static int prefill_tn(int M, int N)
     return tiles128 >= cus ? 128 : 64;
 }
 
-template <int WM, int WN, int S, int D, int OCC, bool XF16>
+template <int WM, int WN, int S, int D, int OCC, bool XF16, int WGM = 2, int WGN = 2>
 static void launch_prefill(PrefillArgs a)
 {
-    using G = PGeo<WM, WN, S>;
+    using G = PGeo<WM, WN, S, WGM, WGN>;
     a.ntm = (a.M + G::TM - 1) / G::TM;
     a.tiles = a.ntm * ((a.N + G::TN - 1) / G::TN);
-    auto kern = gemm_q4_0_f16_k<WM, WN, S, D, OCC, XF16>;
+    auto kern = gemm_q4_0_f16_k<WM, WN, S, D, OCC, XF16, WGM, WGN>;
     static bool attr = false;
     if (!attr) {
         HOLO_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS));
@@ -423,9 +425,9 @@ static void launch_prefill(PrefillArgs a)
     }
     hipEvent_t e0, e1;
     if (take_launch_events(&e0, &e1))
-        hipExtLaunchKernelGGL(kern, dim3(a.tiles), dim3(256), G::LDS, stream(), e0, e1, 0, a);
+        hipExtLaunchKernelGGL(kern, dim3(a.tiles), dim3(G::NT), G::LDS, stream(), e0, e1, 0, a);
     else
-        hipLaunchKernelGGL(kern, dim3(a.tiles), dim3(256), G::LDS, stream(), a);
+        hipLaunchKernelGGL(kern, dim3(a.tiles), dim3(G::NT), G::LDS, stream(), a);
     HOLO_LAUNCH_CHECK();
 }
 
@@ -501,27 +503,32 @@ static void gemm_multi(float *const *Y, const void *const *W, const int *N, int 
     // Variant per shape (measured at the prompt-forward shapes, M = 512):
     // 128 x 128 tiles with 2-block stages when there are at least as many
     // such tiles as CUs (q/k/v, gate/up), with two stages of loads in flight
-    // for the f16 product (95 and 181 us) and one for the Q8_0 product, whose
-    // extra scale registers leave no room for a second (137 and 254 us);
+    // for the f16 product (95 and 181 us; gate/up, two tiles per CU and more,
+    // on 8 waves of 64 x 32: 166 us) and one for the Q8_0 product, whose extra
+    // scale registers leave no room for a second (137 and 254 us);
     // otherwise 64 x 64 tiles, 4-block stages, two in flight (o, down: f16
     // 47 and 113 us, Q8_0 58 and 142 us, against 90 and 223 us on the 128 x 64
     // tile).  HOLO_PREFILL_CFG=<tile rows>,<tile columns>,<stage blocks>,
-    // <stages in flight>,<workgroups per CU> selects one of the compiled
-    // variants (128,128,2,1,2  128,128,2,2,2 (f16 only)  128,64,2,2,2
-    // 64,64,4,1,2  64,64,4,2,2) instead.
+    // <stages in flight>,<waves per EU>[,<waves per workgroup>] selects one
+    // of the compiled variants (128,128,2,1,2  128,128,2,2,2 (f16 only)
+    // 128,128,2,2,2,8  128,64,2,2,2  64,64,4,1,2  64,64,4,2,2) instead.
     static int cfg = -1;
     if (cfg < 0) {
         const char *e = getenv("HOLO_PREFILL_CFG");
-        int tm = 0, tn = 0, st = 0, d = 0, o = 0;
-        cfg = (e && sscanf(e, "%d,%d,%d,%d,%d", &tm, &tn, &st, &d, &o) == 5)
-                  ? (tm / 64) * 10000 + (tn / 64) * 1000 + st * 100 + d * 10 + o
-                  : 0;
+        int tm = 0, tn = 0, st = 0, d = 0, o = 0, w = 4;
+        const int got = e ? sscanf(e, "%d,%d,%d,%d,%d,%d", &tm, &tn, &st, &d, &o, &w) : 0;
+        cfg = got >= 5 ? (w == 8 ? 100000 : 0) + (tm / 64) * 10000 + (tn / 64) * 1000 + st * 100 + d * 10 + o : 0;
     }
     auto go = [&](auto xfc) {
         constexpr bool XF = decltype(xfc)::value;
-        const int def = prefill_tn(M, ntot) == 128 ? (XF ? 22222 : 22212) : 11422;
+        const int tiles128 = ((M + 127) / 128) * ((ntot + 127) / 128);
+        const int def = prefill_tn(M, ntot) != 128 ? 11422
+                        : !XF                       ? 22212
+                        : tiles128 >= 2 * num_cus() ? 122222
+                                                    : 22222;
         switch (cfg ? cfg : def) {
         case 21222: launch_prefill<2, 1, 2, 2, 2, XF>(a); break;
+        case 122222: launch_prefill<2, 1, 2, 2, 2, XF, 2, 4>(a); break;
         case 11412: launch_prefill<1, 1, 4, 1, 2, XF>(a); break;
         case 11422: launch_prefill<1, 1, 4, 2, 2, XF>(a); break;
         case 22222:  // the Q8_0 product has no registers for a second stage: one

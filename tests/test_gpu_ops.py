@@ -163,7 +163,7 @@ def test_matmul_batch_dispatch(holo, synth, oracle):
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 128, 256), (77, 150, 4096), (512, 4096, 4096), (512, 11008, 4096),
-                                   (512, 4096, 11008)], ids=str)
+                                   (512, 4096, 11008), (512, 16384, 4096)], ids=str)
 def test_gemm_q4_0_f16(holo, synth, oracle, M, N, K):
     """The f16 product against the float64 truth of the f16-rounded operands
     (oracle_gemm_q4_0_f16), elementwise within the fp32 accumulation bound, and
@@ -184,7 +184,7 @@ def test_gemm_q4_0_f16(holo, synth, oracle, M, N, K):
 
 
 @pytest.mark.parametrize("M,Ns,K", [(100, (256, 128, 128), 512), (512, (4096, 1024, 1024), 4096),
-                                    (64, (384, 384), 256), (77, (150,), 1024)], ids=str)
+                                    (64, (384, 384), 256), (77, (150,), 1024), (512, (11008, 11008), 4096)], ids=str)
 def test_gemm_multi_matches_single(holo, synth, oracle, M, Ns, K):
     """Several matrices over the same activations in one launch: every output
     bit-identical to its single-matrix launch (Q8_0 and f16 products), and the
