@@ -42,10 +42,11 @@ def down(buf, n, dtype=np.float32):
 
 # ---- row-batched ops against the single-vector ops -----------------------------------------
 
-def test_rms_norm_rows(holo, synth):
-    print("case rms_norm_rows", flush=True)
+@pytest.mark.parametrize("n", [4096, 11008, 4098])  # 16-byte kernel (two register sizes), scalar kernel
+def test_rms_norm_rows(holo, synth, n):
+    print(f"case rms_norm_rows n {n}", flush=True)
     lib = holo.lib()
-    rows, n = 37, 4096
+    rows = 37
     x = synth.normal(rows * n, seed=3).reshape(rows, n) * np.float32(3)
     w = synth.normal(n, seed=4)
     dx, dw, dy, d1 = up(holo, x), up(holo, w), holo.DeviceBuffer(4 * rows * n), holo.DeviceBuffer(4 * n)
