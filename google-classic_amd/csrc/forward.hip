@@ -208,6 +208,8 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
         holo_attention_prefill(att, q, kc, vc, n, pos0, hd, m->n_heads, m->n_kv_heads);
         if (one && fused_gemv_type(L.wo_type)) {
             holo_matmul_add(x, L.wo, att, x, dim, q_dim, L.wo_type);
+        } else if (gemm_rows(L.wo_type, n, q_dim, exact)) {
+            holo_matmul_batch_q4_0_add(x, L.wo, att, x, n, dim, q_dim);  // the add in the GEMM's store
         } else {
             holo_matmul_rows(xb, L.wo, att, n, dim, q_dim, L.wo_type, exact);
             cuda_vec_add(x, x, xb, n * dim);
@@ -217,10 +219,23 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
             holo_batched_ffn_gate_up_norm(hb, L.w1, L.w3, x, L.ffn_norm, m->rms_eps, xb, ffn, dim, L.w1_type);
         } else {
             norm_or_copy(xb, x, L.ffn_norm, n, dim, m->rms_eps);
+            if (L.w3_type == L.w1_type && gemm_rows(L.w1_type, n, dim, exact) && ffn % 128 == 0 &&
+                gemm_rows(L.w2_type, n, ffn, exact)) {
+                // gate and up in one GEMM; the SwiGLU goes into the down GEMM's
+                // activation panel and the residual add into its store
+                float *Y[2] = {hb, hb2};
+                const void *W[2] = {L.w1, L.w3};
+                const int N[2] = {ffn, ffn};
+                holo_matmul_batch_q4_0_multi(Y, W, N, 2, xb, n, dim, nullptr);
+                holo_matmul_batch_q4_0_swiglu_add(x, L.w2, hb, hb2, x, n, dim, ffn);
+                continue;
+            }
             matmul_gate_up(hb, hb2, L, xb, n, ffn, dim, exact);
         }
         if (one && fused_gemv_type(L.w2_type)) {
             holo_matmul_add(x, L.w2, hb, x, dim, ffn, L.w2_type);
+        } else if (gemm_rows(L.w2_type, n, ffn, exact)) {
+            holo_matmul_batch_q4_0_add(x, L.w2, hb, x, n, dim, ffn);
         } else {
             holo_matmul_rows(xb, L.w2, hb, n, dim, ffn, L.w2_type, exact);
             cuda_vec_add(x, x, xb, n * dim);

@@ -106,6 +106,30 @@ __global__ __launch_bounds__(256) void x16_panel_k(uint4 *__restrict__ P, const 
                       __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3));
 }
 
+// The same from the SwiGLU of two activation matrices: P = f16_rne(silu(g) * u)
+// with silu(g) * u as cuda_silu_mul computes it (cuda_ops.cu:304-314).
+
+__global__ __launch_bounds__(256) void x16_swiglu_panel_k(uint4 *__restrict__ P, const float *__restrict__ G,
+                                                          const float *__restrict__ U, int64_t n8)
+{
+    int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n8) return;
+    float v[8], u[8];
+    *(float4 *)&v[0] = ((const float4 *)G)[2 * g];
+    *(float4 *)&v[4] = ((const float4 *)G)[2 * g + 1];
+    *(float4 *)&u[0] = ((const float4 *)U)[2 * g];
+    *(float4 *)&u[4] = ((const float4 *)U)[2 * g + 1];
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float a = (v[2 * j] / (1.0f + expf(-v[2 * j]))) * u[2 * j];
+        const float b = (v[2 * j + 1] / (1.0f + expf(-v[2 * j + 1]))) * u[2 * j + 1];
+        const h2 h = {(_Float16)a, (_Float16)b};
+        o[j] = __builtin_bit_cast(uint32_t, h);
+    }
+    P[g] = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 // ---- GEMM ------------------------------------------------------------------------
 // Workgroup: 4 waves in a 2 x 2 grid, each wave owning WM x WN tiles of
 // 32 x 32 outputs; the workgroup tile is TM = 64*WM rows (activations) by
@@ -138,6 +162,7 @@ struct PrefillArgs {
     const uint16_t *D;               // f16 bits [M][nb]
     int M, N, nb;                    // N: all matrices' columns
     int ntm, tiles;                  // row tiles, all tiles
+    const float *R;                  // one matrix only: Y = R + product (R [M][N], may be Y)
 };
 
 // The matrix of a column tile, its first column and its width.
@@ -396,7 +421,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_q4_0_f16_k(PrefillAr
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + wm0 + 32 * mi + (r & 3) + 4 * h + 8 * (r >> 2);
-                if (m < a.M && n < w.N) w.Y[(int64_t)m * w.N + n] = acc[mi][ni][r];
+                if (m < a.M && n < w.N) {
+                    const int64_t o = (int64_t)m * w.N + n;
+                    w.Y[o] = a.R ? a.R[o] + acc[mi][ni][r] : acc[mi][ni][r];
+                }
             }
         }
 }
@@ -458,9 +486,10 @@ void holo_quantize_act_q8_0(void *dst_blocks, const float *X, int rows, int k)
 
 // One launch over nmat matrices (holo_gemm_q4_0_q8_0 and its multi-matrix form).
 // Xq (Q8_0 blocks): the Q8_0 product; otherwise X (fp32, 16-byte aligned):
-// the f16 product.
+// the f16 product, of silu(X) * U when U is given.  R: Y = R + product (one
+// matrix).
 static void gemm_multi(float *const *Y, const void *const *W, const int *N, int nmat, const void *Xq, const float *X,
-                       int M, int K)
+                       int M, int K, const float *U = nullptr, const float *R = nullptr)
 {
     const bool xf16 = Xq == nullptr;
     const int nb = K / 32;
@@ -475,7 +504,11 @@ static void gemm_multi(float *const *Y, const void *const *W, const int *N, int 
     uint16_t *D = xf16 ? nullptr : (uint16_t *)((uint8_t *)ws + pbytes);
     if (xf16) {
         const int64_t n8 = nblk * 4;
-        hipLaunchKernelGGL(x16_panel_k, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, stream(), P, X, n8);
+        if (U)
+            hipLaunchKernelGGL(x16_swiglu_panel_k, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, stream(), P, X,
+                               U, n8);
+        else
+            hipLaunchKernelGGL(x16_panel_k, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, stream(), P, X, n8);
     } else {
         hipLaunchKernelGGL(q8_panel_k, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, stream(), P, D,
                            (const uint8_t *)Xq, nblk, nblk * 34);
@@ -500,6 +533,7 @@ static void gemm_multi(float *const *Y, const void *const *W, const int *N, int 
     a.M = M;
     a.N = ntot;
     a.nb = nb;
+    a.R = nmat == 1 ? R : nullptr;
     // Variant per shape (measured at the prompt-forward shapes, M = 512):
     // 128 x 128 tiles with 2-block stages when there are at least as many
     // such tiles as CUs (q/k/v, gate/up), with two stages of loads in flight
@@ -652,6 +686,46 @@ void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int 
     holo_quantize_act_q8_0(q, X, M, K);
     holo_gemm_q4_0_q8_0(Y, W, q, M, N, K);
     if (!scratch_q8) HOLO_CHECK(hipFreeAsync(q, stream()));
+}
+
+void holo_matmul_batch_q4_0_add(float *Y, const void *W, const float *X, const float *R, int M, int N, int K)
+{
+    if (M <= 0 || N <= 0) return;
+    if (!Y || !W || !X || !R || K % 32 != 0 || K <= 0) {
+        HOLO_REJECT("holo_matmul_batch_q4_0_add: null pointer or K not a positive multiple of 32");
+        return;
+    }
+    if (M < 64) {
+        for (int m = 0; m < M; m++)
+            holo_matmul_add(Y + (int64_t)m * N, W, X + (int64_t)m * K, R + (int64_t)m * N, N, K, HOLO_TYPE_Q4_0);
+        return;
+    }
+    if (g_prefill_mode == HOLO_PREFILL_F16 && !((uintptr_t)X & 15u)) {
+        gemm_multi(&Y, &W, &N, 1, nullptr, X, M, K, nullptr, R);
+        return;
+    }
+    void *q = nullptr;
+    HOLO_CHECK(hipMallocAsync(&q, (size_t)M * (K / 32) * 34, stream()));
+    if (!q) return;
+    holo_quantize_act_q8_0(q, X, M, K);
+    gemm_multi(&Y, &W, &N, 1, q, nullptr, M, K, nullptr, R);
+    HOLO_CHECK(hipFreeAsync(q, stream()));
+}
+
+void holo_matmul_batch_q4_0_swiglu_add(float *Y, const void *W, float *G, const float *U, const float *R, int M,
+                                       int N, int K)
+{
+    if (M <= 0 || N <= 0) return;
+    if (!Y || !W || !G || !U || !R || K % 32 != 0 || K <= 0) {
+        HOLO_REJECT("holo_matmul_batch_q4_0_swiglu_add: null pointer or K not a positive multiple of 32");
+        return;
+    }
+    if (M >= 64 && g_prefill_mode == HOLO_PREFILL_F16 && !(((uintptr_t)G | (uintptr_t)U) & 15u)) {
+        gemm_multi(&Y, &W, &N, 1, nullptr, G, M, K, U, R);
+        return;
+    }
+    cuda_silu_mul(G, G, U, M * K);
+    holo_matmul_batch_q4_0_add(Y, W, G, R, M, N, K);
 }
 
 void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const int *N, int nmat, const float *X,

@@ -145,6 +145,8 @@ _SIGS = {
     "holo_batched_qkv_norm": (None, [_P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _I, _I, _I, _I]),
     "holo_batched_ffn_gate_up_norm": (None, [_P, _P, _P, _P, _P, C.c_float, _P, _I, _I, _I]),
     "holo_matmul_add": (None, [_P, _P, _P, _P, _I, _I, _I]),
+    "holo_matmul_batch_q4_0_add": (None, [_P, _P, _P, _P, _I, _I, _I]),
+    "holo_matmul_batch_q4_0_swiglu_add": (None, [_P, _P, _P, _P, _P, _I, _I, _I]),
     # GGUF files (include/holo_gguf.h)
     "holo_gguf_open": (_P, [C.c_char_p]),
     "holo_gguf_close": (None, [_P]),

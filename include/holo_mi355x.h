@@ -190,6 +190,15 @@ void holo_gemm_q4_0_f16_multi(float *const *Y, const void *const *W, const int *
 /* Which product holo_matmul_batch_q4_0(_multi) runs for M >= 64: the f16
  * product (default; also taken only when X is 16-byte aligned) or the Q8_0
  * product above.                                                            */
+/* The prompt layer's residual products (no reference counterpart; the batched
+ * analogue of holo_matmul_add): Y = R + X . W^T, and Y = R + (silu(G) * U) .
+ * W^T with silu(g) * u as cuda_silu_mul computes it -- the add in the
+ * GEMM's output store, the SwiGLU in its f16 activation panel.  Y may alias
+ * R.  M < 64 runs GEMVs; outside the f16 product (Q8_0 mode, misaligned G/U,
+ * M < 64) the SwiGLU is stored into G first, so G's contents are not kept. */
+void holo_matmul_batch_q4_0_add(float *Y, const void *W, const float *X, const float *R, int M, int N, int K);
+void holo_matmul_batch_q4_0_swiglu_add(float *Y, const void *W, float *G, const float *U, const float *R,
+                                       int M, int N, int K);
 #define HOLO_PREFILL_F16 0
 #define HOLO_PREFILL_Q8_0 1
 void holo_prefill_set_mode(int mode);

@@ -227,6 +227,54 @@ def test_gemm_multi_matches_single(holo, synth, oracle, M, Ns, K):
         assert np.array_equal(got.reshape(M, n)[:rows].view(np.uint32), want.view(np.uint32)), i
 
 
+@pytest.mark.parametrize("M,mode", [(100, 0), (8, 0), (100, 1)], ids=["f16", "gemv_rows", "q8_0"])
+def test_batch_add_and_swiglu(holo, synth, oracle, M, mode):
+    """Y = R + X.W^T and Y = R + (silu(G)*U).W^T with the add in the GEMM's
+    store and the SwiGLU in its panel: bit-identical to the unfused sequence
+    (cuda_silu_mul, the batched product, an fp32 add), in place and out of
+    place; M < 64 runs GEMVs, within 1e-3 of the oracle."""
+    print(f"case batch add/swiglu M {M} mode {mode}", flush=True)
+    lib = holo.lib()
+    N, K = 256, 512
+    W = synth.blocks(Q4_0, N, K, seed=31)
+    X = synth.normal(M * K, seed=32).reshape(M, K)
+    G = synth.normal(M * K, seed=33).reshape(M, K)
+    U = synth.normal(M * K, seed=34).reshape(M, K)
+    R = synth.normal(M * N, seed=35).reshape(M, N) * 5.0
+    dW, dX, dU = up(holo, W), up(holo, X), up(holo, U)
+    lib.holo_prefill_set_mode(mode)
+    try:
+        # unfused reference on the GPU: H = silu(G)*U, T = H.W^T, T2 = X.W^T
+        dG, dH = up(holo, G), holo.DeviceBuffer(4 * M * K)
+        lib.cuda_silu_mul(dH.ptr, dG.ptr, dU.ptr, M * K)
+        dT, dT2 = holo.DeviceBuffer(4 * M * N), holo.DeviceBuffer(4 * M * N)
+        lib.holo_matmul_batch_q4_0(dT.ptr, dW.ptr, dH.ptr, M, N, K, None)
+        lib.holo_matmul_batch_q4_0(dT2.ptr, dW.ptr, dX.ptr, M, N, K, None)
+        dY, dR = holo.DeviceBuffer(4 * M * N), up(holo, R)
+        lib.holo_matmul_batch_q4_0_add(dY.ptr, dW.ptr, dX.ptr, dR.ptr, M, N, K)
+        dS = up(holo, R)  # in place: S += X.W^T
+        lib.holo_matmul_batch_q4_0_add(dS.ptr, dW.ptr, dX.ptr, dS.ptr, M, N, K)
+        dG2, dZ = up(holo, G), up(holo, R)  # in place: Z += swiglu(G, U).W^T
+        lib.holo_matmul_batch_q4_0_swiglu_add(dZ.ptr, dW.ptr, dG2.ptr, dU.ptr, dZ.ptr, M, N, K)
+        lib.cuda_sync()
+        holo.check("batch add")
+    finally:
+        lib.holo_prefill_set_mode(0)
+    t2 = down(dT2, M * N).reshape(M, N)
+    want = (R + t2).astype(np.float32)
+    got = down(dY, M * N).reshape(M, N)
+    if M >= 64:
+        assert np.array_equal(got, want)
+        assert np.array_equal(down(dZ, M * N).reshape(M, N), (R + down(dT, M * N).reshape(M, N)).astype(np.float32))
+    else:
+        ref = R + np.stack([oracle.matmul(Q4_0, W, X[m], N, K) for m in range(M)])
+        assert normwise_err(got, ref) <= 1e-3
+        h = (G / (1.0 + np.exp(-G.astype(np.float64))) * U).astype(np.float32)
+        refz = R + np.stack([oracle.matmul(Q4_0, W, h[m], N, K) for m in range(M)])
+        assert normwise_err(down(dZ, M * N).reshape(M, N), refz) <= 1e-3
+    assert np.array_equal(down(dS, M * N).reshape(M, N), got)
+
+
 def test_gemm_multi_rejects(holo, synth):
     import ctypes as C
     lib = holo.lib()
