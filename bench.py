@@ -32,7 +32,8 @@ The printed JSON line carries
                 a bounded sample of the same layer
   extra         the unfused drop-in layer (7 cuda_matmul_q4_0 calls), the layer
                 as one multi-stage launch (holo_gemv_chain), configs
-                1 and 3 (Q8_0 4096x4096; Q4_K Llama-3-8B FFN), config 4 (batched
+                1 and 3 (Q8_0 4096x4096; Q4_K Llama-3-8B FFN), the Q6_K GEMV
+                (32000x4096 head and 4096x11008 down), config 4 (batched
                 prefill GEMM on the f16 matrix cores: useful TOP/s = 2*M*N*K per
                 kernel time, and its fraction of the dense f16 and int8 peaks;
                 and a 512-token prompt through the 32 layers in one pass),
@@ -63,6 +64,7 @@ from holo_mi355x import synth  # noqa: E402
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 F16_PEAK_TFLOPS = 2500.0   # MI355X dense f16 MFMA
 Q4_0, Q8_0, Q4_K = holo.TYPE_Q4_0, holo.TYPE_Q8_0, holo.TYPE_Q4_K
+Q6_K = 14
 BASE_SEED = 20251201
 DIM, FFN, VOCAB = 4096, 11008, 32000
 
@@ -71,6 +73,7 @@ LAYER = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 40
          ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
 CONFIG1 = [("w", 4096, 4096)]                             # Q8_0 GEMV
 CONFIG3 = [("gate", 14336, 4096), ("down", 4096, 14336)]  # Q4_K, Llama-3-8B FFN
+Q6K_SHAPES = [("output", 32000, 4096), ("down", 4096, 11008)]  # Q6_K head and down of a Q4_K_M Llama-2-7B
 
 
 def log(*a):
@@ -238,7 +241,8 @@ def mean_launch_us(lib, layers, A, steps, which, kernel_only):
 
 def single_gemv_gbs(lib, qtype, sets, steps):
     """Back-to-back launches of one config's matrices, rotating over copies."""
-    fn = {Q4_0: lib.cuda_matmul_q4_0, Q8_0: lib.cuda_matmul_q8_0, Q4_K: lib.cuda_matmul_q4_k}[qtype]
+    fn = {Q4_0: lib.cuda_matmul_q4_0, Q8_0: lib.cuda_matmul_q8_0, Q4_K: lib.cuda_matmul_q4_k,
+          Q6_K: lib.cuda_matmul_q6_k}[qtype]
     A = sets["acts"]
 
     def run(k):
@@ -257,6 +261,22 @@ def single_gemv_gbs(lib, qtype, sets, steps):
     holo.check("single gemv")
     b = weight_bytes(qtype, sets["mats"][0].shapes)
     return steps * b / (ms * 1e-3) / 1e9, ms * 1e3 / (steps * len(sets["mats"][0].shapes))
+
+
+def single_gemvs(lib, A):
+    """Configs 1 and 3 and the Q6_K GEMV, each over enough copies of its
+    matrices to defeat the MALL."""
+    out = {}
+    for qt, cfg, name, shapes, copies in ((Q8_0, 1, "config1_q8_0_4096x4096", CONFIG1, 32),
+                                          (Q4_K, 3, "config3_q4_k_llama3_ffn", CONFIG3, 10),
+                                          (Q6_K, 6, "q6_k_head_and_down_llama2_7b", Q6K_SHAPES, 4)):
+        sets = {"mats": [Mats(qt, i, cfg, shapes) for i in range(copies)], "acts": A}
+        g, us = single_gemv_gbs(lib, qt, sets, 4 * copies)
+        out[name] = {"gbs": round(g, 1), "us_per_launch": round(us, 2),
+                     "bytes_per_launch": weight_bytes(qt, shapes) / len(shapes)}
+        log(f"{name}: {g:.0f} GB/s, {us:.2f} us per launch")
+        del sets
+    return out
 
 
 # ---- config 5: full decode step ----------------------------------------------------------
@@ -498,6 +518,8 @@ def main():
                     help="only run config 4 (prefill GEMM), print its JSON and exit (for profiling)")
     ap.add_argument("--prompt-only", action="store_true",
                     help="only run the 512-token prompt forward over 32 layers, print its JSON and exit")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only run the single-GEMV measurements (configs 1 and 3, Q6_K), print their JSON and exit")
     ap.add_argument("--attention-only", action="store_true",
                     help="only run the decode-attention measurement, print its JSON and exit")
     a = ap.parse_args()
@@ -524,6 +546,9 @@ def main():
         return
     if a.prefill_only:
         print(json.dumps({"config4_prefill_m512": prefill_tops(lib)}), flush=True)
+        return
+    if a.gemv_only:
+        print(json.dumps(single_gemvs(lib, Acts())), flush=True)
         return
     if a.attention_only:
         print(json.dumps({"decode_attention_llama2_7b": decode_attention(lib)}), flush=True)
@@ -601,15 +626,7 @@ def main():
 
         del layers
 
-        # configs 1 and 3 over enough copies to defeat the MALL
-        for qt, cfg, name, shapes, copies in ((Q8_0, 1, "config1_q8_0_4096x4096", CONFIG1, 32),
-                                              (Q4_K, 3, "config3_q4_k_llama3_ffn", CONFIG3, 10)):
-            sets = {"mats": [Mats(qt, i, cfg, shapes) for i in range(copies)], "acts": A}
-            g, us = single_gemv_gbs(lib, qt, sets, 4 * copies)
-            extra[name] = {"gbs": round(g, 1), "us_per_launch": round(us, 2),
-                           "bytes_per_launch": weight_bytes(qt, shapes) / len(shapes)}
-            log(f"{name}: {g:.0f} GB/s, {us:.2f} us per launch")
-            del sets
+        extra.update(single_gemvs(lib, A))
         extra["config4_prefill_m512"] = prefill_tops(lib)
         log(f"config 4 prefill: {extra['config4_prefill_m512']}")
         extra["decode_attention_llama2_7b"] = decode_attention(lib)

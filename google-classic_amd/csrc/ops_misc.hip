@@ -370,6 +370,142 @@ static void launch_attn_prefill_mfma(float *out, const float *q, const float *kc
     HOLO_LAUNCH_CHECK();
 }
 
+// ---- Q6_K GEMV (cuda_matmul_q6_k) ---------------------------------------------------
+//
+// 210-byte superblocks of 256 weights (quant.h:103-110): ql[128] low
+// nibbles, qh[64] high bit pairs, int8 scales[16], f16 d.  dequantize_row_q6_k
+// (quant.c:241-271) gives, for half h and l = 0..31, the 4 weights
+//   y[128h + 32j + l] = (d * sc[8h + l/16 + 2j]) * (q_j - 32),
+//   q_j = ((ql[64h + l + 32(j&1)] >> 4(j>>1)) & 15) | (((qh[32h + l] >> 2j) & 3) << 4).
+// Lane task (b, h, s): superblock b, half h, l = 16s .. 16s + 15, all four j:
+// 64 weights from three 16-byte runs (ql low part, ql high part, qh), the
+// half's 8 scale bytes and d.  The 16 weights of (task, j) share one scale,
+// so they contribute (d*sc) * (sum q x - 32 sum x), with q's bytes built in a
+// register (and, shift, or) and converted by v_cvt_f32_ubyte.  Each wave takes
+// R rows (4, 2 or 1), which share the activation loads.  Measured on MI355X:
+// 32000x4096 30.3 us (3.5 TB/s), 11008x4096 13.5 us, 4096x11008 14.9 us
+// (2.5 TB/s); issuing the next task's loads ahead of the current task's
+// arithmetic (software pipelining) measured slower at every R.
+
+// 4 dwords of bytes [p, p + 16) for a 2-byte-aligned p (one aligned 16-byte
+// load and one dword: both inside the superblock for every run used here).
+__device__ __forceinline__ void q6_run16(const uint8_t *p, uint32_t (&w)[4])
+{
+    const uintptr_t a = (uintptr_t)p;
+    const uint32_t sh = (uint32_t)(a & 3u);
+    const uint32_t *b = (const uint32_t *)(a - sh);
+    const uint4 v = *(const uint4 *)b;
+    const uint32_t e = b[4];
+    w[0] = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+    w[1] = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+    w[2] = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+    w[3] = __builtin_amdgcn_alignbyte(e, v.w, sh);
+}
+
+__device__ __forceinline__ float q6_ubyte_dot(uint32_t q, const float4 x)
+{
+    // (float)((q >> 8k) & 255) compiles to v_cvt_f32_ubyte<k>
+    float a = (float)(q & 255u) * x.x;
+    a = fmaf((float)((q >> 8) & 255u), x.y, a);
+    a = fmaf((float)((q >> 16) & 255u), x.z, a);
+    return fmaf((float)(q >> 24), x.w, a);
+}
+
+// The weights of the wave's R rows for one task, loaded before the activations.
+struct Q6Task {
+    uint32_t qa[4], qb[4], qh[4];  // ql[64h + 16s ..], ql[64h + 32 + 16s ..], qh[32h + 16s ..]
+    uint32_t sc0, sc1;             // sc[8h .. 8h + 7]
+    float d;
+};
+
+__device__ __forceinline__ void q6_load_task(const uint8_t *sb, int h, int sl, Q6Task &t)
+{
+    q6_run16(sb + 64 * h + 16 * sl, t.qa);
+    q6_run16(sb + 64 * h + 32 + 16 * sl, t.qb);
+    q6_run16(sb + 128 + 32 * h + 16 * sl, t.qh);
+    // 8 scale bytes at a 2-byte-aligned offset: at most three dwords, the
+    // last ending at the superblock's end
+    const uintptr_t a = (uintptr_t)(sb + 192 + 8 * h);
+    const uint32_t sh = (uint32_t)(a & 3u);
+    const uint32_t *w = (const uint32_t *)(a - sh);
+    const uint32_t w0 = w[0], w1 = w[1], w2 = sh ? w[2] : 0u;
+    t.sc0 = __builtin_amdgcn_alignbyte(w1, w0, sh);
+    t.sc1 = __builtin_amdgcn_alignbyte(w2, w1, sh);
+    t.d = half_bits_to_float(*(const uint16_t *)(sb + 208));
+}
+
+template <int R>
+__global__ __launch_bounds__(256) void gemv_q6_k2_k(float *dst, const uint8_t *M, const float *v, int out, int in)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = (blockIdx.x * 4 + wave) * R;
+    if (r0 >= out) return;  // whole wave
+    const int nrow = min(R, out - r0);
+    const int nsb = in / 256, ntask = nsb * 4;
+    const int64_t row_bytes = (int64_t)nsb * 210;
+    float acc[R];
+#pragma unroll
+    for (int rr = 0; rr < R; rr++) acc[rr] = 0.f;
+    const uint8_t *rowp[R];
+#pragma unroll
+    for (int rr = 0; rr < R; rr++) rowp[rr] = M + (int64_t)(r0 + min(rr, nrow - 1)) * row_bytes;  // rows past the end
+                                                                                               // repeat the last
+    for (int t = lane; t < ntask; t += 64) {
+        const int b = t >> 2, h = (t >> 1) & 1, sl = t & 1;
+        Q6Task w[R];
+#pragma unroll
+        for (int rr = 0; rr < R; rr++) q6_load_task(rowp[rr] + (int64_t)b * 210, h, sl, w[rr]);
+        const float *xp = v + b * 256 + h * 128 + sl * 16;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float4 x[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) x[c] = *(const float4 *)(xp + 32 * j + 4 * c);
+            const float sx = ((x[0].x + x[0].y) + (x[0].z + x[0].w)) + ((x[1].x + x[1].y) + (x[1].z + x[1].w)) +
+                             ((x[2].x + x[2].y) + (x[2].z + x[2].w)) + ((x[3].x + x[3].y) + (x[3].z + x[3].w));
+            const int shq = 4 * (j >> 1);
+            // sc[8h + 16s/16 + 2j]: byte s + 2j of the half's 8
+            const int k = sl + 2 * j;
+#pragma unroll
+            for (int rr = 0; rr < R; rr++) {
+                const uint32_t *ql = (j & 1) ? w[rr].qb : w[rr].qa;
+                float sq = 0.f;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const uint32_t nib = (ql[c] >> shq) & 0x0F0F0F0Fu;
+                    const uint32_t hb = (w[rr].qh[c] >> (2 * j)) & 0x03030303u;
+                    sq += q6_ubyte_dot(nib | (hb << 4), x[c]);
+                }
+                const uint32_t scw = k < 4 ? w[rr].sc0 : w[rr].sc1;
+                const float sc = (float)(int8_t)(scw >> (8 * (k & 3)));
+                acc[rr] = fmaf(w[rr].d * sc, sq - 32.0f * sx, acc[rr]);
+            }
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < R; rr++) {
+        const float s = wave_reduce_sum(acc[rr]);
+        if (lane == 0 && rr < nrow) dst[r0 + rr] = s;
+    }
+}
+
+// Rows per wave: the most (of 4, 2, 1) that still give two workgroups per CU
+// (MI355X: 4 rows at 32000 and 11008 rows, 2 at 4096).  HOLO_Q6K_ROWS=1|2|4
+// forces a value.
+static int q6_rows_per_wave(int out_dim)
+{
+    static const int forced = [] {
+        const char *e = getenv("HOLO_Q6K_ROWS");
+        const int v = e ? atoi(e) : 0;
+        return (v == 1 || v == 2 || v == 4) ? v : 0;
+    }();
+    if (forced) return forced;
+    for (int r = 4; r > 1; r /= 2)
+        if ((out_dim + 4 * r - 1) / (4 * r) >= 2 * num_cus()) return r;
+    return 1;
+}
+
+
 // ---- decode attention: one query row per head, keys split over workgroups ----------
 //
 // softmax((q . k_p) / sqrt(hd)) . v over cached positions p < kv_len, as
@@ -1173,8 +1309,27 @@ void cuda_matmul_f16(float *dst, const void *M, const float *v, int out_dim, int
 void cuda_matmul_q6_k(float *dst, const void *M, const float *v, int out_dim, int in_dim)
 {
     if (out_dim <= 0) return;
-    hipLaunchKernelGGL(gemv_q6_k_k, dim3(blocks_for(out_dim, 4)), dim3(256), 0, stream(), dst, (const uint8_t *)M, v,
-                       out_dim, in_dim);
+    if (!M) {
+        // matmul_q with a NULL matrix writes zeros (llm.c:772-775)
+        HOLO_CHECK(hipMemsetAsync(dst, 0, sizeof(float) * out_dim, stream()));
+        return;
+    }
+    if (((uintptr_t)M & 1u) || ((uintptr_t)v & 15u)) {
+        // the task kernel needs 2-byte-aligned blocks and 16-byte-aligned activations
+        hipLaunchKernelGGL(gemv_q6_k_k, dim3(blocks_for(out_dim, 4)), dim3(256), 0, stream(), dst,
+                           (const uint8_t *)M, v, out_dim, in_dim);
+        HOLO_LAUNCH_CHECK();
+        return;
+    }
+    const int R = q6_rows_per_wave(out_dim);
+    const dim3 grid((out_dim + 4 * R - 1) / (4 * R));
+    const uint8_t *W = (const uint8_t *)M;
+    if (R == 4)
+        hipLaunchKernelGGL(gemv_q6_k2_k<4>, grid, dim3(256), 0, stream(), dst, W, v, out_dim, in_dim);
+    else if (R == 2)
+        hipLaunchKernelGGL(gemv_q6_k2_k<2>, grid, dim3(256), 0, stream(), dst, W, v, out_dim, in_dim);
+    else
+        hipLaunchKernelGGL(gemv_q6_k2_k<1>, grid, dim3(256), 0, stream(), dst, W, v, out_dim, in_dim);
     HOLO_LAUNCH_CHECK();
 }
 

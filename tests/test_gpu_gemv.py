@@ -83,3 +83,38 @@ def test_dequant_bit_exact(holo, synth, oracle, qtype):
     holo.check("holo_dequant")
     got = d_out.download(np.float32, n)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# Q6_K (cuda_matmul_q6_k): odd superblock counts put every other row at a
+# 2-byte (not 4-byte) offset; odd out_dim leaves a wave with one row.
+Q6_K = 14
+Q6_CASES = [(1, 256), (3, 512), (37, 256 * 9), (130, 4096), (4096, 4096), (4096, 11008), (11008, 4096),
+            (32000, 4096), (5, 256 * 43)]
+
+
+@pytest.mark.parametrize("out_dim,in_dim", Q6_CASES, ids=[f"{o}x{i}" for o, i in Q6_CASES])
+@pytest.mark.parametrize("x_offset", [0, 1], ids=["x16", "x4"])
+def test_gemv_q6_k_parity(holo, synth, oracle, out_dim, in_dim, x_offset):
+    """x_offset 1 shifts the activations by one float, off 16-byte alignment
+    (the per-weight kernel); 0 runs the 64-weight task kernel."""
+    if x_offset and out_dim * in_dim > 4096 * 4096:
+        pytest.skip("alignment fallback checked on the smaller shapes")
+    print(f"case q6_k {out_dim}x{in_dim} x_offset={x_offset}", flush=True)
+    seed = out_dim * 7919 + in_dim
+    W = synth.blocks(Q6_K, out_dim, in_dim, seed)
+    x = synth.normal(in_dim, seed ^ 0xABCDEF)
+    dW = holo.DeviceBuffer.from_array(W)
+    dx = holo.DeviceBuffer.from_array(np.concatenate([np.zeros(x_offset, np.float32), x]))
+    dy = holo.DeviceBuffer(out_dim * 4)
+    holo.lib().cuda_matmul_q6_k(dy.ptr, dW.ptr, dx.ptr + 4 * x_offset, out_dim, in_dim)
+    holo.lib().cuda_sync()
+    holo.check("cuda_matmul_q6_k")
+    got = dy.download(np.float32, out_dim)
+    want = oracle.matmul(Q6_K, W, x, out_dim, in_dim)
+    truth = oracle.truth(Q6_K, W, x, out_dim, in_dim)
+    e_n, e_r = normwise_err(got, want), max_rel_err(got, want)
+    t_n, t_r = normwise_err(got, truth), max_rel_err(got, truth)
+    print(f"  vs oracle normwise {e_n:.2e} elementwise {e_r:.2e}; vs fp64 {t_n:.2e} {t_r:.2e}", flush=True)
+    assert np.all(np.isfinite(got))
+    assert e_n <= TOL and e_r <= TOL
+    assert t_n <= TOL and t_r <= TOL
