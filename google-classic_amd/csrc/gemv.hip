@@ -693,7 +693,13 @@ struct Geo {
     static constexpr int PR = SEGB / 16;                       // 16-byte pieces per row
     static constexpr int NP = 16 * PR;                         // pieces per item
     static constexpr int NL = (NP + 63) / 64;                  // load instructions per item
-    static constexpr int STAGE = 16 * SEGB;                    // LDS stage bytes per wave
+    // Stage rows sit RS = SEGB + 16 bytes apart.  At the unpadded stride the
+    // lanes n = 0..15 of a chunk read rows at dword offsets 72n or 136n, both
+    // 8n mod 64, so rows n and n + 8 hit the same LDS banks; at SEGB + 16
+    // (76n or 140n, both 12n mod 64) the 16 rows start in distinct banks, and
+    // pieces stay 16-byte aligned.
+    static constexpr int RS = SEGB + 24;
+    static constexpr int STAGE = 16 * RS;                      // LDS stage bytes per wave
 };
 
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4)));   // 16-byte aligned
@@ -705,7 +711,7 @@ struct Raw2 {
     u32x4a v[Geo<FMT>::NL];
 };
 
-// Lane (n, g)'s chunk from the wave's stage (row n of the item at n * SEGB):
+// Lane (n, g)'s chunk from the wave's stage (row n of the item at n * RS):
 // Q4_0 / Q8_0 units 4g..4g+3 = bytes [72g, +72) / [136g, +136) of the row
 // (8-byte aligned); Q4_K the header of superblock g/2 and the 64 quant bytes
 // of its half g&1 (16-byte aligned).
@@ -713,18 +719,18 @@ template <int FMT>
 __device__ __forceinline__ void read_chunk(Chunk<FMT> &c, const uint8_t *stage, int n, int g)
 {
     if constexpr (FMT == FMT_Q4_K) {
-        const uint8_t *b = stage + n * 288 + 144 * (g >> 1);
-        const u32x4a h = *(const u32x4a *)b;
-        c.h = (u32x4){h.x, h.y, h.z, h.w};
+        const uint8_t *b = stage + n * Geo<FMT>::RS + 144 * (g >> 1);
+        const u32x2a h0 = *(const u32x2a *)b, h1 = *(const u32x2a *)(b + 8);
+        c.h = (u32x4){h0.x, h0.y, h1.x, h1.y};
         const uint8_t *q = b + 16 + 64 * (g & 1);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const u32x4a v = *(const u32x4a *)(q + 16 * i);
-            c.q[i] = (u32x4){v.x, v.y, v.z, v.w};
+            const u32x2a lo = *(const u32x2a *)(q + 16 * i), hi = *(const u32x2a *)(q + 16 * i + 8);
+            c.q[i] = (u32x4){lo.x, lo.y, hi.x, hi.y};
         }
     } else {
         constexpr int NQ = FMT == FMT_Q4_0 ? 4 : 8;
-        const uint8_t *b = stage + n * Geo<FMT>::SEGB + (FMT == FMT_Q4_0 ? 72 : 136) * g;
+        const uint8_t *b = stage + n * Geo<FMT>::RS + (FMT == FMT_Q4_0 ? 72 : 136) * g;
 #pragma unroll
         for (int i = 0; i < NQ; i++) {
             const u32x2a lo = *(const u32x2a *)(b + 16 * i);
@@ -1054,13 +1060,18 @@ struct MfmaStage {
         }
     }
 
-    // the item into the wave's stage (16-byte piece p at 16 p)
+    // the item into the wave's stage (16-byte piece p of row p / PR)
     __device__ __forceinline__ void stage_write(const Raw2<FMT> &b) const
     {
 #pragma unroll
         for (int i = 0; i < GE::NL; i++) {
             const int pc = 64 * i + lane;
-            if (GE::NP % 64 == 0 || pc < GE::NP) *(u32x4a *)(stage + 16 * pc) = b.v[i];
+            // piece pc = row * PR + col goes to row * RS + 16 col = 16 (pc + row)
+            if (GE::NP % 64 == 0 || pc < GE::NP) {
+                uint8_t *p = stage + 16 * pc + (GE::RS - GE::SEGB) * (pc / GE::PR);
+                *(u32x2a *)p = (u32x2a){b.v[i].x, b.v[i].y};
+                *(u32x2a *)(p + 8) = (u32x2a){b.v[i].z, b.v[i].w};
+            }
         }
     }
 
