@@ -657,6 +657,14 @@ typedef __attribute__((address_space(1))) const u32x2 gu32x2;
 
 constexpr int kZeroBytes = 384;  // >= 3*96 + 32: the A reads of non-plane lanes
 
+// Byte offset of the zero region after x_lds bytes of staged activations.  A
+// plane lane (g, p) reads its unit-T operand at dword 384j + 96g + 8p + 24T
+// (banks 32g + 24T + [0, 24) mod 64); the zero lanes of its 8-lane group read
+// dword zero/4 + 24T + [0, 8).  With zero = 96 mod 128 those start at bank
+// 24 + 24T, outside the plane lanes' window for either parity of g, so a
+// broadcast read and a plane read never wait on one bank.
+__host__ __device__ constexpr uint32_t zero_region_off(uint32_t x_lds) { return ((x_lds + 127u) & ~127u) + 96u; }
+
 template <int FMT>
 struct Chunk;
 template <>
@@ -932,7 +940,7 @@ struct MfmaStage {
         g = lane >> 4;
         units = a.units;
         G = a.nsegs;
-        zero_off = (uint32_t)a.x_lds_bytes;
+        zero_off = zero_region_off((uint32_t)a.x_lds_bytes);
         stage = ldsb + zero_off + kZeroBytes + wave * GE::STAGE;
         tpart = (float *)(ldsb + zero_off + kZeroBytes + kWaves * GE::STAGE);  // [max_tiles][kWaves][16]
         tcnt = (uint32_t *)(tpart + a.max_tiles * kWaves * 16);               // [max_tiles]
@@ -1413,7 +1421,8 @@ template <int FMT>
 static size_t mfma_lds_bytes(int units, int max_tiles)
 {
     const size_t x_lds = ((size_t)units * lds_bytes_per_unit<XM_I24>() + 15) & ~(size_t)15;
-    return x_lds + kZeroBytes + (size_t)kWaves * Geo<FMT>::STAGE + (size_t)max_tiles * (kWaves * 16 * 4 + 4);
+    return zero_region_off((uint32_t)x_lds) + kZeroBytes + (size_t)kWaves * Geo<FMT>::STAGE +
+           (size_t)max_tiles * (kWaves * 16 * 4 + 4);
 }
 
 static int mfma_max_tiles(int total_rows, int tr, int grid)
@@ -1674,17 +1683,18 @@ static bool gemv_multi(int fmt, int mode, int nseg, const void *const *W, float 
         HOLO_REJECT("gemv: in_dim too large (at most 32 segments of 64 units per row)");
         return true;
     }
-    // Q8_0 rows carry twice the bytes per weight, so the F32 path is already
-    // load-bound on them and measured faster (MI355X); the MFMA path serves
-    // Q4_0 and Q4_K unless HOLO_GEMV_XMODE=mfma asks for it on Q8_0 too.
-    if (tn.xmode == XM_MFMA && (fmt != FMT_Q8_0 || tn.mfma_q8)) {
+    // Q8_0 rows carry twice the bytes per weight, so the F32 path streams
+    // them well at in_dim 4096: on MI355X it is faster at 32000x4096 (26.9
+    // against 31.3 us) and level or faster at 4096x4096 and 11008x4096.  At
+    // 4096x11008 the MFMA path is faster (12.8 against 15.1 us).  Q8_0
+    // therefore takes the MFMA path when in_dim > 8192 (always with
+    // HOLO_GEMV_XMODE=mfma); Q4_0 and Q4_K always.
+    int total = 0;
+    for (int s = 0; s < nseg; s++) total += rows[s];
+    if (mode == MODE_GATEUP) total = rows[0];
+    if (tn.xmode == XM_MFMA && (fmt != FMT_Q8_0 || tn.mfma_q8 || a.units > 256)) {
         bool aligned16 = ((uintptr_t)x & 3u) == 0;
-        int total = 0;
-        for (int s = 0; s < nseg; s++) {
-            aligned16 = aligned16 && (((uintptr_t)W[s] & 15u) == 0);
-            total += rows[s];
-        }
-        if (mode == MODE_GATEUP) total = rows[0];
+        for (int s = 0; s < nseg; s++) aligned16 = aligned16 && (((uintptr_t)W[s] & 15u) == 0);
         const bool norm_ok = !nw || (a.units % 8 == 0 && a.units <= 256 && ((uintptr_t)nw & 15u) == 0);
         if (aligned16 && norm_ok && mfma_fits(fmt, a.units, total, mode == MODE_GATEUP ? 8 : 16)) {
             gemv_mfma(fmt, mode, nseg, W, y, rows, x, a.units, a.row_bytes, nw, eps, r);
