@@ -323,6 +323,63 @@ def decode_step(lib, layers, head, A, ones, matmuls_only, fused=False):
 
 # ---- config 4 end to end: a prompt through the whole model ------------------------------
 
+class MixedLayer:
+    """One synthetic layer in the mix of a Q4_K_M file: Q4_K q/k/o/gate/up,
+    Q6_K v and down."""
+    TYPES = {"q": Q4_K, "k": Q4_K, "v": Q6_K, "o": Q4_K, "gate": Q4_K, "up": Q4_K, "down": Q6_K}
+
+    def __init__(self, idx):
+        self.buf = {name: holo.DeviceBuffer.from_array(
+            synth.blocks(self.TYPES[name], o, i, synth.tensor_seed(BASE_SEED, 7, idx, m)))
+            for m, (name, o, i) in enumerate(LAYER)}
+
+
+def prompt_forward_q4_k_m(lib, n_tokens=512):
+    """The 512-token prompt of prompt_forward on a Q4_K_M-style Llama-2-7B:
+    Q4_K embeddings, q/k/o/gate/up; Q6_K v, down and output head.  Every
+    matrix takes the batched product over an f16 panel dequantised first
+    (holo_matmul_batch); before that path, every non-Q4_0 matrix of a prompt
+    ran one GEMV per token."""
+    layers = [MixedLayer(i) for i in range(32)]
+    emb = holo.DeviceBuffer.from_array(synth.blocks(Q4_K, VOCAB, DIM, synth.tensor_seed(BASE_SEED, 7, 32, 0)))
+    head = holo.DeviceBuffer.from_array(synth.blocks(Q6_K, VOCAB, DIM, synth.tensor_seed(BASE_SEED, 7, 32, 1)))
+    ones = holo.DeviceBuffer.from_array(np.ones(DIM, np.float32))
+    T = MixedLayer.TYPES
+    L = (holo.LlamaLayer * 32)()
+    for i, Ls in enumerate(layers):
+        b = Ls.buf
+        L[i] = holo.LlamaLayer(ones.ptr, b["q"].ptr, b["k"].ptr, b["v"].ptr, b["o"].ptr, T["q"], T["k"], T["v"],
+                               T["o"], ones.ptr, b["gate"].ptr, b["down"].ptr, b["up"].ptr, T["gate"], T["down"],
+                               T["up"])
+    kv_floats = 32 * n_tokens * DIM
+    kc, vc = holo.DeviceBuffer(4 * kv_floats), holo.DeviceBuffer(4 * kv_floats)
+    logits = holo.DeviceBuffer(4 * VOCAB)
+    m = holo.LlamaModel(n_layers=32, dim=DIM, n_heads=32, n_kv_heads=32, head_dim=128, ffn_dim=FFN, vocab=VOCAB,
+                        max_seq=n_tokens, rms_eps=1e-5, rope_base=10000.0, tok_emb=emb.ptr, emb_type=Q4_K,
+                        out_norm=ones.ptr, output=head.ptr, out_type=Q6_K, key_cache=kc.ptr, value_cache=vc.ptr,
+                        layers=L)
+    tokens = np.random.default_rng(6).integers(0, VOCAB, size=n_tokens).astype(np.int32)
+
+    def run():
+        rc = lib.holo_llama_forward(C.byref(m), tokens.ctypes.data, n_tokens, 0, logits.ptr, 0)
+        if rc != 0:
+            raise holo.HoloError(f"holo_llama_forward returned {rc}")
+
+    run()
+    lib.cuda_sync()
+    ev = holo.Events()
+    reps = 3
+    ev.start()
+    for _ in range(reps):
+        run()
+    ms = ev.stop() / reps
+    ev.close()
+    holo.check("prompt forward q4_k_m")
+    return {"prompt_tokens": n_tokens, "prompt_ms": round(ms, 2),
+            "prompt_tokens_per_s": round(n_tokens / (ms * 1e-3), 1),
+            "types": "Q4_K q/k/o/gate/up and embeddings; Q6_K v, down and head"}
+
+
 def prompt_forward(lib, layers, head, ones, graph_step_ms, n_tokens=512, decode_steps=32):
     """A 512-token prompt through the 32 synthetic Llama-2-7B layers in one pass
     (holo_llama_forward): Q4_0 matmuls on the MFMA prefill GEMM, causal prefill
@@ -558,6 +615,8 @@ def main():
         head = holo.DeviceBuffer.from_array(synth.blocks(Q8_0, VOCAB, DIM, synth.tensor_seed(BASE_SEED, 5, 0, 7)))
         ones = holo.DeviceBuffer.from_array(np.ones(DIM, np.float32))
         print(json.dumps({"config4_prompt_forward_512": prompt_forward(lib, layers, head, ones, None)}), flush=True)
+        del layers
+        print(json.dumps({"prompt_forward_512_q4_k_m": prompt_forward_q4_k_m(lib)}), flush=True)
         return
     stream = lib.holo_stream_create()
     lib.holo_set_stream(stream)  # graphs capture a non-null stream
@@ -622,6 +681,8 @@ def main():
                 f"(unfused {unfused_ms:.3f} ms)")
             extra["config4_prompt_forward_512"] = prompt_forward(lib, layers, head, ones, full_ms)
             log(f"config 4 prompt forward: {extra['config4_prompt_forward_512']}")
+            extra["prompt_forward_512_q4_k_m"] = prompt_forward_q4_k_m(lib)
+            log(f"prompt forward, Q4_K_M mix: {extra['prompt_forward_512_q4_k_m']}")
             del head
 
         del layers

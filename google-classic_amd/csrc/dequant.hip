@@ -13,49 +13,100 @@
 
 namespace holo {
 
-__global__ __launch_bounds__(256) void dequant_q4_0_kernel(float *__restrict__ y, const uint8_t *__restrict__ W,
+// Output element: the fp32 dequantised value, or that value rounded to f16
+// (round to nearest even: v_cvt_f16_f32), the weight panel of the batched
+// f16 product.
+template <typename T>
+__device__ __forceinline__ T out_of(float v);
+template <>
+__device__ __forceinline__ float out_of<float>(float v)
+{
+    return v;
+}
+template <>
+__device__ __forceinline__ _Float16 out_of<_Float16>(float v)
+{
+    // The empty asm makes v a register value: without it the compiler folds
+    // the last multiply and the conversion into v_fma_mixlo_f16(a, b, +0),
+    // which rounds the exact product to f16 once (not f32, then f16) and
+    // turns a -0 product into +0.
+    asm("" : "+v"(v));
+    return (_Float16)v;
+}
+
+// The 32 values of one block to o: fp32 as 32 stores (o is only 4-byte
+// aligned in holo_dequant); f16 packed in pairs and written as four 16-byte
+// stores (holo_dequant_f16 requires a 16-byte-aligned panel).
+template <typename T>
+__device__ __forceinline__ void store32(T *o, const float (&v)[32]);
+template <>
+__device__ __forceinline__ void store32<float>(float *o, const float (&v)[32])
+{
+#pragma unroll
+    for (int i = 0; i < 32; i++) o[i] = v[i];
+}
+template <>
+__device__ __forceinline__ void store32<_Float16>(_Float16 *o, const float (&v)[32])
+{
+    uint32_t w[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const uint32_t lo = __builtin_bit_cast(uint16_t, out_of<_Float16>(v[2 * i]));
+        const uint32_t hi = __builtin_bit_cast(uint16_t, out_of<_Float16>(v[2 * i + 1]));
+        w[i] = lo | (hi << 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) ((uint4 *)o)[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void dequant_q4_0_kernel(T *__restrict__ y, const uint8_t *__restrict__ W,
                                                             int64_t nblocks)
 {
     int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= nblocks) return;
     Q4_0Unit u = load_q4_0(W, g, nblocks * 18);
-    float *o = y + g * 32;
+    float v[32];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             uint32_t b = (u.q[i] >> (8 * k)) & 0xFFu;
-            o[4 * i + k] = u.d * (float)((int)(b & 15u) - 8);
-            o[16 + 4 * i + k] = u.d * (float)((int)(b >> 4) - 8);
+            v[4 * i + k] = u.d * (float)((int)(b & 15u) - 8);
+            v[16 + 4 * i + k] = u.d * (float)((int)(b >> 4) - 8);
         }
     }
+    store32<T>(y + g * 32, v);
 }
 
-__global__ __launch_bounds__(256) void dequant_q8_0_kernel(float *__restrict__ y, const uint8_t *__restrict__ W,
+template <typename T>
+__global__ __launch_bounds__(256) void dequant_q8_0_kernel(T *__restrict__ y, const uint8_t *__restrict__ W,
                                                             int64_t nblocks)
 {
     int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= nblocks) return;
     Q8_0Unit u = load_q8_0(W, g, nblocks * 34);
-    float *o = y + g * 32;
+    float v[32];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             int q = (int)(int8_t)((u.q[i] >> (8 * k)) & 0xFFu);
-            o[4 * i + k] = u.d * (float)q;
+            v[4 * i + k] = u.d * (float)q;
         }
     }
+    store32<T>(y + g * 32, v);
 }
 
 // One thread per sub-block (32 weights).
-__global__ __launch_bounds__(256) void dequant_q4_k_kernel(float *__restrict__ y, const uint8_t *__restrict__ W,
+template <typename T>
+__global__ __launch_bounds__(256) void dequant_q4_k_kernel(T *__restrict__ y, const uint8_t *__restrict__ W,
                                                             int64_t nunits)
 {
     int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= nunits) return;
     Q4_KUnit u = load_q4_k(W, g);
-    float *o = y + g * 32;
+    float v[32];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
 #pragma unroll
@@ -63,15 +114,17 @@ __global__ __launch_bounds__(256) void dequant_q4_k_kernel(float *__restrict__ y
             uint32_t b = (u.q[i] >> (8 * k)) & 0xFFu;
             float p0 = u.dsc * (float)(b & 15u);
             float p1 = u.dsc * (float)(b >> 4);
-            o[4 * i + k] = p0 - u.dmn;
-            o[16 + 4 * i + k] = p1 - u.dmn;
+            v[4 * i + k] = p0 - u.dmn;
+            v[16 + 4 * i + k] = p1 - u.dmn;
         }
     }
+    store32<T>(y + g * 32, v);
 }
 
 // One thread per (superblock, half, l): 4 outputs at l, l+32, l+64, l+96 of
 // the half (quant.c:252-268).
-__global__ __launch_bounds__(256) void dequant_q6_k_kernel(float *__restrict__ y, const uint8_t *__restrict__ W,
+template <typename T>
+__global__ __launch_bounds__(256) void dequant_q6_k_kernel(T *__restrict__ y, const uint8_t *__restrict__ W,
                                                             int64_t nsb)
 {
     int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -89,11 +142,67 @@ __global__ __launch_bounds__(256) void dequant_q6_k_kernel(float *__restrict__ y
     int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
     int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
     int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
-    float *o = y + sbi * 256 + 128 * half;
-    o[l] = (d * (float)sc[is + 0]) * (float)q1;
-    o[l + 32] = (d * (float)sc[is + 2]) * (float)q2;
-    o[l + 64] = (d * (float)sc[is + 4]) * (float)q3;
-    o[l + 96] = (d * (float)sc[is + 6]) * (float)q4;
+    T *o = y + sbi * 256 + 128 * half;
+    o[l] = out_of<T>((d * (float)sc[is + 0]) * (float)q1);
+    o[l + 32] = out_of<T>((d * (float)sc[is + 2]) * (float)q2);
+    o[l + 64] = out_of<T>((d * (float)sc[is + 4]) * (float)q3);
+    o[l + 96] = out_of<T>((d * (float)sc[is + 6]) * (float)q4);
+}
+
+// F32 rows to f16 (8 per thread; n a multiple of 8).
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(_Float16 *__restrict__ y, const float *__restrict__ x,
+                                                         int64_t n8)
+{
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n8) return;
+    const float4 a = ((const float4 *)x)[2 * g], b = ((const float4 *)x)[2 * g + 1];
+    _Float16 *o = y + 8 * g;
+    o[0] = (_Float16)a.x;
+    o[1] = (_Float16)a.y;
+    o[2] = (_Float16)a.z;
+    o[3] = (_Float16)a.w;
+    o[4] = (_Float16)b.x;
+    o[5] = (_Float16)b.y;
+    o[6] = (_Float16)b.z;
+    o[7] = (_Float16)b.w;
+}
+
+// Launch the dequant of n weights of `type` into y; false for a type without
+// a block kernel here.
+template <typename T>
+static bool dequant_into(T *y, const uint8_t *W, int64_t n, int type)
+{
+    switch (type) {
+    case HOLO_TYPE_Q4_0: {
+        const int64_t nb = n / 32;
+        if (nb)
+            hipLaunchKernelGGL(dequant_q4_0_kernel<T>, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, stream(), y,
+                               W, nb);
+        return true;
+    }
+    case HOLO_TYPE_Q8_0: {
+        const int64_t nb = n / 32;
+        if (nb)
+            hipLaunchKernelGGL(dequant_q8_0_kernel<T>, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, stream(), y,
+                               W, nb);
+        return true;
+    }
+    case HOLO_TYPE_Q4_K: {
+        const int64_t nu = (n / 256) * 8;
+        if (nu)
+            hipLaunchKernelGGL(dequant_q4_k_kernel<T>, dim3((unsigned)((nu + 255) / 256)), dim3(256), 0, stream(), y,
+                               W, nu);
+        return true;
+    }
+    case HOLO_TYPE_Q6_K: {
+        const int64_t nsb = n / 256;
+        if (nsb)
+            hipLaunchKernelGGL(dequant_q6_k_kernel<T>, dim3((unsigned)((nsb * 64 + 255) / 256)), dim3(256), 0,
+                               stream(), y, W, nsb);
+        return true;
+    }
+    default: return false;
+    }
 }
 
 // Bit-identity holds for every finite scale (zeros, subnormals and normals).
@@ -115,30 +224,35 @@ extern "C" void holo_dequant(float *dst, const void *src, int64_t n, int type)
         HOLO_REJECT("holo_dequant: source must be 4-byte aligned");
         return;
     }
-    const uint8_t *W = (const uint8_t *)src;
-    switch (type) {
-    case HOLO_TYPE_Q4_0: {
-        int64_t nb = n / 32;
-        if (nb) hipLaunchKernelGGL(dequant_q4_0_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, stream(), dst, W, nb);
-        break;
-    }
-    case HOLO_TYPE_Q8_0: {
-        int64_t nb = n / 32;
-        if (nb) hipLaunchKernelGGL(dequant_q8_0_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, stream(), dst, W, nb);
-        break;
-    }
-    case HOLO_TYPE_Q4_K: {
-        int64_t nu = (n / 256) * 8;
-        if (nu) hipLaunchKernelGGL(dequant_q4_k_kernel, dim3((unsigned)((nu + 255) / 256)), dim3(256), 0, stream(), dst, W, nu);
-        break;
-    }
-    case HOLO_TYPE_Q6_K: {
-        int64_t nsb = n / 256;
-        if (nsb) hipLaunchKernelGGL(dequant_q6_k_kernel, dim3((unsigned)((nsb * 64 + 255) / 256)), dim3(256), 0, stream(), dst, W, nsb);
-        break;
-    }
-    default:
+    if (!dequant_into(dst, (const uint8_t *)src, n, type)) {
         HOLO_REJECT("holo_dequant: unsupported type");
+        return;
+    }
+    HOLO_LAUNCH_CHECK();
+}
+
+extern "C" void holo_dequant_f16(void *dst, const void *src, int64_t n, int type)
+{
+    if (n <= 0) return;
+    if (!dst || !src) {
+        HOLO_REJECT("holo_dequant_f16: null pointer");
+        return;
+    }
+    if ((((uintptr_t)src | (uintptr_t)dst) & 15u) != 0 || n % 32 != 0) {
+        HOLO_REJECT("holo_dequant_f16: source and destination must be 16-byte aligned, n a multiple of 32");
+        return;
+    }
+    _Float16 *y = (_Float16 *)dst;
+    if (type == HOLO_TYPE_F16) {
+        HOLO_CHECK(hipMemcpyAsync(y, src, (size_t)n * 2, hipMemcpyDeviceToDevice, stream()));
+        return;
+    }
+    if (type == HOLO_TYPE_F32) {
+        const int64_t n8 = n / 8;
+        hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, stream(), y,
+                           (const float *)src, n8);
+    } else if (!dequant_into(y, (const uint8_t *)src, n, type)) {
+        HOLO_REJECT("holo_dequant_f16: unsupported type");
         return;
     }
     HOLO_LAUNCH_CHECK();

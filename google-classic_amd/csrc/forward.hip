@@ -57,10 +57,21 @@ void norm_or_copy(float *dst, const float *x, const float *w, int rows, int n, f
 
 bool fused_gemv_type(int t) { return t == HOLO_TYPE_Q4_0 || t == HOLO_TYPE_Q8_0 || t == HOLO_TYPE_Q4_K; }
 
-// The prefill GEMM takes the rows: Q4_0, at least 64 rows, not in exact mode.
+// The batched product takes the rows: at least 64, not in exact mode, in_dim
+// whole blocks of the type (holo_matmul_batch: Q4_0 on its own kernels, the
+// other types on a dequantised f16 panel).
 bool gemm_rows(int type, int rows, int in_dim, int exact)
 {
-    return type == HOLO_TYPE_Q4_0 && rows >= 64 && !exact && in_dim % 32 == 0;
+    if (rows < 64 || exact) return false;
+    switch (type) {
+    case HOLO_TYPE_Q4_0:
+    case HOLO_TYPE_Q8_0:
+    case HOLO_TYPE_F16:
+    case HOLO_TYPE_F32: return in_dim % 32 == 0;
+    case HOLO_TYPE_Q4_K:
+    case HOLO_TYPE_Q6_K: return in_dim % 256 == 0;
+    default: return false;
+    }
 }
 
 // q, k, v of n rows of xb.  One GEMM over the three matrices when the rows
@@ -75,7 +86,7 @@ void matmul_qkv(float *q, float *k, float *v, const holo_llama_layer_t &L, const
         float *Y[3] = {q, k, v};
         const void *W[3] = {L.wq, L.wk, L.wv};
         const int N[3] = {q_dim, kv_dim, kv_dim};
-        holo_matmul_batch_q4_0_multi(Y, W, N, 3, xb, n, dim, nullptr);
+        holo_matmul_batch_multi(Y, W, N, 3, xb, n, dim, t);
         return;
     }
     if (same && fused_gemv_type(t) && !gemm_rows(t, n, dim, exact)) {
@@ -100,7 +111,7 @@ void matmul_gate_up(float *h, float *h2, const holo_llama_layer_t &L, const floa
         float *Y[2] = {h, h2};
         const void *W[2] = {L.w1, L.w3};
         const int N[2] = {ffn, ffn};
-        holo_matmul_batch_q4_0_multi(Y, W, N, 2, xb, n, dim, nullptr);
+        holo_matmul_batch_multi(Y, W, N, 2, xb, n, dim, t);
     } else if (same && fused_gemv_type(t) && !gemm_rows(t, n, dim, exact)) {
         for (int r = 0; r < n; r++)
             holo_batched_ffn_gate_up(h + (int64_t)r * ffn, L.w1, L.w3, xb + (int64_t)r * dim, ffn, dim, t);
@@ -120,8 +131,8 @@ void holo_matmul_rows(float *Y, const void *W, const float *X, int rows, int out
                       int exact)
 {
     if (rows <= 0 || out_dim <= 0) return;
-    if (type == HOLO_TYPE_Q4_0 && rows >= 64 && !exact && in_dim % 32 == 0) {
-        holo_matmul_batch_q4_0(Y, W, X, rows, out_dim, in_dim, nullptr);
+    if (gemm_rows(type, rows, in_dim, exact)) {
+        holo_matmul_batch(Y, W, X, rows, out_dim, in_dim, type);
         return;
     }
     for (int r = 0; r < rows; r++)
@@ -209,7 +220,7 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
         if (one && fused_gemv_type(L.wo_type)) {
             holo_matmul_add(x, L.wo, att, x, dim, q_dim, L.wo_type);
         } else if (gemm_rows(L.wo_type, n, q_dim, exact)) {
-            holo_matmul_batch_q4_0_add(x, L.wo, att, x, n, dim, q_dim);  // the add in the GEMM's store
+            holo_matmul_batch_add(x, L.wo, att, x, n, dim, q_dim, L.wo_type);  // the add in the GEMM's store
         } else {
             holo_matmul_rows(xb, L.wo, att, n, dim, q_dim, L.wo_type, exact);
             cuda_vec_add(x, x, xb, n * dim);
@@ -226,8 +237,8 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
                 float *Y[2] = {hb, hb2};
                 const void *W[2] = {L.w1, L.w3};
                 const int N[2] = {ffn, ffn};
-                holo_matmul_batch_q4_0_multi(Y, W, N, 2, xb, n, dim, nullptr);
-                holo_matmul_batch_q4_0_swiglu_add(x, L.w2, hb, hb2, x, n, dim, ffn);
+                holo_matmul_batch_multi(Y, W, N, 2, xb, n, dim, L.w1_type);
+                holo_matmul_batch_swiglu_add(x, L.w2, hb, hb2, x, n, dim, ffn, L.w2_type);
                 continue;
             }
             matmul_gate_up(hb, hb2, L, xb, n, ffn, dim, exact);
@@ -235,7 +246,7 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
         if (one && fused_gemv_type(L.w2_type)) {
             holo_matmul_add(x, L.w2, hb, x, dim, ffn, L.w2_type);
         } else if (gemm_rows(L.w2_type, n, ffn, exact)) {
-            holo_matmul_batch_q4_0_add(x, L.w2, hb, x, n, dim, ffn);
+            holo_matmul_batch_add(x, L.w2, hb, x, n, dim, ffn, L.w2_type);
         } else {
             holo_matmul_rows(xb, L.w2, hb, n, dim, ffn, L.w2_type, exact);
             cuda_vec_add(x, x, xb, n * dim);

@@ -188,7 +188,9 @@ struct PGeo {
     static constexpr int NA = TM * S * 4 / NT;         // 16-byte activation pieces per thread
     static constexpr int ND = (TM * S + NT - 1) / NT;  // activation scales per thread
     static constexpr int NB = (TN * S + NT - 1) / NT;  // weight blocks per thread
+    static constexpr int NWP = TN * S * 4 / NT;        // 16-byte weight-panel pieces per thread
     static_assert((TM * S * 4) % NT == 0, "activation pieces must split evenly over the threads");
+    static_assert((TN * S * 4) % NT == 0, "weight-panel pieces must split evenly over the threads");
 };
 
 // f16 (q - 8) of the eight nibbles of x = qs[4j..4j+3]: lo[0..1] hold k = 4j..4j+3
@@ -211,13 +213,17 @@ __device__ __forceinline__ void nib_f16(uint32_t x, uint32_t lo[2], uint32_t hi[
 // indices past the row's last block read the last block again (in bounds,
 // never used).
 // XF16: f16 activations without scales, weights dequantised to f16 as they
-// are staged (the f16 product); otherwise the Q8_0 product.
-template <int WM, int WN, int S, bool XF16, int WGM = 2, int WGN = 2>
+// are staged (the f16 product); otherwise the Q8_0 product.  WP (with XF16):
+// the weights are an f16 panel [N][K] already (any block format, dequantised
+// by holo_dequant_f16), fetched and staged as the activations are.
+template <int WM, int WN, int S, bool XF16, int WGM = 2, int WGN = 2, bool WP = false>
 struct PStage {
     using G = PGeo<WM, WN, S, WGM, WGN>;
+    static_assert(!WP || XF16, "a weight panel needs f16 activations");
     v4u ra[G::NA];
     uint32_t rd[G::ND];
-    Q4_0Unit rb[G::NB];
+    Q4_0Unit rb[WP ? 1 : G::NB];
+    v4u rw[WP ? G::NWP : 1];
 
     __device__ __forceinline__ void fetch(const PrefillArgs &a, const PrefillMat &w, int tid, int m0, int n0, int kb0)
     {
@@ -235,6 +241,16 @@ struct PStage {
                 const int v = min(tid + G::NT * i, G::TM * S - 1), r = v / S, b = min(kb0 + v % S, nb - 1);
                 rd[i] = a.D[(int64_t)min(m0 + r, a.M - 1) * nb + b];
             }
+        }
+        if constexpr (WP) {
+            const _Float16 *wp = (const _Float16 *)w.W;
+#pragma unroll
+            for (int i = 0; i < G::NWP; i++) {
+                const int p = tid + G::NT * i, n = p / (4 * S), c = p % (4 * S);
+                const int b = min(kb0 + c / 4, nb - 1);
+                rw[i] = *(const v4u *)(wp + (int64_t)min(n0 + n, w.N - 1) * K + (int64_t)b * 32 + (c % 4) * 8);
+            }
+            return;
         }
 #pragma unroll
         for (int i = 0; i < G::NB; i++) {
@@ -257,6 +273,15 @@ struct PStage {
                 const int v = tid + G::NT * i;
                 if (v < G::TM * S) ((uint16_t *)(base + G::AD_OFF))[v] = (uint16_t)rd[i];
             }
+        }
+        if constexpr (WP) {
+            // the same k order as the unpacked blocks below: row n, k = 8c .. 8c + 7
+#pragma unroll
+            for (int i = 0; i < G::NWP; i++) {
+                const int p = tid + G::NT * i, n = p / (4 * S), c = p % (4 * S);
+                *(v4u *)(base + G::B_OFF + (n * G::ROW + c * 8) * 2) = rw[i];
+            }
+            return;
         }
 #pragma unroll
         for (int i = 0; i < G::NB; i++) {
@@ -288,7 +313,7 @@ struct PStage {
 
 // D: stages of global loads in flight (1 or 2); OCC: workgroups per CU the
 // register allocation is bounded for.
-template <int WM, int WN, int S, int D, int OCC, bool XF16, int WGM = 2, int WGN = 2>
+template <int WM, int WN, int S, int D, int OCC, bool XF16, int WGM = 2, int WGN = 2, bool WP = false>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_q4_0_f16_k(PrefillArgs a)
 {
     using G = PGeo<WM, WN, S, WGM, WGN>;
@@ -377,7 +402,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_q4_0_f16_k(PrefillAr
         }
     };
 
-    PStage<WM, WN, S, XF16, WGM, WGN> pa;
+    PStage<WM, WN, S, XF16, WGM, WGN, WP> pa;
     pa.fetch(a, w, tid, m0, n0, 0);
     pa.stash(lds, tid);
     if constexpr (D == 1) {
@@ -392,7 +417,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_q4_0_f16_k(PrefillAr
     } else {
         // two register sets carry stages st+1 and st+2 while stage st is
         // multiplied, so each stage's loads have two stages of products to land
-        PStage<WM, WN, S, XF16, WGM, WGN> pb;
+        PStage<WM, WN, S, XF16, WGM, WGN, WP> pb;
         if (nst > 1) pa.fetch(a, w, tid, m0, n0, S);
         if (nst > 2) pb.fetch(a, w, tid, m0, n0, 2 * S);
         __syncthreads();
@@ -439,13 +464,13 @@ static int prefill_tn(int M, int N)
     return tiles128 >= cus ? 128 : 64;
 }
 
-template <int WM, int WN, int S, int D, int OCC, bool XF16, int WGM = 2, int WGN = 2>
+template <int WM, int WN, int S, int D, int OCC, bool XF16, int WGM = 2, int WGN = 2, bool WP = false>
 static void launch_prefill(PrefillArgs a)
 {
     using G = PGeo<WM, WN, S, WGM, WGN>;
     a.ntm = (a.M + G::TM - 1) / G::TM;
     a.tiles = a.ntm * ((a.N + G::TN - 1) / G::TN);
-    auto kern = gemm_q4_0_f16_k<WM, WN, S, D, OCC, XF16, WGM, WGN>;
+    auto kern = gemm_q4_0_f16_k<WM, WN, S, D, OCC, XF16, WGM, WGN, WP>;
     static bool attr = false;
     if (!attr) {
         HOLO_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS));
@@ -487,9 +512,10 @@ void holo_quantize_act_q8_0(void *dst_blocks, const float *X, int rows, int k)
 // One launch over nmat matrices (holo_gemm_q4_0_q8_0 and its multi-matrix form).
 // Xq (Q8_0 blocks): the Q8_0 product; otherwise X (fp32, 16-byte aligned):
 // the f16 product, of silu(X) * U when U is given.  R: Y = R + product (one
-// matrix).
+// matrix).  wp: W[i] are f16 panels [N_i][K] (f16 product only), otherwise
+// Q4_0 block streams.
 static void gemm_multi(float *const *Y, const void *const *W, const int *N, int nmat, const void *Xq, const float *X,
-                       int M, int K, const float *U = nullptr, const float *R = nullptr)
+                       int M, int K, const float *U = nullptr, const float *R = nullptr, bool wp = false)
 {
     const bool xf16 = Xq == nullptr;
     const int nb = K / 32;
@@ -553,27 +579,29 @@ static void gemm_multi(float *const *Y, const void *const *W, const int *N, int 
         const int got = e ? sscanf(e, "%d,%d,%d,%d,%d,%d", &tm, &tn, &st, &d, &o, &w) : 0;
         cfg = got >= 5 ? (w == 8 ? 100000 : 0) + (tm / 64) * 10000 + (tn / 64) * 1000 + st * 100 + d * 10 + o : 0;
     }
-    auto go = [&](auto xfc) {
-        constexpr bool XF = decltype(xfc)::value;
+    auto go = [&](auto xfc, auto wpc) {
+        constexpr bool XF = decltype(xfc)::value, WP = decltype(wpc)::value;
+        static_assert(!WP || XF, "a weight panel needs the f16 product");
         const int tiles128 = ((M + 127) / 128) * ((ntot + 127) / 128);
         const int def = prefill_tn(M, ntot) != 128 ? 11422
                         : !XF                       ? 22212
                         : tiles128 >= 2 * num_cus() ? 122222
                                                     : 22222;
         switch (cfg ? cfg : def) {
-        case 21222: launch_prefill<2, 1, 2, 2, 2, XF>(a); break;
-        case 122222: launch_prefill<2, 1, 2, 2, 2, XF, 2, 4>(a); break;
-        case 11412: launch_prefill<1, 1, 4, 1, 2, XF>(a); break;
-        case 11422: launch_prefill<1, 1, 4, 2, 2, XF>(a); break;
+        case 21222: launch_prefill<2, 1, 2, 2, 2, XF, 2, 2, WP>(a); break;
+        case 122222: launch_prefill<2, 1, 2, 2, 2, XF, 2, 4, WP>(a); break;
+        case 11412: launch_prefill<1, 1, 4, 1, 2, XF, 2, 2, WP>(a); break;
+        case 11422: launch_prefill<1, 1, 4, 2, 2, XF, 2, 2, WP>(a); break;
         case 22222:  // the Q8_0 product has no registers for a second stage: one
-            if constexpr (XF) launch_prefill<2, 2, 2, 2, 2, true>(a);
+            if constexpr (XF) launch_prefill<2, 2, 2, 2, 2, true, 2, 2, WP>(a);
             else launch_prefill<2, 2, 2, 1, 2, false>(a);
             break;
-        default: launch_prefill<2, 2, 2, 1, 2, XF>(a); break;
+        default: launch_prefill<2, 2, 2, 1, 2, XF, 2, 2, WP>(a); break;
         }
     };
-    if (xf16) go(std::true_type{});
-    else go(std::false_type{});
+    if (wp) go(std::true_type{}, std::true_type{});
+    else if (xf16) go(std::true_type{}, std::false_type{});
+    else go(std::false_type{}, std::false_type{});
     HOLO_CHECK(hipFreeAsync(ws, stream()));
 }
 
@@ -750,6 +778,143 @@ void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const i
     holo_quantize_act_q8_0(q, X, M, K);
     holo_gemm_q4_0_q8_0_multi(Y, W, N, nmat, q, M, K);
     if (!scratch_q8) HOLO_CHECK(hipFreeAsync(q, stream()));
+}
+
+
+}  // extern "C"
+
+// ---- any weight format: dequantised to an f16 panel, then the f16 product -----------
+//
+// Q8_0, Q4_K, Q6_K, F16 and F32 weights are dequantised bit-exactly (the
+// reference's dequantize_row_*, quant.c:118-311) and rounded to f16 into a
+// stream-ordered workspace, w16 = f16_rne(w); the product over that panel is
+// the f16 product above: Y = sum_k f16_rne(x) * w16, accumulated in fp32 on
+// the matrix cores.  Q4_0 keeps its own kernels (its w16 = f16_rne(f16(dw) *
+// (q - 8)) is the same value, unpacked in the GEMM).
+
+// The formats the panel path takes, with K whole blocks.
+static bool panel_ok(int type, int K)
+{
+    switch (type) {
+    case HOLO_TYPE_Q8_0:
+    case HOLO_TYPE_F16:
+    case HOLO_TYPE_F32: return K % 32 == 0;
+    case HOLO_TYPE_Q4_K:
+    case HOLO_TYPE_Q6_K: return K % 256 == 0;
+    default: return false;
+    }
+}
+
+static bool panel_src_aligned(const void *W, int type)
+{
+    const uintptr_t a = (uintptr_t)W;
+    return type == HOLO_TYPE_F32 ? (a & 15u) == 0 : type == HOLO_TYPE_F16 ? (a & 1u) == 0 : (a & 3u) == 0;
+}
+
+static void gemm_panel(float *const *Y, const void *const *W, const int *N, int nmat, const float *X, int M, int K,
+                       int type, const float *U, const float *R)
+{
+    size_t total = 0;
+    for (int i = 0; i < nmat; i++) total += (size_t)N[i] * K * 2;  // each a multiple of 64 bytes
+    void *ws = nullptr;
+    HOLO_CHECK(hipMallocAsync(&ws, total, stream()));
+    if (!ws) return;
+    const void *P[kPrefillMats];
+    size_t off = 0;
+    for (int i = 0; i < nmat; i++) {
+        P[i] = (const uint8_t *)ws + off;
+        holo_dequant_f16((void *)P[i], W[i], (int64_t)N[i] * K, type);
+        off += (size_t)N[i] * K * 2;
+    }
+    gemm_multi(Y, P, N, nmat, nullptr, X, M, K, U, R, true);
+    HOLO_CHECK(hipFreeAsync(ws, stream()));
+}
+
+extern "C" {
+
+void holo_matmul_batch(float *Y, const void *W, const float *X, int M, int N, int K, int type)
+{
+    if (M <= 0 || N <= 0) return;
+    if (type == HOLO_TYPE_Q4_0) {
+        holo_matmul_batch_q4_0(Y, W, X, M, N, K, nullptr);
+        return;
+    }
+    if (!Y || !W || !X) {
+        HOLO_REJECT("holo_matmul_batch: null pointer");
+        return;
+    }
+    if (M < 64 || !panel_ok(type, K) || !panel_src_aligned(W, type) || ((uintptr_t)X & 15u)) {
+        for (int m = 0; m < M; m++) holo_matmul(Y + (int64_t)m * N, W, X + (int64_t)m * K, N, K, type);
+        return;
+    }
+    gemm_panel(&Y, &W, &N, 1, X, M, K, type, nullptr, nullptr);
+}
+
+void holo_matmul_batch_multi(float *const *Y, const void *const *W, const int *N, int nmat, const float *X, int M,
+                             int K, int type)
+{
+    if (M <= 0) return;
+    if (type == HOLO_TYPE_Q4_0) {
+        holo_matmul_batch_q4_0_multi(Y, W, N, nmat, X, M, K, nullptr);
+        return;
+    }
+    if (!Y || !W || !N || !X || !multi_fits(N, nmat)) {
+        HOLO_REJECT("holo_matmul_batch_multi: null array, or not 1..3 matrices whose N are multiples of 128");
+        return;
+    }
+    bool ok = M >= 64 && panel_ok(type, K) && !((uintptr_t)X & 15u);
+    for (int i = 0; i < nmat; i++) ok = ok && Y[i] && W[i] && panel_src_aligned(W[i], type);
+    if (!ok) {
+        for (int i = 0; i < nmat; i++) holo_matmul_batch(Y[i], W[i], X, M, N[i], K, type);
+        return;
+    }
+    gemm_panel(Y, W, N, nmat, X, M, K, type, nullptr, nullptr);
+}
+
+void holo_matmul_batch_add(float *Y, const void *W, const float *X, const float *R, int M, int N, int K, int type)
+{
+    if (M <= 0 || N <= 0) return;
+    if (type == HOLO_TYPE_Q4_0) {
+        holo_matmul_batch_q4_0_add(Y, W, X, R, M, N, K);
+        return;
+    }
+    if (!Y || !W || !X || !R) {
+        HOLO_REJECT("holo_matmul_batch_add: null pointer");
+        return;
+    }
+    if (M >= 64 && panel_ok(type, K) && panel_src_aligned(W, type) && !((uintptr_t)X & 15u)) {
+        gemm_panel(&Y, &W, &N, 1, X, M, K, type, nullptr, R);  // the add in the GEMM's store
+        return;
+    }
+    // row by row; Y may alias R, so each row's product goes through a scratch row
+    float *t = nullptr;
+    HOLO_CHECK(hipMallocAsync((void **)&t, sizeof(float) * (size_t)N, stream()));
+    if (!t) return;
+    for (int m = 0; m < M; m++) {
+        holo_matmul(t, W, X + (int64_t)m * K, N, K, type);
+        cuda_vec_add(Y + (int64_t)m * N, R + (int64_t)m * N, t, N);
+    }
+    HOLO_CHECK(hipFreeAsync(t, stream()));
+}
+
+void holo_matmul_batch_swiglu_add(float *Y, const void *W, float *G, const float *U, const float *R, int M, int N,
+                                  int K, int type)
+{
+    if (M <= 0 || N <= 0) return;
+    if (type == HOLO_TYPE_Q4_0) {
+        holo_matmul_batch_q4_0_swiglu_add(Y, W, G, U, R, M, N, K);
+        return;
+    }
+    if (!Y || !W || !G || !U || !R) {
+        HOLO_REJECT("holo_matmul_batch_swiglu_add: null pointer");
+        return;
+    }
+    if (M >= 64 && panel_ok(type, K) && panel_src_aligned(W, type) && !(((uintptr_t)G | (uintptr_t)U) & 15u)) {
+        gemm_panel(&Y, &W, &N, 1, G, M, K, type, U, R);  // silu(G) * U in the activation panel
+        return;
+    }
+    cuda_silu_mul(G, G, U, M * K);
+    holo_matmul_batch_add(Y, W, G, R, M, N, K, type);
 }
 
 }  // extern "C"

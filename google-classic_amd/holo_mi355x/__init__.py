@@ -131,6 +131,7 @@ _SIGS = {
     "holo_gemv_chain_status": (_I, []),
     "holo_gemv_set_launch": (None, [_I, _I]),
     "holo_dequant": (None, [_P, _P, _I64, _I]),
+    "holo_dequant_f16": (None, [_P, _P, _I64, _I]),
     "holo_batched_qkv": (None, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I]),
     "holo_batched_ffn_gate_up": (None, [_P, _P, _P, _P, _I, _I, _I]),
     "holo_quantize_act_q8_0": (None, [_P, _P, _I, _I]),
@@ -147,6 +148,10 @@ _SIGS = {
     "holo_matmul_add": (None, [_P, _P, _P, _P, _I, _I, _I]),
     "holo_matmul_batch_q4_0_add": (None, [_P, _P, _P, _P, _I, _I, _I]),
     "holo_matmul_batch_q4_0_swiglu_add": (None, [_P, _P, _P, _P, _P, _I, _I, _I]),
+    "holo_matmul_batch": (None, [_P, _P, _P, _I, _I, _I, _I]),
+    "holo_matmul_batch_multi": (None, [_P, _P, _P, _I, _P, _I, _I, _I]),
+    "holo_matmul_batch_add": (None, [_P, _P, _P, _P, _I, _I, _I, _I]),
+    "holo_matmul_batch_swiglu_add": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
     # GGUF files (include/holo_gguf.h)
     "holo_gguf_open": (_P, [C.c_char_p]),
     "holo_gguf_close": (None, [_P]),

@@ -9,7 +9,9 @@
  * (src/ai/llm_cuda.c:574-891).  holo_llama_forward computes the same result
  * for tokens[0..n) at positions pos0..pos0+n-1:
  *   - each matrix multiplies all n rows at once (holo_matmul_rows: the MFMA
- *     prefill GEMM for Q4_0 with n >= 64, otherwise one GEMV per row);
+ *     prefill GEMM with n >= 64 -- Q4_0 unpacked in the GEMM, the other
+ *     types over an f16 panel dequantised first -- otherwise one GEMV per
+ *     row);
  *   - RoPE, the KV-cache writes and the norms take all rows in one launch;
  *   - attention is causal over the prompt (holo_attention_prefill): row m sees
  *     positions 0..pos0+m, as token pos0+m does in the reference.
@@ -48,8 +50,8 @@ void holo_embedding_rows(float *dst, const void *embeddings, const int *tokens, 
 void holo_attention_prefill(float *out, const float *q, const float *k_cache, const float *v_cache, int rows,
                             int pos0, int head_dim, int n_heads, int n_kv_heads);
 /* Y[rows][out] = X[rows][in] . W^T for any GEMV type (holo_matmul per row).
- * Q4_0 with rows >= 64 takes the MFMA GEMM over Q8_0-quantised activations
- * (holo_matmul_batch_q4_0) unless `exact` is set.                             */
+ * rows >= 64 with in_dim whole blocks takes the batched MFMA product
+ * (holo_matmul_batch) unless `exact` is set.                                  */
 void holo_matmul_rows(float *Y, const void *W, const float *X, int rows, int out_dim, int in_dim, int type,
                       int exact);
 

@@ -120,6 +120,11 @@ void holo_time_next_launch(void *start_event, void *stop_event);
  * CPU routines dequantize_row_q8_0 / q4_0 / q4_k / q6_k
  * (src/ai/quant.c:118-128, 136-153, 277-311, 241-271).                     */
 void holo_dequant(float *dst, const void *src, int64_t n, int type);
+/* dst[n] (f16) = f16_rne of the same values, for Q8_0 / Q4_0 / Q4_K / Q6_K
+ * blocks, and of F32 (16-byte aligned) and F16 (copied) rows: the weight panel
+ * of the batched f16 product.  dst 16-byte aligned, n a multiple of 32.
+ * No reference counterpart (the reference dequantises to fp32 only).       */
+void holo_dequant_f16(void *dst, const void *src, int64_t n, int type);
 
 /* ---- fused multi-GEMV for every served format --------------------------------
  * Same contract as cuda_batched_qkv_q8_0 / cuda_batched_ffn_gate_up_q8_0
@@ -205,6 +210,20 @@ void holo_prefill_set_mode(int mode);
 int holo_prefill_get_mode(void);
 void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const int *N, int nmat,
                                   const float *X, int M, int K, void *scratch_q8);
+/* The batched products for any weight type the GEMVs serve (Q4_0, Q8_0, Q4_K,
+ * Q6_K, F16, F32), with the contracts of the Q4_0 calls above.  Q4_0 goes to
+ * them.  Every other type, for M >= 64 and K whole blocks (Q4_K, Q6_K: K a
+ * multiple of 256), is dequantised into a stream-ordered f16 panel workspace
+ * (holo_dequant_f16, N*K*2 bytes per matrix) and multiplied on the f16
+ * product: Y = sum_k f16_rne(x) * f16_rne(w), fp32 accumulation.  Otherwise
+ * one holo_matmul GEMV per row.  No reference counterpart (the reference runs
+ * one GEMV per token, llm.c:1049).                                          */
+void holo_matmul_batch(float *Y, const void *W, const float *X, int M, int N, int K, int type);
+void holo_matmul_batch_multi(float *const *Y, const void *const *W, const int *N, int nmat, const float *X,
+                             int M, int K, int type);
+void holo_matmul_batch_add(float *Y, const void *W, const float *X, const float *R, int M, int N, int K, int type);
+void holo_matmul_batch_swiglu_add(float *Y, const void *W, float *G, const float *U, const float *R, int M, int N,
+                                  int K, int type);
 
 #ifdef __cplusplus
 }
