@@ -184,17 +184,9 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
     float *x = (float *)bufs[1], *xb = (float *)bufs[2], *q = (float *)bufs[3], *k = (float *)bufs[4];
     float *v = (float *)bufs[5], *att = (float *)bufs[6], *hb = (float *)bufs[7], *hb2 = (float *)bufs[8];
 
-    // embeddings
-    if (m->emb_type == HOLO_TYPE_Q4_K) {
-        // no lookup kernel: exact dequantisation of each token's row
-        for (int t = 0; t < n; t++)
-            holo_dequant(x + (int64_t)t * dim,
-                         (const uint8_t *)m->tok_emb + (int64_t)tokens[t] * row_bytes(HOLO_TYPE_Q4_K, dim),
-                         dim, HOLO_TYPE_Q4_K);
-    } else {
-        HOLO_CHECK(hipMemcpyAsync(dtok, tokens, (size_t)n * sizeof(int), hipMemcpyHostToDevice, stream()));
-        holo_embedding_rows(x, m->tok_emb, dtok, n, dim, m->emb_type);
-    }
+    // embeddings: all n rows in one launch
+    HOLO_CHECK(hipMemcpyAsync(dtok, tokens, (size_t)n * sizeof(int), hipMemcpyHostToDevice, stream()));
+    holo_embedding_rows(x, m->tok_emb, dtok, n, dim, m->emb_type);
 
     for (int l = 0; l < m->n_layers; l++) {
         const holo_llama_layer_t &L = m->layers[l];

@@ -909,6 +909,16 @@ __global__ __launch_bounds__(256) void rms_norm_rows4_k(float *dst, const float 
 
 // Embedding rows: row r is token tokens[r] of the table, exact dequantisation
 // (the per-token lookups above, get_embedding of llm.c:941-1008).
+// Weight p (0..31) of a Q4_K unit: (d*sc)*q - dmin*m with both roundings, as
+// dequantize_row_q4_k computes it (quant.c:277-311, no contraction).
+__device__ __forceinline__ float q4_k_weight(const Q4_KUnit &u, int p)
+{
+#pragma clang fp contract(off)
+    const uint32_t b = (u.q[(p & 15) >> 2] >> (8 * (p & 3))) & 0xFFu;
+    const float pv = u.dsc * (float)(p < 16 ? (b & 15u) : (b >> 4));
+    return pv - u.dmn;
+}
+
 __global__ void emb_rows_k(float *dst, const uint8_t *e, const int *tokens, int dim, int type)
 {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -931,6 +941,7 @@ __global__ void emb_rows_k(float *dst, const uint8_t *e, const int *tokens, int 
         break;
     }
     case HOLO_TYPE_Q6_K: v = q6_k_value(e + (t * (dim / 256) + i / 256) * 210, i % 256); break;
+    case HOLO_TYPE_Q4_K: v = q4_k_weight(load_q4_k(e, t * (dim / 32) + i / 32), i % 32); break;
     default: v = ((const float *)e)[t * dim + i]; break;
     }
     dst[r * dim + i] = v;
@@ -1372,7 +1383,7 @@ void holo_embedding_rows(float *dst, const void *embeddings, const int *tokens, 
         return;
     }
     if (type != HOLO_TYPE_F32 && type != HOLO_TYPE_F16 && type != HOLO_TYPE_Q8_0 && type != HOLO_TYPE_Q4_0 &&
-        type != HOLO_TYPE_Q6_K) {
+        type != HOLO_TYPE_Q6_K && type != HOLO_TYPE_Q4_K) {
         HOLO_REJECT("holo_embedding_rows: type without a lookup kernel");
         return;
     }

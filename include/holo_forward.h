@@ -41,7 +41,9 @@ void holo_rms_norm_rows(float *dst, const float *x, const float *weight, int row
 void holo_rope_rows(float *q, float *k, int rows, int pos0, int head_dim, int n_heads, int n_kv_heads,
                     float freq_base);
 /* cuda_get_embedding_* (cuda_ops.h:121-129) for tokens[0..rows) (a device
- * array of int): F32, F16, Q8_0, Q4_0, Q6_K.                                  */
+ * array of int): F32, F16, Q8_0, Q4_0, Q6_K; and Q4_K, which has no lookup
+ * op in the reference, as the bit-exact dequantize_row_q4_k of each row
+ * (quant.c:277-311), as llm.c:998-1003 looks Q4_K rows up.                 */
 void holo_embedding_rows(float *dst, const void *embeddings, const int *tokens, int rows, int dim, int type);
 /* Causal attention: row m of q (position pos0 + m) against positions
  * 0..pos0+m of this layer's caches [pos][n_kv_heads*head_dim], which must

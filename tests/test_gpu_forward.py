@@ -78,8 +78,8 @@ def test_rope_rows(holo, synth, hd, nh, nkv):
     holo.check("rope_rows")
 
 
-@pytest.mark.parametrize("t", [0, 1, 2, 8, 14], ids=["f32", "f16", "q4_0", "q8_0", "q6_k"])
-def test_embedding_rows(holo, synth, t):
+@pytest.mark.parametrize("t", [0, 1, 2, 8, 14, 12], ids=["f32", "f16", "q4_0", "q8_0", "q6_k", "q4_k"])
+def test_embedding_rows(holo, synth, oracle, t):
     print(f"case embedding_rows {t}", flush=True)
     lib = holo.lib()
     vocab, dim = 300, 512
@@ -93,6 +93,11 @@ def test_embedding_rows(holo, synth, t):
     de, dt, dy, d1 = up(holo, table), up(holo, tokens), holo.DeviceBuffer(4 * len(tokens) * dim), holo.DeviceBuffer(4 * dim)
     lib.holo_embedding_rows(dy.ptr, de.ptr, dt.ptr, len(tokens), dim, t)
     got = down(dy, len(tokens) * dim).reshape(len(tokens), dim)
+    if t == 12:  # no reference lookup op: the bit-exact dequantised rows
+        want = oracle.dequant(12, table, vocab * dim).reshape(vocab, dim)[tokens]
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        holo.check("embedding_rows")
+        return
     fn = {0: lib.cuda_get_embedding_f32, 1: lib.cuda_get_embedding_f16, 2: lib.cuda_get_embedding_q4_0,
           8: lib.cuda_get_embedding_q8_0, 14: lib.cuda_get_embedding_q6_k}[t]
     for r, tok in enumerate(tokens):
