@@ -238,8 +238,11 @@ extern "C" void holo_dequant_f16(void *dst, const void *src, int64_t n, int type
         HOLO_REJECT("holo_dequant_f16: null pointer");
         return;
     }
-    if ((((uintptr_t)src | (uintptr_t)dst) & 15u) != 0 || n % 32 != 0) {
-        HOLO_REJECT("holo_dequant_f16: source and destination must be 16-byte aligned, n a multiple of 32");
+    const uintptr_t sa = (uintptr_t)src;
+    const bool src_ok = type == HOLO_TYPE_F32 ? (sa & 15u) == 0 : type == HOLO_TYPE_F16 ? (sa & 1u) == 0 : (sa & 3u) == 0;
+    if (((uintptr_t)dst & 15u) != 0 || !src_ok || n % 32 != 0) {
+        HOLO_REJECT("holo_dequant_f16: dst must be 16-byte aligned, src 16- (F32), 2- (F16) or 4-byte aligned "
+                    "(blocks), n a multiple of 32");
         return;
     }
     _Float16 *y = (_Float16 *)dst;

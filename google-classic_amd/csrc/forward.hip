@@ -89,6 +89,16 @@ void matmul_qkv(float *q, float *k, float *v, const holo_llama_layer_t &L, const
         holo_matmul_batch_multi(Y, W, N, 3, xb, n, dim, t);
         return;
     }
+    if (!same && gemm_rows(t, n, dim, exact) && gemm_rows(L.wk_type, n, dim, exact) &&
+        gemm_rows(L.wv_type, n, dim, exact) && q_dim % 128 == 0 && kv_dim % 128 == 0) {
+        // mixed types (Q4_K_M: Q6_K v): one launch over the three dequantised panels
+        float *Y[3] = {q, k, v};
+        const void *W[3] = {L.wq, L.wk, L.wv};
+        const int T[3] = {L.wq_type, L.wk_type, L.wv_type};
+        const int N[3] = {q_dim, kv_dim, kv_dim};
+        holo_matmul_batch_multi_types(Y, W, T, N, 3, xb, n, dim);
+        return;
+    }
     if (same && fused_gemv_type(t) && !gemm_rows(t, n, dim, exact)) {
         for (int r = 0; r < n; r++)
             holo_batched_qkv(q + (int64_t)r * q_dim, k + (int64_t)r * kv_dim, v + (int64_t)r * kv_dim, L.wq, L.wk, L.wv,

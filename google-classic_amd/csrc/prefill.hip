@@ -796,6 +796,7 @@ void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const i
 static bool panel_ok(int type, int K)
 {
     switch (type) {
+    case HOLO_TYPE_Q4_0:
     case HOLO_TYPE_Q8_0:
     case HOLO_TYPE_F16:
     case HOLO_TYPE_F32: return K % 32 == 0;
@@ -811,8 +812,9 @@ static bool panel_src_aligned(const void *W, int type)
     return type == HOLO_TYPE_F32 ? (a & 15u) == 0 : type == HOLO_TYPE_F16 ? (a & 1u) == 0 : (a & 3u) == 0;
 }
 
+// Matrix i of type types[i] (or all of `type` when types is null).
 static void gemm_panel(float *const *Y, const void *const *W, const int *N, int nmat, const float *X, int M, int K,
-                       int type, const float *U, const float *R)
+                       int type, const float *U, const float *R, const int *types = nullptr)
 {
     size_t total = 0;
     for (int i = 0; i < nmat; i++) total += (size_t)N[i] * K * 2;  // each a multiple of 64 bytes
@@ -823,7 +825,7 @@ static void gemm_panel(float *const *Y, const void *const *W, const int *N, int 
     size_t off = 0;
     for (int i = 0; i < nmat; i++) {
         P[i] = (const uint8_t *)ws + off;
-        holo_dequant_f16((void *)P[i], W[i], (int64_t)N[i] * K, type);
+        holo_dequant_f16((void *)P[i], W[i], (int64_t)N[i] * K, types ? types[i] : type);
         off += (size_t)N[i] * K * 2;
     }
     gemm_multi(Y, P, N, nmat, nullptr, X, M, K, U, R, true);
@@ -869,6 +871,30 @@ void holo_matmul_batch_multi(float *const *Y, const void *const *W, const int *N
         return;
     }
     gemm_panel(Y, W, N, nmat, X, M, K, type, nullptr, nullptr);
+}
+
+void holo_matmul_batch_multi_types(float *const *Y, const void *const *W, const int *types, const int *N, int nmat,
+                                   const float *X, int M, int K)
+{
+    if (M <= 0) return;
+    if (!Y || !W || !types || !N || !X || !multi_fits(N, nmat)) {
+        HOLO_REJECT("holo_matmul_batch_multi_types: null array, or not 1..3 matrices whose N are multiples of 128");
+        return;
+    }
+    bool same = true;
+    for (int i = 1; i < nmat; i++) same = same && types[i] == types[0];
+    if (same) {
+        holo_matmul_batch_multi(Y, W, N, nmat, X, M, K, types[0]);
+        return;
+    }
+    bool ok = M >= 64 && !((uintptr_t)X & 15u);
+    for (int i = 0; i < nmat; i++)
+        ok = ok && Y[i] && W[i] && panel_ok(types[i], K) && panel_src_aligned(W[i], types[i]);
+    if (!ok) {
+        for (int i = 0; i < nmat; i++) holo_matmul_batch(Y[i], W[i], X, M, N[i], K, types[i]);
+        return;
+    }
+    gemm_panel(Y, W, N, nmat, X, M, K, 0, nullptr, nullptr, types);
 }
 
 void holo_matmul_batch_add(float *Y, const void *W, const float *X, const float *R, int M, int N, int K, int type)

@@ -150,6 +150,7 @@ _SIGS = {
     "holo_matmul_batch_q4_0_swiglu_add": (None, [_P, _P, _P, _P, _P, _I, _I, _I]),
     "holo_matmul_batch": (None, [_P, _P, _P, _I, _I, _I, _I]),
     "holo_matmul_batch_multi": (None, [_P, _P, _P, _I, _P, _I, _I, _I]),
+    "holo_matmul_batch_multi_types": (None, [_P, _P, _P, _P, _I, _P, _I, _I]),
     "holo_matmul_batch_add": (None, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "holo_matmul_batch_swiglu_add": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
     # GGUF files (include/holo_gguf.h)

@@ -122,7 +122,8 @@ void holo_time_next_launch(void *start_event, void *stop_event);
 void holo_dequant(float *dst, const void *src, int64_t n, int type);
 /* dst[n] (f16) = f16_rne of the same values, for Q8_0 / Q4_0 / Q4_K / Q6_K
  * blocks, and of F32 (16-byte aligned) and F16 (copied) rows: the weight panel
- * of the batched f16 product.  dst 16-byte aligned, n a multiple of 32.
+ * of the batched f16 product.  dst 16-byte aligned, src 4-byte aligned (F32:
+ * 16, F16: 2), n a multiple of 32.
  * No reference counterpart (the reference dequantises to fp32 only).       */
 void holo_dequant_f16(void *dst, const void *src, int64_t n, int type);
 
@@ -221,6 +222,12 @@ void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const i
 void holo_matmul_batch(float *Y, const void *W, const float *X, int M, int N, int K, int type);
 void holo_matmul_batch_multi(float *const *Y, const void *const *W, const int *N, int nmat, const float *X,
                              int M, int K, int type);
+/* The multi form with a type per matrix (q/k/v of a Q4_K_M file: Q4_K, Q4_K,
+ * Q6_K): mixed types share one activation panel and one launch, every weight
+ * matrix dequantised to its f16 panel (Q4_0 too, to the same f16 values its
+ * own kernel unpacks); one type throughout is holo_matmul_batch_multi.      */
+void holo_matmul_batch_multi_types(float *const *Y, const void *const *W, const int *types, const int *N, int nmat,
+                                   const float *X, int M, int K);
 void holo_matmul_batch_add(float *Y, const void *W, const float *X, const float *R, int M, int N, int K, int type);
 void holo_matmul_batch_swiglu_add(float *Y, const void *W, float *G, const float *U, const float *R, int M, int N,
                                   int K, int type);

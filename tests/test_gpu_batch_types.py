@@ -175,3 +175,33 @@ def test_matmul_batch_few_rows(holo, synth, oracle, t):
     ref = np.stack([oracle.matmul(t, src, X[m], N, K) for m in range(M)])
     assert normwise_err(down(dY, M * N).reshape(M, N), ref) <= 1e-3
     assert normwise_err(down(dS, M * N).reshape(M, N), R + ref) <= 1e-3
+
+
+def test_matmul_batch_multi_types(holo, synth, oracle):
+    """q/k/v of different types (Q4_K, Q4_0, Q6_K) in one launch: each output
+    bit-identical to its own single-type call -- the Q4_0 panel holds the same
+    f16 values the Q4_0 kernel unpacks, and the accumulation order is the
+    same -- and within the f16 bound of the float64 truth."""
+    lib = holo.lib()
+    M, K = 100, 512
+    types, Ns = (Q4_K, Q4_0, Q6_K), (256, 128, 128)
+    srcs, ws = zip(*[weights(synth, oracle, t, n, K, seed=80 + i) for i, (t, n) in enumerate(zip(types, Ns))])
+    X = synth.normal(M * K, seed=81).reshape(M, K)
+    dWs, dX = [up(holo, s) for s in srcs], up(holo, X)
+    dYm = [holo.DeviceBuffer(4 * M * n) for n in Ns]
+    k = len(Ns)
+    lib.holo_matmul_batch_multi_types((C.c_void_p * k)(*[d.ptr for d in dYm]), (C.c_void_p * k)(*[d.ptr for d in dWs]),
+                                      (C.c_int * k)(*types), (C.c_int * k)(*Ns), k, dX.ptr, M, K)
+    singles = []
+    for i, n in enumerate(Ns):
+        d = holo.DeviceBuffer(4 * M * n)
+        lib.holo_matmul_batch(d.ptr, dWs[i].ptr, dX.ptr, M, n, K, types[i])
+        singles.append(d)
+    lib.cuda_sync()
+    holo.check("batch multi types")
+    x16 = X.astype(np.float16).astype(np.float64)
+    for i, n in enumerate(Ns):
+        got = down(dYm[i], M * n).reshape(M, n)
+        assert np.array_equal(got.view(np.uint32), down(singles[i], M * n).reshape(M, n).view(np.uint32)), i
+        w16 = ws[i].reshape(n, K).astype(np.float16).astype(np.float64)
+        assert np.all(np.abs(got - x16 @ w16.T) <= f16_bound(K, np.abs(x16) @ np.abs(w16).T)), i
