@@ -27,7 +27,7 @@ CASES = [
     # MFMA path: rows ending in an 8-unit segment (24 and 136 units), a
     # ragged last tile, and in_dim 16384 (4 items per wave)
     (Q4_0, 23, 256 * 3), (Q8_0, 19, 256 * 3), (Q4_0, 33, 256 * 17), (Q4_K, 9, 256 * 3), (Q8_0, 40, 16384),
-    # BASELINE configs 1-3 and the config-5 head
+    # BASELINE.json configs 1-3 and the config-5 head
     (Q8_0, 4096, 4096), (Q4_0, 4096, 4096), (Q4_0, 11008, 4096), (Q4_0, 4096, 11008),
     (Q4_K, 14336, 4096), (Q4_K, 4096, 14336), (Q8_0, 32000, 4096),
     # in_dim beyond the LDS staging limit (x read from global memory)
