@@ -36,9 +36,11 @@ The printed JSON line carries
                 (32000x4096 head and 4096x11008 down), config 4 (batched
                 prefill GEMM on the f16 matrix cores: useful TOP/s = 2*M*N*K per
                 kernel time, and its fraction of the dense f16 and int8 peaks;
-                and a 512-token prompt through the 32 layers in one pass),
+                and a 512-token prompt through the 32 layers in one pass,
+                also on a Q4_K_M-style mix of Q4_K and Q6_K matrices),
                 config 5 (full synthetic
-                Llama-2-7B Q4_0 decode step: end-to-end and matmuls-only ms)
+                Llama-2-7B Q4_0 decode step: end-to-end and matmuls-only ms),
+                decode attention at 512 / 2048 / 4096 cached positions
 
 Only the CPU-baseline leg touches oracle/.
 """
