@@ -9,6 +9,8 @@
 #include "common.h"
 #include "quant_blocks.h"
 
+#include <type_traits>
+
 #pragma clang fp contract(off)
 
 namespace holo {
@@ -149,6 +151,49 @@ __global__ __launch_bounds__(256) void dequant_q6_k_kernel(T *__restrict__ y, co
     o[l + 96] = out_of<T>((d * (float)sc[is + 6]) * (float)q4);
 }
 
+// Q6_K to f16 panel values, one thread per (superblock, half h, slice s):
+// l = 16s .. 16s + 15 of the half, all four j, i.e. y[256b + 128h + 32j + l]
+// = (d * sc[8h + s + 2j]) * (q_j - 32) with both roundings as
+// dequantize_row_q6_k (quant.c:252-268), then to f16.  The 64 values come
+// from three 16-byte runs (ql low / high part, qh) and leave as eight 16-byte
+// stores.
+__global__ __launch_bounds__(256) void dequant_q6_k_f16_kernel(_Float16 *__restrict__ y, const uint8_t *__restrict__ W,
+                                                               int64_t ntask)
+{
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= ntask) return;
+    const int64_t b = t >> 2;
+    const int h = (int)((t >> 1) & 1), sl = (int)(t & 1);
+    const uint8_t *sb = W + b * 210;
+    uint32_t qa[4], qb[4], qh[4];
+    q6_run16(sb + 64 * h + 16 * sl, qa);
+    q6_run16(sb + 64 * h + 32 + 16 * sl, qb);
+    q6_run16(sb + 128 + 32 * h + 16 * sl, qh);
+    const int8_t *sc = (const int8_t *)(sb + 192) + 8 * h;
+    const float d = half_bits_to_float_exact((uint32_t)sb[208] | ((uint32_t)sb[209] << 8));
+    _Float16 *o = y + b * 256 + 128 * h + 16 * sl;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t *ql = (j & 1) ? qb : qa;
+        const float ds = d * (float)sc[sl + 2 * j];
+        uint32_t w[8];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t q = ((ql[c] >> (4 * (j >> 1))) & 0x0F0F0F0Fu) | (((qh[c] >> (2 * j)) & 0x03030303u) << 4);
+            float v[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) v[k] = ds * (float)((int)((q >> (8 * k)) & 0xFFu) - 32);
+            w[2 * c] = (uint32_t)__builtin_bit_cast(uint16_t, out_of<_Float16>(v[0])) |
+                       ((uint32_t)__builtin_bit_cast(uint16_t, out_of<_Float16>(v[1])) << 16);
+            w[2 * c + 1] = (uint32_t)__builtin_bit_cast(uint16_t, out_of<_Float16>(v[2])) |
+                           ((uint32_t)__builtin_bit_cast(uint16_t, out_of<_Float16>(v[3])) << 16);
+        }
+        uint4 *p = (uint4 *)(o + 32 * j);
+        p[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        p[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    }
+}
+
 // F32 rows to f16 (8 per thread; n a multiple of 8).
 __global__ __launch_bounds__(256) void f32_to_f16_kernel(_Float16 *__restrict__ y, const float *__restrict__ x,
                                                          int64_t n8)
@@ -196,7 +241,11 @@ static bool dequant_into(T *y, const uint8_t *W, int64_t n, int type)
     }
     case HOLO_TYPE_Q6_K: {
         const int64_t nsb = n / 256;
-        if (nsb)
+        if (!nsb) return true;
+        if constexpr (std::is_same<T, _Float16>::value)
+            hipLaunchKernelGGL(dequant_q6_k_f16_kernel, dim3((unsigned)((nsb * 4 + 255) / 256)), dim3(256), 0,
+                               stream(), y, W, nsb * 4);
+        else
             hipLaunchKernelGGL(dequant_q6_k_kernel<T>, dim3((unsigned)((nsb * 64 + 255) / 256)), dim3(256), 0,
                                stream(), y, W, nsb);
         return true;

@@ -387,21 +387,6 @@ static void launch_attn_prefill_mfma(float *out, const float *q, const float *kc
 // (2.5 TB/s); issuing the next task's loads ahead of the current task's
 // arithmetic (software pipelining) measured slower at every R.
 
-// 4 dwords of bytes [p, p + 16) for a 2-byte-aligned p (one aligned 16-byte
-// load and one dword: both inside the superblock for every run used here).
-__device__ __forceinline__ void q6_run16(const uint8_t *p, uint32_t (&w)[4])
-{
-    const uintptr_t a = (uintptr_t)p;
-    const uint32_t sh = (uint32_t)(a & 3u);
-    const uint32_t *b = (const uint32_t *)(a - sh);
-    const uint4 v = *(const uint4 *)b;
-    const uint32_t e = b[4];
-    w[0] = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
-    w[1] = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
-    w[2] = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
-    w[3] = __builtin_amdgcn_alignbyte(e, v.w, sh);
-}
-
 __device__ __forceinline__ float q6_ubyte_dot(uint32_t q, const float4 x)
 {
     // (float)((q >> 8k) & 255) compiles to v_cvt_f32_ubyte<k>

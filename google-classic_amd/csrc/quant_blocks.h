@@ -170,4 +170,23 @@ __device__ __forceinline__ Q4_KUnit load_q4_k(const uint8_t *__restrict__ W, int
     return r;
 }
 
+// ---- Q6_K ------------------------------------------------------------------
+// 4 dwords of bytes [p, p + 16) for a 2-byte-aligned p inside a 210-byte
+// superblock that starts 4-byte aligned or 2 past it: one aligned 16-byte load
+// from p rounded down to 4 bytes and one dword after it, realigned.  For the
+// runs of a Q6_K superblock read here (ql, qh at offsets up to 176) both loads
+// stay inside the superblock or the one before it.
+__device__ __forceinline__ void q6_run16(const uint8_t *p, uint32_t (&w)[4])
+{
+    const uintptr_t a = (uintptr_t)p;
+    const uint32_t sh = (uint32_t)(a & 3u);
+    const uint32_t *b = (const uint32_t *)(a - sh);
+    const uint4 v = *(const uint4 *)b;
+    const uint32_t e = b[4];
+    w[0] = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+    w[1] = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+    w[2] = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+    w[3] = __builtin_amdgcn_alignbyte(e, v.w, sh);
+}
+
 }  // namespace holo
