@@ -3,8 +3,9 @@
 //
 // Per layer, with all n rows at once (the reference runs this body once per
 // token: llm.c:1063-1247 on the CPU, llm_cuda.c:598-880 on the GPU):
-//   xb = rms_norm(x); q, k, v = Wq xb, Wk xb, Wv xb; rope(q, k) at pos0 + r;
-//   cache[pos0 + r] = k, v; att = causal attention; x += Wo att;
+//   xb = rms_norm(x); q = Wq xb; cache rows pos0 + r: k = Wk xb, v = Wv xb
+//   (written in place); rope(q, k) at pos0 + r; att = causal attention;
+//   x += Wo att;
 //   xb = rms_norm(x); h = silu(W1 xb) * (W3 xb); x += W2 h
 // then the last row: rms_norm, output head -> logits (llm.c:1249-1263).
 #include "common.h"
@@ -174,25 +175,26 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
     const int exact = flags & HOLO_FORWARD_EXACT;
     const int64_t layer_cache = (int64_t)m->max_seq * kv_dim;
 
-    // stream-ordered scratch: token ids, x, xb, q, k, v, att, hb, hb2
+    // stream-ordered scratch: token ids, x, xb, q, att, hb, hb2 (k and v are
+    // written straight into the caches)
     const size_t rowsz = (size_t)n * sizeof(float);
     const size_t sz_tok = ((size_t)n * sizeof(int) + 255) & ~(size_t)255;
-    const size_t sizes[] = {sz_tok, rowsz * dim, rowsz * dim, rowsz * q_dim, rowsz * kv_dim, rowsz * kv_dim,
-                            rowsz * q_dim, rowsz * ffn, rowsz * ffn};
+    const size_t sizes[] = {sz_tok, rowsz * dim, rowsz * dim, rowsz * q_dim, rowsz * q_dim, rowsz * ffn, rowsz * ffn};
+    constexpr int kBufs = sizeof(sizes) / sizeof(sizes[0]);
     size_t total = 0;
     for (size_t s : sizes) total += (s + 255) & ~(size_t)255;
     void *ws = nullptr;
     HOLO_CHECK(hipMallocAsync(&ws, total, stream()));
     if (!ws) return HOLO_EINVAL;
     uint8_t *p = (uint8_t *)ws;
-    void *bufs[9];
-    for (int i = 0; i < 9; i++) {
+    void *bufs[kBufs];
+    for (int i = 0; i < kBufs; i++) {
         bufs[i] = p;
         p += (sizes[i] + 255) & ~(size_t)255;
     }
     int *dtok = (int *)bufs[0];
-    float *x = (float *)bufs[1], *xb = (float *)bufs[2], *q = (float *)bufs[3], *k = (float *)bufs[4];
-    float *v = (float *)bufs[5], *att = (float *)bufs[6], *hb = (float *)bufs[7], *hb2 = (float *)bufs[8];
+    float *x = (float *)bufs[1], *xb = (float *)bufs[2], *q = (float *)bufs[3], *att = (float *)bufs[4];
+    float *hb = (float *)bufs[5], *hb2 = (float *)bufs[6];
 
     // embeddings: all n rows in one launch
     HOLO_CHECK(hipMemcpyAsync(dtok, tokens, (size_t)n * sizeof(int), hipMemcpyHostToDevice, stream()));
@@ -201,6 +203,9 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
     for (int l = 0; l < m->n_layers; l++) {
         const holo_llama_layer_t &L = m->layers[l];
         float *kc = m->key_cache + l * layer_cache, *vc = m->value_cache + l * layer_cache;
+        // this call's rows of the caches: the k and v products land there
+        // directly ([pos][kv_dim] is their row-major output layout)
+        float *k = kc + (int64_t)pos0 * kv_dim, *v = vc + (int64_t)pos0 * kv_dim;
         // One row (a decode step): the norms run inside the q/k/v and gate/up
         // GEMVs and the residual adds inside the o and down GEMVs.
         const bool one = n == 1;
@@ -215,9 +220,7 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
             norm_or_copy(xb, x, L.attn_norm, n, dim, m->rms_eps);
             matmul_qkv(q, k, v, L, xb, n, q_dim, kv_dim, dim, exact);
         }
-        holo_rope_rows(q, k, n, pos0, hd, m->n_heads, m->n_kv_heads, m->rope_base);
-        HOLO_CHECK(hipMemcpyAsync(kc + (int64_t)pos0 * kv_dim, k, rowsz * kv_dim, hipMemcpyDeviceToDevice, stream()));
-        HOLO_CHECK(hipMemcpyAsync(vc + (int64_t)pos0 * kv_dim, v, rowsz * kv_dim, hipMemcpyDeviceToDevice, stream()));
+        holo_rope_rows(q, k, n, pos0, hd, m->n_heads, m->n_kv_heads, m->rope_base);  // k rotated in the cache
         holo_attention_prefill(att, q, kc, vc, n, pos0, hd, m->n_heads, m->n_kv_heads);
         if (one && fused_gemv_type(L.wo_type)) {
             holo_matmul_add(x, L.wo, att, x, dim, q_dim, L.wo_type);
