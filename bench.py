@@ -370,14 +370,16 @@ def prompt_forward_q4_k_m(lib, n_tokens=512):
     run()
     lib.cuda_sync()
     ev = holo.Events()
-    reps = 3
-    ev.start()
-    for _ in range(reps):
+    times = []
+    for _ in range(5):  # each prompt timed alone; the median is reported (single prompts vary by up to 20%)
+        ev.start()
         run()
-    ms = ev.stop() / reps
+        times.append(ev.stop())
     ev.close()
     holo.check("prompt forward q4_k_m")
+    ms = statistics.median(times)
     return {"prompt_tokens": n_tokens, "prompt_ms": round(ms, 2),
+            "prompt_ms_min_max": [round(min(times), 2), round(max(times), 2)],
             "prompt_tokens_per_s": round(n_tokens / (ms * 1e-3), 1),
             "types": "Q4_K q/k/o/gate/up and embeddings; Q6_K v, down and head"}
 

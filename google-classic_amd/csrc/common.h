@@ -29,6 +29,7 @@ void gemv_chain_release();
 // without them decode attention runs one range per head.
 bool attention_scratch_init();
 void attention_scratch_release();
+void panel_workspace_release();  // the batched products' panel buffers (prefill.hip)
 
 // Events that holo_time_next_launch requested for the next timed kernel
 // launch (MFMA GEMV or prefill GEMM): returns them once and clears them.

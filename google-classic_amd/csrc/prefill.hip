@@ -509,6 +509,37 @@ void holo_quantize_act_q8_0(void *dst_blocks, const float *X, int rows, int k)
 
 }  // extern "C"
 
+// Workspaces of the batched products: slot 0 holds the weight panels
+// (gemm_panel), slot 1 the activation panel (gemm_multi).  Each is one device
+// buffer kept by the library and grown (outside graph capture) to the largest
+// request, reused in stream order by every call.  Per-call stream-ordered
+// allocations of these sizes (tens to hundreds of MB, interleaved) made single
+// prompts stall for up to 15 ms while the pool mapped memory.  Under graph
+// capture, or when growing fails, the call allocates stream-ordered instead.  Calls
+// that overlap on different streams would share a buffer: the library issues
+// on one stream.
+static void *g_ws[2] = {nullptr, nullptr};
+static size_t g_ws_bytes[2] = {0, 0};
+
+static void *workspace(int slot, size_t bytes)
+{
+    // never under capture: a graph must not hold a buffer a later growth frees
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream(), &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
+    if (bytes <= g_ws_bytes[slot]) return g_ws[slot];
+    HOLO_CHECK(hipStreamSynchronize(stream()));  // earlier calls may still use the old buffer
+    if (g_ws[slot]) HOLO_CHECK(hipFree(g_ws[slot]));
+    g_ws[slot] = nullptr;
+    g_ws_bytes[slot] = 0;
+    if (hipMalloc(&g_ws[slot], bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        g_ws[slot] = nullptr;
+        return nullptr;
+    }
+    g_ws_bytes[slot] = bytes;
+    return g_ws[slot];
+}
+
 // One launch over nmat matrices (holo_gemm_q4_0_q8_0 and its multi-matrix form).
 // Xq (Q8_0 blocks): the Q8_0 product; otherwise X (fp32, 16-byte aligned):
 // the f16 product, of silu(X) * U when U is given.  R: Y = R + product (one
@@ -523,8 +554,9 @@ static void gemm_multi(float *const *Y, const void *const *W, const int *N, int 
     int ntot = 0;
     for (int i = 0; i < nmat; i++) ntot += N[i];
     const size_t pbytes = (size_t)nblk * 64, dbytes = xf16 ? 0 : ((size_t)nblk * 2 + 255) & ~(size_t)255;
-    void *ws = nullptr;
-    HOLO_CHECK(hipMallocAsync(&ws, pbytes + dbytes, stream()));
+    void *ws = workspace(1, pbytes + dbytes);
+    const bool own = ws == nullptr;
+    if (own) HOLO_CHECK(hipMallocAsync(&ws, pbytes + dbytes, stream()));
     if (!ws) return;
     uint4 *P = (uint4 *)ws;
     uint16_t *D = xf16 ? nullptr : (uint16_t *)((uint8_t *)ws + pbytes);
@@ -602,7 +634,7 @@ static void gemm_multi(float *const *Y, const void *const *W, const int *N, int 
     if (wp) go(std::true_type{}, std::true_type{});
     else if (xf16) go(std::true_type{}, std::false_type{});
     else go(std::false_type{}, std::false_type{});
-    HOLO_CHECK(hipFreeAsync(ws, stream()));
+    if (own) HOLO_CHECK(hipFreeAsync(ws, stream()));
 }
 
 // Several matrices in one launch: each N_i a multiple of 128 (a column tile
@@ -818,8 +850,9 @@ static void gemm_panel(float *const *Y, const void *const *W, const int *N, int 
 {
     size_t total = 0;
     for (int i = 0; i < nmat; i++) total += (size_t)N[i] * K * 2;  // each a multiple of 64 bytes
-    void *ws = nullptr;
-    HOLO_CHECK(hipMallocAsync(&ws, total, stream()));
+    void *ws = workspace(0, total);
+    const bool own = ws == nullptr;
+    if (own) HOLO_CHECK(hipMallocAsync(&ws, total, stream()));
     if (!ws) return;
     const void *P[kPrefillMats];
     size_t off = 0;
@@ -829,8 +862,20 @@ static void gemm_panel(float *const *Y, const void *const *W, const int *N, int 
         off += (size_t)N[i] * K * 2;
     }
     gemm_multi(Y, P, N, nmat, nullptr, X, M, K, U, R, true);
-    HOLO_CHECK(hipFreeAsync(ws, stream()));
+    if (own) HOLO_CHECK(hipFreeAsync(ws, stream()));
 }
+
+namespace holo {
+void panel_workspace_release()
+{
+    (void)hipDeviceSynchronize();
+    for (int i = 0; i < 2; i++) {
+        if (g_ws[i]) (void)hipFree(g_ws[i]);
+        g_ws[i] = nullptr;
+        g_ws_bytes[i] = 0;
+    }
+}
+}  // namespace holo
 
 extern "C" {
 

@@ -87,6 +87,7 @@ void cuda_cleanup(void)
     g_copy_stream = nullptr;
     holo::gemv_chain_release();
     holo::attention_scratch_release();
+    holo::panel_workspace_release();
     g_stream = nullptr;
     g_initialized = false;
 }
