@@ -214,10 +214,12 @@ void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const i
 /* The batched products for any weight type the GEMVs serve (Q4_0, Q8_0, Q4_K,
  * Q6_K, F16, F32), with the contracts of the Q4_0 calls above.  Q4_0 goes to
  * them.  Every other type, for M >= 64 and K whole blocks (Q4_K, Q6_K: K a
- * multiple of 256), is dequantised into a stream-ordered f16 panel workspace
- * (holo_dequant_f16, N*K*2 bytes per matrix) and multiplied on the f16
- * product: Y = sum_k f16_rne(x) * f16_rne(w), fp32 accumulation.  Otherwise
- * one holo_matmul GEMV per row.  No reference counterpart (the reference runs
+ * multiple of 256), is dequantised into an f16 panel (holo_dequant_f16, N*K*2
+ * bytes per matrix) and multiplied on the f16 product: Y = sum_k f16_rne(x) *
+ * f16_rne(w), fp32 accumulation.  The panels live in a device buffer the
+ * library keeps and grows (hipMalloc, outside graph capture; under capture a
+ * stream-ordered allocation per call); calls on one stream reuse it in order.
+ * Otherwise one holo_matmul GEMV per row.  No reference counterpart (the reference runs
  * one GEMV per token, llm.c:1049).                                          */
 void holo_matmul_batch(float *Y, const void *W, const float *X, int M, int N, int K, int type);
 void holo_matmul_batch_multi(float *const *Y, const void *const *W, const int *N, int nmat, const float *X,
