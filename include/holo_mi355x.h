@@ -165,8 +165,9 @@ void holo_matmul_add(float *y, const void *M, const float *v, const float *r,
  * (d=0 -> q=0).  Y[M][N] accumulates, over blocks b in order,
  *   acc = fmaf((float)I_b, f16(dw)*f16(dx), acc)
  * with the exact integer block dot I_b (the scale product is exact in fp32).
- * holo_gemm_q4_0_q8_0 stages the activations as f16 in a stream-ordered
- * workspace (hipMallocAsync, M*K*2 + M*(K/32)*2 bytes) for the call.       */
+ * holo_gemm_q4_0_q8_0 stages the activations as f16 in a workspace of
+ * M*K*2 + M*(K/32)*2 bytes: a device buffer the library keeps and grows
+ * outside graph capture, a stream-ordered allocation under capture.       */
 void holo_quantize_act_q8_0(void *dst_blocks, const float *X, int rows, int k);
 void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, int K);
 /* Y[M][N] = X[M][K] . W[N][K]^T for W in Q4_0: M >= 64 runs the f16 product
@@ -187,8 +188,8 @@ void holo_gemm_q4_0_q8_0_multi(float *const *Y, const void *const *W, const int 
  * f16_rne(f16(dw) * (q - 8)), Y = sum_k x16 * w16 accumulated in fp32 on the
  * matrix cores (order of the hardware: within the fp32 accumulation bound of
  * the float64 sum of the rounded operands, not bit-reproducible on the CPU).
- * X[M][K] fp32, 16-byte aligned, K a multiple of 32; a stream-ordered
- * workspace of M*K*2 bytes.  No reference counterpart (build-defined, like
+ * X[M][K] fp32, 16-byte aligned, K a multiple of 32; a workspace of M*K*2
+ * bytes, as above.  No reference counterpart (build-defined, like
  * the Q8_0 product).                                                       */
 void holo_gemm_q4_0_f16(float *Y, const void *W, const float *X, int M, int N, int K);
 void holo_gemm_q4_0_f16_multi(float *const *Y, const void *const *W, const int *N, int nmat,
