@@ -194,6 +194,39 @@ __global__ __launch_bounds__(256) void dequant_q6_k_f16_kernel(_Float16 *__restr
     }
 }
 
+// Q4_K to f16 panel values, four threads per 32-weight unit: thread t of
+// unit u writes weights 8t .. 8t + 7, the low nibbles of qs[8t ..] for
+// t < 2 and the high nibbles of qs[8(t-2) ..] for t >= 2 (the unit layout of
+// dequant_q4_k_kernel), so a wave's 16-byte stores are contiguous.  Same
+// arithmetic: (d*sc)*q - dmin*m, both roundings, then f16.
+__global__ __launch_bounds__(256) void dequant_q4_k_f16_kernel(_Float16 *__restrict__ y, const uint8_t *__restrict__ W,
+                                                               int64_t nthreads)
+{
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= nthreads) return;
+    const int64_t u = g >> 2;
+    const int t = (int)(g & 3);
+    const uint8_t *sb = W + (u >> 3) * 144;
+    const uint32_t j = (uint32_t)(u & 7);
+    const u32x4 h = *(const u32x4 *)sb;
+    const uint2 q = *(const uint2 *)(sb + 16 + 16 * j + 8 * (t & 1));
+    uint32_t sc, mn;
+    q4_k_scale_min(h.y, h.z, h.w, j, sc, mn);
+    const float dsc = half_bits_to_float(h.x) * (float)sc;
+    const float dmn = half_bits_to_float(h.x >> 16) * (float)mn;
+    const int shift = t >= 2 ? 4 : 0;
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t word = i < 2 ? q.x : q.y;
+        const uint32_t b0 = (word >> (16 * (i & 1) + shift)) & 15u, b1 = (word >> (16 * (i & 1) + 8 + shift)) & 15u;
+        const float p0 = dsc * (float)b0, p1 = dsc * (float)b1;
+        w[i] = (uint32_t)__builtin_bit_cast(uint16_t, out_of<_Float16>(p0 - dmn)) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, out_of<_Float16>(p1 - dmn)) << 16);
+    }
+    ((uint4 *)(y + u * 32 + 8 * t))[0] = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // F32 rows to f16 (8 per thread; n a multiple of 8).
 __global__ __launch_bounds__(256) void f32_to_f16_kernel(_Float16 *__restrict__ y, const float *__restrict__ x,
                                                          int64_t n8)
@@ -234,7 +267,11 @@ static bool dequant_into(T *y, const uint8_t *W, int64_t n, int type)
     }
     case HOLO_TYPE_Q4_K: {
         const int64_t nu = (n / 256) * 8;
-        if (nu)
+        if (!nu) return true;
+        if constexpr (std::is_same<T, _Float16>::value)
+            hipLaunchKernelGGL(dequant_q4_k_f16_kernel, dim3((unsigned)((nu * 4 + 255) / 256)), dim3(256), 0,
+                               stream(), y, W, nu * 4);
+        else
             hipLaunchKernelGGL(dequant_q4_k_kernel<T>, dim3((unsigned)((nu + 255) / 256)), dim3(256), 0, stream(), y,
                                W, nu);
         return true;
