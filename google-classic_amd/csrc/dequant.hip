@@ -227,6 +227,41 @@ __global__ __launch_bounds__(256) void dequant_q4_k_f16_kernel(_Float16 *__restr
     ((uint4 *)(y + u * 32 + 8 * t))[0] = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Q4_0 / Q8_0 to f16 panel values, four threads per 32-weight block: thread t
+// writes weights 8t .. 8t + 7 as one 16-byte store (contiguous across the
+// wave).  Each thread decodes the whole block with the realigning loaders
+// (the four loads of a block hit the same lines) and takes its 8 weights:
+// Q8_0 qs[8t ..]; Q4_0 the low nibbles of qs[8t ..] for t < 2, the high
+// nibbles of qs[8(t-2) ..] for t >= 2.  d*q is exact in fp32, then f16.
+template <bool Q8>
+__global__ __launch_bounds__(256) void dequant_q8_q4_f16_kernel(_Float16 *__restrict__ y, const uint8_t *__restrict__ W,
+                                                                int64_t nthreads, int64_t nblocks)
+{
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= nthreads) return;
+    const int64_t b = g >> 2;
+    const int t = (int)(g & 3);
+    float v[8];
+    if constexpr (Q8) {
+        const Q8_0Unit u = load_q8_0(W, b, nblocks * 34);
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            v[k] = u.d * (float)(int)(int8_t)((u.q[2 * t + (k >> 2)] >> (8 * (k & 3))) & 0xFFu);
+    } else {
+        const Q4_0Unit u = load_q4_0(W, b, nblocks * 18);
+        const int shift = t >= 2 ? 4 : 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            v[k] = u.d * (float)((int)((u.q[2 * (t & 1) + (k >> 2)] >> (8 * (k & 3) + shift)) & 15u) - 8);
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        w[i] = (uint32_t)__builtin_bit_cast(uint16_t, out_of<_Float16>(v[2 * i])) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, out_of<_Float16>(v[2 * i + 1])) << 16);
+    ((uint4 *)(y + b * 32 + 8 * t))[0] = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // F32 rows to f16 (8 per thread; n a multiple of 8).
 __global__ __launch_bounds__(256) void f32_to_f16_kernel(_Float16 *__restrict__ y, const float *__restrict__ x,
                                                          int64_t n8)
@@ -251,18 +286,20 @@ template <typename T>
 static bool dequant_into(T *y, const uint8_t *W, int64_t n, int type)
 {
     switch (type) {
-    case HOLO_TYPE_Q4_0: {
-        const int64_t nb = n / 32;
-        if (nb)
-            hipLaunchKernelGGL(dequant_q4_0_kernel<T>, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, stream(), y,
-                               W, nb);
-        return true;
-    }
+    case HOLO_TYPE_Q4_0:
     case HOLO_TYPE_Q8_0: {
         const int64_t nb = n / 32;
-        if (nb)
-            hipLaunchKernelGGL(dequant_q8_0_kernel<T>, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, stream(), y,
-                               W, nb);
+        if (!nb) return true;
+        const bool q8 = type == HOLO_TYPE_Q8_0;
+        if constexpr (std::is_same<T, _Float16>::value) {
+            const dim3 grid((unsigned)((nb * 4 + 255) / 256));
+            if (q8) hipLaunchKernelGGL(dequant_q8_q4_f16_kernel<true>, grid, dim3(256), 0, stream(), y, W, nb * 4, nb);
+            else hipLaunchKernelGGL(dequant_q8_q4_f16_kernel<false>, grid, dim3(256), 0, stream(), y, W, nb * 4, nb);
+        } else {
+            const dim3 grid((unsigned)((nb + 255) / 256));
+            if (q8) hipLaunchKernelGGL(dequant_q8_0_kernel<T>, grid, dim3(256), 0, stream(), y, W, nb);
+            else hipLaunchKernelGGL(dequant_q4_0_kernel<T>, grid, dim3(256), 0, stream(), y, W, nb);
+        }
         return true;
     }
     case HOLO_TYPE_Q4_K: {
