@@ -35,6 +35,14 @@ void panel_workspace_release();  // the batched products' panel buffers (prefill
 // launch (MFMA GEMV or prefill GEMM): returns them once and clears them.
 bool take_launch_events(hipEvent_t *start, hipEvent_t *stop);
 
+// n bytes at p set to `value` by a kernel on the library stream.  Used
+// instead of hipMemsetAsync wherever a call may be captured into a graph
+// (memset nodes are avoided in captured graphs).
+void fill_bytes(void *p, int value, size_t n);
+
+// True while the library stream is being captured into a graph.
+bool stream_capturing();
+
 }  // namespace holo
 
 #define HOLO_CHECK(call)                                                        \

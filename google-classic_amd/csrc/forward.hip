@@ -265,12 +265,34 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
     return 0;
 }
 
+// This forward is the plain Llama body.  The reference also runs Gemma
+// (embedding scale, post-norms, a 1M RoPE base on global layers) and Qwen
+// (q/k/v biases, QK-norm) variants (llm.c:451-475, 480-485, 516-521,
+// 1037-1133); a file that needs one of them is rejected rather than run with
+// the wrong arithmetic.
+int holo_llama_gguf_check(const holo_gguf_t *g)
+{
+    if (!g) return -1;
+    const holo_gguf_model_t *p = holo_gguf_model(g);
+    if (strstr(p->arch, "gemma") || strstr(p->arch, "Gemma")) return -1;
+    static const char *const kUnsupported[] = {"attn_q.bias", "attn_k.bias", "attn_v.bias", "attn_q_norm.weight",
+                                               "attn_k_norm.weight", "post_attention_norm.weight",
+                                               "post_ffw_norm.weight"};
+    for (int l = 0; l < (int)p->block_count; l++)
+        for (const char *suffix : kUnsupported) {
+            const std::string name = "blk." + std::to_string(l) + "." + suffix;
+            if (holo_gguf_find_tensor(g, name.c_str())) return -1;
+        }
+    return 0;
+}
+
 int holo_llama_from_gguf(const holo_gguf_t *g, holo_llama_t *m, holo_llama_layer_t *layers, int max_layers)
 {
     if (!g || !m || !layers || !holo_gguf_device_base(g)) return -1;
     const holo_gguf_model_t *p = holo_gguf_model(g);
     const int n_layers = (int)p->block_count;
     if (n_layers <= 0 || n_layers > max_layers) return -1;
+    if (holo_llama_gguf_check(g) != 0) return -1;
     memset(m, 0, sizeof(*m));
     memset(layers, 0, sizeof(*layers) * (size_t)n_layers);
     auto find = [&](const std::string &name, int *type) -> const void * {

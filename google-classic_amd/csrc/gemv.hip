@@ -1321,11 +1321,15 @@ __global__ __launch_bounds__(kThreads) void gemv_chain_kernel(ChainArgs ca)
             st.run(b0, b1);
         });
         if (s + 1 < ca.nstages) {
-            // the stage's outputs are device-coherent stores and the next
-            // stage reads them device-coherently: completing the stores
-            // (workgroup-scope release: no cache maintenance) is all the
-            // ordering the barrier needs
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            // Every wave may have stored outputs of this stage (the last wave
+            // to finish a tile stores it).  Each wave's agent-scope release
+            // fence waits for its own stores to complete (s_waitcnt vmcnt(0),
+            // after an L2 write-back), and only then does the wave reach the
+            // workgroup barrier, so every output store of the workgroup has
+            // completed at agent scope before thread 0 arrives.  The next
+            // stage reads its input with device-coherent (sc1) loads, which
+            // are not answered from a line an L2 cached before the store.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
             __syncthreads();
             if (wave != 0) {
                 with_stage<FMT>(ca.key[s + 1], ca.st[s + 1], ldsb, [&](auto &st) { st.issue(b0, 0); });
@@ -1683,6 +1687,18 @@ static bool gemv_multi(int fmt, int mode, int nseg, const void *const *W, float 
         HOLO_REJECT("gemv: in_dim too large (at most 32 segments of 64 units per row)");
         return true;
     }
+    if (a.units == 0) {
+        // No complete block per row: every dot product is empty (gate/up:
+        // silu(0) * 0 = 0).
+        if (r) {
+            if (r != y[0])
+                HOLO_CHECK(hipMemcpyAsync(y[0], r, sizeof(float) * rows[0], hipMemcpyDeviceToDevice, stream()));
+            return true;
+        }
+        for (int s = 0; s < (mode == MODE_GATEUP ? 1 : nseg); s++)
+            if (rows[s] > 0) fill_bytes(y[s], 0, sizeof(float) * rows[s]);
+        return true;
+    }
     // Q8_0 rows carry twice the bytes per weight, so the F32 path streams
     // them well at in_dim 4096: on MI355X it is faster at 32000x4096 (26.9
     // against 31.3 us) and level or faster at 4096x4096 and 11008x4096.  At
@@ -1734,17 +1750,6 @@ static bool gemv_multi(int fmt, int mode, int nseg, const void *const *W, float 
     if (mode == MODE_GATEUP) tiles = (rows[0] + TR - 1) / TR;
     a.ntiles = tiles;
     if (tiles == 0) return true;
-    if (a.units == 0) {
-        // No complete block per row: every dot product is empty.
-        if (r) {
-            if (r != y[0])
-                HOLO_CHECK(hipMemcpyAsync(y[0], r, sizeof(float) * rows[0], hipMemcpyDeviceToDevice, stream()));
-            return true;
-        }
-        for (int s = 0; s < (mode == MODE_GATEUP ? 1 : nseg); s++)
-            HOLO_CHECK(hipMemsetAsync(y[s], 0, sizeof(float) * rows[s], stream()));
-        return true;
-    }
 #define HOLO_DISPATCH(F)                                                             \
     if (xm == XM_F32) {                                                              \
         if (mode == MODE_PLAIN) launch_r<F, XM_F32, MODE_PLAIN>(a, R, P);            \
@@ -1773,7 +1778,7 @@ static void gemv_one(int fmt, float *dst, const void *M, const float *v, int out
     if (out_dim <= 0) return;
     if (!M) {
         // matmul_q with a NULL matrix writes zeros (llm.c:772-775).
-        HOLO_CHECK(hipMemsetAsync(dst, 0, sizeof(float) * out_dim, stream()));
+        fill_bytes(dst, 0, sizeof(float) * out_dim);
         return;
     }
     const void *W[1] = {M};

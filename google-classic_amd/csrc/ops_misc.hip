@@ -1307,7 +1307,7 @@ void cuda_matmul_q6_k(float *dst, const void *M, const float *v, int out_dim, in
     if (out_dim <= 0) return;
     if (!M) {
         // matmul_q with a NULL matrix writes zeros (llm.c:772-775)
-        HOLO_CHECK(hipMemsetAsync(dst, 0, sizeof(float) * out_dim, stream()));
+        fill_bytes(dst, 0, sizeof(float) * out_dim);
         return;
     }
     if (((uintptr_t)M & 1u) || ((uintptr_t)v & 15u)) {

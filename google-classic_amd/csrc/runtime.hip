@@ -34,6 +34,39 @@ void latch_error(int code, const char *what, const char *file, int line)
     fprintf(stderr, "holo_mi355x error %d (%s) at %s:%d: %s\n", code, msg, file, line, what);
 }
 
+// One thread per 16-byte piece of the 16-byte-aligned span that covers
+// [p, p + n): whole pieces take one vector store, the two end pieces store
+// their covered bytes one at a time.
+__global__ __launch_bounds__(256) void fill_bytes_k(uint8_t *p, uint32_t byte, size_t n)
+{
+    const uintptr_t a = (uintptr_t)p, end = a + n;
+    const uintptr_t c = (a & ~(uintptr_t)15) + 16 * ((uintptr_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (c >= end) return;
+    const uint32_t w = byte * 0x01010101u;
+    if (c >= a && c + 16 <= end) {
+        *(uint4 *)c = make_uint4(w, w, w, w);
+        return;
+    }
+    for (uintptr_t b = c; b < c + 16; b++)
+        if (b >= a && b < end) *(uint8_t *)b = (uint8_t)byte;
+}
+
+void fill_bytes(void *p, int value, size_t n)
+{
+    if (n == 0) return;
+    const uintptr_t a = (uintptr_t)p;
+    const size_t pieces = (((a + n + 15) & ~(uintptr_t)15) - (a & ~(uintptr_t)15)) / 16;
+    hipLaunchKernelGGL(fill_bytes_k, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, g_stream, (uint8_t *)p,
+                       (uint32_t)(value & 0xFF), n);
+    HOLO_LAUNCH_CHECK();
+}
+
+bool stream_capturing()
+{
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(g_stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
 }  // namespace holo
 
 extern "C" {
@@ -174,11 +207,15 @@ void cuda_memcpy_d2h_async(void *dst, const void *src, size_t size)  // cuda_ops
     HOLO_CHECK(hipMemcpyAsync(dst, src, size, hipMemcpyDeviceToHost, holo::copy_stream()));
 }
 
+// cuda_ops.cu:220-222.  A fill kernel rather than hipMemsetAsync, so that the
+// call may sit inside a graph capture; the synchronisation that makes it
+// blocking like the reference's cudaMemset is skipped while capturing (a
+// capture cannot synchronise its stream).
 void cuda_memset(void *ptr, int value, size_t size)
 {
     if (size == 0) return;
-    HOLO_CHECK(hipMemsetAsync(ptr, value, size, g_stream));
-    HOLO_CHECK(hipStreamSynchronize(g_stream));
+    holo::fill_bytes(ptr, value, size);
+    if (!holo::stream_capturing()) HOLO_CHECK(hipStreamSynchronize(g_stream));
 }
 
 void cuda_sync(void) { HOLO_CHECK(hipDeviceSynchronize()); }  // cuda_ops.cu:222-224

@@ -182,6 +182,7 @@ _SIGS = {
     "holo_matmul_rows": (None, [_P, _P, _P, _I, _I, _I, _I, _I]),
     "holo_llama_forward": (_I, [_P, _P, _I, _I, _P, _I]),
     "holo_llama_from_gguf": (_I, [_P, _P, _P, _I]),
+    "holo_llama_gguf_check": (_I, [_P]),
 }
 
 _lib: C.CDLL | None = None

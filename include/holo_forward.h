@@ -96,8 +96,16 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
  * attn_q, attn_k, attn_v, attn_output, ffn_norm, ffn_gate, ffn_down,
  * ffn_up}, output_norm, output (tied to token_embd when absent).  vocab is
  * token_embd's row count.  The caller sets max_seq and the caches.
- * 0, or -1 when a required tensor is missing or n_layers > max_layers.       */
+ * 0, or -1 when a required tensor is missing, n_layers > max_layers, or
+ * holo_llama_gguf_check rejects the file.                                   */
 int holo_llama_from_gguf(const holo_gguf_t *g, holo_llama_t *m, holo_llama_layer_t *layers, int max_layers);
+/* 0 when a parsed GGUF file (host-side parse is enough) is the plain Llama
+ * body this forward runs; -1 when it needs a branch of the reference's
+ * forward that is not built here: a Gemma architecture (general.architecture
+ * contains "gemma"), or any blk.N.attn_{q,k,v}.bias, attn_{q,k}_norm.weight,
+ * post_attention_norm.weight or post_ffw_norm.weight tensor (the Qwen and
+ * Gemma branches of llm.c:451-521, 1037-1133).                               */
+int holo_llama_gguf_check(const holo_gguf_t *g);
 
 #ifdef __cplusplus
 }

@@ -295,3 +295,32 @@ def test_inputs_that_divide_by_zero_in_the_reference(L, tmp_path):
         assert m.attention_head_count == 0 and m.attention_key_length == 0 and m.attention_head_count_kv == 0
     finally:
         L.holo_gguf_close(g)
+
+
+def test_llama_check_rejects_unbuilt_branches(L, tmp_path):
+    """holo_llama_gguf_check: a plain Llama file passes; the Qwen (q/k/v
+    biases, QK-norm) and Gemma (architecture name, post-norms) branches of
+    the reference forward (llm.c:451-521, 1037-1133), which this forward
+    does not run, are rejected on the host-side parse."""
+    base = [("general.architecture", gf.STR, "llama"), ("llama.block_count", gf.U32, 2)]
+
+    def check(kvs, extra, name):
+        ts = [gf.Tensor("token_embd.weight", [32, 4], 0), gf.Tensor("blk.0.attn_q.weight", [32, 32], 0)]
+        ts += [gf.Tensor(n, [32], 0) for n in extra]
+        path = tmp_path / name
+        gf.write(path, kvs, ts)
+        g = L.holo_gguf_open(str(path).encode())
+        assert g
+        try:
+            return L.holo_llama_gguf_check(g)
+        finally:
+            L.holo_gguf_close(g)
+
+    assert check(base, [], "plain.gguf") == 0
+    for j, extra in enumerate(["blk.1.attn_q.bias", "blk.0.attn_k.bias", "blk.0.attn_v.bias",
+                               "blk.1.attn_q_norm.weight", "blk.0.attn_k_norm.weight",
+                               "blk.0.post_attention_norm.weight", "blk.1.post_ffw_norm.weight"]):
+        assert check(base, [extra], f"extra{j}.gguf") == -1, extra
+    gemma = [("general.architecture", gf.STR, "gemma3"), ("gemma3.block_count", gf.U32, 2)]
+    assert check(gemma, [], "gemma.gguf") == -1
+    assert L.holo_llama_gguf_check(None) == -1
