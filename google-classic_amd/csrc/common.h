@@ -30,6 +30,9 @@ void gemv_chain_release();
 bool attention_scratch_init();
 void attention_scratch_release();
 void panel_workspace_release();  // the batched products' panel buffers (prefill.hip)
+// Device address of the fixed scratch array of holo_gemm_q4_0_q8_0_noalloc on
+// the current device (prefill.hip), looked up once per device; nullptr on failure.
+void *noalloc_scratch();
 
 // Events that holo_time_next_launch requested for the next timed kernel
 // launch (MFMA GEMV or prefill GEMM): returns them once and clears them.

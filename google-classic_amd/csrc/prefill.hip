@@ -545,16 +545,27 @@ static void *workspace(int slot, size_t bytes)
 // the f16 product, of silu(X) * U when U is given.  R: Y = R + product (one
 // matrix).  wp: W[i] are f16 panels [N_i][K] (f16 product only), otherwise
 // Q4_0 block streams.
+// Bytes of the activation panel (and, for the Q8_0 product, its scale
+// array) that gemm_multi stages M x K activations into.
+static size_t act_panel_bytes(int M, int K, bool xf16)
+{
+    const int64_t nblk = (int64_t)M * (K / 32);
+    return (size_t)nblk * 64 + (xf16 ? 0 : (((size_t)nblk * 2 + 255) & ~(size_t)255));
+}
+
+// ws_given: a caller-provided workspace of at least act_panel_bytes bytes
+// (nothing is allocated); otherwise the library's kept workspace.
 static void gemm_multi(float *const *Y, const void *const *W, const int *N, int nmat, const void *Xq, const float *X,
-                       int M, int K, const float *U = nullptr, const float *R = nullptr, bool wp = false)
+                       int M, int K, const float *U = nullptr, const float *R = nullptr, bool wp = false,
+                       void *ws_given = nullptr)
 {
     const bool xf16 = Xq == nullptr;
     const int nb = K / 32;
     const int64_t nblk = (int64_t)M * nb;
     int ntot = 0;
     for (int i = 0; i < nmat; i++) ntot += N[i];
-    const size_t pbytes = (size_t)nblk * 64, dbytes = xf16 ? 0 : ((size_t)nblk * 2 + 255) & ~(size_t)255;
-    void *ws = workspace(1, pbytes + dbytes);
+    const size_t pbytes = (size_t)nblk * 64, dbytes = act_panel_bytes(M, K, xf16) - pbytes;
+    void *ws = ws_given ? ws_given : workspace(1, pbytes + dbytes);
     const bool own = ws == nullptr;
     if (own) HOLO_CHECK(hipMallocAsync(&ws, pbytes + dbytes, stream()));
     if (!ws) return;
@@ -657,6 +668,42 @@ static bool gemm_args_ok(const void *Xq, int K)
     return true;
 }
 
+// ---- the allocation-free variant of holo_gemm_q4_0_q8_0 ---------------------------
+//
+// Its activation panel lives in `scratch`, a file-scope device array of
+// kNoAllocScratchBytes that every device the library runs on holds from
+// module load until the process ends.  In host code `scratch` names a
+// host-side stand-in, not device memory: its device address is taken once
+// per device with hipGetSymbolAddress (cuda_init for device 0, or the entry
+// point's first call on another device) and only that address is used.
+// Every call on one device shares the array, and the last call's contents
+// stay there: the panel kernel overwrites every byte a call reads, so nothing
+// needs clearing; calls that overlap on one device (two streams) race.
+constexpr size_t kNoAllocScratchBytes = (size_t)24 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+static void *g_scratch_dev[kMaxDevices];
+
+namespace holo {
+// The device address of `scratch` on the current device, looked up once per
+// device; nullptr if the lookup fails.
+void *noalloc_scratch()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    if (!g_scratch_dev[dev]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) {
+            latch_error((int)e, "hipGetSymbolAddress(scratch)", __FILE__, __LINE__);
+            return nullptr;
+        }
+        g_scratch_dev[dev] = ptr;
+    }
+    return g_scratch_dev[dev];
+}
+}  // namespace holo
+
 extern "C" {
 
 void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, int K)
@@ -671,6 +718,28 @@ void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, 
         return;
     }
     gemm_multi(&Y, &W, &N, 1, Xq, nullptr, M, K);
+}
+
+int holo_gemm_q4_0_q8_0_noalloc(float *Y, const void *W, const void *Xq, int M, int N, int K)
+{
+    if (M <= 0 || N <= 0) return 0;
+    if (!Y || !W || !Xq || K % 32 != 0 || K <= 0) {
+        HOLO_REJECT("holo_gemm_q4_0_q8_0_noalloc: null pointer or K not a positive multiple of 32");
+        return HOLO_EINVAL;
+    }
+    if ((((uintptr_t)W) & 3u) || (((uintptr_t)Xq) & 3u)) {
+        HOLO_REJECT("holo_gemm_q4_0_q8_0_noalloc: W and Xq must be 4-byte aligned");
+        return HOLO_EINVAL;
+    }
+    if (act_panel_bytes(M, K, false) > kNoAllocScratchBytes) {
+        HOLO_REJECT("holo_gemm_q4_0_q8_0_noalloc: M*K too large for the fixed scratch (M*K*33/16 bytes must fit "
+                    "in 24 MiB)");
+        return HOLO_EINVAL;
+    }
+    void *ws = noalloc_scratch();
+    if (!ws) return HOLO_EINVAL;
+    gemm_multi(&Y, &W, &N, 1, Xq, nullptr, M, K, nullptr, nullptr, false, ws);
+    return 0;
 }
 
 void holo_gemm_q4_0_q8_0_multi(float *const *Y, const void *const *W, const int *N, int nmat, const void *Xq, int M,

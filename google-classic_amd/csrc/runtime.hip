@@ -107,6 +107,10 @@ int cuda_init(void)
         fprintf(stderr, "holo_mi355x: cannot allocate the decode-attention scratch\n");
         return -1;
     }
+    if (!holo::noalloc_scratch()) {
+        fprintf(stderr, "holo_mi355x: cannot look up the fixed scratch array\n");
+        return -1;
+    }
     g_initialized = true;
     return 0;
 }

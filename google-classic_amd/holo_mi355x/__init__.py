@@ -136,6 +136,7 @@ _SIGS = {
     "holo_batched_ffn_gate_up": (None, [_P, _P, _P, _P, _I, _I, _I]),
     "holo_quantize_act_q8_0": (None, [_P, _P, _I, _I]),
     "holo_gemm_q4_0_q8_0": (None, [_P, _P, _P, _I, _I, _I]),
+    "holo_gemm_q4_0_q8_0_noalloc": (_I, [_P, _P, _P, _I, _I, _I]),
     "holo_matmul_batch_q4_0": (None, [_P, _P, _P, _I, _I, _I, _P]),
     "holo_gemm_q4_0_q8_0_multi": (None, [_P, _P, _P, _I, _P, _I, _I]),
     "holo_matmul_batch_q4_0_multi": (None, [_P, _P, _P, _I, _P, _I, _I, _P]),

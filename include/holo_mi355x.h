@@ -170,6 +170,18 @@ void holo_matmul_add(float *y, const void *M, const float *v, const float *r,
  * outside graph capture, a stream-ordered allocation under capture.       */
 void holo_quantize_act_q8_0(void *dst_blocks, const float *X, int rows, int k);
 void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, int K);
+/* The same product with no allocation anywhere in the call: no hipMalloc,
+ * hipFree or allocating library routine.  No counterpart in the reference;
+ * it is for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation).  The activation
+ * panel (M*K*2 + M*K/16 bytes, rounded up to 256) is staged in a fixed
+ * 24 MiB device array that the library holds on each device until the
+ * process ends, so M*K*33/16 must fit in 24 MiB (M = 512 takes K up to
+ * 23,831: every config-4 shape); larger calls are rejected (HOLO_EINVAL,
+ * nothing launched).  Returns 0 or HOLO_EINVAL.  The array keeps the last
+ * call's contents and every call on a device shares it: calls that overlap
+ * on one device (issued on two streams) race.                              */
+int holo_gemm_q4_0_q8_0_noalloc(float *Y, const void *W, const void *Xq, int M, int N, int K);
 /* Y[M][N] = X[M][K] . W[N][K]^T for W in Q4_0: M >= 64 runs the f16 product
  * below (or, in HOLO_PREFILL_Q8_0 mode, quantises X and runs the Q8_0 product
  * above); M < 64 runs M fp32-activation GEMVs.                               */
