@@ -486,7 +486,8 @@ def prefill_tops(lib, reps=10):
         lib.holo_quantize_act_q8_0(Xq.ptr, X.ptr, M, K)
         ev = holo.Events()
         calls = {"q8_0": lambda: lib.holo_gemm_q4_0_q8_0(Y.ptr, W.ptr, Xq.ptr, M, N, K),
-                 "f16": lambda: lib.holo_gemm_q4_0_f16(Y.ptr, W.ptr, X.ptr, M, N, K)}
+                 "f16": lambda: lib.holo_gemm_q4_0_f16(Y.ptr, W.ptr, X.ptr, M, N, K),
+                 "exact": lambda: lib.holo_matmul_batch_q4_0(Y.ptr, W.ptr, X.ptr, M, N, K, None)}
         out[name] = {}
         for prod, call in calls.items():
             call()

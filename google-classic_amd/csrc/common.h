@@ -30,6 +30,17 @@ void gemv_chain_release();
 bool attention_scratch_init();
 void attention_scratch_release();
 void panel_workspace_release();  // the batched products' panel buffers (prefill.hip)
+// The batched products' kept workspaces (prefill.hip): slot 0 weight panels,
+// slot 1 activation panels.  A device buffer of at least `bytes`, grown with
+// hipMalloc outside graph capture and reused in stream order; nullptr under
+// capture or when growing fails (the caller then allocates stream-ordered).
+void *workspace(int slot, size_t bytes);
+// The exact batched product (prefill_exact.hip): whether a weight type and
+// stream take it, and the product itself (Y[i] = X . W[i]^T, or of silu(X) *
+// U, plus R for one matrix).
+bool exact_ok(int type, int K, const void *W);
+void exact_product(float *const *Y, const void *const *W, const int *types, const int *N, int nmat, const float *X,
+                   const float *U, const float *R, int M, int K);
 // Device address of the fixed scratch array of holo_gemm_q4_0_q8_0_noalloc on
 // the current device (prefill.hip), looked up once per device; nullptr on failure.
 void *noalloc_scratch();

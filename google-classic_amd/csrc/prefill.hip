@@ -521,7 +521,8 @@ void holo_quantize_act_q8_0(void *dst_blocks, const float *X, int rows, int k)
 static void *g_ws[2] = {nullptr, nullptr};
 static size_t g_ws_bytes[2] = {0, 0};
 
-static void *workspace(int slot, size_t bytes)
+namespace holo {
+void *workspace(int slot, size_t bytes)
 {
     // never under capture: a graph must not hold a buffer a later growth frees
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
@@ -539,6 +540,7 @@ static void *workspace(int slot, size_t bytes)
     g_ws_bytes[slot] = bytes;
     return g_ws[slot];
 }
+}  // namespace holo
 
 // One launch over nmat matrices (holo_gemm_q4_0_q8_0 and its multi-matrix form).
 // Xq (Q8_0 blocks): the Q8_0 product; otherwise X (fp32, 16-byte aligned):
@@ -785,23 +787,45 @@ void holo_gemm_q4_0_f16(float *Y, const void *W, const float *X, int M, int N, i
     holo_gemm_q4_0_f16_multi(&Y, &W, &N, 1, X, M, K);
 }
 
-static int g_prefill_mode = HOLO_PREFILL_F16;
+static int g_prefill_mode = HOLO_PREFILL_EXACT;
 
 void holo_prefill_set_mode(int mode)
 {
-    if (mode != HOLO_PREFILL_F16 && mode != HOLO_PREFILL_Q8_0) {
-        HOLO_REJECT("holo_prefill_set_mode: HOLO_PREFILL_F16 or HOLO_PREFILL_Q8_0");
+    if (mode != HOLO_PREFILL_F16 && mode != HOLO_PREFILL_Q8_0 && mode != HOLO_PREFILL_EXACT) {
+        HOLO_REJECT("holo_prefill_set_mode: HOLO_PREFILL_EXACT, HOLO_PREFILL_F16 or HOLO_PREFILL_Q8_0");
         return;
     }
     g_prefill_mode = mode;
 }
+
+}  // extern "C"
+
+// Exact mode (the default): the exact product (prefill_exact.hip) when every
+// operand fits it; otherwise the callers run fp32-activation GEMVs per row,
+// never a lower-precision product.
+static bool exact_fits(const void *const *W, const int *types, int nmat, const float *X, const float *U, int K)
+{
+    if (!X || ((uintptr_t)X & 15u) || ((uintptr_t)U & 15u)) return false;
+    for (int i = 0; i < nmat; i++)
+        if (!W[i] || !exact_ok(types[i], K, W[i])) return false;
+    return true;
+}
+
+static bool exact_mode() { return g_prefill_mode == HOLO_PREFILL_EXACT; }
+
+extern "C" {
 
 int holo_prefill_get_mode(void) { return g_prefill_mode; }
 
 void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int N, int K, void *scratch_q8)
 {
     if (M <= 0 || N <= 0) return;
-    if (M < 64) {
+    const int t = HOLO_TYPE_Q4_0;
+    if (M >= 64 && exact_mode() && exact_fits(&W, &t, 1, X, nullptr, K)) {
+        exact_product(&Y, &W, &t, &N, 1, X, nullptr, nullptr, M, K);
+        return;
+    }
+    if (M < 64 || exact_mode()) {
         for (int m = 0; m < M; m++) cuda_matmul_q4_0(Y + (int64_t)m * N, W, X + (int64_t)m * K, N, K);
         return;
     }
@@ -824,7 +848,12 @@ void holo_matmul_batch_q4_0_add(float *Y, const void *W, const float *X, const f
         HOLO_REJECT("holo_matmul_batch_q4_0_add: null pointer or K not a positive multiple of 32");
         return;
     }
-    if (M < 64) {
+    const int t = HOLO_TYPE_Q4_0;
+    if (M >= 64 && exact_mode() && exact_fits(&W, &t, 1, X, nullptr, K)) {
+        exact_product(&Y, &W, &t, &N, 1, X, nullptr, R, M, K);
+        return;
+    }
+    if (M < 64 || exact_mode()) {
         for (int m = 0; m < M; m++)
             holo_matmul_add(Y + (int64_t)m * N, W, X + (int64_t)m * K, R + (int64_t)m * N, N, K, HOLO_TYPE_Q4_0);
         return;
@@ -849,6 +878,11 @@ void holo_matmul_batch_q4_0_swiglu_add(float *Y, const void *W, float *G, const 
         HOLO_REJECT("holo_matmul_batch_q4_0_swiglu_add: null pointer or K not a positive multiple of 32");
         return;
     }
+    const int t = HOLO_TYPE_Q4_0;
+    if (M >= 64 && exact_mode() && exact_fits(&W, &t, 1, G, U, K)) {
+        exact_product(&Y, &W, &t, &N, 1, G, U, R, M, K);
+        return;
+    }
     if (M >= 64 && g_prefill_mode == HOLO_PREFILL_F16 && !(((uintptr_t)G | (uintptr_t)U) & 15u)) {
         gemm_multi(&Y, &W, &N, 1, nullptr, G, M, K, U, R);
         return;
@@ -865,7 +899,12 @@ void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const i
         HOLO_REJECT("holo_matmul_batch_q4_0_multi: null array, or not 1..3 matrices whose N are multiples of 128");
         return;
     }
-    if (M < 64) {
+    const int T[3] = {HOLO_TYPE_Q4_0, HOLO_TYPE_Q4_0, HOLO_TYPE_Q4_0};
+    if (M >= 64 && exact_mode() && exact_fits(W, T, nmat, X, nullptr, K)) {
+        exact_product(Y, W, T, N, nmat, X, nullptr, nullptr, M, K);
+        return;
+    }
+    if (M < 64 || exact_mode()) {
         for (int i = 0; i < nmat; i++) holo_matmul_batch_q4_0(Y[i], W[i], X, M, N[i], K, scratch_q8);
         return;
     }
@@ -959,7 +998,11 @@ void holo_matmul_batch(float *Y, const void *W, const float *X, int M, int N, in
         HOLO_REJECT("holo_matmul_batch: null pointer");
         return;
     }
-    if (M < 64 || !panel_ok(type, K) || !panel_src_aligned(W, type) || ((uintptr_t)X & 15u)) {
+    if (M >= 64 && exact_mode() && exact_fits(&W, &type, 1, X, nullptr, K)) {
+        exact_product(&Y, &W, &type, &N, 1, X, nullptr, nullptr, M, K);
+        return;
+    }
+    if (M < 64 || exact_mode() || !panel_ok(type, K) || !panel_src_aligned(W, type) || ((uintptr_t)X & 15u)) {
         for (int m = 0; m < M; m++) holo_matmul(Y + (int64_t)m * N, W, X + (int64_t)m * K, N, K, type);
         return;
     }
@@ -978,7 +1021,12 @@ void holo_matmul_batch_multi(float *const *Y, const void *const *W, const int *N
         HOLO_REJECT("holo_matmul_batch_multi: null array, or not 1..3 matrices whose N are multiples of 128");
         return;
     }
-    bool ok = M >= 64 && panel_ok(type, K) && !((uintptr_t)X & 15u);
+    const int T[3] = {type, type, type};
+    if (M >= 64 && exact_mode() && exact_fits(W, T, nmat, X, nullptr, K)) {
+        exact_product(Y, W, T, N, nmat, X, nullptr, nullptr, M, K);
+        return;
+    }
+    bool ok = M >= 64 && !exact_mode() && panel_ok(type, K) && !((uintptr_t)X & 15u);
     for (int i = 0; i < nmat; i++) ok = ok && Y[i] && W[i] && panel_src_aligned(W[i], type);
     if (!ok) {
         for (int i = 0; i < nmat; i++) holo_matmul_batch(Y[i], W[i], X, M, N[i], K, type);
@@ -1001,7 +1049,11 @@ void holo_matmul_batch_multi_types(float *const *Y, const void *const *W, const 
         holo_matmul_batch_multi(Y, W, N, nmat, X, M, K, types[0]);
         return;
     }
-    bool ok = M >= 64 && !((uintptr_t)X & 15u);
+    if (M >= 64 && exact_mode() && exact_fits(W, types, nmat, X, nullptr, K)) {
+        exact_product(Y, W, types, N, nmat, X, nullptr, nullptr, M, K);
+        return;
+    }
+    bool ok = M >= 64 && !exact_mode() && !((uintptr_t)X & 15u);
     for (int i = 0; i < nmat; i++)
         ok = ok && Y[i] && W[i] && panel_ok(types[i], K) && panel_src_aligned(W[i], types[i]);
     if (!ok) {
@@ -1022,7 +1074,11 @@ void holo_matmul_batch_add(float *Y, const void *W, const float *X, const float 
         HOLO_REJECT("holo_matmul_batch_add: null pointer");
         return;
     }
-    if (M >= 64 && panel_ok(type, K) && panel_src_aligned(W, type) && !((uintptr_t)X & 15u)) {
+    if (M >= 64 && exact_mode() && exact_fits(&W, &type, 1, X, nullptr, K)) {
+        exact_product(&Y, &W, &type, &N, 1, X, nullptr, R, M, K);  // the add in the GEMM's store
+        return;
+    }
+    if (M >= 64 && !exact_mode() && panel_ok(type, K) && panel_src_aligned(W, type) && !((uintptr_t)X & 15u)) {
         gemm_panel(&Y, &W, &N, 1, X, M, K, type, nullptr, R);  // the add in the GEMM's store
         return;
     }
@@ -1049,7 +1105,12 @@ void holo_matmul_batch_swiglu_add(float *Y, const void *W, float *G, const float
         HOLO_REJECT("holo_matmul_batch_swiglu_add: null pointer");
         return;
     }
-    if (M >= 64 && panel_ok(type, K) && panel_src_aligned(W, type) && !(((uintptr_t)G | (uintptr_t)U) & 15u)) {
+    if (M >= 64 && exact_mode() && exact_fits(&W, &type, 1, G, U, K)) {
+        exact_product(&Y, &W, &type, &N, 1, G, U, R, M, K);  // silu(G) * U in the activation halves
+        return;
+    }
+    if (M >= 64 && !exact_mode() && panel_ok(type, K) && panel_src_aligned(W, type) &&
+        !(((uintptr_t)G | (uintptr_t)U) & 15u)) {
         gemm_panel(&Y, &W, &N, 1, G, M, K, type, U, R);  // silu(G) * U in the activation panel
         return;
     }

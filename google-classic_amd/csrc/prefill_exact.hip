@@ -1,0 +1,657 @@
+// prefill_exact.hip -- the batched product Y[M][N] = X[M][K] . W[N][K]^T at
+// fp32 accuracy on the f16 matrix cores: the default of every batched
+// matmul (holo_matmul_batch*, the prompt forward).
+//
+// The reference has no batched path: its prompt loop multiplies one token at
+// a time in fp32 (src/ai/llm.c:1049, matmul_q llm.c:770-926).  The product
+// here holds every operand exactly or to 22 bits:
+//   activations  x = xh + xl, xh = f16(x), xl = f16(x - xh): |x - xh - xl|
+//                <= 2^-22 |x| (xl rounds once more; both halves are f16)
+//   weights      the block's integers, exact in f16, with the block's scales
+//                in fp32 (every scale product of the formats is exact):
+//                  Q4_0  q - 8                 scale d            (quant.c:136-153)
+//                  Q8_0  q                     scale d            (quant.c:118-128)
+//                  Q4_K  q (0..15), sub-block scale d*sc and min dmin*m
+//                                                                 (quant.c:277-311)
+//                  Q6_K  q - 32, 16-weight group scale d*sc       (quant.c:241-271)
+//                  F16   the weight itself, no scale
+// Per 32-block b, output (m, n), the matrix cores accumulate the block's
+// integer-weight dot over both activation halves in fp32,
+//   C = sum_k (xh[m,k] + xl[m,k]) * w[n,k]      (four v_mfma_f32_32x32x16_f16)
+// and the fp32 epilogue folds it in, in block order:
+//   acc = fmaf(scale[n,b], C, acc)          (Q6_K: once per 16-weight group)
+//   acc = fmaf(-dmin*m[n,b], sum_k x[m,k], acc)    (Q4_K only)
+// so the result carries fp32 accumulation error plus the 2^-22 split, not
+// the 2^-11 of an f16 operand.  f16 range: |x| must stay below 65504.
+//
+// Workgroup: 4 waves in a 2 x 2 grid, each owning WM x WN 32 x 32 tiles; K
+// advances S blocks per stage through a double-buffered LDS stage, the next
+// stage's global loads in registers while the current one is multiplied.
+#include "common.h"
+#include "quant_blocks.h"
+
+#include <hip/hip_ext.h>
+#include <limits.h>
+
+#include <type_traits>
+
+#pragma clang fp contract(off)
+
+namespace holo {
+
+namespace {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// Weight source of one launch.
+enum ExactW { EW_Q4_0 = 0, EW_Q8_0 = 1, EW_Q4_K = 2, EW_P16 = 3, EW_F16 = 4 };
+
+constexpr int kExactMats = 3;
+
+struct ExactArgs {
+    float *Y[kExactMats];
+    const uint8_t *W[kExactMats];  // block stream, or f16 panel [N_i][K] (EW_P16, EW_F16)
+    const float *WS[kExactMats];   // EW_P16: group scales [N_i][K/16]
+    int n_end[kExactMats];         // prefix sums of N_i; unused entries INT_MAX
+    const _Float16 *Ah, *Al;       // activation halves [M][K]
+    const float *Sx;               // [M][nb] block sums of x (EW_Q4_K)
+    int M, N, nb;
+    int ntm, tiles;
+    const float *R;                // one matrix only: Y = R + product (may alias Y)
+};
+
+struct ExactMat {
+    const uint8_t *W;
+    const float *WS;
+    float *Y;
+    int nbase, N;
+    int64_t w_bytes;
+};
+
+// ---- integers of a block in f16 ----------------------------------------------------
+// v_perm pairs a byte with 0x64, giving the f16 value 1024 + byte; one
+// packed f16 add removes the bias, exactly.
+
+__device__ __forceinline__ uint32_t f16_pair(uint32_t bytes, uint32_t sel, _Float16 bias)
+{
+    const h2 b2 = {bias, bias};
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, bytes, sel)) + b2);
+}
+
+// Eight nibbles of x (four bytes): lo[0..1] = low nibbles (k = 4j..4j+3 of the
+// block), hi[0..1] = high nibbles (k = 16+4j..), each as f16 (nibble + off).
+__device__ __forceinline__ void nibbles_f16(uint32_t x, _Float16 off, uint32_t lo[2], uint32_t hi[2])
+{
+    const uint32_t t0 = x & 0x0F0F0F0Fu, t1 = (x >> 4) & 0x0F0F0F0Fu;
+    const _Float16 bias = (_Float16)(-1024.0f) + off;
+    lo[0] = f16_pair(t0, 0x04010400u, bias);
+    lo[1] = f16_pair(t0, 0x04030402u, bias);
+    hi[0] = f16_pair(t1, 0x04010400u, bias);
+    hi[1] = f16_pair(t1, 0x04030402u, bias);
+}
+
+// Four signed bytes as f16: byte ^ 0x80 is q + 128 in 0..255.
+__device__ __forceinline__ void int8s_f16(uint32_t x, uint32_t out[2])
+{
+    const uint32_t t = x ^ 0x80808080u;
+    out[0] = f16_pair(t, 0x04010400u, (_Float16)-1152.0f);
+    out[1] = f16_pair(t, 0x04030402u, (_Float16)-1152.0f);
+}
+
+template <int WM, int WN, int S>
+struct XGeo {
+    static constexpr int NT = 256;
+    static constexpr int TM = 64 * WM, TN = 64 * WN;
+    static constexpr int ROW = 32 * S + 8;  // f16 per LDS row; the 16-byte pad spreads rows over the banks
+    static constexpr int AH = 0;
+    static constexpr int AL = AH + TM * ROW * 2;
+    static constexpr int B = AL + TM * ROW * 2;
+    static constexpr int BS = B + TN * ROW * 2;   // fp32 [TN][2S]: scale of each 16-weight half-block
+    static constexpr int BM = BS + TN * 2 * S * 4;  // fp32 [TN][S]: Q4_K mins
+    static constexpr int AS = BM + TN * S * 4;    // fp32 [S][TM]: block sums of x
+    static constexpr int STAGE = (AS + S * TM * 4 + 15) & ~15;
+    static constexpr int LDS = 2 * STAGE;
+    static constexpr int NA = TM * S * 4 / NT;           // 16-byte activation pieces per thread and half
+    static constexpr int NAS = (TM * S + NT - 1) / NT;   // block sums per thread
+    static constexpr int NB = (TN * S + NT - 1) / NT;    // weight blocks per thread
+    static constexpr int NWP = (TN * S * 4 + NT - 1) / NT;  // 16-byte weight-panel pieces per thread
+    static constexpr int NWS = (TN * 2 * S + NT - 1) / NT;  // group scales per thread
+    static_assert((TM * S * 4) % NT == 0, "activation pieces must split evenly over the threads");
+};
+
+template <int WF>
+struct WRaw;
+template <>
+struct WRaw<EW_Q4_0> {
+    Q4_0Unit u;
+};
+template <>
+struct WRaw<EW_Q8_0> {
+    Q8_0Unit u;
+};
+template <>
+struct WRaw<EW_Q4_K> {
+    v4u h, q;
+    uint32_t j;
+};
+
+// Registers of one stage between its global loads and its LDS writes: blocks
+// kb0 .. kb0+S-1 of the workgroup's rows and columns.  Indices past the last
+// row, column or block re-read the last one (in bounds, never used).
+template <int WF, int WM, int WN, int S>
+struct XStage {
+    using G = XGeo<WM, WN, S>;
+    static constexpr bool PANEL = WF == EW_P16 || WF == EW_F16;
+    v4u ah[G::NA], al[G::NA];
+    float as[WF == EW_Q4_K ? G::NAS : 1];
+    WRaw<WF == EW_Q4_0 || WF == EW_Q8_0 || WF == EW_Q4_K ? WF : EW_Q4_0> rb[PANEL ? 1 : G::NB];
+    v4u rw[PANEL ? G::NWP : 1];
+    float rs[WF == EW_P16 ? G::NWS : 1];
+
+    __device__ __forceinline__ void fetch(const ExactArgs &a, const ExactMat &w, int tid, int m0, int n0, int kb0)
+    {
+        const int nb = a.nb;
+        const int64_t K = (int64_t)nb * 32;
+#pragma unroll
+        for (int i = 0; i < G::NA; i++) {
+            const int p = tid + G::NT * i, r = p / (4 * S), c = p % (4 * S);
+            const int64_t o = (int64_t)min(m0 + r, a.M - 1) * K + (int64_t)min(kb0 + c / 4, nb - 1) * 32 + (c % 4) * 8;
+            ah[i] = *(const v4u *)(a.Ah + o);
+            al[i] = *(const v4u *)(a.Al + o);
+        }
+        if constexpr (WF == EW_Q4_K) {
+#pragma unroll
+            for (int i = 0; i < G::NAS; i++) {
+                const int v = min(tid + G::NT * i, G::TM * S - 1), sb = v / G::TM, r = v % G::TM;
+                as[i] = a.Sx[(int64_t)min(m0 + r, a.M - 1) * nb + min(kb0 + sb, nb - 1)];
+            }
+        }
+        if constexpr (PANEL) {
+            const _Float16 *wp = (const _Float16 *)w.W;
+#pragma unroll
+            for (int i = 0; i < G::NWP; i++) {
+                const int p = min(tid + G::NT * i, G::TN * S * 4 - 1), n = p / (4 * S), c = p % (4 * S);
+                rw[i] = *(const v4u *)(wp + (int64_t)min(n0 + n, w.N - 1) * K + (int64_t)min(kb0 + c / 4, nb - 1) * 32 +
+                                      (c % 4) * 8);
+            }
+            if constexpr (WF == EW_P16) {
+#pragma unroll
+                for (int i = 0; i < G::NWS; i++) {
+                    const int v = min(tid + G::NT * i, G::TN * 2 * S - 1), n = v / (2 * S), j = v % (2 * S);
+                    rs[i] = w.WS[(int64_t)min(n0 + n, w.N - 1) * (2 * nb) + min(2 * kb0 + j, 2 * nb - 1)];
+                }
+            }
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < G::NB; i++) {
+            const int v = min(tid + G::NT * i, G::TN * S - 1), n = v / S, b = min(kb0 + v % S, nb - 1);
+            const int64_t g = (int64_t)min(n0 + n, w.N - 1) * nb + b;
+            if constexpr (WF == EW_Q4_0) {
+                rb[i].u = load_q4_0(w.W, g, w.w_bytes);
+            } else if constexpr (WF == EW_Q8_0) {
+                rb[i].u = load_q8_0(w.W, g, w.w_bytes);
+            } else if constexpr (WF == EW_Q4_K) {
+                // unit g: superblock g / 8 (144 bytes, 16-byte aligned), sub-block g % 8
+                const uint8_t *sb = w.W + (g >> 3) * 144;
+                rb[i].j = (uint32_t)(g & 7);
+                rb[i].h = *(const v4u *)sb;
+                rb[i].q = *(const v4u *)(sb + 16 + 16 * rb[i].j);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void stash(uint8_t *base, int tid) const
+    {
+#pragma unroll
+        for (int i = 0; i < G::NA; i++) {
+            const int p = tid + G::NT * i, r = p / (4 * S), c = p % (4 * S);
+            *(v4u *)(base + G::AH + (r * G::ROW + c * 8) * 2) = ah[i];
+            *(v4u *)(base + G::AL + (r * G::ROW + c * 8) * 2) = al[i];
+        }
+        if constexpr (WF == EW_Q4_K) {
+#pragma unroll
+            for (int i = 0; i < G::NAS; i++) {
+                const int v = tid + G::NT * i;
+                if (v < G::TM * S) ((float *)(base + G::AS))[v] = as[i];  // [S][TM]
+            }
+        }
+        if constexpr (PANEL) {
+#pragma unroll
+            for (int i = 0; i < G::NWP; i++) {
+                const int p = tid + G::NT * i, n = p / (4 * S), c = p % (4 * S);
+                if (p < G::TN * S * 4) *(v4u *)(base + G::B + (n * G::ROW + c * 8) * 2) = rw[i];
+            }
+            if constexpr (WF == EW_P16) {
+#pragma unroll
+                for (int i = 0; i < G::NWS; i++) {
+                    const int v = tid + G::NT * i;
+                    if (v < G::TN * 2 * S) ((float *)(base + G::BS))[v] = rs[i];
+                }
+            }
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < G::NB; i++) {
+            const int v = tid + G::NT * i, n = v / S, sb = v % S;
+            if (v >= G::TN * S) continue;
+            uint32_t lo[8], hi[8];
+            float scale, mn = 0.f;
+            if constexpr (WF == EW_Q4_0) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) nibbles_f16(rb[i].u.q[j], (_Float16)-8.0f, &lo[2 * j], &hi[2 * j]);
+                scale = rb[i].u.d;
+            } else if constexpr (WF == EW_Q8_0) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    int8s_f16(rb[i].u.q[j], &lo[2 * j]);
+                    int8s_f16(rb[i].u.q[4 + j], &hi[2 * j]);
+                }
+                scale = rb[i].u.d;
+            } else if constexpr (WF == EW_Q4_K) {
+                const v4u q = rb[i].q;
+#pragma unroll
+                for (int j = 0; j < 4; j++) nibbles_f16(q[j], (_Float16)0.0f, &lo[2 * j], &hi[2 * j]);
+                uint32_t sc, m6;
+                q4_k_scale_min(rb[i].h.y, rb[i].h.z, rb[i].h.w, rb[i].j, sc, m6);
+                scale = half_bits_to_float(rb[i].h.x) * (float)sc;  // exact: 11-bit x 6-bit
+                mn = half_bits_to_float(rb[i].h.x >> 16) * (float)m6;
+            }
+            v4u *dst = (v4u *)(base + G::B + (n * G::ROW + sb * 32) * 2);
+            dst[0] = v4u{lo[0], lo[1], lo[2], lo[3]};  // k = 0..7
+            dst[1] = v4u{lo[4], lo[5], lo[6], lo[7]};  // k = 8..15
+            dst[2] = v4u{hi[0], hi[1], hi[2], hi[3]};  // k = 16..23
+            dst[3] = v4u{hi[4], hi[5], hi[6], hi[7]};  // k = 24..31
+            ((float *)(base + G::BS))[n * 2 * S + 2 * sb] = scale;
+            if constexpr (WF == EW_Q4_K) ((float *)(base + G::BM))[n * S + sb] = mn;
+        }
+    }
+};
+
+__device__ __forceinline__ v16f mfma16(v8h a, v8h b, v16f c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// v_mfma_f32_32x32x16_f16 (wave64): lane l supplies A[l%32][8*(l/32)+t] and
+// B[8*(l/32)+t][l%32], t = 0..7; D[i][j] lands in lane j + 32*((i/4)%2),
+// register (i%4) + 4*(i/8).  A lane's 16 outputs share one column n, so a
+// block's scale is one value per lane.
+template <int WF, int WM, int WN, int S, int OCC>
+__global__ __launch_bounds__(256, OCC) void gemm_exact_k(ExactArgs a)
+{
+    using G = XGeo<WM, WN, S>;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, c32 = lane & 31;
+
+    // Tile of this workgroup: XCD x (workgroups go to the 8 XCDs round
+    // robin) takes a contiguous run of tiles when the count allows, so the
+    // row tiles that share a weight tile share that XCD's L2.
+    const int g = blockIdx.x;
+    const int t = (a.tiles & 7) ? g : (g & 7) * (a.tiles >> 3) + (g >> 3);
+    const int m0 = (t % a.ntm) * G::TM, ng = (t / a.ntm) * G::TN;
+    const int sel = (ng >= a.n_end[0]) + (ng >= a.n_end[1]);
+    ExactMat w;
+    w.W = sel == 2 ? a.W[2] : sel == 1 ? a.W[1] : a.W[0];
+    w.WS = sel == 2 ? a.WS[2] : sel == 1 ? a.WS[1] : a.WS[0];
+    w.Y = sel == 2 ? a.Y[2] : sel == 1 ? a.Y[1] : a.Y[0];
+    w.nbase = sel == 2 ? a.n_end[1] : sel == 1 ? a.n_end[0] : 0;
+    w.N = (sel == 2 ? a.n_end[2] : sel == 1 ? a.n_end[1] : a.n_end[0]) - w.nbase;
+    w.w_bytes = (int64_t)w.N * a.nb * (WF == EW_Q4_0 ? 18 : 34);
+    const int n0 = ng - w.nbase;
+    const int wm0 = (wave >> 1) * 32 * WM, wn0 = (wave & 1) * 32 * WN;
+    const int nb = a.nb;
+    const int nst = (nb + S - 1) / S;
+    v16f acc[WM][WN];
+#pragma unroll
+    for (int mi = 0; mi < WM; mi++)
+#pragma unroll
+        for (int ni = 0; ni < WN; ni++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[mi][ni][r] = 0.f;
+
+    auto compute = [&](int buf, int kb0) {
+        const uint8_t *base = lds + buf * G::STAGE;
+        const _Float16 *lAh = (const _Float16 *)(base + G::AH);
+        const _Float16 *lAl = (const _Float16 *)(base + G::AL);
+        const _Float16 *lB = (const _Float16 *)(base + G::B);
+        const float *lBs = (const float *)(base + G::BS);
+        const float *lBm = (const float *)(base + G::BM);
+        const float *lAs = (const float *)(base + G::AS);
+        const v16f zero = {};
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            if (kb0 + s >= nb) break;
+            v8h ah0[WM], ah1[WM], al0[WM], al1[WM], b0[WN], b1[WN];
+            float sc0[WN], sc1[WN], mn[WN];
+            float4 sx[WM][4];
+#pragma unroll
+            for (int mi = 0; mi < WM; mi++) {
+                const int r = wm0 + 32 * mi + c32;
+                const int o = r * G::ROW + s * 32 + 8 * h;
+                ah0[mi] = *(const v8h *)(lAh + o);
+                ah1[mi] = *(const v8h *)(lAh + o + 16);
+                al0[mi] = *(const v8h *)(lAl + o);
+                al1[mi] = *(const v8h *)(lAl + o + 16);
+                if constexpr (WF == EW_Q4_K) {
+                    // rows (r & 3) + 4h + 8(r >> 2) of register r: four runs of four
+#pragma unroll
+                    for (int q = 0; q < 4; q++) sx[mi][q] = *(const float4 *)(lAs + s * G::TM + wm0 + 32 * mi + 8 * q + 4 * h);
+                }
+            }
+#pragma unroll
+            for (int ni = 0; ni < WN; ni++) {
+                const int n = wn0 + 32 * ni + c32;
+                const int o = n * G::ROW + s * 32 + 8 * h;
+                b0[ni] = *(const v8h *)(lB + o);
+                b1[ni] = *(const v8h *)(lB + o + 16);
+                sc0[ni] = lBs[n * 2 * S + 2 * s];
+                sc1[ni] = lBs[n * 2 * S + 2 * s + 1];
+                mn[ni] = WF == EW_Q4_K ? lBm[n * S + s] : 0.f;
+            }
+#pragma unroll
+            for (int mi = 0; mi < WM; mi++)
+#pragma unroll
+                for (int ni = 0; ni < WN; ni++) {
+                    if constexpr (WF == EW_F16) {
+                        acc[mi][ni] = mfma16(ah0[mi], b0[ni], acc[mi][ni]);
+                        acc[mi][ni] = mfma16(ah1[mi], b1[ni], acc[mi][ni]);
+                        acc[mi][ni] = mfma16(al0[mi], b0[ni], acc[mi][ni]);
+                        acc[mi][ni] = mfma16(al1[mi], b1[ni], acc[mi][ni]);
+                    } else if constexpr (WF == EW_P16) {
+                        v16f c = mfma16(al0[mi], b0[ni], mfma16(ah0[mi], b0[ni], zero));
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[mi][ni][r] = __builtin_fmaf(sc0[ni], c[r], acc[mi][ni][r]);
+                        c = mfma16(al1[mi], b1[ni], mfma16(ah1[mi], b1[ni], zero));
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[mi][ni][r] = __builtin_fmaf(sc1[ni], c[r], acc[mi][ni][r]);
+                    } else {
+                        v16f c = mfma16(ah0[mi], b0[ni], zero);
+                        c = mfma16(ah1[mi], b1[ni], c);
+                        c = mfma16(al0[mi], b0[ni], c);
+                        c = mfma16(al1[mi], b1[ni], c);
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[mi][ni][r] = __builtin_fmaf(sc0[ni], c[r], acc[mi][ni][r]);
+                        if constexpr (WF == EW_Q4_K) {
+#pragma unroll
+                            for (int r = 0; r < 16; r++)
+                                acc[mi][ni][r] = __builtin_fmaf(-mn[ni], sx[mi][r >> 2][r & 3], acc[mi][ni][r]);
+                        }
+                    }
+                }
+        }
+    };
+
+    XStage<WF, WM, WN, S> st;
+    st.fetch(a, w, tid, m0, n0, 0);
+    st.stash(lds, tid);
+    __syncthreads();
+    for (int k = 0; k < nst; k++) {
+        if (k + 1 < nst) st.fetch(a, w, tid, m0, n0, (k + 1) * S);
+        compute(k & 1, k * S);
+        if (k + 1 < nst) st.stash(lds + ((k + 1) & 1) * G::STAGE, tid);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int mi = 0; mi < WM; mi++)
+#pragma unroll
+        for (int ni = 0; ni < WN; ni++) {
+            const int n = n0 + wn0 + 32 * ni + c32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm0 + 32 * mi + (r & 3) + 4 * h + 8 * (r >> 2);
+                if (m < a.M && n < w.N) {
+                    const int64_t o = (int64_t)m * w.N + n;
+                    w.Y[o] = a.R ? a.R[o] + acc[mi][ni][r] : acc[mi][ni][r];
+                }
+            }
+        }
+}
+
+// ---- the activation halves: Ah, Al [M][K] f16 and the block sums Sx [M][K/32] ----
+// One thread per 8 values; the 4 threads of a 32-block sit in an aligned
+// lane quad, whose partial sums meet with two DPP steps.  SWIGLU: the
+// activations are silu(g) * u as cuda_silu_mul computes them
+// (cuda_ops.cu:304-314).
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(256) void xsplit_k(uint4 *__restrict__ Ah, uint4 *__restrict__ Al, float *__restrict__ Sx,
+                                                const float *__restrict__ X, const float *__restrict__ U, int64_t n8)
+{
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = g < n8;
+    const int64_t gi = live ? g : n8 - 1;
+    float v[8];
+    *(float4 *)&v[0] = ((const float4 *)X)[2 * gi];
+    *(float4 *)&v[4] = ((const float4 *)X)[2 * gi + 1];
+    if constexpr (SWIGLU) {
+        float u[8];
+        *(float4 *)&u[0] = ((const float4 *)U)[2 * gi];
+        *(float4 *)&u[4] = ((const float4 *)U)[2 * gi + 1];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = (v[j] / (1.0f + expf(-v[j]))) * u[j];
+    }
+    uint32_t hw[4], lw[4];
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const _Float16 h0 = (_Float16)v[2 * j], h1 = (_Float16)v[2 * j + 1];
+        const _Float16 l0 = (_Float16)(v[2 * j] - (float)h0), l1 = (_Float16)(v[2 * j + 1] - (float)h1);
+        hw[j] = __builtin_bit_cast(uint32_t, h2{h0, h1});
+        lw[j] = __builtin_bit_cast(uint32_t, h2{l0, l1});
+        s += v[2 * j] + v[2 * j + 1];
+    }
+    // sum over the quad (lanes 4q .. 4q+3 = the block's 32 values, in order)
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+    if (!live) return;
+    Ah[g] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    Al[g] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    if (Sx && (g & 3) == 0) Sx[g >> 2] = s;
+}
+
+// ---- Q6_K integer panel: (q - 32) in f16 [N][K] and the group scales d*sc [N][K/16] ----
+// One thread per (superblock, half h, slice s): l = 16s .. 16s + 15 of the
+// half, all four j, the values y[256b + 128h + 32j + l] of
+// dequantize_row_q6_k (quant.c:252-268) without their scale, which goes to
+// group (256b + 128h + 32j + 16s) / 16.
+
+__global__ __launch_bounds__(256) void q6_k_int_panel_k(_Float16 *__restrict__ y, float *__restrict__ ys,
+                                                        const uint8_t *__restrict__ W, int64_t ntask)
+{
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= ntask) return;
+    const int64_t b = t >> 2;
+    const int hf = (int)((t >> 1) & 1), sl = (int)(t & 1);
+    const uint8_t *sb = W + b * 210;
+    uint32_t qa[4], qb[4], qh[4];
+    q6_run16(sb + 64 * hf + 16 * sl, qa);
+    q6_run16(sb + 64 * hf + 32 + 16 * sl, qb);
+    q6_run16(sb + 128 + 32 * hf + 16 * sl, qh);
+    const int8_t *sc = (const int8_t *)(sb + 192) + 8 * hf;
+    const float d = half_bits_to_float_exact((uint32_t)sb[208] | ((uint32_t)sb[209] << 8));
+    _Float16 *o = y + b * 256 + 128 * hf + 16 * sl;
+    float *os = ys + b * 16 + 8 * hf + sl;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t *ql = (j & 1) ? qb : qa;
+        os[2 * j] = d * (float)sc[sl + 2 * j];  // exact: 11-bit x 8-bit
+        uint32_t wv[8];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t q = ((ql[c] >> (4 * (j >> 1))) & 0x0F0F0F0Fu) | (((qh[c] >> (2 * j)) & 0x03030303u) << 4);
+            wv[2 * c] = f16_pair(q, 0x04010400u, (_Float16)-1056.0f);      // 1024 + q - 1056 = q - 32
+            wv[2 * c + 1] = f16_pair(q, 0x04030402u, (_Float16)-1056.0f);
+        }
+        uint4 *p = (uint4 *)(o + 32 * j);
+        p[0] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+        p[1] = make_uint4(wv[4], wv[5], wv[6], wv[7]);
+    }
+}
+
+template <int WF, int WM, int WN, int S, int OCC>
+void launch_exact(ExactArgs a)
+{
+    using G = XGeo<WM, WN, S>;
+    a.ntm = (a.M + G::TM - 1) / G::TM;
+    a.tiles = a.ntm * ((a.N + G::TN - 1) / G::TN);
+    auto kern = gemm_exact_k<WF, WM, WN, S, OCC>;
+    static bool attr = false;
+    if (!attr) {
+        HOLO_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS));
+        attr = true;
+    }
+    hipEvent_t e0, e1;
+    if (take_launch_events(&e0, &e1))
+        hipExtLaunchKernelGGL(kern, dim3(a.tiles), dim3(G::NT), G::LDS, stream(), e0, e1, 0, a);
+    else
+        hipLaunchKernelGGL(kern, dim3(a.tiles), dim3(G::NT), G::LDS, stream(), a);
+    HOLO_LAUNCH_CHECK();
+}
+
+// 128 x 128 workgroup tiles (64 x 64 per wave, one block per stage) when there
+// are at least as many as CUs; otherwise 64 x 64 (32 x 32 per wave, two
+// blocks per stage) for four times the workgroups.
+template <int WF>
+void launch_exact_for(const ExactArgs &a)
+{
+    const long tiles128 = (long)((a.M + 127) / 128) * ((a.N + 127) / 128);
+    if (tiles128 >= num_cus()) launch_exact<WF, 2, 2, 1, 2>(a);
+    else launch_exact<WF, 1, 1, 2, 2>(a);
+}
+
+int exact_kind(int type)
+{
+    switch (type) {
+    case HOLO_TYPE_Q4_0: return EW_Q4_0;
+    case HOLO_TYPE_Q8_0: return EW_Q8_0;
+    case HOLO_TYPE_Q4_K: return EW_Q4_K;
+    case HOLO_TYPE_Q6_K: return EW_P16;
+    case HOLO_TYPE_F16: return EW_F16;
+    default: return -1;
+    }
+}
+
+}  // namespace
+
+// Takes the exact product: M >= 1, K whole blocks of the type (Q4_K, Q6_K: a
+// multiple of 256), activations 16-byte aligned; the weight stream
+// aligned as its loads need (Q4_0/Q8_0: 4 bytes, Q4_K: 16, Q6_K: 2, F16:
+// 16).
+bool exact_ok(int type, int K, const void *W)
+{
+    const uintptr_t w = (uintptr_t)W;
+    switch (type) {
+    case HOLO_TYPE_Q4_0:
+    case HOLO_TYPE_Q8_0: return K % 32 == 0 && K > 0 && (w & 3u) == 0;
+    case HOLO_TYPE_Q4_K: return K % 256 == 0 && K > 0 && (w & 15u) == 0;
+    case HOLO_TYPE_Q6_K: return K % 256 == 0 && K > 0 && (w & 1u) == 0;
+    case HOLO_TYPE_F16: return K % 32 == 0 && K > 0 && (w & 15u) == 0;
+    default: return false;
+    }
+}
+
+// Y[i] = X . W[i]^T (or (silu(X) * U) . W[i]^T, plus R for one matrix) for
+// nmat matrices sharing the activations; every type must pass exact_ok, and
+// with several matrices of one type every N[i] must be a multiple of 128.
+// Matrices of one type share a launch; the activation halves are built once.
+void exact_product(float *const *Y, const void *const *W, const int *types, const int *N, int nmat, const float *X,
+                   const float *U, const float *R, int M, int K)
+{
+    const int nb = K / 32;
+    const size_t half = ((size_t)M * K * 2 + 255) & ~(size_t)255;
+    const size_t abytes = 2 * half + (size_t)M * nb * 4;
+    void *aws = workspace(1, abytes);
+    const bool own_a = aws == nullptr;
+    if (own_a) HOLO_CHECK(hipMallocAsync(&aws, abytes, stream()));
+    if (!aws) return;
+    _Float16 *Ah = (_Float16 *)aws, *Al = (_Float16 *)((uint8_t *)aws + half);
+    float *Sx = (float *)((uint8_t *)aws + 2 * half);
+    bool need_sx = false;
+    size_t pbytes = 0;
+    for (int i = 0; i < nmat; i++) {
+        need_sx = need_sx || types[i] == HOLO_TYPE_Q4_K;
+        if (types[i] == HOLO_TYPE_Q6_K) pbytes += (size_t)N[i] * K * 2 + (size_t)N[i] * (K / 16) * 4;
+    }
+    const int64_t n8 = (int64_t)M * K / 8;
+    const unsigned grid = (unsigned)((n8 + 255) / 256);
+    if (U)
+        hipLaunchKernelGGL(xsplit_k<true>, dim3(grid), dim3(256), 0, stream(), (uint4 *)Ah, (uint4 *)Al,
+                           need_sx ? Sx : nullptr, X, U, n8);
+    else
+        hipLaunchKernelGGL(xsplit_k<false>, dim3(grid), dim3(256), 0, stream(), (uint4 *)Ah, (uint4 *)Al,
+                           need_sx ? Sx : nullptr, X, nullptr, n8);
+    HOLO_LAUNCH_CHECK();
+    // Q6_K matrices: their integer panels and group scales
+    void *pws = nullptr;
+    bool own_p = false;
+    const void *PW[kExactMats] = {nullptr, nullptr, nullptr};
+    const float *PS[kExactMats] = {nullptr, nullptr, nullptr};
+    if (pbytes) {
+        pws = workspace(0, pbytes);
+        own_p = pws == nullptr;
+        if (own_p) HOLO_CHECK(hipMallocAsync(&pws, pbytes, stream()));
+        if (!pws) return;
+        size_t off = 0;
+        for (int i = 0; i < nmat; i++) {
+            if (types[i] != HOLO_TYPE_Q6_K) continue;
+            _Float16 *p = (_Float16 *)((uint8_t *)pws + off);
+            off += (size_t)N[i] * K * 2;
+            float *ps = (float *)((uint8_t *)pws + off);
+            off += (size_t)N[i] * (K / 16) * 4;
+            const int64_t ntask = (int64_t)N[i] * (K / 256) * 4;
+            hipLaunchKernelGGL(q6_k_int_panel_k, dim3((unsigned)((ntask + 255) / 256)), dim3(256), 0, stream(), p, ps,
+                               (const uint8_t *)W[i], ntask);
+            HOLO_LAUNCH_CHECK();
+            PW[i] = p;
+            PS[i] = ps;
+        }
+    }
+    // one launch per weight kind, over that kind's matrices in order
+    bool done[kExactMats] = {false, false, false};
+    for (int i = 0; i < nmat; i++) {
+        if (done[i]) continue;
+        const int kind = exact_kind(types[i]);
+        ExactArgs a = {};
+        int cnt = 0, acc = 0;
+        for (int j = i; j < nmat; j++) {
+            if (done[j] || exact_kind(types[j]) != kind) continue;
+            done[j] = true;
+            acc += N[j];
+            a.Y[cnt] = Y[j];
+            a.W[cnt] = (const uint8_t *)(PW[j] ? PW[j] : W[j]);
+            a.WS[cnt] = PS[j];
+            a.n_end[cnt] = acc;
+            cnt++;
+        }
+        for (int j = cnt; j < kExactMats; j++) {
+            a.Y[j] = a.Y[0];
+            a.W[j] = a.W[0];
+            a.WS[j] = a.WS[0];
+            a.n_end[j] = INT_MAX;
+        }
+        a.Ah = Ah;
+        a.Al = Al;
+        a.Sx = Sx;
+        a.M = M;
+        a.N = acc;
+        a.nb = nb;
+        a.R = (nmat == 1) ? R : nullptr;
+        switch (kind) {
+        case EW_Q4_0: launch_exact_for<EW_Q4_0>(a); break;
+        case EW_Q8_0: launch_exact_for<EW_Q8_0>(a); break;
+        case EW_Q4_K: launch_exact_for<EW_Q4_K>(a); break;
+        case EW_P16: launch_exact_for<EW_P16>(a); break;
+        default: launch_exact_for<EW_F16>(a); break;
+        }
+    }
+    if (own_p) HOLO_CHECK(hipFreeAsync(pws, stream()));
+    if (own_a) HOLO_CHECK(hipFreeAsync(aws, stream()));
+}
+
+}  // namespace holo

@@ -220,6 +220,7 @@ void holo_matmul_batch_q4_0_swiglu_add(float *Y, const void *W, float *G, const 
                                        int M, int N, int K);
 #define HOLO_PREFILL_F16 0
 #define HOLO_PREFILL_Q8_0 1
+#define HOLO_PREFILL_EXACT 2
 void holo_prefill_set_mode(int mode);
 int holo_prefill_get_mode(void);
 void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const int *N, int nmat,

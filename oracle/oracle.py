@@ -91,6 +91,11 @@ class Oracle:
         W = self.dequant(qtype, M, out_dim * in_dim).reshape(out_dim, in_dim)
         return self.matmul_f64(W, v[:in_dim])
 
+    def truth_batch(self, qtype: int, M: np.ndarray, X: np.ndarray, out_dim: int, in_dim: int) -> np.ndarray:
+        """float64 X . W^T over the bit-exact dequantised weights (rows of X)."""
+        W = self.dequant(qtype, M, out_dim * in_dim).reshape(out_dim, in_dim).astype(np.float64)
+        return np.asarray(X, dtype=np.float64) @ W.T
+
     def q4_k_unpack_scales(self, sp: bytes):
         a = np.frombuffer(bytes(sp), dtype=np.uint8).copy()
         sc = np.empty(8, np.uint8)

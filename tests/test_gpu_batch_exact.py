@@ -1,0 +1,172 @@
+"""GPU parity of the exact batched product (HOLO_PREFILL_EXACT, the default of
+holo_matmul_batch* and of the prompt forward), through the C ABI.
+
+The product (prefill_exact.hip) holds the activations as two f16 halves
+(x = xh + xl to 2^-22), the weights as the blocks' exact integers with
+their fp32 scales, and accumulates in fp32.  Its truth is the float64 product
+of the fp32 activations and the bit-exact dequantised weights (the reference's
+dequantize_row_* restated in the oracle, quant.c:118-311), the quantity the
+reference's fp32 forward approximates one token at a time (llm.c:1049).
+Bars:
+  * elementwise |got - truth| <= (nb + 70) 2^-24 sum_k |x w| (the split, the
+    matrix core's fp32 accumulation of a block's 64 products and one fp32
+    rounding per block), with nb = K / 32; doubled for Q4_K, whose min term
+    adds a block sum of x;
+  * normwise against the truth <= 1e-5, and against the reference's own fp32
+    GEMV (oracle matmul_q) <= 1e-5 on a few rows;
+  * the multi form, mixed types, the add in the store and the SwiGLU in the
+    activation halves: bit-identical to the single product and the unfused
+    sequence.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle.oracle import normwise_err
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
+NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+EXACT = 2
+
+
+def up(holo, a):
+    return holo.DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+def down(buf, n, dtype=np.float32):
+    return buf.download(dtype, n)
+
+
+def weights(synth, oracle, t, N, K, seed):
+    """(the stream handed to the library, its fp32 dequantisation [N][K])."""
+    if t == F32:
+        w = synth.normal(N * K, seed) * np.float32(0.05)
+        return w, w.reshape(N, K)
+    if t == F16:
+        w16 = (synth.normal(N * K, seed) * np.float32(0.05)).astype(np.float16)
+        return w16.view(np.uint16), w16.astype(np.float32).reshape(N, K)
+    b = synth.blocks(t, N, K, seed)
+    return b, oracle.dequant(t, b, N * K).reshape(N, K)
+
+
+def check_rows(got, X, w, rows, t, K):
+    """got[rows] against the float64 truth, elementwise and normwise."""
+    Xr = X[rows].astype(np.float64)
+    W = w.astype(np.float64)
+    truth = Xr @ W.T
+    A = np.abs(Xr) @ np.abs(W).T
+    bound = (K / 32 + 70) * 2.0 ** -24 * A * (2.0 if t == Q4_K else 1.0)
+    err = np.abs(got[rows] - truth)
+    e_n = normwise_err(got[rows], truth)
+    print(f"  max |err| / bound {np.max(err / np.maximum(bound, 1e-30)):.3f}, normwise {e_n:.2e}", flush=True)
+    assert np.all(err <= bound)
+    assert e_n <= 1e-5
+
+
+@pytest.fixture(autouse=True)
+def exact_mode(holo):
+    lib = holo.lib()
+    assert lib.holo_prefill_get_mode() == EXACT  # the default
+    yield
+    lib.holo_prefill_set_mode(EXACT)
+
+
+CASES = [(Q4_0, 64, 128, 256), (Q4_0, 77, 150, 4096), (Q4_0, 512, 11008, 4096), (Q4_0, 512, 4096, 11008),
+         (Q8_0, 100, 256, 512), (Q8_0, 512, 4096, 4096), (Q4_K, 128, 512, 2048), (Q4_K, 512, 14336, 4096),
+         (Q4_K, 512, 4096, 14336), (Q6_K, 96, 384, 1024), (Q6_K, 512, 4096, 11008), (F16, 80, 256, 256),
+         (F16, 512, 1024, 4096), (F32, 70, 200, 128)]
+
+
+@pytest.mark.parametrize("t,M,N,K", CASES, ids=[f"{NAMES[t]}-{m}x{n}x{k}" for t, m, n, k in CASES])
+def test_exact_product(holo, synth, oracle, t, M, N, K):
+    print(f"case exact product {NAMES[t]} {M}x{N}x{K}", flush=True)
+    src, w = weights(synth, oracle, t, N, K, seed=M + N + K)
+    X = synth.normal(M * K, seed=K + 5).reshape(M, K)
+    dW, dX, dY = up(holo, src), up(holo, X), holo.DeviceBuffer(4 * M * N)
+    holo.lib().holo_matmul_batch(dY.ptr, dW.ptr, dX.ptr, M, N, K, t)
+    holo.lib().cuda_sync()
+    holo.check("exact product")
+    got = down(dY, M * N).reshape(M, N)
+    assert np.all(np.isfinite(got))
+    rows = np.arange(M) if M * N * K <= 64 * 4096 * 4096 else np.r_[0:12, M - 4:M]
+    check_rows(got, X, w, rows, t, K)
+    if t in (Q4_0, Q8_0, Q4_K, Q6_K):
+        ref = np.stack([oracle.matmul(t, src, X[m], N, K) for m in range(3)])
+        e = normwise_err(got[:3], ref)
+        print(f"  vs the reference fp32 GEMV {e:.2e}", flush=True)
+        assert e <= 1e-5
+
+
+@pytest.mark.parametrize("t", [Q4_0, Q8_0, Q4_K, Q6_K, F16], ids=lambda t: NAMES[t])
+def test_exact_multi_and_fused(holo, synth, oracle, t):
+    """Three matrices in one launch equal three single launches bit for bit;
+    Y = R + X.W^T (add in the store, in place) and Y = R + (silu(G)*U).W^T
+    (SwiGLU in the activation halves) equal the unfused sequence
+    (cuda_silu_mul, the product, an fp32 add)."""
+    print(f"case exact multi/fused {NAMES[t]}", flush=True)
+    lib = holo.lib()
+    M, K, Ns = 100, 512, (256, 128, 128)
+    srcs = [weights(synth, oracle, t, n, K, seed=60 + i)[0] for i, n in enumerate(Ns)]
+    X = synth.normal(M * K, seed=61).reshape(M, K)
+    dWs, dX = [up(holo, s) for s in srcs], up(holo, X)
+    dYm = [holo.DeviceBuffer(4 * M * n) for n in Ns]
+    k = len(Ns)
+    lib.holo_matmul_batch_multi((C.c_void_p * k)(*[d.ptr for d in dYm]), (C.c_void_p * k)(*[d.ptr for d in dWs]),
+                                (C.c_int * k)(*Ns), k, dX.ptr, M, K, t)
+    singles = []
+    for i, n in enumerate(Ns):
+        d = holo.DeviceBuffer(4 * M * n)
+        lib.holo_matmul_batch(d.ptr, dWs[i].ptr, dX.ptr, M, n, K, t)
+        singles.append(d)
+    N = Ns[0]
+    G = synth.normal(M * K, seed=62).reshape(M, K)
+    U = synth.normal(M * K, seed=63).reshape(M, K)
+    R = synth.normal(M * N, seed=64).reshape(M, N) * 5.0
+    dG, dU, dH = up(holo, G), up(holo, U), holo.DeviceBuffer(4 * M * K)
+    lib.cuda_silu_mul(dH.ptr, dG.ptr, dU.ptr, M * K)
+    dT = holo.DeviceBuffer(4 * M * N)
+    lib.holo_matmul_batch(dT.ptr, dWs[0].ptr, dH.ptr, M, N, K, t)
+    dS = up(holo, R)
+    lib.holo_matmul_batch_add(dS.ptr, dWs[0].ptr, dX.ptr, dS.ptr, M, N, K, t)
+    dZ = up(holo, R)
+    lib.holo_matmul_batch_swiglu_add(dZ.ptr, dWs[0].ptr, dG.ptr, dU.ptr, dZ.ptr, M, N, K, t)
+    lib.cuda_sync()
+    holo.check("exact multi/fused")
+    for i, n in enumerate(Ns):
+        assert np.array_equal(down(dYm[i], M * n).view(np.uint32), down(singles[i], M * n).view(np.uint32)), i
+    y0 = down(singles[0], M * N).reshape(M, N)
+    assert np.array_equal(down(dS, M * N).reshape(M, N), (R + y0).astype(np.float32))
+    assert np.array_equal(down(dZ, M * N).reshape(M, N), (R + down(dT, M * N).reshape(M, N)).astype(np.float32))
+
+
+def test_exact_multi_types(holo, synth, oracle):
+    """q/k/v of different types (a Q4_K_M file's Q4_K, Q4_K, Q6_K, and a Q4_0
+    and Q8_0 mix): each output bit-identical to its own single-type call and
+    within the bound of the float64 truth."""
+    lib = holo.lib()
+    M, K = 100, 512
+    for types in ((Q4_K, Q4_K, Q6_K), (Q4_0, Q4_0, Q8_0)):
+        print(f"case exact multi types {[NAMES[t] for t in types]}", flush=True)
+        Ns = (256, 128, 128)
+        srcs, ws = zip(*[weights(synth, oracle, t, n, K, seed=80 + i) for i, (t, n) in enumerate(zip(types, Ns))])
+        X = synth.normal(M * K, seed=81).reshape(M, K)
+        dWs, dX = [up(holo, s) for s in srcs], up(holo, X)
+        dYm = [holo.DeviceBuffer(4 * M * n) for n in Ns]
+        k = len(Ns)
+        lib.holo_matmul_batch_multi_types((C.c_void_p * k)(*[d.ptr for d in dYm]),
+                                          (C.c_void_p * k)(*[d.ptr for d in dWs]), (C.c_int * k)(*types),
+                                          (C.c_int * k)(*Ns), k, dX.ptr, M, K)
+        singles = []
+        for i, n in enumerate(Ns):
+            d = holo.DeviceBuffer(4 * M * n)
+            lib.holo_matmul_batch(d.ptr, dWs[i].ptr, dX.ptr, M, n, K, types[i])
+            singles.append(d)
+        lib.cuda_sync()
+        holo.check("exact multi types")
+        for i, n in enumerate(Ns):
+            got = down(dYm[i], M * n).reshape(M, n)
+            assert np.array_equal(got.view(np.uint32), down(singles[i], M * n).reshape(M, n).view(np.uint32)), i
+            check_rows(got, X, ws[i], np.arange(M), types[i], K)

@@ -2,8 +2,9 @@
 (holo_matmul_batch and its multi / add / SwiGLU-add forms, holo_dequant_f16),
 through the C ABI.
 
-Q8_0, Q4_K, Q6_K, F16 and F32 weights are dequantised to an f16 panel and
-multiplied on the f16 product:
+In HOLO_PREFILL_F16 mode (set for every test here), Q8_0, Q4_K, Q6_K, F16
+and F32 weights are dequantised to an f16 panel and multiplied on the f16
+product:
   w16 = f16_rne(dequantize_row_*(W))   (quant.c:118-311, bit-exact oracle)
   x16 = f16_rne(x),  Y = sum_k x16 * w16, fp32 accumulation.
 Bars:
@@ -52,6 +53,15 @@ def weights(synth, oracle, t, N, K, seed):
 
 def f16_bound(K, A):
     return 2.0 * (K / 16 + 2) * 2.0 ** -24 * A
+
+
+@pytest.fixture(autouse=True)
+def f16_mode(holo):
+    """These tests hold the f16 product (HOLO_PREFILL_F16) to its bound; the
+    default exact product is tested in test_gpu_batch_exact.py."""
+    holo.lib().holo_prefill_set_mode(0)
+    yield
+    holo.lib().holo_prefill_set_mode(2)
 
 
 @pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q6_K, F32, F16], ids=lambda t: NAMES[t])

@@ -134,26 +134,32 @@ def f16_bound(K, A):
     return 2.0 * (K / 16 + 2) * 2.0 ** -24 * A
 
 
+EXACT = 2
+
+
 def test_matmul_batch_dispatch(holo, synth, oracle):
-    """M >= 64: the f16 product by default, the Q8_0 product in Q8_0 mode; M < 64:
-    one fp32 GEMV per row."""
+    """M >= 64: the exact product by default, the f16 product in F16 mode, the
+    Q8_0 product in Q8_0 mode; M < 64: one fp32 GEMV per row."""
     N, K = 256, 512
     W = synth.blocks(Q4_0, N, K, seed=1)
     dW = up(holo, W)
     lib = holo.lib()
-    assert lib.holo_prefill_get_mode() == 0
-    for M, mode in ((8, 0), (64, 0), (64, 1)):
+    assert lib.holo_prefill_get_mode() == EXACT
+    for M, mode in ((8, EXACT), (64, EXACT), (64, 0), (64, 1)):
         lib.holo_prefill_set_mode(mode)
         X = synth.normal(M * K, seed=M).reshape(M, K)
         dX, dY = up(holo, X), holo.DeviceBuffer(4 * M * N)
         lib.holo_matmul_batch_q4_0(dY.ptr, dW.ptr, dX.ptr, M, N, K, None)
         lib.cuda_sync()
-        lib.holo_prefill_set_mode(0)
+        lib.holo_prefill_set_mode(EXACT)
         holo.check("batch")
         got = down(dY, M * N).reshape(M, N)
         if M < 64:
             want = np.stack([oracle.matmul(Q4_0, W, X[m], N, K) for m in range(M)])
             assert normwise_err(got, want) <= 1e-3
+        elif mode == EXACT:
+            truth = oracle.truth_batch(Q4_0, W, X, N, K)
+            assert normwise_err(got, truth) <= 1e-5
         elif mode == 0:
             Y, A = oracle.gemm_q4_0_f16(W, X, M, N, K)
             assert np.all(np.abs(got - Y) <= f16_bound(K, A))
@@ -205,7 +211,11 @@ def test_gemm_multi_matches_single(holo, synth, oracle, M, Ns, K):
     Np = (C.c_int * k)(*Ns)
     lib.holo_gemm_q4_0_q8_0_multi(Yp, Wp, Np, k, dXq.ptr, M, K)
     Yb = (C.c_void_p * k)(*[d.ptr for d in dYb])
-    lib.holo_matmul_batch_q4_0_multi(Yb, Wp, Np, k, dX.ptr, M, K, None)  # the f16 product (default mode)
+    lib.holo_prefill_set_mode(0)  # the f16 product
+    try:
+        lib.holo_matmul_batch_q4_0_multi(Yb, Wp, Np, k, dX.ptr, M, K, None)
+    finally:
+        lib.holo_prefill_set_mode(EXACT)
     dYf = [holo.DeviceBuffer(4 * M * n) for n in Ns]
     lib.holo_gemm_q4_0_f16_multi((C.c_void_p * k)(*[d.ptr for d in dYf]), Wp, Np, k, dX.ptr, M, K)
     lib.cuda_sync()
@@ -227,7 +237,7 @@ def test_gemm_multi_matches_single(holo, synth, oracle, M, Ns, K):
         assert np.array_equal(got.reshape(M, n)[:rows].view(np.uint32), want.view(np.uint32)), i
 
 
-@pytest.mark.parametrize("M,mode", [(100, 0), (8, 0), (100, 1)], ids=["f16", "gemv_rows", "q8_0"])
+@pytest.mark.parametrize("M,mode", [(100, 2), (100, 0), (8, 2), (100, 1)], ids=["exact", "f16", "gemv_rows", "q8_0"])
 def test_batch_add_and_swiglu(holo, synth, oracle, M, mode):
     """Y = R + X.W^T and Y = R + (silu(G)*U).W^T with the add in the GEMM's
     store and the SwiGLU in its panel: bit-identical to the unfused sequence
@@ -259,7 +269,7 @@ def test_batch_add_and_swiglu(holo, synth, oracle, M, mode):
         lib.cuda_sync()
         holo.check("batch add")
     finally:
-        lib.holo_prefill_set_mode(0)
+        lib.holo_prefill_set_mode(EXACT)
     t2 = down(dT2, M * N).reshape(M, N)
     want = (R + t2).astype(np.float32)
     got = down(dY, M * N).reshape(M, N)
