@@ -25,6 +25,9 @@ int num_cus();
 // cuda_init so that no allocation happens inside a graph capture.
 bool gemv_chain_init();
 void gemv_chain_release();
+// Barrier words of the persistent decode-step kernel (gemv_stream.hip).
+bool gemv_stream_init();
+void gemv_stream_release();
 // The decode-attention range partials (16 MiB), allocated once by cuda_init;
 // without them decode attention runs one range per head.
 bool attention_scratch_init();

@@ -1,0 +1,807 @@
+// gemv_stream.hip -- a whole chain of dependent GEMV stages (a decode step:
+// every layer's q/k/v, o, gate/up and down) in one persistent launch that
+// keeps the weight stream running across the stage boundaries.
+//
+// The reference issues one launch per matrix and token (the decode loop of
+// src/ai/llm_cuda.c:604-918; kernels cuda_ops.cu:618-676, 976-1060); the
+// results here are those of the separate GEMV calls (the MFMA path of
+// gemv.hip: 24-bit activations in three int8 planes, exact int32 block dots,
+// fp32 accumulation), with the rms_norm of the stage's input folded into its
+// staging and the residual add into its stores.
+//
+// Why one launch: a GEMV launch pays its ramp (dispatch, activation staging,
+// the first HBM round trip of its weights) and its tail (the slowest
+// workgroup), and a decode step's stages depend on each other, so those
+// costs add up stage after stage.  Here the weight loads do not wait for
+// the stage boundary: weights do not depend on the activations, so each
+// compute wave keeps D items of its own future work in flight in registers
+// and issues the next one as soon as a register set frees, whatever stage it
+// belongs to.  While the grid synchronises between two stages, the weight
+// stream for the next stage keeps arriving.
+//
+// Workgroup (one per CU, all resident): 8 compute waves and 1 control wave.
+//   compute wave w  items of its tiles (an item is 16 rows x one 16-unit
+//                   segment, as the MFMA GEMV), dots on v_mfma_i32_16x16x64_i8,
+//                   one partial per row and tile into LDS; it never stores to
+//                   global memory, so its vector-memory counter holds only
+//                   loads and each item's wait is exact.
+//   control wave    at a stage's end: sums the 8 partials of each of the
+//                   workgroup's rows, applies the epilogue (silu(g)*u, or
+//                   r + acc), stores the outputs device-coherently, completes
+//                   them (agent-scope release) and takes part in the grid
+//                   barrier.  It issues no weight loads.
+// Stage boundary (3 workgroup barriers): A  all partials of stage s in LDS;
+// the control wave stores, synchronises the grid and loads x of stage s+1
+// (and its norm weight) straight into LDS as fp32 (device-coherent
+// global_load_lds); B  x is in LDS; all waves convert it (rms_norm if asked,
+// then the int8 planes); C  compute resumes.  The compute waves never load
+// activations, so nothing but their own weight items counts against their
+// vector-memory counter.
+#include "gemv_mfma.h"
+
+#include <hip/hip_ext.h>
+#include <limits.h>
+
+namespace holo {
+
+namespace {
+
+constexpr int kNCW = 8;                     // compute waves
+constexpr int kStreamThreads = 64 * (kNCW + 1);
+constexpr int kStreamMaxTiles = 16;         // tiles of one stage per workgroup
+constexpr uint32_t kStreamPolls = 1u << 18;  // bounded barrier wait (~0.1-0.3 s)
+
+// Barrier words, each on its own 256-byte line: group counters, top counter,
+// timeout flag (the layout of the multi-stage GEMV's barrier).
+constexpr int kSBarGroups = 8;
+constexpr int kSBarStride = 64;
+constexpr int kSBarTop = kSBarGroups * kSBarStride;
+constexpr int kSBarFlag = kSBarTop + kSBarStride;
+constexpr size_t kSBarBytes = (size_t)(kSBarFlag + kSBarStride) * 4;
+
+// One stage of the plan, in device memory (read with scalar loads).
+struct StreamStage {
+    uint64_t W[3];        // matrices (gate/up: gate, up)
+    uint64_t y[3];        // outputs (gate/up: y[0])
+    uint64_t x;           // input vector, units * 32 floats
+    uint64_t nw;          // rms-norm weight (units * 32 floats) or 0
+    uint64_t r;           // residual: y[0] = r + W x (plain, one matrix), or 0
+    int64_t row_bytes;
+    int row_end[3];       // prefix sums of the matrices' rows (plain); INT_MAX unused
+    int mode;             // MODE_PLAIN / MODE_GATEUP
+    int units;            // 32-weight units per row
+    int G;                // 16-unit segments per row
+    int P;                // item slots per compute wave per tile: ceil(G / kNCW)
+    int total_rows;       // rows of all matrices (plain) or of one (gate/up)
+    int full_tiles;       // tiles dealt round robin to every workgroup
+    int rem_start;        // first row of the remainder
+    float eps;
+    int fast;             // full tiles never straddle two matrices and every
+                          // lane offset of a full item fits 32 bits
+    uint64_t wlo;         // gate/up: the lower of the two bases
+    uint32_t dg, du;      // gate/up: gate and up base minus wlo
+};
+
+// The stage table is read through the constant address space: its loads are
+// then scalar (the kernel's own global stores cannot make the compiler fall
+// back to vector loads, whose waits would also drain the weight ring).
+typedef __attribute__((address_space(4))) const StreamStage cstage;
+
+struct StreamArgs {
+    uint64_t table;       // device address of the stage table (read as cstage)
+    int nstages;
+    uint32_t *bar;
+    uint32_t zero_off;    // LDS: zero region (after the largest stage's planes)
+    uint32_t stage_off;   // LDS: the compute waves' item stages
+    uint32_t tpart_off;   // LDS: tile partials [kStreamMaxTiles][kNCW][16]
+    uint32_t red_off;     // LDS: norm reduction [16]
+    uint32_t xbuf_off;    // LDS: x of the next stage as fp32, then its norm weight
+};
+
+__device__ __forceinline__ cstage &stage_at(const StreamArgs &a, int s) { return ((cstage *)(uintptr_t)a.table)[s]; }
+
+// Wave-uniform by construction; readfirstlane tells the compiler, so stage
+// table reads become scalar loads (a vector load would need a vmcnt wait
+// that also drains the compute waves' weight ring).
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ uint64_t uni64(uint64_t v)
+{
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ float unif(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+// This workgroup's tiles of a stage: F full tiles dealt round robin (tile k
+// = global tile k*W + b), then an even share of the remaining rows as one
+// short tile.
+struct Tiles {
+    int F, ex0, ex1, n, TR;
+    __device__ __forceinline__ void init(cstage &s, uint32_t W, uint32_t b)
+    {
+        TR = uni(s.mode == MODE_GATEUP ? 8 : 16);
+        F = uni(s.full_tiles);
+        const uint32_t rem = (uint32_t)(s.total_rows - s.rem_start);
+        ex0 = uni(s.rem_start + (int)((b * rem) / W));
+        ex1 = uni(s.rem_start + (int)(((b + 1) * rem) / W));
+        n = uni(F + (ex1 > ex0 ? 1 : 0));
+    }
+    __device__ __forceinline__ void rows(int k, uint32_t W, uint32_t b, int &row0, int &rend) const
+    {
+        if (k < F) {
+            row0 = (k * (int)W + (int)b) * TR;
+            rend = row0 + TR;
+        } else {
+            row0 = ex0;
+            rend = ex1;
+        }
+    }
+};
+
+__device__ __forceinline__ void split_row(cstage &s, int v, int &m, int &r)
+{
+    const int re0 = uni(s.row_end[0]), re1 = uni(s.row_end[1]);
+    const int a1 = v >= re0, a2 = v >= re1;
+    m = a1 + a2;
+    r = v - (a2 ? re1 : a1 ? re0 : 0);
+}
+
+// A compute wave's walk over its item slots, in order: stage s, tile k of
+// this workgroup's n tiles, slot p < P of the tile (segment cw + kNCW * p).
+// Tracked incrementally (no division per slot); the stage constants are
+// read once per stage, into scalar registers.  A stage with no tile for this
+// workgroup is skipped; s = nstages is past the end, where the issue fields
+// are those of the last stage (the dummy loads read its first item).
+struct Walk {
+    int s, k, p;
+    int n, P, G, F, TR, units;
+    int row0, rend, ex0, ex1;
+    // issue fields
+    uint64_t w0, w1, w2, wlo;
+    int64_t rb;
+    int re0, re1, gu, fast;
+
+    __device__ __forceinline__ void set_tile(uint32_t W, uint32_t b)
+    {
+        if (k < F) {
+            row0 = uni((k * (int)W + (int)b) * TR);
+            rend = row0 + TR;
+        } else {
+            row0 = ex0;
+            rend = ex1;
+        }
+    }
+    __device__ __forceinline__ void enter(const StreamArgs &a, int stage, uint32_t W, uint32_t b)
+    {
+        // locals, assigned to the members once: a loop over the members
+        // themselves keeps the struct in scratch memory
+        int ss = stage, tr = 16, f = 0, e0 = 0, e1 = 0, nn = 0;
+        for (; ss < a.nstages; ss++) {
+            cstage &st = stage_at(a, ss);
+            tr = st.mode == MODE_GATEUP ? 8 : 16;
+            f = st.full_tiles;
+            const uint32_t rem = (uint32_t)(st.total_rows - st.rem_start);
+            e0 = st.rem_start + (int)((b * rem) / W);
+            e1 = st.rem_start + (int)(((b + 1) * rem) / W);
+            nn = f + (e1 > e0 ? 1 : 0);
+            if (nn > 0) break;
+        }
+        s = uni(ss);
+        TR = uni(tr);
+        F = uni(f);
+        ex0 = uni(e0);
+        ex1 = uni(e1);
+        n = uni(nn);
+        k = 0;
+        p = 0;
+        cstage &st = stage_at(a, s < a.nstages ? s : a.nstages - 1);
+        G = uni(st.G);
+        units = uni(st.units);
+        w0 = uni64(st.W[0]);
+        w1 = uni64(st.W[1]);
+        w2 = uni64(st.W[2]);
+        wlo = uni64(st.wlo);
+        rb = (int64_t)uni64((uint64_t)st.row_bytes);
+        re0 = uni(st.row_end[0]);
+        re1 = uni(st.row_end[1]);
+        gu = uni(st.mode) == MODE_GATEUP;
+        fast = uni(st.fast);
+        if (s >= a.nstages) {
+            P = 1;
+            row0 = 0;
+            rend = 1;
+            return;
+        }
+        P = uni(st.P);
+        set_tile(W, b);
+    }
+    // to the next slot; true when it entered another stage
+    __device__ __forceinline__ bool next(const StreamArgs &a, uint32_t W, uint32_t b)
+    {
+        if (s >= a.nstages) return false;
+        p = uni(p + 1);
+        if (p < P) return false;
+        p = 0;
+        k = uni(k + 1);
+        if (k < n) {
+            set_tile(W, b);
+            return false;
+        }
+        enter(a, s + 1, W, b);
+        return true;
+    }
+};
+
+// Per-lane byte offsets of a full item's pieces from the item's first byte
+// (rows of one matrix, or 8 gate + 8 up rows from wlo), for the issuing
+// stage: the full-tile loads are then buffer loads from a scalar base with
+// no lane arithmetic.
+template <int FMT>
+struct IssueOffsets {
+    uint32_t loff[Geo<FMT>::NL];
+    __device__ __forceinline__ void set(cstage &st, int lane)
+    {
+        const uint64_t rb = uni64((uint64_t)st.row_bytes);
+        const bool gu = uni(st.mode) == MODE_GATEUP;
+        const uint32_t dg = uni((int)st.dg), du = uni((int)st.du);
+#pragma unroll
+        for (int i = 0; i < Geo<FMT>::NL; i++) {
+            const Piece pc = item_piece(FMT, 64 * i + lane, false);
+            loff[i] = gu ? (uint32_t)((pc.row >> 3 ? du : dg) + (uint64_t)(pc.row & 7) * rb + 16u * pc.col)
+                         : (uint32_t)((uint64_t)pc.row * rb + 16u * pc.col);
+        }
+    }
+};
+
+// Item of the issue walk's slot into registers: NL 16-byte loads per lane.
+// Every slot issues exactly NL loads, so the compiler's vmcnt wait for any
+// slot is exact: a slot with no segment for this wave re-reads the tile's
+// last segment, and a slot past the last stage re-reads an item of the
+// last stage (0 of its first tile).  The data of such slots is never used.
+// Full tiles inside one matrix take the scalar-base path; the short tile,
+// an 8-unit last segment and tiles across two matrices the per-lane path.
+template <int FMT>
+__device__ __forceinline__ void stream_issue(Raw2<FMT> &buf, const StreamArgs &a, const Walk &c,
+                                             const IssueOffsets<FMT> &io, int cw, int lane)
+{
+    using GE = Geo<FMT>;
+    const bool past = c.s >= a.nstages;
+    const int units = c.units, G = c.G;
+    const int seg = past ? 0 : uni(min(cw + kNCW * c.p, G - 1));
+    const int row0 = past ? 0 : c.row0;
+    const int rend = past ? 1 : c.rend;
+    const bool half = 16 * seg + 16 > units;
+    const bool gu = c.gu;
+    const uint64_t w0 = c.w0, w1 = c.w1, w2 = c.w2;
+    const int re0 = c.re0, re1 = c.re1;
+    const int64_t rb = c.rb;
+    if (!past && !half && c.k < c.F && c.fast) {
+        uint64_t base;
+        if (gu) {
+            base = c.wlo + (uint64_t)row0 * (uint64_t)rb;
+        } else {
+            const int a1 = row0 >= re0, a2 = row0 >= re1;
+            const int r = row0 - (a2 ? re1 : a1 ? re0 : 0);
+            base = (a2 ? w2 : a1 ? w1 : w0) + (uint64_t)r * (uint64_t)rb;
+        }
+        base = uni64(base + (uint64_t)seg * GE::SEGB);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, -1, kBufferWord3);
+#pragma unroll
+        for (int i = 0; i < GE::NL; i++)
+            buf.v[i] =
+                __builtin_bit_cast(u32x4a, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)io.loff[i], 0, kNonTemporal));
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < GE::NL; i++) {
+        const Piece pc = item_piece(FMT, 64 * i + lane, half);
+        int m, row;
+        if (gu) {
+            m = pc.row >> 3;
+            row = min(row0 + (pc.row & 7), rend - 1);
+        } else {
+            const int v = min(row0 + pc.row, rend - 1);
+            const int a1 = v >= re0, a2 = v >= re1;
+            m = a1 + a2;
+            row = v - (a2 ? re1 : a1 ? re0 : 0);
+        }
+        const uint64_t base = m == 2 ? w2 : m == 1 ? w1 : w0;
+        gbyte *ap = (gbyte *)base + (int64_t)row * rb + seg * GE::SEGB + 16 * pc.col;
+        buf.v[i] = __builtin_nontemporal_load((gu32x4a *)ap);
+    }
+}
+
+// The item into the wave's LDS stage (row n at n * RS).
+template <int FMT>
+__device__ __forceinline__ void stream_stage_write(const Raw2<FMT> &b, uint8_t *stage, int lane)
+{
+    using GE = Geo<FMT>;
+#pragma unroll
+    for (int i = 0; i < GE::NL; i++) {
+        const int pc = 64 * i + lane;
+        if (GE::NP % 64 == 0 || pc < GE::NP) {
+            uint8_t *p = stage + 16 * pc + (GE::RS - GE::SEGB) * (pc / GE::PR);
+            *(u32x2a *)p = (u32x2a){b.v[i].x, b.v[i].y};
+            *(u32x2a *)(p + 8) = (u32x2a){b.v[i].z, b.v[i].w};
+        }
+    }
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void gvoid;
+
+// x of a stage (units * 32 floats) and, with a norm, its weight into the fp32
+// LDS buffer, by one wave: each global_load_lds_dwordx4 moves 64 lanes x 16
+// contiguous bytes into 1 KB of LDS.  Device-coherent (sc1): an earlier
+// stage of this launch wrote x.  The caller waits (vmcnt) before the
+// workgroup barrier that publishes the buffer.
+__device__ __forceinline__ void stream_fetch_x(cstage &st, uint8_t *xbuf, int lane)
+{
+    const int units = uni(st.units), n = units / 8;  // 1 KB pieces (units is a multiple of 8)
+    const float *x = (const float *)uni64(st.x);
+    for (int j = 0; j < n; j++)
+        __builtin_amdgcn_global_load_lds((gvoid *)(x + 256 * j + 4 * lane), (lds_void *)(xbuf + 1024 * j), 16, 0,
+                                         kDeviceScope);
+    const uint64_t nw = uni64(st.nw);
+    if (nw) {
+        const float *w = (const float *)nw;
+        uint8_t *wb = xbuf + units * 128;
+        for (int j = 0; j < n; j++)
+            __builtin_amdgcn_global_load_lds((gvoid *)(w + 256 * j + 4 * lane), (lds_void *)(wb + 1024 * j), 16, 0, 0);
+    }
+}
+
+// The fp32 x in LDS into the int8 planes and {dx, c} pairs, by all threads;
+// with a norm weight, x * (1/sqrt(mean(x^2) + eps)) * w first (cuda_rms_norm's
+// formula, cuda_ops.cu:1479-1504), the 9 waves' sums of squares meeting in red.
+template <int FMT>
+__device__ __forceinline__ void stream_convert_x(cstage &st, uint8_t *ldsb, const uint8_t *xbuf, float *red)
+{
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int units = uni(st.units), chunks = units * 8;
+    const bool norm = uni64(st.nw) != 0;
+    const float4 *xv = (const float4 *)xbuf;
+    float scale = 1.f;
+    if (norm) {
+        float ss = 0.f;
+        for (int i = tid; i < chunks; i += kStreamThreads) {
+            const float4 v = xv[i];
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w <= kNCW; w++) tot += red[w];
+        scale = 1.0f / sqrtf(tot / (float)(units * 32) + unif(st.eps));
+    }
+    const float4 *wv = (const float4 *)(xbuf + units * 128);
+    for (int i = tid; i < chunks; i += kStreamThreads) {
+        float4 v = xv[i];
+        if (norm) {
+            const float4 w4 = wv[i];
+            v = make_float4(v.x * scale * w4.x, v.y * scale * w4.y, v.z * scale * w4.z, v.w * scale * w4.w);
+        }
+        x_convert<FMT, XM_MFMA>(v, i, units, (void *)ldsb);
+    }
+}
+
+// The control wave's stores of stage s: every tile's 16 (gate/up: 8) rows,
+// the 8 compute waves' partials summed in wave order.
+__device__ __forceinline__ void stream_epilogue(cstage &st, const Tiles &t, const float *tpart,
+                                                const float (&rr)[kStreamMaxTiles], uint32_t W, uint32_t b, int lane)
+{
+    const bool gu = uni(st.mode) == MODE_GATEUP;
+    const uint64_t y0 = uni64(st.y[0]), y1 = uni64(st.y[1]), y2 = uni64(st.y[2]);
+    const bool res = uni64(st.r) != 0;
+#pragma unroll
+    for (int k = 0; k < kStreamMaxTiles; k++) {
+        int row0, rend;
+        t.rows(k, W, b, row0, rend);
+        const int v = row0 + lane;
+        if (k < t.n && lane < t.TR && v < rend) {  // a predicated body: rr stays in registers
+            const float *pt = tpart + k * (kNCW * 16);
+            float s0 = 0.f;
+#pragma unroll
+            for (int w = 0; w < kNCW; w++) s0 += pt[w * 16 + lane];
+            if (gu) {
+                float s1 = 0.f;
+#pragma unroll
+                for (int w = 0; w < kNCW; w++) s1 += pt[w * 16 + 8 + lane];
+                __hip_atomic_store((gfloat *)y0 + v, silu(s0) * s1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                int m, row;
+                split_row(st, v, m, row);
+                if (res) s0 = rr[k] + s0;
+                gfloat *yb = (gfloat *)(m == 2 ? y2 : m == 1 ? y1 : y0);
+                __hip_atomic_store(yb + row, s0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+}
+
+// Arrival and wait of one workgroup (one thread), two-level monotonic
+// counters as the multi-stage GEMV's barrier: the state is valid across
+// launches and graph replays, and a bounded wait sets the flag instead of
+// hanging.
+__device__ __forceinline__ void stream_grid_barrier(uint32_t *bar)
+{
+    const uint32_t G = gridDim.x;
+    const uint32_t ng = G < kSBarGroups ? G : kSBarGroups;
+    const uint32_t gi = blockIdx.x % ng;
+    const uint32_t size = G / ng + (gi < G % ng ? 1u : 0u);
+    const uint32_t a = __hip_atomic_fetch_add(bar + gi * kSBarStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t k = a / size + 1;
+    const uint32_t target = k * ng;
+    if (a + 1 == k * size) {
+        const uint32_t t = __hip_atomic_fetch_add(bar + kSBarTop, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t + 1 == target) return;
+    }
+    for (uint32_t polls = 0;; polls++) {
+        const uint32_t c = __hip_atomic_load(bar + kSBarTop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((int32_t)(c - target) >= 0) return;
+        if (polls == kStreamPolls) {
+            __hip_atomic_store(bar + kSBarFlag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+template <int FMT, int D>
+__global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs a)
+{
+    using GE = Geo<FMT>;
+    extern __shared__ uint4 lds_[];
+    uint8_t *ldsb = (uint8_t *)lds_;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t W = gridDim.x, b = blockIdx.x;
+    float *tpart = (float *)(ldsb + a.tpart_off);
+    float *red = (float *)(ldsb + a.red_off);
+    const int nst = a.nstages;
+
+    uint8_t *xbuf = ldsb + a.xbuf_off;
+
+    if (tid < kZeroBytes / 16) ((uint4 *)(ldsb + a.zero_off))[tid] = make_uint4(0, 0, 0, 0);
+
+    if (wave < kNCW) {
+        // ---- compute wave ----
+        const int cw = wave;
+        const int n = lane & 15, g = lane >> 4;
+        const bool plane_lane = (n >> 2) == g && (n & 3) < 3;
+        const uint32_t plane_off = (uint32_t)(n & 3) * 32u;
+        uint8_t *stage = ldsb + a.stage_off + cw * GE::STAGE;
+        Walk ci, cp;  // the issue walk runs D slots ahead of the process walk
+        ci.enter(a, 0, W, b);
+        cp = ci;
+        IssueOffsets<FMT> io;
+        if (ci.s < nst) io.set(stage_at(a, ci.s), lane);
+        Raw2<FMT> ring[D];
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            stream_issue<FMT>(ring[d], a, ci, io, cw, lane);
+            if (ci.next(a, W, b) && ci.s < nst) io.set(stage_at(a, ci.s), lane);
+        }
+        __syncthreads();  // B of stage 0: x in LDS
+        stream_convert_x<FMT>(stage_at(a, 0), ldsb, xbuf, red);
+        __syncthreads();  // C of stage 0
+        int s = 0;        // the stage whose boundary comes next
+        float acc = 0.f;
+        bool done = false;
+        while (!done) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                // the boundaries of every stage before the next slot's (cp.s is
+                // nst once this wave's slots are all done)
+                while (s < cp.s) {
+                    __syncthreads();  // A
+                    __syncthreads();  // B
+                    if (s + 1 < nst) {
+                        stream_convert_x<FMT>(stage_at(a, s + 1), ldsb, xbuf, red);
+                        __syncthreads();  // C
+                    }
+                    s++;
+                }
+                if (s >= nst) {
+                    done = true;
+                    break;
+                }
+                stream_stage_write<FMT>(ring[d], stage, lane);
+                stream_issue<FMT>(ring[d], a, ci, io, cw, lane);
+                if (ci.next(a, W, b) && ci.s < nst) io.set(stage_at(a, ci.s), lane);
+                // the slot's dots against the staged x of stage s
+                const int j = cw + kNCW * cp.p;
+                if (j < cp.G) {
+                    const int units = cp.units;
+                    Chunk<FMT> c;
+                    read_chunk<FMT>(c, stage, n, g);
+                    const int cs0 = 16 * j + 4 * g;
+                    const bool valid = cs0 < units;  // false only in an 8-unit last segment
+                    const int cs = valid ? cs0 : units - 4;
+                    const uint32_t abase = plane_lane ? (uint32_t)cs * 96u + plane_off : a.zero_off;
+                    acc += item_dot<FMT>(c, ldsb, abase, (uint32_t)units * 96u + (uint32_t)cs * 8u, (uint32_t)cs,
+                                         valid ? 0 : 4, j == cp.G - 1);
+                }
+                if (cp.p == cp.P - 1) {
+                    float r = acc;
+                    r += __shfl_xor(r, 16);
+                    r += __shfl_xor(r, 32);
+                    acc = 0.f;
+                    if (lane < 16) tpart[(cp.k * kNCW + cw) * 16 + lane] = r;
+                }
+                cp.next(a, W, b);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the last (dummy) item loads have returned
+    } else {
+        // ---- control wave ----
+        stream_fetch_x(stage_at(a, 0), xbuf, lane);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the LDS-direct loads have landed
+        __syncthreads();                     // B of stage 0
+        stream_convert_x<FMT>(stage_at(a, 0), ldsb, xbuf, red);
+        __syncthreads();  // C of stage 0
+        for (int s = 0; s < nst; s++) {
+            cstage &st = stage_at(a, s);
+            Tiles t;
+            t.init(st, W, b);
+            // residual rows of this stage's tiles, loaded while the stage runs
+            float rr[kStreamMaxTiles];
+#pragma unroll
+            for (int k = 0; k < kStreamMaxTiles; k++) rr[k] = 0.f;
+            const uint64_t rp = uni64(st.r);
+            if (rp && uni(st.mode) == MODE_PLAIN) {
+#pragma unroll
+                for (int k = 0; k < kStreamMaxTiles; k++) {
+                    int row0, rend;
+                    t.rows(k, W, b, row0, rend);
+                    if (k < t.n && lane < 16 && row0 + lane < rend)
+                        rr[k] = __hip_atomic_load((gcfloat *)rp + row0 + lane, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            __syncthreads();  // A: every partial of stage s is in LDS
+            stream_epilogue(st, t, tpart, rr, W, b, lane);
+            if (s + 1 < nst) {
+                // Every output of this stage is an agent-scope atomic store
+                // (sc1), performed at agent scope; the wave waits for them to
+                // complete (vmcnt(0)) before the arrival.  No other store of
+                // the kernel needs publishing, so the L2 write-back of a full
+                // agent-scope release fence (1.5 us a stage) is not needed.
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // compiler ordering
+                __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0)
+                if (lane == 0) stream_grid_barrier(a.bar);
+                stream_fetch_x(stage_at(a, s + 1), xbuf, lane);
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+            }
+            __syncthreads();  // B
+            if (s + 1 < nst) {
+                stream_convert_x<FMT>(stage_at(a, s + 1), ldsb, xbuf, red);
+                __syncthreads();  // C
+            }
+        }
+    }
+}
+
+// ---- host ----------------------------------------------------------------------------
+
+uint32_t *g_stream_bar = nullptr;
+
+struct StreamPlan {
+    StreamStage *dev = nullptr;  // the stage table
+    int nstages = 0;
+    int fmt = 0;
+    size_t lds = 0;
+    StreamArgs args{};
+};
+
+size_t stream_lds(int fmt, int max_units, int max_xbuf, uint32_t &zero_off, uint32_t &stage_off,
+                  uint32_t &tpart_off, uint32_t &red_off, uint32_t &xbuf_off)
+{
+    const size_t x_lds = ((size_t)max_units * lds_bytes_per_unit<XM_I24>() + 15) & ~(size_t)15;
+    zero_off = zero_region_off((uint32_t)x_lds);
+    stage_off = zero_off + kZeroBytes;
+    const int stage = fmt == FMT_Q4_0 ? Geo<FMT_Q4_0>::STAGE : fmt == FMT_Q8_0 ? Geo<FMT_Q8_0>::STAGE
+                                                                                : Geo<FMT_Q4_K>::STAGE;
+    tpart_off = (stage_off + kNCW * stage + 15) & ~15u;
+    red_off = tpart_off + kStreamMaxTiles * kNCW * 16 * 4;
+    xbuf_off = red_off + 16 * 4;
+    return xbuf_off + (size_t)max_xbuf;
+}
+
+template <int FMT, int D>
+bool stream_launch_t(StreamPlan &p)
+{
+    auto kern = gemv_stream_kernel<FMT, D>;
+    static bool attr = false;
+    if (!attr) {
+        HOLO_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        attr = true;
+    }
+    // every workgroup must be resident at once (grid barrier): one per CU
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)kern, kStreamThreads, p.lds) != hipSuccess)
+        per_cu = 0;
+    if (per_cu < 1) return false;
+    hipEvent_t e0, e1;
+    if (take_launch_events(&e0, &e1))
+        hipExtLaunchKernelGGL(kern, dim3(num_cus()), dim3(kStreamThreads), p.lds, stream(), e0, e1, 0, p.args);
+    else
+        hipLaunchKernelGGL(kern, dim3(num_cus()), dim3(kStreamThreads), p.lds, stream(), p.args);
+    HOLO_LAUNCH_CHECK();
+    return true;
+}
+
+constexpr int kStreamD = 4;  // items in flight per compute wave
+
+template <int FMT>
+bool stream_launch_f(StreamPlan &p)
+{
+    return stream_launch_t<FMT, kStreamD>(p);
+}
+
+}  // namespace
+
+bool gemv_stream_init()
+{
+    if (g_stream_bar) return true;
+    if (hipMalloc((void **)&g_stream_bar, kSBarBytes) != hipSuccess) {
+        g_stream_bar = nullptr;
+        return false;
+    }
+    return hipMemset(g_stream_bar, 0, kSBarBytes) == hipSuccess && hipDeviceSynchronize() == hipSuccess;
+}
+
+void gemv_stream_release()
+{
+    if (g_stream_bar) hipFree(g_stream_bar);
+    g_stream_bar = nullptr;
+}
+
+}  // namespace holo
+
+using namespace holo;
+
+extern "C" {
+
+void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, int type)
+{
+    const int fmt = type == HOLO_TYPE_Q4_0 ? FMT_Q4_0 : type == HOLO_TYPE_Q4_K ? FMT_Q4_K : -1;
+    if (!stages || nstages < 1 || fmt < 0 || !g_stream_bar) {
+        HOLO_REJECT("holo_gemv_stream_create: no stages, a type other than Q4_0/Q4_K, or cuda_init not called");
+        return nullptr;
+    }
+    if (stream_capturing()) {
+        HOLO_REJECT("holo_gemv_stream_create: allocates; create the plan outside graph capture");
+        return nullptr;
+    }
+    const int grid = num_cus();
+    StreamStage *host = new StreamStage[nstages];
+    int max_units = 0, max_xbuf = 0;
+    for (int s = 0; s < nstages; s++) {
+        const holo_stream_stage_t &in = stages[s];
+        StreamStage &o = host[s];
+        o = StreamStage{};
+        const bool gu = in.gate_up != 0;
+        const int nmat = gu ? 2 : in.nmat;
+        bool ok = nmat >= 1 && nmat <= 3 && in.x && !((uintptr_t)in.x & 15u) && in.in_dim > 0;
+        o.units = units_per_row(fmt, in.in_dim);
+        o.row_bytes = row_bytes_of(fmt, in.in_dim);
+        ok = ok && o.units >= 8 && (o.units & 7) == 0 && o.units * 32 == in.in_dim && o.units <= 576;
+        ok = ok && (!in.norm_w || !((uintptr_t)in.norm_w & 15u));
+        ok = ok && (!in.r || (!gu && nmat == 1));
+        int total = 0;
+        for (int m = 0; m < 3; m++) {
+            if (m < nmat) {
+                const int rows = in.rows[gu ? 0 : m];
+                float *y = in.y[gu ? 0 : m];
+                ok = ok && in.W[m] && !((uintptr_t)in.W[m] & 15u) && rows > 0 && y;
+                o.W[m] = (uint64_t)in.W[m];
+                o.y[m] = (uint64_t)y;
+                total += rows;
+                o.row_end[m] = total;
+            } else {
+                o.W[m] = (uint64_t)in.W[0];
+                o.y[m] = (uint64_t)in.y[0];
+                o.row_end[m] = INT_MAX;
+            }
+        }
+        if (!ok) {
+            delete[] host;
+            HOLO_REJECT("holo_gemv_stream_create: a stage outside the supported set (16-byte aligned matrices and "
+                        "vectors, in_dim a multiple of 256 up to 18432, 1-3 matrices, residual on one plain matrix)");
+            return nullptr;
+        }
+        o.mode = gu ? MODE_GATEUP : MODE_PLAIN;
+        o.x = (uint64_t)in.x;
+        o.nw = (uint64_t)in.norm_w;
+        o.eps = in.eps;
+        o.r = (uint64_t)in.r;
+        o.G = (o.units + 15) / 16;
+        o.P = (o.G + kNCW - 1) / kNCW;
+        const int tr = gu ? 8 : 16;
+        o.total_rows = gu ? in.rows[0] : total;
+        o.full_tiles = o.total_rows / (grid * tr);
+        o.rem_start = o.full_tiles * grid * tr;
+        // the scalar-base issue path: full tiles inside one matrix, lane
+        // offsets within 32 bits
+        o.fast = (uint64_t)tr * (uint64_t)o.row_bytes < (1ull << 32);
+        if (gu) {
+            const bool up_low = in.W[1] < in.W[0];
+            o.wlo = up_low ? o.W[1] : o.W[0];
+            const uint64_t dg = o.W[0] - o.wlo, du = o.W[1] - o.wlo;
+            o.fast = o.fast && (dg > du ? dg : du) + (uint64_t)tr * (uint64_t)o.row_bytes < (1ull << 32);
+            o.dg = (uint32_t)dg;
+            o.du = (uint32_t)du;
+        } else {
+            for (int m = 0; m < nmat; m++) o.fast = o.fast && in.rows[m] % tr == 0;
+        }
+        if (o.full_tiles + 1 > kStreamMaxTiles) {
+            delete[] host;
+            HOLO_REJECT("holo_gemv_stream_create: a stage with more rows than 16 tiles per CU");
+            return nullptr;
+        }
+        max_units = o.units > max_units ? o.units : max_units;
+        const int xb = o.units * 128 * (in.norm_w ? 2 : 1);
+        max_xbuf = xb > max_xbuf ? xb : max_xbuf;
+    }
+    StreamPlan *p = new StreamPlan;
+    p->nstages = nstages;
+    p->fmt = fmt;
+    p->lds = stream_lds(fmt, max_units, max_xbuf, p->args.zero_off, p->args.stage_off, p->args.tpart_off,
+                        p->args.red_off, p->args.xbuf_off);
+    if (p->lds > 160 * 1024 || hipMalloc((void **)&p->dev, sizeof(StreamStage) * nstages) != hipSuccess) {
+        (void)hipGetLastError();
+        delete[] host;
+        delete p;
+        HOLO_REJECT("holo_gemv_stream_create: LDS or device memory for the plan");
+        return nullptr;
+    }
+    HOLO_CHECK(hipMemcpy(p->dev, host, sizeof(StreamStage) * nstages, hipMemcpyHostToDevice));
+    delete[] host;
+    p->args.table = (uint64_t)(uintptr_t)p->dev;
+    p->args.nstages = nstages;
+    p->args.bar = g_stream_bar;
+    return p;
+}
+
+int holo_gemv_stream_launch(void *plan)
+{
+    StreamPlan *p = (StreamPlan *)plan;
+    if (!p || !p->dev) {
+        HOLO_REJECT("holo_gemv_stream_launch: no plan");
+        return HOLO_EINVAL;
+    }
+    const bool ok = p->fmt == FMT_Q4_0 ? stream_launch_f<FMT_Q4_0>(*p) : stream_launch_f<FMT_Q4_K>(*p);
+    if (!ok) {
+        HOLO_REJECT("holo_gemv_stream_launch: a workgroup per CU does not fit");
+        return HOLO_EINVAL;
+    }
+    return 0;
+}
+
+void holo_gemv_stream_destroy(void *plan)
+{
+    StreamPlan *p = (StreamPlan *)plan;
+    if (!p) return;
+    if (p->dev) HOLO_CHECK(hipFree(p->dev));
+    delete p;
+}
+
+int holo_gemv_stream_status(void)
+{
+    if (!g_stream_bar) return 0;
+    uint32_t flag = 0;
+    HOLO_CHECK(hipStreamSynchronize(stream()));
+    HOLO_CHECK(hipMemcpy(&flag, g_stream_bar + kSBarFlag, sizeof(flag), hipMemcpyDeviceToHost));
+    if (flag == 0) return 0;
+    HOLO_CHECK(hipMemset(g_stream_bar, 0, kSBarBytes));
+    HOLO_CHECK(hipDeviceSynchronize());
+    return HOLO_ECHAIN;
+}
+
+}  // extern "C"

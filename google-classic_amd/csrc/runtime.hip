@@ -103,6 +103,10 @@ int cuda_init(void)
         fprintf(stderr, "holo_mi355x: cannot allocate the GEMV chain barrier\n");
         return -1;
     }
+    if (!holo::gemv_stream_init()) {
+        fprintf(stderr, "holo_mi355x: cannot allocate the GEMV stream barrier\n");
+        return -1;
+    }
     if (!holo::attention_scratch_init()) {
         fprintf(stderr, "holo_mi355x: cannot allocate the decode-attention scratch\n");
         return -1;
@@ -123,6 +127,7 @@ void cuda_cleanup(void)
     if (g_copy_stream) hipStreamDestroy(g_copy_stream);
     g_copy_stream = nullptr;
     holo::gemv_chain_release();
+    holo::gemv_stream_release();
     holo::attention_scratch_release();
     holo::panel_workspace_release();
     g_stream = nullptr;

@@ -129,6 +129,10 @@ _SIGS = {
     "holo_time_next_launch": (None, [_P, _P]),
     "holo_gemv_chain": (_I, [_P, _I, _I]),
     "holo_gemv_chain_status": (_I, []),
+    "holo_gemv_stream_create": (_P, [_P, _I, _I]),
+    "holo_gemv_stream_launch": (_I, [_P]),
+    "holo_gemv_stream_destroy": (None, [_P]),
+    "holo_gemv_stream_status": (_I, []),
     "holo_gemv_set_launch": (None, [_I, _I]),
     "holo_dequant": (None, [_P, _P, _I64, _I]),
     "holo_dequant_f16": (None, [_P, _P, _I64, _I]),
@@ -219,6 +223,58 @@ def gemv_chain(stages, qtype: int) -> int:
     """holo_gemv_chain over a list of GemvStage; returns its status code."""
     arr = (GemvStage * len(stages))(*stages)
     return lib().holo_gemv_chain(C.cast(arr, C.c_void_p), len(stages), qtype)
+
+
+class StreamStage(C.Structure):
+    """holo_stream_stage_t (include/holo_mi355x.h): one stage of a
+    holo_gemv_stream plan."""
+    _fields_ = [("W", C.c_void_p * 3), ("y", C.c_void_p * 3), ("rows", C.c_int * 3), ("nmat", C.c_int),
+                ("gate_up", C.c_int), ("x", C.c_void_p), ("in_dim", C.c_int), ("norm_w", C.c_void_p),
+                ("eps", C.c_float), ("r", C.c_void_p)]
+
+
+def stream_stage(W, y, rows, x, in_dim, gate_up=False, norm_w=None, eps=1e-5, r=None) -> StreamStage:
+    """A stream stage from device pointers (as gemv_stage, plus the optional
+    rms-norm weight of the input and the residual of the output)."""
+    s = StreamStage()
+    for i, w in enumerate(W):
+        s.W[i] = w
+    for i, o in enumerate(y):
+        s.y[i] = o
+    for i, n in enumerate(rows):
+        s.rows[i] = n
+    s.nmat = len(W)
+    s.gate_up = 1 if gate_up else 0
+    s.x = x
+    s.in_dim = in_dim
+    s.norm_w = norm_w
+    s.eps = eps
+    s.r = r
+    return s
+
+
+class StreamPlan:
+    """A holo_gemv_stream plan (device stage table) for a list of StreamStage."""
+
+    def __init__(self, stages, qtype: int):
+        arr = (StreamStage * len(stages))(*stages)
+        self.p = lib().holo_gemv_stream_create(C.cast(arr, C.c_void_p), len(stages), qtype)
+        if not self.p:
+            raise HoloError(f"holo_gemv_stream_create rejected the plan: {lib().holo_last_error()}")
+
+    def launch(self) -> int:
+        return lib().holo_gemv_stream_launch(self.p)
+
+    def close(self):
+        if self.p:
+            lib().holo_gemv_stream_destroy(self.p)
+            self.p = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class GgufTensor(C.Structure):
