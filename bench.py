@@ -32,15 +32,22 @@ The printed JSON line carries
                 a bounded sample of the same layer
   extra         the unfused drop-in layer (7 cuda_matmul_q4_0 calls), the layer
                 as one multi-stage launch (holo_gemv_chain), configs
-                1 and 3 (Q8_0 4096x4096; Q4_K Llama-3-8B FFN), the Q6_K GEMV
-                (32000x4096 head and 4096x11008 down), config 4 (batched
-                prefill GEMM on the f16 matrix cores: useful TOP/s = 2*M*N*K per
-                kernel time, and its fraction of the dense f16 and int8 peaks;
-                and a 512-token prompt through the 32 layers in one pass,
-                also on a Q4_K_M-style mix of Q4_K and Q6_K matrices),
-                config 5 (full synthetic
-                Llama-2-7B Q4_0 decode step: end-to-end and matmuls-only ms),
-                decode attention at 512 / 2048 / 4096 cached positions
+                1 and 3 (Q8_0 4096x4096; Q4_K Llama-3-8B FFN; per matrix the
+                median kernel time over >= 128 launches and its fraction of
+                HBM peak), the Q6_K GEMV (32000x4096 head and 4096x11008
+                down), config 4 (the batched prefill products: useful TOP/s
+                = 2*M*N*K per kernel time, and its fraction of the dense f16
+                and int8 peaks; and a 512-token prompt through the 32 layers
+                in one pass, also on a Q4_K_M-style mix of Q4_K and Q6_K
+                matrices), config 5 (full synthetic Llama-2-7B Q4_0 decode
+                step: end-to-end and matmuls-only ms, as 4 launches a layer
+                and as one persistent launch for all 128 layer GEMVs), decode
+                attention at 512 / 2048 / 4096 cached positions.  Configs 1,
+                3, 4 and 5 carry a cpu_baseline of their own: the reference's
+                matmul_q on the same shapes (Q8_0 on its OpenMP threads, Q4_0
+                and Q4_K on one core; config 4 as 512 sequential GEMVs, the
+                reference's token-by-token prompt loop; config 5 as one
+                layer x 32 + the head)
 
 Only the CPU-baseline leg touches oracle/.
 """
@@ -65,6 +72,7 @@ from holo_mi355x import synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 F16_PEAK_TFLOPS = 2500.0   # MI355X dense f16 MFMA
+I8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA
 Q4_0, Q8_0, Q4_K = holo.TYPE_Q4_0, holo.TYPE_Q8_0, holo.TYPE_Q4_K
 Q6_K = 14
 BASE_SEED = 20251201
@@ -241,6 +249,24 @@ def mean_launch_us(lib, layers, A, steps, which, kernel_only):
     return 1e3 * statistics.mean(durs)
 
 
+def kernel_median_us(lib, call, n):
+    """Median kernel duration of call(i), i < n, issued back to back with one
+    synchronisation at the end: HIP events that each launch records at its
+    kernel's start and end (holo_time_next_launch, the span rocprofv3's
+    kernel trace measures)."""
+    evs = [(lib.holo_event_create(), lib.holo_event_create()) for _ in range(n)]
+    for i in range(n):
+        lib.holo_time_next_launch(evs[i][0], evs[i][1])
+        call(i)
+    lib.cuda_sync()
+    durs = [lib.holo_event_elapsed_ms(a, b) for a, b in evs]
+    for a, b in evs:
+        lib.holo_event_destroy(a)
+        lib.holo_event_destroy(b)
+    holo.check("kernel medians")
+    return 1e3 * statistics.median(durs)
+
+
 def single_gemv_gbs(lib, qtype, sets, steps):
     """Back-to-back launches of one config's matrices, rotating over copies."""
     fn = {Q4_0: lib.cuda_matmul_q4_0, Q8_0: lib.cuda_matmul_q8_0, Q4_K: lib.cuda_matmul_q4_k,
@@ -265,18 +291,32 @@ def single_gemv_gbs(lib, qtype, sets, steps):
     return steps * b / (ms * 1e-3) / 1e9, ms * 1e3 / (steps * len(sets["mats"][0].shapes))
 
 
-def single_gemvs(lib, A):
+def single_gemvs(lib, A, cpu_budget=None):
     """Configs 1 and 3 and the Q6_K GEMV, each over enough copies of its
-    matrices to defeat the MALL."""
+    matrices to defeat the MALL.  Per matrix shape: the median kernel time
+    over >= 128 launches (rotating over the copies) and its fraction of HBM
+    peak; per config: the aggregate rate of back-to-back launches and, with a
+    CPU budget, the reference CPU path on the same shapes."""
     out = {}
+    fn = {Q8_0: lib.cuda_matmul_q8_0, Q4_K: lib.cuda_matmul_q4_k, Q6_K: lib.cuda_matmul_q6_k}
     for qt, cfg, name, shapes, copies in ((Q8_0, 1, "config1_q8_0_4096x4096", CONFIG1, 32),
                                           (Q4_K, 3, "config3_q4_k_llama3_ffn", CONFIG3, 10),
                                           (Q6_K, 6, "q6_k_head_and_down_llama2_7b", Q6K_SHAPES, 4)):
         sets = {"mats": [Mats(qt, i, cfg, shapes) for i in range(copies)], "acts": A}
         g, us = single_gemv_gbs(lib, qt, sets, 4 * copies)
-        out[name] = {"gbs": round(g, 1), "us_per_launch": round(us, 2),
-                     "bytes_per_launch": weight_bytes(qt, shapes) / len(shapes)}
-        log(f"{name}: {g:.0f} GB/s, {us:.2f} us per launch")
+        per = {}
+        for mname, o, i in shapes:
+            bpl = holo.row_bytes(qt, i) * o
+            med = kernel_median_us(lib, lambda k, mname=mname, o=o, i=i: fn[qt](
+                A[f"y{o}"], sets["mats"][k % copies].buf[mname].ptr, A[f"x{i}"], o, i), max(128, 4 * copies))
+            per[f"{o}x{i}"] = {"kernel_us_median": round(med, 2), "bytes_per_launch": bpl,
+                               "gbs": round(bpl / (med * 1e-6) / 1e9, 1),
+                               "frac": round(bpl / (med * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        out[name] = {"gbs": round(g, 1), "frac": round(g / HBM_PEAK_GBS, 4), "us_per_launch": round(us, 2),
+                     "bytes_per_launch": weight_bytes(qt, shapes) / len(shapes), "per_matrix": per}
+        if cpu_budget and qt in (Q8_0, Q4_K):
+            out[name]["cpu_baseline"] = cpu_gemvs(qt, cfg, shapes, cpu_budget, 8 if qt == Q8_0 else 2)
+        log(f"{name}: {out[name]}")
         del sets
     return out
 
@@ -320,6 +360,39 @@ def decode_step(lib, layers, head, A, ones, matmuls_only, fused=False):
             lib.cuda_vec_add(x, x, A["y11008"], DIM)
     if not matmuls_only:
         lib.cuda_rms_norm(xb, x, ones.ptr, DIM, 1e-5)
+    lib.cuda_matmul_q8_0(A["y32000"], head.ptr, xb, VOCAB, DIM)
+
+
+def stream_step_plans(layers, A, ones):
+    """The config-5 step's 128 layer GEMVs as one persistent launch each
+    (holo_gemv_stream): `matmuls` on the buffers of decode_step(matmuls_only),
+    `fused` with the norms in the q/k/v and gate/up staging and the residual
+    adds in the o and down stores, in place on x (decode_step(fused))."""
+    x, xb = A["x4096"], A["y4096"]
+    mm, fz = [], []
+    for L in layers:
+        b = L.buf
+        qkv = [b["q"].ptr, b["k"].ptr, b["v"].ptr]
+        gu = [b["gate"].ptr, b["up"].ptr]
+        mm += [holo.stream_stage(qkv, [A["q"], A["k"], A["v"]], [DIM] * 3, xb, DIM),
+               holo.stream_stage([b["o"].ptr], [A["y11008"]], [DIM], A["v"], DIM),
+               holo.stream_stage(gu, [A["h"]], [FFN], xb, DIM, gate_up=True),
+               holo.stream_stage([b["down"].ptr], [A["y11008"]], [DIM], A["h"], FFN)]
+        fz += [holo.stream_stage(qkv, [A["q"], A["k"], A["v"]], [DIM] * 3, x, DIM, norm_w=ones.ptr),
+               holo.stream_stage([b["o"].ptr], [x], [DIM], A["v"], DIM, r=x),
+               holo.stream_stage(gu, [A["h"]], [FFN], x, DIM, gate_up=True, norm_w=ones.ptr),
+               holo.stream_stage([b["down"].ptr], [x], [DIM], A["h"], FFN, r=x)]
+    return holo.StreamPlan(mm, Q4_0), holo.StreamPlan(fz, Q4_0)
+
+
+def decode_step_stream(lib, plan, head, A, ones, fused):
+    """One stream launch for the layers, then (fused) the final norm and the
+    Q8_0 head GEMV."""
+    if plan.launch() != 0:
+        raise holo.HoloError("holo_gemv_stream_launch failed")
+    xb = A["y4096"]
+    if fused:
+        lib.cuda_rms_norm(xb, A["x4096"], ones.ptr, DIM, 1e-5)
     lib.cuda_matmul_q8_0(A["y32000"], head.ptr, xb, VOCAB, DIM)
 
 
@@ -505,7 +578,8 @@ def prefill_tops(lib, reps=10):
             kms = statistics.median(kernel)
             tops = 2.0 * M * N * K / (kms * 1e-3) / 1e12
             out[name][prod] = {"gemm_us": round(ms * 1e3, 2), "kernel_us": round(kms * 1e3, 2),
-                               "tops": round(tops, 1), "frac_of_f16_peak": round(tops / F16_PEAK_TFLOPS, 4)}
+                               "tops": round(tops, 1), "frac_of_f16_peak": round(tops / F16_PEAK_TFLOPS, 4),
+                               "frac_of_int8_peak": round(tops / I8_PEAK_TOPS, 4)}
         ev.start()
         for _ in range(reps):
             lib.holo_quantize_act_q8_0(Xq.ptr, X.ptr, M, K)
@@ -528,36 +602,115 @@ def measured_traffic(xmode: str):
     return json.loads(p.read_text())["traffic_bytes_per_launch"]
 
 
-def cpu_baseline(budget_s: float) -> dict:
-    """The reference CPU path on one layer's 7 Q4_0 matrices (bounded sample)."""
+def ref_matmul():
+    """(kind, matmul(qtype, M, v, out_dim, in_dim), description) of the CPU
+    path timed beside the GPU numbers: the reference's own matmul_q
+    (src/ai/llm.c:770) compiled into oracle/_ref/ with its release flags when
+    that build exists, else the oracle's restatement of it."""
     sys.path.insert(0, str(ROOT))
     from oracle import oracle as orc  # checker / baseline only
     if orc.ref_available("release"):
         ref = orc.RefBuild("release")
-        kind, fn = "reference", (lambda M, v, o, i: ref.matmul(Q4_0, M, v, o, i))
-        what = ("oracle/_ref/libholo_ref_release.so: matmul_q of the reference sources built with "
+        return ("reference", lambda t, M, v, o, i: ref.matmul(t, M, v, o, i),
+                "oracle/_ref/libholo_ref_release.so: matmul_q of the reference sources built with "
                 "-O3 -ffast-math -mavx2 -mfma -fopenmp")
-    else:
-        o_ = orc.Oracle()
-        kind, fn = "port", (lambda M, v, o, i: o_.matmul(Q4_0, M, v, o, i))
-        what = "oracle/liboracle.so: the oracle's restatement of matmul_q"
+    o_ = orc.Oracle()
+    return ("port", lambda t, M, v, o, i: o_.matmul(t, M, v, o, i),
+            "oracle/liboracle.so: the oracle's restatement of matmul_q")
+
+
+def omp_threads() -> int:
+    return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+
+
+def cpu_median(calls, budget_s: float):
+    """Median seconds of one pass over `calls` (after one warm-up pass), over
+    as many passes as fit in budget_s (at least 3); (median, passes, total s)."""
+    for c in calls:
+        c()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 5000):
+        t0 = time.perf_counter()
+        for c in calls:
+            c()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times), sum(times)
+
+
+def cores_of(qtype) -> int:
+    """Threads the reference's matmul_q branch uses: its Q8_0 (and F32) AVX2
+    loops carry `#pragma omp parallel for` (llm.c:838); the Q4_0 branch
+    (llm.c:893-915) and mat_vec_q4_k (quant.c:626-633) are single-threaded."""
+    return omp_threads() if qtype == Q8_0 else 1
+
+
+def cpu_gemvs(qtype, cfg, shapes, budget_s: float, copies: int) -> dict:
+    """The reference CPU path on `copies` copies of a config's matrices (the
+    GPU's synthetic weights, the same seeds), one pass = every matrix of every
+    copy, so the pass streams more bytes than a host's last-level cache."""
+    kind, mm, what = ref_matmul()
+    mats = [(synth.blocks(qtype, o, i, synth.tensor_seed(BASE_SEED, cfg, c, m)), o, i)
+            for c in range(copies) for m, (_, o, i) in enumerate(shapes)]
+    xs = {i: synth.normal(i, i) for _, _, i in shapes}
+    med, n, tot = cpu_median([lambda M=M, o=o, i=i: mm(qtype, M, xs[i], o, i) for M, o, i in mats], budget_s)
+    b = copies * weight_bytes(qtype, shapes)
+    return {"value": round(b / med / 1e9, 3), "unit": "GB/s", "cores": cores_of(qtype), "kind": kind,
+            "sample": f"{n} passes (median {med * 1e3:.2f} ms, {tot:.1f} s of CPU work) over {copies} copies of "
+                      f"{', '.join(f'{o}x{i}' for _, o, i in shapes)} ({b} weight bytes a pass) with {what}; host "
+                      f"has {os.cpu_count()} logical CPUs, OMP_NUM_THREADS="
+                      f"{os.environ.get('OMP_NUM_THREADS', 'unset')}"}
+
+
+def cpu_prefill(budget_s: float, M: int = 512) -> dict:
+    """Config 4 on the reference CPU path: it has no batched product, its
+    prompt loop runs one decode step per token (llm.c:1049), so M tokens cost
+    M sequential matmul_q GEMVs per matrix; the sample times single GEMVs of
+    each shape and scales by M."""
+    kind, mm, what = ref_matmul()
+    out = {}
+    for name, (N, K) in (("11008x4096", (FFN, DIM)), ("4096x11008", (DIM, FFN))):
+        W = synth.blocks(Q4_0, N, K, seed=N + K)
+        x = synth.normal(K, seed=K)
+        med, n, tot = cpu_median([lambda: mm(Q4_0, W, x, N, K)], budget_s / 2)
+        ms = M * med * 1e3
+        out[name] = {"value": round(2.0 * M * N * K / (M * med) / 1e12, 5), "unit": "TOP/s",
+                     "ms_for_512_tokens": round(ms, 1), "cores": 1, "kind": kind,
+                     "sample": f"{n} GEMVs (median {med * 1e3:.2f} ms, {tot:.1f} s of CPU work) scaled by {M}, "
+                               f"with {what}"}
+    return out
+
+
+def cpu_decode_step(budget_s: float) -> dict:
+    """Config 5 on the reference CPU path: one layer's 7 Q4_0 GEMVs (1 core)
+    and the 32000x4096 Q8_0 head (OpenMP) timed, the step = 32 layers + head."""
+    kind, mm, what = ref_matmul()
+    mats = [(synth.blocks(Q4_0, o, i, synth.tensor_seed(BASE_SEED, 2, 0, m)), o, i)
+            for m, (_, o, i) in enumerate(LAYER)]
+    xs = {4096: synth.normal(4096, 11), 11008: synth.normal(11008, 12)}
+    head = synth.blocks(Q8_0, VOCAB, DIM, synth.tensor_seed(BASE_SEED, 5, 0, 7))
+    t_layer, n1, tot1 = cpu_median([lambda M=M, o=o, i=i: mm(Q4_0, M, xs[i], o, i) for M, o, i in mats],
+                                   budget_s * 0.75)
+    t_head, n2, tot2 = cpu_median([lambda: mm(Q8_0, head, xs[4096], VOCAB, DIM)], budget_s * 0.25)
+    ms = (32 * t_layer + t_head) * 1e3
+    b = 32 * weight_bytes(Q4_0, LAYER) + holo.row_bytes(Q8_0, DIM) * VOCAB
+    return {"value": round(ms, 1), "unit": "ms per step (matmuls)", "gbs": round(b / (ms * 1e-3) / 1e9, 3),
+            "cores": f"1 (Q4_0 layers), {omp_threads()} (Q8_0 head, OpenMP)", "kind": kind,
+            "sample": f"{n1} passes over one layer's 7 Q4_0 GEMVs (median {t_layer * 1e3:.1f} ms) x 32 + {n2} "
+                      f"head GEMVs (median {t_head * 1e3:.1f} ms), {tot1 + tot2:.1f} s of CPU work, with {what}"}
+
+
+def cpu_baseline(budget_s: float) -> dict:
+    """The reference CPU path on one layer's 7 Q4_0 matrices (bounded sample)."""
+    kind, mm, what = ref_matmul()
     mats = [(synth.blocks(Q4_0, o, i, synth.tensor_seed(BASE_SEED, 2, 0, m)), o, i)
             for m, (_, o, i) in enumerate(LAYER)]
     x = {4096: synth.normal(4096, 11), 11008: synth.normal(11008, 12)}
-    for M, o, i in mats:  # warm-up
-        fn(M, x[i], o, i)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 5000):
-        t0 = time.perf_counter()
-        for M, o, i in mats:
-            fn(M, x[i], o, i)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    med, n, tot = cpu_median([lambda M=M, o=o, i=i: mm(Q4_0, M, x[i], o, i) for M, o, i in mats], budget_s)
     b = weight_bytes(Q4_0, LAYER)
     return {"value": round(b / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"{len(times)} runs (median {med * 1e3:.1f} ms) of one Llama-2-7B layer's 7 Q4_0 GEMVs "
-                      f"({b} weight bytes, {sum(times):.1f} s of CPU work) with {what}; the reference's Q4_0 "
+            "sample": f"{n} runs (median {med * 1e3:.1f} ms) of one Llama-2-7B layer's 7 Q4_0 GEMVs "
+                      f"({b} weight bytes, {tot:.1f} s of CPU work) with {what}; the reference's Q4_0 "
                       f"branch has no OpenMP pragma (llm.c:893-915), so 1 core; host has {os.cpu_count()} "
                       f"logical CPUs"}
 
@@ -610,7 +763,7 @@ def main():
         print(json.dumps({"config4_prefill_m512": prefill_tops(lib)}), flush=True)
         return
     if a.gemv_only:
-        print(json.dumps(single_gemvs(lib, Acts())), flush=True)
+        print(json.dumps(single_gemvs(lib, Acts(), None if a.no_cpu else a.cpu_budget / 3)), flush=True)
         return
     if a.attention_only:
         print(json.dumps({"decode_attention_llama2_7b": decode_attention(lib)}), flush=True)
@@ -673,17 +826,37 @@ def main():
             mm_ms = time_graphs(lib, [mm], reps, 2) / reps
             full_ms = time_graphs(lib, [fz], reps, 2) / reps
             lib.holo_graph_destroy(fz)
+            # the same step with the 128 layer GEMVs in one persistent launch
+            plan_mm, plan_fz = stream_step_plans(layers[:32], A, ones)
+            smm = capture(lib, lambda: decode_step_stream(lib, plan_mm, head, A, ones, False))
+            sfz = capture(lib, lambda: decode_step_stream(lib, plan_fz, head, A, ones, True))
+            smm_ms = time_graphs(lib, [smm], reps, 2) / reps
+            sfz_ms = time_graphs(lib, [sfz], reps, 2) / reps
+            if lib.holo_gemv_stream_status() != 0:
+                raise holo.HoloError("the persistent decode-step launch could not synchronise")
+            for g in (smm, sfz):
+                lib.holo_graph_destroy(g)
+            plan_mm.close()
+            plan_fz.close()
             step_bytes = 32 * bytes_step + holo.row_bytes(Q8_0, DIM) * VOCAB
+            best_mm = min(mm_ms, smm_ms)
             extra["config5_decode_step"] = {
                 "matmuls_ms": round(mm_ms, 4), "end_to_end_ms": round(full_ms, 4),
                 "end_to_end_unfused_ms": round(unfused_ms, 4),
+                "matmuls_stream_ms": round(smm_ms, 4), "end_to_end_stream_ms": round(sfz_ms, 4),
                 "weight_bytes": step_bytes, "matmul_weight_gbs": round(step_bytes / (mm_ms * 1e-3) / 1e9, 1),
                 "end_to_end_weight_gbs": round(step_bytes / (full_ms * 1e-3) / 1e9, 1),
-                "launches": {"matmuls": 32 * 4 + 1, "end_to_end": 32 * 4 + 2, "end_to_end_unfused": 32 * 8 + 2}}
+                "frac": round(step_bytes / (best_mm * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "frac_basis": "weight bytes of the step / the faster matmuls-only variant's ms, over 8 TB/s",
+                "launches": {"matmuls": 32 * 4 + 1, "end_to_end": 32 * 4 + 2, "end_to_end_unfused": 32 * 8 + 2,
+                             "matmuls_stream": 2, "end_to_end_stream": 3}}
+            if not a.no_cpu:
+                extra["config5_decode_step"]["cpu_baseline"] = cpu_decode_step(a.cpu_budget / 2)
             lib.holo_graph_destroy(full)
             lib.holo_graph_destroy(mm)
             log(f"config 5 decode step: matmuls {mm_ms:.3f} ms, end-to-end {full_ms:.3f} ms "
-                f"(unfused {unfused_ms:.3f} ms)")
+                f"(unfused {unfused_ms:.3f} ms); one stream launch: matmuls {smm_ms:.3f} ms, "
+                f"end-to-end {sfz_ms:.3f} ms")
             extra["config4_prompt_forward_512"] = prompt_forward(lib, layers, head, ones, full_ms)
             log(f"config 4 prompt forward: {extra['config4_prompt_forward_512']}")
             extra["prompt_forward_512_q4_k_m"] = prompt_forward_q4_k_m(lib)
@@ -692,8 +865,10 @@ def main():
 
         del layers
 
-        extra.update(single_gemvs(lib, A))
+        extra.update(single_gemvs(lib, A, None if a.no_cpu else a.cpu_budget / 3))
         extra["config4_prefill_m512"] = prefill_tops(lib)
+        if not a.no_cpu:
+            extra["config4_prefill_m512"]["cpu_baseline"] = cpu_prefill(a.cpu_budget / 3)
         log(f"config 4 prefill: {extra['config4_prefill_m512']}")
         extra["decode_attention_llama2_7b"] = decode_attention(lib)
         log(f"decode attention: {extra['decode_attention_llama2_7b']}")

@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 #include <stdio.h>
 
@@ -51,6 +52,18 @@ void *noalloc_scratch();
 // Events that holo_time_next_launch requested for the next timed kernel
 // launch (MFMA GEMV or prefill GEMM): returns them once and clears them.
 bool take_launch_events(hipEvent_t *start, hipEvent_t *stop);
+
+// A launch on the library stream that records the events armed by
+// holo_time_next_launch, if any, at the kernel's own start and end.
+template <typename... KArgs, typename... Args>
+inline void launch_timed(void (*kern)(KArgs...), dim3 grid, dim3 block, size_t lds, Args... args)
+{
+    hipEvent_t e0, e1;
+    if (take_launch_events(&e0, &e1))
+        hipExtLaunchKernelGGL(kern, grid, block, lds, stream(), e0, e1, 0, args...);
+    else
+        hipLaunchKernelGGL(kern, grid, block, lds, stream(), args...);
+}
 
 // n bytes at p set to `value` by a kernel on the library stream.  Used
 // instead of hipMemsetAsync wherever a call may be captured into a graph

@@ -932,7 +932,7 @@ static void launch_t(GemvArgs &a)
     int blocks = a.ntiles;
     int cap = num_cus() * wpc;
     if (blocks > cap) blocks = cap;
-    hipLaunchKernelGGL((gemv_kernel<FMT, XM, R, P, MODE>), dim3(blocks), dim3(kThreads), lds, stream(), a);
+    launch_timed(gemv_kernel<FMT, XM, R, P, MODE>, dim3(blocks), dim3(kThreads), lds, a);
     HOLO_LAUNCH_CHECK();
 }
 

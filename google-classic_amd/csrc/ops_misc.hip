@@ -1312,8 +1312,8 @@ void cuda_matmul_q6_k(float *dst, const void *M, const float *v, int out_dim, in
     }
     if (((uintptr_t)M & 1u) || ((uintptr_t)v & 15u)) {
         // the task kernel needs 2-byte-aligned blocks and 16-byte-aligned activations
-        hipLaunchKernelGGL(gemv_q6_k_k, dim3(blocks_for(out_dim, 4)), dim3(256), 0, stream(), dst,
-                           (const uint8_t *)M, v, out_dim, in_dim);
+        launch_timed(gemv_q6_k_k, dim3(blocks_for(out_dim, 4)), dim3(256), 0, dst, (const uint8_t *)M, v, out_dim,
+                     in_dim);
         HOLO_LAUNCH_CHECK();
         return;
     }
@@ -1321,11 +1321,11 @@ void cuda_matmul_q6_k(float *dst, const void *M, const float *v, int out_dim, in
     const dim3 grid((out_dim + 4 * R - 1) / (4 * R));
     const uint8_t *W = (const uint8_t *)M;
     if (R == 4)
-        hipLaunchKernelGGL(gemv_q6_k2_k<4>, grid, dim3(256), 0, stream(), dst, W, v, out_dim, in_dim);
+        launch_timed(gemv_q6_k2_k<4>, grid, dim3(256), 0, dst, W, v, out_dim, in_dim);
     else if (R == 2)
-        hipLaunchKernelGGL(gemv_q6_k2_k<2>, grid, dim3(256), 0, stream(), dst, W, v, out_dim, in_dim);
+        launch_timed(gemv_q6_k2_k<2>, grid, dim3(256), 0, dst, W, v, out_dim, in_dim);
     else
-        hipLaunchKernelGGL(gemv_q6_k2_k<1>, grid, dim3(256), 0, stream(), dst, W, v, out_dim, in_dim);
+        launch_timed(gemv_q6_k2_k<1>, grid, dim3(256), 0, dst, W, v, out_dim, in_dim);
     HOLO_LAUNCH_CHECK();
 }
 
