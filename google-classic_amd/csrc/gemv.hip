@@ -871,14 +871,19 @@ __global__ __launch_bounds__(kThreads) void gemv_chain_kernel(ChainArgs ca)
         });
         if (s + 1 < ca.nstages) {
             // Every wave may have stored outputs of this stage (the last wave
-            // to finish a tile stores it).  Each wave's agent-scope release
-            // fence waits for its own stores to complete (s_waitcnt vmcnt(0),
-            // after an L2 write-back), and only then does the wave reach the
-            // workgroup barrier, so every output store of the workgroup has
-            // completed at agent scope before thread 0 arrives.  The next
-            // stage reads its input with device-coherent (sc1) loads, which
-            // are not answered from a line an L2 cached before the store.
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            // to finish a tile stores it), each one an agent-scope atomic
+            // store (sc1, written through the L2).  Each wave waits for its
+            // own stores to complete (s_waitcnt vmcnt(0)) and only then
+            // reaches the workgroup barrier, so every output store of the
+            // workgroup has completed at agent scope before thread 0 arrives.
+            // The kernel makes no other store that another workgroup reads,
+            // so the L2 write-back of a full agent-scope release fence is not
+            // needed (issued by 8 waves on every CU it cost about 14 us a
+            // stage).  The next stage reads its input with device-coherent
+            // (sc1) loads, which are not answered from a line an L2 cached
+            // before the store.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // compiler ordering
+            __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0)
             __syncthreads();
             if (wave != 0) {
                 with_stage<FMT>(ca.key[s + 1], ca.st[s + 1], ldsb, [&](auto &st) { st.issue(b0, 0); });
