@@ -42,6 +42,8 @@
 #include <hip/hip_ext.h>
 #include <limits.h>
 
+#include <vector>
+
 namespace holo {
 
 namespace {
@@ -76,10 +78,6 @@ struct StreamStage {
     int full_tiles;       // tiles dealt round robin to every workgroup
     int rem_start;        // first row of the remainder
     float eps;
-    int fast;             // full tiles never straddle two matrices and every
-                          // lane offset of a full item fits 32 bits
-    uint64_t wlo;         // gate/up: the lower of the two bases
-    uint32_t dg, du;      // gate/up: gate and up base minus wlo
 };
 
 // The stage table is read through the constant address space: its loads are
@@ -89,6 +87,8 @@ typedef __attribute__((address_space(4))) const StreamStage cstage;
 
 struct StreamArgs {
     uint64_t table;       // device address of the stage table (read as cstage)
+    uint64_t slots;       // device address of int[grid]: item slots per compute
+                          // wave of each workgroup, rounded up to a multiple of D
     int nstages;
     uint32_t *bar;
     uint32_t zero_off;    // LDS: zero region (after the largest stage's planes)
@@ -158,10 +158,6 @@ struct Walk {
     int s, k, p;
     int n, P, G, F, TR, units;
     int row0, rend, ex0, ex1;
-    // issue fields
-    uint64_t w0, w1, w2, wlo;
-    int64_t rb;
-    int re0, re1, gu, fast;
 
     __device__ __forceinline__ void set_tile(uint32_t W, uint32_t b)
     {
@@ -199,16 +195,8 @@ struct Walk {
         cstage &st = stage_at(a, s < a.nstages ? s : a.nstages - 1);
         G = uni(st.G);
         units = uni(st.units);
-        w0 = uni64(st.W[0]);
-        w1 = uni64(st.W[1]);
-        w2 = uni64(st.W[2]);
-        wlo = uni64(st.wlo);
-        rb = (int64_t)uni64((uint64_t)st.row_bytes);
-        re0 = uni(st.row_end[0]);
-        re1 = uni(st.row_end[1]);
-        gu = uni(st.mode) == MODE_GATEUP;
-        fast = uni(st.fast);
         if (s >= a.nstages) {
+            // past the last stage: the (unused) item 0 of the last stage's row 0
             P = 1;
             row0 = 0;
             rend = 1;
@@ -217,99 +205,83 @@ struct Walk {
         P = uni(st.P);
         set_tile(W, b);
     }
-    // to the next slot; true when it entered another stage
-    __device__ __forceinline__ bool next(const StreamArgs &a, uint32_t W, uint32_t b)
+    // to the next slot: 0 same tile, 1 another tile of the stage, 2 another
+    // stage (or past the last)
+    __device__ __forceinline__ int next(const StreamArgs &a, uint32_t W, uint32_t b)
     {
-        if (s >= a.nstages) return false;
+        if (s >= a.nstages) return 0;
         p = uni(p + 1);
-        if (p < P) return false;
+        if (p < P) return 0;
         p = 0;
         k = uni(k + 1);
         if (k < n) {
             set_tile(W, b);
-            return false;
+            return 1;
         }
         enter(a, s + 1, W, b);
-        return true;
+        return 2;
     }
 };
 
-// Per-lane byte offsets of a full item's pieces from the item's first byte
-// (rows of one matrix, or 8 gate + 8 up rows from wlo), for the issuing
-// stage: the full-tile loads are then buffer loads from a scalar base with
-// no lane arithmetic.
+// The issue side of a compute wave: every item load is a global load of
+// piece i at rowaddr[i] + col + the 16-unit segment's offset, one code path
+// for every tile and segment.  rowaddr (per tile) is the lane's row: its
+// piece row clamped to the tile's last row (short tiles re-read that row), in
+// the matrix the row falls in (rows of several matrices, or 8 gate + 8 up
+// rows).  The column part is the piece's 16-byte column (colF), or in an
+// 8-unit last segment the column taken modulo half the segment (item_piece's
+// half mapping: the missing half re-reads the first), so no load leaves the
+// row.
 template <int FMT>
-struct IssueOffsets {
-    uint32_t loff[Geo<FMT>::NL];
-    __device__ __forceinline__ void set(cstage &st, int lane)
+struct Issuer {
+    uint32_t colF[Geo<FMT>::NL];
+    uint64_t rowaddr[Geo<FMT>::NL];
+
+    __device__ __forceinline__ void init(int lane)
+    {
+#pragma unroll
+        for (int i = 0; i < Geo<FMT>::NL; i++) colF[i] = 16u * (uint32_t)item_piece(FMT, 64 * i + lane, false).col;
+    }
+    __device__ __forceinline__ void set_tile(cstage &st, const Walk &c, int lane)
     {
         const uint64_t rb = uni64((uint64_t)st.row_bytes);
         const bool gu = uni(st.mode) == MODE_GATEUP;
-        const uint32_t dg = uni((int)st.dg), du = uni((int)st.du);
+        const uint64_t w0 = uni64(st.W[0]), w1 = uni64(st.W[1]), w2 = uni64(st.W[2]);
+        const int re0 = uni(st.row_end[0]), re1 = uni(st.row_end[1]);
+        const int row0 = c.row0, last = c.rend - 1;
 #pragma unroll
         for (int i = 0; i < Geo<FMT>::NL; i++) {
-            const Piece pc = item_piece(FMT, 64 * i + lane, false);
-            loff[i] = gu ? (uint32_t)((pc.row >> 3 ? du : dg) + (uint64_t)(pc.row & 7) * rb + 16u * pc.col)
-                         : (uint32_t)((uint64_t)pc.row * rb + 16u * pc.col);
+            const int pr = item_piece(FMT, 64 * i + lane, false).row;
+            if (gu) {
+                const int v = min(row0 + (pr & 7), last);
+                rowaddr[i] = ((pr >> 3) ? w1 : w0) + (uint64_t)v * rb;
+            } else {
+                const int v = min(row0 + pr, last);
+                const int a1 = v >= re0, a2 = v >= re1;
+                const int r = v - (a2 ? re1 : a1 ? re0 : 0);
+                rowaddr[i] = (a2 ? w2 : a1 ? w1 : w0) + (uint64_t)r * rb;
+            }
         }
     }
 };
 
-// Item of the issue walk's slot into registers: NL 16-byte loads per lane.
-// Every slot issues exactly NL loads, so the compiler's vmcnt wait for any
-// slot is exact: a slot with no segment for this wave re-reads the tile's
-// last segment, and a slot past the last stage re-reads an item of the
-// last stage (0 of its first tile).  The data of such slots is never used.
-// Full tiles inside one matrix take the scalar-base path; the short tile,
-// an 8-unit last segment and tiles across two matrices the per-lane path.
+// Item of the issue walk's slot into registers: NL 16-byte loads per lane,
+// the kernel's only weight loads.  Every slot issues exactly NL loads from
+// this one site, so the compiler's vmcnt wait for any slot is exact: a slot
+// with no segment for this wave re-reads the tile's last segment, and a slot
+// past the last stage re-reads item 0 of the last stage.  The data of such
+// slots is never used.
 template <int FMT>
-__device__ __forceinline__ void stream_issue(Raw2<FMT> &buf, const StreamArgs &a, const Walk &c,
-                                             const IssueOffsets<FMT> &io, int cw, int lane)
+__device__ __forceinline__ void stream_issue(Raw2<FMT> &buf, const Walk &c, const Issuer<FMT> &is, int cw)
 {
     using GE = Geo<FMT>;
-    const bool past = c.s >= a.nstages;
-    const int units = c.units, G = c.G;
-    const int seg = past ? 0 : uni(min(cw + kNCW * c.p, G - 1));
-    const int row0 = past ? 0 : c.row0;
-    const int rend = past ? 1 : c.rend;
-    const bool half = 16 * seg + 16 > units;
-    const bool gu = c.gu;
-    const uint64_t w0 = c.w0, w1 = c.w1, w2 = c.w2;
-    const int re0 = c.re0, re1 = c.re1;
-    const int64_t rb = c.rb;
-    if (!past && !half && c.k < c.F && c.fast) {
-        uint64_t base;
-        if (gu) {
-            base = c.wlo + (uint64_t)row0 * (uint64_t)rb;
-        } else {
-            const int a1 = row0 >= re0, a2 = row0 >= re1;
-            const int r = row0 - (a2 ? re1 : a1 ? re0 : 0);
-            base = (a2 ? w2 : a1 ? w1 : w0) + (uint64_t)r * (uint64_t)rb;
-        }
-        base = uni64(base + (uint64_t)seg * GE::SEGB);
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, -1, kBufferWord3);
-#pragma unroll
-        for (int i = 0; i < GE::NL; i++)
-            buf.v[i] =
-                __builtin_bit_cast(u32x4a, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)io.loff[i], 0, kNonTemporal));
-        return;
-    }
+    const int seg = uni(min(cw + kNCW * c.p, c.G - 1));
+    const bool half = 16 * seg + 16 > c.units;
+    const uint32_t segoff = (uint32_t)seg * GE::SEGB;
 #pragma unroll
     for (int i = 0; i < GE::NL; i++) {
-        const Piece pc = item_piece(FMT, 64 * i + lane, half);
-        int m, row;
-        if (gu) {
-            m = pc.row >> 3;
-            row = min(row0 + (pc.row & 7), rend - 1);
-        } else {
-            const int v = min(row0 + pc.row, rend - 1);
-            const int a1 = v >= re0, a2 = v >= re1;
-            m = a1 + a2;
-            row = v - (a2 ? re1 : a1 ? re0 : 0);
-        }
-        const uint64_t base = m == 2 ? w2 : m == 1 ? w1 : w0;
-        gbyte *ap = (gbyte *)base + (int64_t)row * rb + seg * GE::SEGB + 16 * pc.col;
-        buf.v[i] = __builtin_nontemporal_load((gu32x4a *)ap);
+        const uint32_t col = half && is.colF[i] >= 8u * GE::PR ? is.colF[i] - 8u * GE::PR : is.colF[i];
+        buf.v[i] = __builtin_nontemporal_load((gu32x4a *)(is.rowaddr[i] + (col + segoff)));
     }
 }
 
@@ -479,25 +451,45 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
         Walk ci, cp;  // the issue walk runs D slots ahead of the process walk
         ci.enter(a, 0, W, b);
         cp = ci;
-        IssueOffsets<FMT> io;
-        if (ci.s < nst) io.set(stage_at(a, ci.s), lane);
+        Issuer<FMT> is;
+        is.init(lane);
+        {
+            cstage &st = stage_at(a, ci.s < nst ? ci.s : nst - 1);
+            is.set_tile(st, ci, lane);
+        }
+        // the issue walk to its next slot, with the issuer's stage and tile
+        auto advance = [&]() {
+            const int ev = ci.next(a, W, b);
+            if (ev) {
+                cstage &st = stage_at(a, ci.s < nst ? ci.s : nst - 1);
+                is.set_tile(st, ci, lane);
+            }
+        };
         Raw2<FMT> ring[D];
 #pragma unroll
         for (int d = 0; d < D; d++) {
-            stream_issue<FMT>(ring[d], a, ci, io, cw, lane);
-            if (ci.next(a, W, b) && ci.s < nst) io.set(stage_at(a, ci.s), lane);
+            stream_issue<FMT>(ring[d], ci, is, cw);
+            advance();
         }
         __syncthreads();  // B of stage 0: x in LDS
         stream_convert_x<FMT>(stage_at(a, 0), ldsb, xbuf, red);
         __syncthreads();  // C of stage 0
         int s = 0;        // the stage whose boundary comes next
         float acc = 0.f;
-        bool done = false;
-        while (!done) {
+        // The loop has one exit, at its latch, and a trip count known up front
+        // (the wave's slots, padded to a multiple of D with slots past the last
+        // stage).  An exit inside the unrolled body would be merged into the
+        // latch by the control-flow structurizer, and the compiler's
+        // vector-memory wait analysis would then wait for every load in flight
+        // (vmcnt(0)) at the loop head: the ring would drain once per D slots.
+        // With one exit, the wait before slot d's stage write is exactly its own
+        // loads (vmcnt((D-1)*NL + NL-1-i) for piece i).
+        const int iters = uni(((const __attribute__((address_space(4))) int *)(uintptr_t)a.slots)[b]) / D;
+        for (int it = 0; it < iters; it++) {
 #pragma unroll
             for (int d = 0; d < D; d++) {
-                // the boundaries of every stage before the next slot's (cp.s is
-                // nst once this wave's slots are all done)
+                // the boundaries of every stage before this slot's (cp.s is nst
+                // once this wave's slots are all done)
                 while (s < cp.s) {
                     __syncthreads();  // A
                     __syncthreads();  // B
@@ -507,16 +499,14 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
                     }
                     s++;
                 }
-                if (s >= nst) {
-                    done = true;
-                    break;
-                }
+                // a slot past the last stage writes its (unused) item too, so
+                // every slot's wait counts the same loads
                 stream_stage_write<FMT>(ring[d], stage, lane);
-                stream_issue<FMT>(ring[d], a, ci, io, cw, lane);
-                if (ci.next(a, W, b) && ci.s < nst) io.set(stage_at(a, ci.s), lane);
+                stream_issue<FMT>(ring[d], ci, is, cw);
+                advance();
                 // the slot's dots against the staged x of stage s
                 const int j = cw + kNCW * cp.p;
-                if (j < cp.G) {
+                if (cp.s < nst && j < cp.G) {
                     const int units = cp.units;
                     Chunk<FMT> c;
                     read_chunk<FMT>(c, stage, n, g);
@@ -527,7 +517,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
                     acc += item_dot<FMT>(c, ldsb, abase, (uint32_t)units * 96u + (uint32_t)cs * 8u, (uint32_t)cs,
                                          valid ? 0 : 4, j == cp.G - 1);
                 }
-                if (cp.p == cp.P - 1) {
+                if (cp.s < nst && cp.p == cp.P - 1) {
                     float r = acc;
                     r += __shfl_xor(r, 16);
                     r += __shfl_xor(r, 32);
@@ -536,6 +526,16 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
                 }
                 cp.next(a, W, b);
             }
+        }
+        // the boundaries after this wave's last slot
+        while (s < nst) {
+            __syncthreads();  // A
+            __syncthreads();  // B
+            if (s + 1 < nst) {
+                stream_convert_x<FMT>(stage_at(a, s + 1), ldsb, xbuf, red);
+                __syncthreads();  // C
+            }
+            s++;
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the last (dummy) item loads have returned
     } else {
@@ -593,6 +593,7 @@ uint32_t *g_stream_bar = nullptr;
 
 struct StreamPlan {
     StreamStage *dev = nullptr;  // the stage table
+    int *slots = nullptr;        // item slots per compute wave of each workgroup
     int nstages = 0;
     int fmt = 0;
     size_t lds = 0;
@@ -727,19 +728,6 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
         o.total_rows = gu ? in.rows[0] : total;
         o.full_tiles = o.total_rows / (grid * tr);
         o.rem_start = o.full_tiles * grid * tr;
-        // the scalar-base issue path: full tiles inside one matrix, lane
-        // offsets within 32 bits
-        o.fast = (uint64_t)tr * (uint64_t)o.row_bytes < (1ull << 32);
-        if (gu) {
-            const bool up_low = in.W[1] < in.W[0];
-            o.wlo = up_low ? o.W[1] : o.W[0];
-            const uint64_t dg = o.W[0] - o.wlo, du = o.W[1] - o.wlo;
-            o.fast = o.fast && (dg > du ? dg : du) + (uint64_t)tr * (uint64_t)o.row_bytes < (1ull << 32);
-            o.dg = (uint32_t)dg;
-            o.du = (uint32_t)du;
-        } else {
-            for (int m = 0; m < nmat; m++) o.fast = o.fast && in.rows[m] % tr == 0;
-        }
         if (o.full_tiles + 1 > kStreamMaxTiles) {
             delete[] host;
             HOLO_REJECT("holo_gemv_stream_create: a stage with more rows than 16 tiles per CU");
@@ -762,7 +750,33 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
         return nullptr;
     }
     HOLO_CHECK(hipMemcpy(p->dev, host, sizeof(StreamStage) * nstages, hipMemcpyHostToDevice));
+    // each workgroup's slot count (the compute waves' trip count): its tiles of
+    // every stage times the stage's slots per tile, as the kernel's walk deals
+    // them, rounded up to a multiple of the ring depth
+    std::vector<int> slots(grid, 0);
+    for (int b = 0; b < grid; b++) {
+        long long n = 0;
+        for (int s = 0; s < nstages; s++) {
+            const StreamStage &o = host[s];
+            const uint32_t rem = (uint32_t)(o.total_rows - o.rem_start);
+            const int e0 = o.rem_start + (int)(((uint32_t)b * rem) / (uint32_t)grid);
+            const int e1 = o.rem_start + (int)(((uint32_t)(b + 1) * rem) / (uint32_t)grid);
+            n += (long long)(o.full_tiles + (e1 > e0 ? 1 : 0)) * o.P;
+        }
+        n = (n + kStreamD - 1) / kStreamD * kStreamD;
+        slots[b] = n > INT_MAX ? INT_MAX / kStreamD * kStreamD : (int)n;
+    }
     delete[] host;
+    if (hipMalloc((void **)&p->slots, sizeof(int) * grid) != hipSuccess) {
+        (void)hipGetLastError();
+        p->slots = nullptr;
+        HOLO_CHECK(hipFree(p->dev));
+        delete p;
+        HOLO_REJECT("holo_gemv_stream_create: device memory for the plan");
+        return nullptr;
+    }
+    HOLO_CHECK(hipMemcpy(p->slots, slots.data(), sizeof(int) * grid, hipMemcpyHostToDevice));
+    p->args.slots = (uint64_t)(uintptr_t)p->slots;
     p->args.table = (uint64_t)(uintptr_t)p->dev;
     p->args.nstages = nstages;
     p->args.bar = g_stream_bar;
@@ -789,6 +803,7 @@ void holo_gemv_stream_destroy(void *plan)
     StreamPlan *p = (StreamPlan *)plan;
     if (!p) return;
     if (p->dev) HOLO_CHECK(hipFree(p->dev));
+    if (p->slots) HOLO_CHECK(hipFree(p->slots));
     delete p;
 }
 
