@@ -26,17 +26,33 @@
 //                   global memory, so its vector-memory counter holds only
 //                   loads and each item's wait is exact.
 //   control wave    at a stage's end: sums the 8 partials of each of the
-//                   workgroup's rows, applies the epilogue (silu(g)*u, or
-//                   r + acc), stores the outputs device-coherently, completes
-//                   them (agent-scope release) and takes part in the grid
-//                   barrier.  It issues no weight loads.
+//                   workgroup's rows (64 rows at a time, one per lane), applies
+//                   the epilogue (silu(g)*u, or r + acc), stores the outputs,
+//                   then gathers the next stage's input.  It issues no weight
+//                   loads.
+//
+// How a stage's output reaches the next stage (no grid barrier): besides the
+// plain fp32 output, every output value is also stored as one 64-bit word
+// (tag << 32 | value bits) with a single agent-scope store, into the plan's
+// exchange buffer of that output vector.  The tag names the launch and the
+// stage (base + s + 1, base = launch count * (stages + 1)), so a word is
+// either this stage's value or visibly stale.  A consumer copies the words
+// of its whole input into LDS (device-coherent global_load_lds), checks every
+// tag and copies again only the 1 KB pieces that are not yet current, until
+// all are.  Value and tag travel in one single-copy-atomic 64-bit store, so a
+// current tag implies the current value: no fence, no store-completion wait
+// and no arrival counter sit between a producer's epilogue and its
+// consumers.  The launch count advances when the last workgroup of a launch
+// ends (a counter in the plan), so the next launch's tags differ from every
+// word this launch left behind.
+//
 // Stage boundary (3 workgroup barriers): A  all partials of stage s in LDS;
-// the control wave stores, synchronises the grid and loads x of stage s+1
-// (and its norm weight) straight into LDS as fp32 (device-coherent
-// global_load_lds); B  x is in LDS; all waves convert it (rms_norm if asked,
-// then the int8 planes); C  compute resumes.  The compute waves never load
-// activations, so nothing but their own weight items counts against their
-// vector-memory counter.
+// the control wave stores, then gathers the input of stage s+1 (and its norm
+// weight) into LDS, in the space of the compute waves' item stages, which are
+// idle until C; B  the input is in LDS; all waves convert it (rms_norm if
+// asked, then the int8 planes); C  compute resumes.  The compute waves never
+// load activations, so nothing but their own weight items counts against
+// their vector-memory counter.
 #include "gemv_mfma.h"
 
 #include <hip/hip_ext.h>
@@ -51,15 +67,8 @@ namespace {
 constexpr int kNCW = 8;                     // compute waves
 constexpr int kStreamThreads = 64 * (kNCW + 1);
 constexpr int kStreamMaxTiles = 16;         // tiles of one stage per workgroup
-constexpr uint32_t kStreamPolls = 1u << 18;  // bounded barrier wait (~0.1-0.3 s)
-
-// Barrier words, each on its own 256-byte line: group counters, top counter,
-// timeout flag (the layout of the multi-stage GEMV's barrier).
-constexpr int kSBarGroups = 8;
-constexpr int kSBarStride = 64;
-constexpr int kSBarTop = kSBarGroups * kSBarStride;
-constexpr int kSBarFlag = kSBarTop + kSBarStride;
-constexpr size_t kSBarBytes = (size_t)(kSBarFlag + kSBarStride) * 4;
+constexpr uint32_t kStreamPolls = 1u << 18;  // bounded exchange wait (~0.3 s)
+constexpr int kStreamMaxChunks = 192;        // 1 KB exchange pieces of one input (in_dim <= 24576)
 
 // One stage of the plan, in device memory (read with scalar loads).
 struct StreamStage {
@@ -78,6 +87,10 @@ struct StreamStage {
     int full_tiles;       // tiles dealt round robin to every workgroup
     int rem_start;        // first row of the remainder
     float eps;
+    uint64_t lly[3];      // exchange words of the outputs (gate/up: lly[0])
+    uint64_t llx;         // exchange words of x when an earlier stage wrote it, else 0
+    uint64_t llr;         // exchange words of r when an earlier stage wrote it, else 0
+    int xsrc, rsrc;       // the stage that wrote x / r last before this one
 };
 
 // The stage table is read through the constant address space: its loads are
@@ -90,7 +103,9 @@ struct StreamArgs {
     uint64_t slots;       // device address of int[grid]: item slots per compute
                           // wave of each workgroup, rounded up to a multiple of D
     int nstages;
-    uint32_t *bar;
+    uint32_t *seq;        // [0] launches so far, [64] workgroups done in this launch,
+                          // [128 + b] the tag of the last stage workgroup b stored
+    uint32_t *flag;       // set when an exchange wait gives up
     uint32_t zero_off;    // LDS: zero region (after the largest stage's planes)
     uint32_t stage_off;   // LDS: the compute waves' item stages
     uint32_t tpart_off;   // LDS: tile partials [kStreamMaxTiles][kNCW][16]
@@ -304,46 +319,104 @@ __device__ __forceinline__ void stream_stage_write(const Raw2<FMT> &b, uint8_t *
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void gvoid;
 
-// x of a stage (units * 32 floats) and, with a norm, its weight into the fp32
-// LDS buffer, by one wave: each global_load_lds_dwordx4 moves 64 lanes x 16
-// contiguous bytes into 1 KB of LDS.  Device-coherent (sc1): an earlier
-// stage of this launch wrote x.  The caller waits (vmcnt) before the
+// The input of a stage that no earlier stage of the plan wrote (plain fp32,
+// units * 32 floats), by one wave: each global_load_lds_dwordx4 moves 64 lanes
+// x 16 contiguous bytes into 1 KB of LDS.  The caller waits (vmcnt) before the
 // workgroup barrier that publishes the buffer.
-__device__ __forceinline__ void stream_fetch_x(cstage &st, uint8_t *xbuf, int lane)
+__device__ __forceinline__ void stream_fetch_plain(cstage &st, uint8_t *xbuf, int lane)
 {
     const int units = uni(st.units), n = units / 8;  // 1 KB pieces (units is a multiple of 8)
     const float *x = (const float *)uni64(st.x);
     for (int j = 0; j < n; j++)
-        __builtin_amdgcn_global_load_lds((gvoid *)(x + 256 * j + 4 * lane), (lds_void *)(xbuf + 1024 * j), 16, 0,
-                                         kDeviceScope);
-    const uint64_t nw = uni64(st.nw);
-    if (nw) {
-        const float *w = (const float *)nw;
-        uint8_t *wb = xbuf + units * 128;
-        for (int j = 0; j < n; j++)
-            __builtin_amdgcn_global_load_lds((gvoid *)(w + 256 * j + 4 * lane), (lds_void *)(wb + 1024 * j), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((gvoid *)(x + 256 * j + 4 * lane), (lds_void *)(xbuf + 1024 * j), 16, 0, 0);
+}
+
+// The stage's norm weight (plain fp32) after its input in LDS.
+__device__ __forceinline__ void stream_fetch_norm(cstage &st, uint8_t *wbuf, int lane)
+{
+    const int units = uni(st.units), n = units / 8;
+    const float *w = (const float *)uni64(st.nw);
+    for (int j = 0; j < n; j++)
+        __builtin_amdgcn_global_load_lds((gvoid *)(w + 256 * j + 4 * lane), (lds_void *)(wbuf + 1024 * j), 16, 0, 0);
+}
+
+// Waits until every workgroup has stored its rows of the stage with tag
+// `tag` (its done word holds that tag or a later one of this launch).  A done
+// word is stored right after the workgroup's exchange words, without waiting
+// for them to complete, so it only says that the words are on their way: the
+// gather still checks every word's tag.  The wait keeps the polling to 4
+// bytes per workgroup instead of the whole input.
+__device__ __forceinline__ void stream_wait_done(const uint32_t *done, uint32_t tag, uint32_t *flag, int lane)
+{
+    const int G = (int)gridDim.x;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)done, (short)0, G * 4, kBufferWord3);
+    for (uint32_t polls = 0;; polls++) {
+        bool late = false;
+        for (int j = 0; 256 * j < G; j++) {
+            const u32x4 d = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 1024 * j + 16 * lane, 0, kDeviceScope));
+            const int i0 = 256 * j + 4 * lane;
+#pragma unroll
+            for (int e = 0; e < 4; e++) late |= i0 + e < G && (int32_t)(d[e] - tag) < 0;
+        }
+        if (__ballot(late) == 0) return;
+        if (polls == kStreamPolls) {
+            __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(2);
     }
 }
 
-// The fp32 x in LDS into the int8 planes and {dx, c} pairs, by all threads;
+// The input of a stage that an earlier stage wrote: its exchange words
+// (8 bytes per value) into LDS, 1 KB pieces of 128 words, device-coherent
+// (sc1: never answered from a line this XCD's L2 held before another XCD's
+// store).  The tags are checked while the words are converted
+// (stream_convert_x); stream_stage_in copies again what was not current.
+__device__ __forceinline__ void stream_fetch_tagged(cstage &st, uint8_t *xbuf, int lane)
+{
+    const int units = uni(st.units), nch = units / 4;  // 128 words = 4 units per piece
+    const uint8_t *src = (const uint8_t *)uni64(st.llx);
+    for (int j = 0; j < nch; j++)
+        __builtin_amdgcn_global_load_lds((gvoid *)(src + 1024 * j + 16 * lane), (lds_void *)(xbuf + 1024 * j), 16, 0,
+                                         kDeviceScope);
+}
+
+// x value chunk i (4 values) of the staged input: plain fp32, or exchange
+// words (value, tag) pairs, whose tags must all be `tag` (else `bad`).
+__device__ __forceinline__ float4 staged_x4(const uint8_t *xbuf, int i, bool tagged, uint32_t tag, bool &bad)
+{
+    if (tagged) {
+        const uint4 a = *(const uint4 *)(xbuf + 32 * i), b = *(const uint4 *)(xbuf + 32 * i + 16);
+        bad |= (a.y != tag) | (a.w != tag) | (b.y != tag) | (b.w != tag);
+        return make_float4(__uint_as_float(a.x), __uint_as_float(a.z), __uint_as_float(b.x), __uint_as_float(b.z));
+    }
+    return *(const float4 *)(xbuf + 16 * i);
+}
+
+constexpr int kRedBad = 15;   // red[15]: a stale exchange word was staged
+constexpr int kRedBase = 14;  // red[14]: this launch's tag base, from the control wave
+
+// The staged x in LDS into the int8 planes and {dx, c} pairs, by all threads;
 // with a norm weight, x * (1/sqrt(mean(x^2) + eps)) * w first (cuda_rms_norm's
 // formula, cuda_ops.cu:1479-1504), the 9 waves' sums of squares meeting in red.
 template <int FMT>
-__device__ __forceinline__ void stream_convert_x(cstage &st, uint8_t *ldsb, const uint8_t *xbuf, float *red)
+__device__ __forceinline__ void stream_convert_x(cstage &st, uint8_t *ldsb, const uint8_t *xbuf, float *red,
+                                                 uint32_t tag)
 {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int units = uni(st.units), chunks = units * 8;
     const bool norm = uni64(st.nw) != 0;
-    const float4 *xv = (const float4 *)xbuf;
+    const bool tagged = uni64(st.llx) != 0;
+    bool bad = false;
     float scale = 1.f;
     if (norm) {
         float ss = 0.f;
         for (int i = tid; i < chunks; i += kStreamThreads) {
-            const float4 v = xv[i];
+            const float4 v = staged_x4(xbuf, i, tagged, tag, bad);
             ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        ss = wave_sum(ss);
         if (lane == 0) red[wave] = ss;
         __syncthreads();
         float tot = 0.f;
@@ -351,77 +424,150 @@ __device__ __forceinline__ void stream_convert_x(cstage &st, uint8_t *ldsb, cons
         for (int w = 0; w <= kNCW; w++) tot += red[w];
         scale = 1.0f / sqrtf(tot / (float)(units * 32) + unif(st.eps));
     }
-    const float4 *wv = (const float4 *)(xbuf + units * 128);
+    const float4 *wv = (const float4 *)(xbuf + units * (tagged ? 256 : 128));
     for (int i = tid; i < chunks; i += kStreamThreads) {
-        float4 v = xv[i];
+        float4 v = staged_x4(xbuf, i, tagged, tag, bad);
         if (norm) {
             const float4 w4 = wv[i];
             v = make_float4(v.x * scale * w4.x, v.y * scale * w4.y, v.z * scale * w4.z, v.w * scale * w4.w);
         }
         x_convert<FMT, XM_MFMA>(v, i, units, (void *)ldsb);
     }
+    if (tagged && __ballot(bad) != 0 && lane == 0) ((uint32_t *)red)[kRedBad] = 1u;
 }
 
-// The control wave's stores of stage s: every tile's 16 (gate/up: 8) rows,
-// the 8 compute waves' partials summed in wave order.
-__device__ __forceinline__ void stream_epilogue(cstage &st, const Tiles &t, const float *tpart,
-                                                const float (&rr)[kStreamMaxTiles], uint32_t W, uint32_t b, int lane)
+// After the input of stage `st` was staged (B): all waves convert it (C), and
+// while a stale exchange word was among it, the control wave copies the words
+// again and all waves convert again.  Every wave takes the same rounds (each
+// reads the flag after the same barrier), so the barrier counts agree.  After
+// kStreamPolls rounds the wait gives up and sets the plan's flag.
+template <int FMT>
+__device__ __forceinline__ void stream_stage_in(cstage &st, uint8_t *ldsb, uint8_t *xbuf, float *red, uint32_t base,
+                                                uint32_t *flag, bool control, int lane)
 {
+    const uint32_t tag = base + (uint32_t)uni(st.xsrc) + 1u;
+    stream_convert_x<FMT>(st, ldsb, xbuf, red, tag);
+    __syncthreads();  // C
+    if (uni64(st.llx) == 0) return;
+    uint32_t *badp = (uint32_t *)red + kRedBad;
+    for (uint32_t round = 0; uni((int)*badp) != 0; round++) {
+        __syncthreads();  // every wave has read the flag
+        if (control) {
+            if (lane == 0) *badp = 0u;
+            if (round == kStreamPolls) {
+                __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                __builtin_amdgcn_s_sleep(4);
+                stream_fetch_tagged(st, xbuf, lane);
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+            }
+        }
+        __syncthreads();  // B again
+        if (round < kStreamPolls) stream_convert_x<FMT>(st, ldsb, xbuf, red, tag);
+        __syncthreads();  // C again
+    }
+}
+
+// Row v of this workgroup's rows of a stage for lane `lane` in pass q: 64
+// rows a pass, tile k = q * (64 / TR) + lane / TR, row lane % TR of it.
+__device__ __forceinline__ bool own_row(const Tiles &t, int q, int lane, uint32_t W, uint32_t b, int &k, int &i,
+                                        int &v)
+{
+    const int per = 64 / t.TR;
+    k = q * per + lane / t.TR;
+    i = lane % t.TR;
+    int row0, rend;
+    t.rows(k, W, b, row0, rend);
+    v = row0 + i;
+    return k < t.n && v < rend;
+}
+
+constexpr int kStreamPasses = kStreamMaxTiles * 16 / 64;  // passes of 64 rows over at most 16 tiles
+
+__device__ __forceinline__ uint64_t exchange_word(float v, uint32_t tag)
+{
+    return ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v);
+}
+
+// The residual rows r[v] of this workgroup's rows of stage s (plain stages
+// with r), one per lane and pass: exchange words when an earlier stage wrote
+// r (waited for like the input), else the caller's fp32 values.
+__device__ __forceinline__ void stream_residual(cstage &st, const Tiles &t, float (&rr)[kStreamPasses], uint32_t base,
+                                                uint32_t *flag, uint32_t W, uint32_t b, int lane)
+{
+#pragma unroll
+    for (int q = 0; q < kStreamPasses; q++) rr[q] = 0.f;
+    const uint64_t rp = uni64(st.r), llr = uni64(st.llr);
+    if (!rp || uni(st.mode) != MODE_PLAIN) return;
+    const uint32_t tag = base + (uint32_t)uni(st.rsrc) + 1u;
+#pragma unroll
+    for (int q = 0; q < kStreamPasses; q++) {
+        int k, i, v;
+        const bool mine = own_row(t, q, lane, W, b, k, i, v);
+        if (!llr) {
+            if (mine) rr[q] = ((gcfloat *)rp)[v];
+            continue;
+        }
+        uint64_t w = 0;
+        for (uint32_t polls = 0;; polls++) {
+            if (mine)
+                w = __hip_atomic_load((__attribute__((address_space(1))) uint64_t *)llr + v, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+            if (__ballot(mine && (uint32_t)(w >> 32) != tag) == 0) break;
+            if (polls == kStreamPolls) {
+                __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        rr[q] = __uint_as_float((uint32_t)w);
+    }
+}
+
+// The control wave's stores of stage s: each of the workgroup's rows (one per
+// lane and pass), the 8 compute waves' partials summed in wave order; the
+// plain fp32 output and its exchange word.
+__device__ __forceinline__ void stream_epilogue(cstage &st, const Tiles &t, const float *tpart,
+                                                const float (&rr)[kStreamPasses], uint32_t tag, uint32_t W,
+                                                uint32_t b, int lane)
+{
+    typedef __attribute__((address_space(1))) uint64_t gword;
     const bool gu = uni(st.mode) == MODE_GATEUP;
     const uint64_t y0 = uni64(st.y[0]), y1 = uni64(st.y[1]), y2 = uni64(st.y[2]);
+    const uint64_t l0 = uni64(st.lly[0]), l1 = uni64(st.lly[1]), l2 = uni64(st.lly[2]);
     const bool res = uni64(st.r) != 0;
+    const int per = 64 / t.TR;
 #pragma unroll
-    for (int k = 0; k < kStreamMaxTiles; k++) {
-        int row0, rend;
-        t.rows(k, W, b, row0, rend);
-        const int v = row0 + lane;
-        if (k < t.n && lane < t.TR && v < rend) {  // a predicated body: rr stays in registers
+    for (int q = 0; q < kStreamPasses; q++) {
+        if (q * per >= t.n) break;
+        int k, i, v;
+        if (own_row(t, q, lane, W, b, k, i, v)) {
             const float *pt = tpart + k * (kNCW * 16);
             float s0 = 0.f;
 #pragma unroll
-            for (int w = 0; w < kNCW; w++) s0 += pt[w * 16 + lane];
+            for (int w = 0; w < kNCW; w++) s0 += pt[w * 16 + i];
             if (gu) {
                 float s1 = 0.f;
 #pragma unroll
-                for (int w = 0; w < kNCW; w++) s1 += pt[w * 16 + 8 + lane];
-                __hip_atomic_store((gfloat *)y0 + v, silu(s0) * s1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int w = 0; w < kNCW; w++) s1 += pt[w * 16 + 8 + i];
+                const float o = silu(s0) * s1;
+                ((gfloat *)y0)[v] = o;
+                __hip_atomic_store((gword *)l0 + v, exchange_word(o, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else {
                 int m, row;
                 split_row(st, v, m, row);
-                if (res) s0 = rr[k] + s0;
-                gfloat *yb = (gfloat *)(m == 2 ? y2 : m == 1 ? y1 : y0);
-                __hip_atomic_store(yb + row, s0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (res) s0 = rr[q] + s0;
+                ((gfloat *)(m == 2 ? y2 : m == 1 ? y1 : y0))[row] = s0;
+                __hip_atomic_store((gword *)(m == 2 ? l2 : m == 1 ? l1 : l0) + row, exchange_word(s0, tag),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     }
 }
 
-// Arrival and wait of one workgroup (one thread), two-level monotonic
-// counters as the multi-stage GEMV's barrier: the state is valid across
-// launches and graph replays, and a bounded wait sets the flag instead of
-// hanging.
-__device__ __forceinline__ void stream_grid_barrier(uint32_t *bar)
+__device__ __forceinline__ void stream_mark_done(uint32_t *done, uint32_t tag, uint32_t b, int lane)
 {
-    const uint32_t G = gridDim.x;
-    const uint32_t ng = G < kSBarGroups ? G : kSBarGroups;
-    const uint32_t gi = blockIdx.x % ng;
-    const uint32_t size = G / ng + (gi < G % ng ? 1u : 0u);
-    const uint32_t a = __hip_atomic_fetch_add(bar + gi * kSBarStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t k = a / size + 1;
-    const uint32_t target = k * ng;
-    if (a + 1 == k * size) {
-        const uint32_t t = __hip_atomic_fetch_add(bar + kSBarTop, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (t + 1 == target) return;
-    }
-    for (uint32_t polls = 0;; polls++) {
-        const uint32_t c = __hip_atomic_load(bar + kSBarTop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((int32_t)(c - target) >= 0) return;
-        if (polls == kStreamPolls) {
-            __hip_atomic_store(bar + kSBarFlag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
+    if (lane == 0) __hip_atomic_store(done + b, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int FMT, int D>
@@ -472,7 +618,8 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
             advance();
         }
         __syncthreads();  // B of stage 0: x in LDS
-        stream_convert_x<FMT>(stage_at(a, 0), ldsb, xbuf, red);
+        const uint32_t base = (uint32_t)uni((int)((uint32_t *)red)[kRedBase]);
+        stream_convert_x<FMT>(stage_at(a, 0), ldsb, xbuf, red, 0u);
         __syncthreads();  // C of stage 0
         int s = 0;        // the stage whose boundary comes next
         float acc = 0.f;
@@ -493,10 +640,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
                 while (s < cp.s) {
                     __syncthreads();  // A
                     __syncthreads();  // B
-                    if (s + 1 < nst) {
-                        stream_convert_x<FMT>(stage_at(a, s + 1), ldsb, xbuf, red);
-                        __syncthreads();  // C
-                    }
+                    if (s + 1 < nst) stream_stage_in<FMT>(stage_at(a, s + 1), ldsb, xbuf, red, base, a.flag, false, lane);
                     s++;
                 }
                 // a slot past the last stage writes its (unused) item too, so
@@ -531,57 +675,61 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
         while (s < nst) {
             __syncthreads();  // A
             __syncthreads();  // B
-            if (s + 1 < nst) {
-                stream_convert_x<FMT>(stage_at(a, s + 1), ldsb, xbuf, red);
-                __syncthreads();  // C
-            }
+            if (s + 1 < nst) stream_stage_in<FMT>(stage_at(a, s + 1), ldsb, xbuf, red, base, a.flag, false, lane);
             s++;
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the last (dummy) item loads have returned
     } else {
         // ---- control wave ----
-        stream_fetch_x(stage_at(a, 0), xbuf, lane);
+        const uint32_t seq0 = __hip_atomic_load(a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t base = uni((int)(seq0 * (uint32_t)(nst + 1)));
+        {
+            cstage &st0 = stage_at(a, 0);
+            stream_fetch_plain(st0, xbuf, lane);
+            if (uni64(st0.nw)) stream_fetch_norm(st0, xbuf + uni(st0.units) * 128, lane);
+        }
+        if (lane == 0) ((uint32_t *)red)[kRedBase] = base;
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the LDS-direct loads have landed
         __syncthreads();                     // B of stage 0
-        stream_convert_x<FMT>(stage_at(a, 0), ldsb, xbuf, red);
+        stream_convert_x<FMT>(stage_at(a, 0), ldsb, xbuf, red, 0u);
         __syncthreads();  // C of stage 0
         for (int s = 0; s < nst; s++) {
             cstage &st = stage_at(a, s);
             Tiles t;
             t.init(st, W, b);
-            // residual rows of this stage's tiles, loaded while the stage runs
-            float rr[kStreamMaxTiles];
-#pragma unroll
-            for (int k = 0; k < kStreamMaxTiles; k++) rr[k] = 0.f;
-            const uint64_t rp = uni64(st.r);
-            if (rp && uni(st.mode) == MODE_PLAIN) {
-#pragma unroll
-                for (int k = 0; k < kStreamMaxTiles; k++) {
-                    int row0, rend;
-                    t.rows(k, W, b, row0, rend);
-                    if (k < t.n && lane < 16 && row0 + lane < rend)
-                        rr[k] = __hip_atomic_load((gcfloat *)rp + row0 + lane, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
+            // residual rows of this stage's rows, gathered while the stage runs
+            float rr[kStreamPasses];
+            stream_residual(st, t, rr, base, a.flag, W, b, lane);
             __syncthreads();  // A: every partial of stage s is in LDS
-            stream_epilogue(st, t, tpart, rr, W, b, lane);
+            stream_epilogue(st, t, tpart, rr, base + (uint32_t)s + 1u, W, b, lane);
+            stream_mark_done(a.seq + 128, base + (uint32_t)s + 1u, b, lane);
             if (s + 1 < nst) {
-                // Every output of this stage is an agent-scope atomic store
-                // (sc1), performed at agent scope; the wave waits for them to
-                // complete (vmcnt(0)) before the arrival.  No other store of
-                // the kernel needs publishing, so the L2 write-back of a full
-                // agent-scope release fence (1.5 us a stage) is not needed.
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // compiler ordering
-                __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0)
-                if (lane == 0) stream_grid_barrier(a.bar);
-                stream_fetch_x(stage_at(a, s + 1), xbuf, lane);
+                cstage &st1 = stage_at(a, s + 1);
+                const int units1 = uni(st1.units);
+                const bool tagged = uni64(st1.llx) != 0;
+                // the partial reads above are done before any copy lands in
+                // their space (xbuf aliases the item stages and partials)
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+                if (uni64(st1.nw)) stream_fetch_norm(st1, xbuf + units1 * (tagged ? 256 : 128), lane);
+                if (tagged) {
+                    if (lane == 0) ((uint32_t *)red)[kRedBad] = 0u;
+                    stream_wait_done(a.seq + 128, base + (uint32_t)uni(st1.xsrc) + 1u, a.flag, lane);
+                    stream_fetch_tagged(st1, xbuf, lane);
+                }
+                else
+                    stream_fetch_plain(st1, xbuf, lane);
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             }
             __syncthreads();  // B
-            if (s + 1 < nst) {
-                stream_convert_x<FMT>(stage_at(a, s + 1), ldsb, xbuf, red);
-                __syncthreads();  // C
+            if (s + 1 < nst) stream_stage_in<FMT>(stage_at(a, s + 1), ldsb, xbuf, red, base, a.flag, true, lane);
+        }
+        // the last workgroup to finish advances the launch count (every
+        // workgroup read it at its start, before counting itself done)
+        if (lane == 0) {
+            const uint32_t done = __hip_atomic_fetch_add(a.seq + 64, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (done == W - 1) {
+                __hip_atomic_store(a.seq + 64, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(a.seq, seq0 + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     }
@@ -589,29 +737,36 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
 
 // ---- host ----------------------------------------------------------------------------
 
-uint32_t *g_stream_bar = nullptr;
+uint32_t *g_stream_flag = nullptr;  // set by an exchange wait that gave up
 
 struct StreamPlan {
     StreamStage *dev = nullptr;  // the stage table
     int *slots = nullptr;        // item slots per compute wave of each workgroup
+    uint8_t *words = nullptr;    // launch counter line, done counter line, exchange words
     int nstages = 0;
     int fmt = 0;
     size_t lds = 0;
     StreamArgs args{};
 };
 
+// LDS: [x planes + {dx, c}][zero region][norm reduction][region], where the
+// region holds the compute waves' item stages and the tile partials during a
+// stage, and the staged input (fp32 or exchange words, then the norm weight)
+// during a boundary.
 size_t stream_lds(int fmt, int max_units, int max_xbuf, uint32_t &zero_off, uint32_t &stage_off,
                   uint32_t &tpart_off, uint32_t &red_off, uint32_t &xbuf_off)
 {
     const size_t x_lds = ((size_t)max_units * lds_bytes_per_unit<XM_I24>() + 15) & ~(size_t)15;
     zero_off = zero_region_off((uint32_t)x_lds);
-    stage_off = zero_off + kZeroBytes;
+    red_off = zero_off + kZeroBytes;
+    stage_off = (red_off + 16 * 4 + 15) & ~15u;
     const int stage = fmt == FMT_Q4_0 ? Geo<FMT_Q4_0>::STAGE : fmt == FMT_Q8_0 ? Geo<FMT_Q8_0>::STAGE
                                                                                 : Geo<FMT_Q4_K>::STAGE;
     tpart_off = (stage_off + kNCW * stage + 15) & ~15u;
-    red_off = tpart_off + kStreamMaxTiles * kNCW * 16 * 4;
-    xbuf_off = red_off + 16 * 4;
-    return xbuf_off + (size_t)max_xbuf;
+    xbuf_off = stage_off;
+    const size_t during = tpart_off + (size_t)kStreamMaxTiles * kNCW * 16 * 4;
+    const size_t boundary = xbuf_off + (size_t)max_xbuf;
+    return during > boundary ? during : boundary;
 }
 
 template <int FMT, int D>
@@ -649,18 +804,18 @@ bool stream_launch_f(StreamPlan &p)
 
 bool gemv_stream_init()
 {
-    if (g_stream_bar) return true;
-    if (hipMalloc((void **)&g_stream_bar, kSBarBytes) != hipSuccess) {
-        g_stream_bar = nullptr;
+    if (g_stream_flag) return true;
+    if (hipMalloc((void **)&g_stream_flag, 256) != hipSuccess) {
+        g_stream_flag = nullptr;
         return false;
     }
-    return hipMemset(g_stream_bar, 0, kSBarBytes) == hipSuccess && hipDeviceSynchronize() == hipSuccess;
+    return hipMemset(g_stream_flag, 0, 256) == hipSuccess && hipDeviceSynchronize() == hipSuccess;
 }
 
 void gemv_stream_release()
 {
-    if (g_stream_bar) hipFree(g_stream_bar);
-    g_stream_bar = nullptr;
+    if (g_stream_flag) hipFree(g_stream_flag);
+    g_stream_flag = nullptr;
 }
 
 }  // namespace holo
@@ -672,7 +827,7 @@ extern "C" {
 void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, int type)
 {
     const int fmt = type == HOLO_TYPE_Q4_0 ? FMT_Q4_0 : type == HOLO_TYPE_Q4_K ? FMT_Q4_K : -1;
-    if (!stages || nstages < 1 || fmt < 0 || !g_stream_bar) {
+    if (!stages || nstages < 1 || fmt < 0 || !g_stream_flag) {
         HOLO_REJECT("holo_gemv_stream_create: no stages, a type other than Q4_0/Q4_K, or cuda_init not called");
         return nullptr;
     }
@@ -734,10 +889,100 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
             return nullptr;
         }
         max_units = o.units > max_units ? o.units : max_units;
-        const int xb = o.units * 128 * (in.norm_w ? 2 : 1);
+    }
+    // Exchange buffers: one per distinct output vector (keyed by its address),
+    // as many words as the most rows any stage writes there.  A stage's x or r
+    // that an earlier stage wrote is read from that buffer (xsrc / rsrc: the
+    // last writer before it); an input that overlaps an earlier output in any
+    // other way, an output that overlaps its own stage's x, two outputs of one
+    // stage in one vector, or outputs that partly overlap are rejected.
+    struct OutVec {
+        uint64_t ptr;
+        int rows, last;
+        size_t off;
+    };
+    std::vector<OutVec> outs;
+    std::vector<int> xo(nstages, -1), ro(nstages, -1), yo(3 * (size_t)nstages, -1);
+    auto overlap = [](uint64_t a, uint64_t an, uint64_t b, uint64_t bn) { return a < b + bn && b < a + an; };
+    auto source = [&](uint64_t ptr, int n, int &idx, int &src) {
+        idx = -1;
+        src = -1;
+        for (size_t i = 0; i < outs.size(); i++) {
+            if (outs[i].ptr == ptr) {
+                if (outs[i].rows < n) return false;
+                idx = (int)i;
+                src = outs[i].last;
+            } else if (overlap(ptr, 4ull * n, outs[i].ptr, 4ull * outs[i].rows)) {
+                return false;
+            }
+        }
+        return true;
+    };
+    bool xok = true;
+    for (int s = 0; s < nstages && xok; s++) {
+        const holo_stream_stage_t &in = stages[s];
+        StreamStage &o = host[s];
+        xok = source(o.x, in.in_dim, xo[s], o.xsrc);
+        if (xok && in.r) xok = source(o.r, in.rows[0], ro[s], o.rsrc);
+        const int nout = in.gate_up ? 1 : in.nmat;
+        for (int m = 0; m < nout && xok; m++) {
+            const uint64_t y = (uint64_t)in.y[m];
+            const int rows = in.rows[m];
+            if (overlap(y, 4ull * rows, o.x, 4ull * in.in_dim)) xok = false;
+            int hit = -1;
+            for (size_t i = 0; i < outs.size() && xok; i++) {
+                if (outs[i].ptr == y) hit = (int)i;
+                else if (overlap(y, 4ull * rows, outs[i].ptr, 4ull * outs[i].rows)) xok = false;
+            }
+            if (!xok) break;
+            if (hit < 0) {
+                outs.push_back(OutVec{y, rows, s, 0});
+                hit = (int)outs.size() - 1;
+            } else if (outs[hit].last == s) {
+                xok = false;
+                break;
+            } else {
+                outs[hit].rows = rows > outs[hit].rows ? rows : outs[hit].rows;
+                outs[hit].last = s;
+            }
+            yo[3 * (size_t)s + m] = hit;
+        }
+    }
+    if (!xok) {
+        delete[] host;
+        HOLO_REJECT("holo_gemv_stream_create: a stage input that overlaps an earlier output other than exactly, or "
+                    "an output overlapping its own input or another output");
+        return nullptr;
+    }
+    size_t nwords = 0;
+    for (OutVec &v : outs) {
+        v.off = nwords;
+        nwords += (size_t)v.rows;
+    }
+    // launch counter line, done counter line, one done word per workgroup
+    const size_t kWordsHeader = (512 + 4 * (size_t)grid + 255) & ~(size_t)255;
+    const size_t words_bytes = kWordsHeader + 8 * nwords;
+    uint8_t *words = nullptr;
+    if (hipMalloc((void **)&words, words_bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        delete[] host;
+        HOLO_REJECT("holo_gemv_stream_create: device memory for the exchange buffers");
+        return nullptr;
+    }
+    HOLO_CHECK(hipMemset(words, 0, words_bytes));
+    const uint64_t wbase = (uint64_t)(uintptr_t)words + kWordsHeader;
+    for (int s = 0; s < nstages; s++) {
+        const holo_stream_stage_t &in = stages[s];
+        StreamStage &o = host[s];
+        const int nout = in.gate_up ? 1 : in.nmat;
+        for (int m = 0; m < 3; m++) o.lly[m] = wbase + 8 * outs[yo[3 * (size_t)s + (m < nout ? m : 0)]].off;
+        o.llx = xo[s] >= 0 ? wbase + 8 * outs[xo[s]].off : 0;
+        o.llr = ro[s] >= 0 ? wbase + 8 * outs[ro[s]].off : 0;
+        const int xb = o.units * (o.llx ? 256 : 128) + (in.norm_w ? o.units * 128 : 0);
         max_xbuf = xb > max_xbuf ? xb : max_xbuf;
     }
     StreamPlan *p = new StreamPlan;
+    p->words = words;
     p->nstages = nstages;
     p->fmt = fmt;
     p->lds = stream_lds(fmt, max_units, max_xbuf, p->args.zero_off, p->args.stage_off, p->args.tpart_off,
@@ -745,6 +990,7 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
     if (p->lds > 160 * 1024 || hipMalloc((void **)&p->dev, sizeof(StreamStage) * nstages) != hipSuccess) {
         (void)hipGetLastError();
         delete[] host;
+        HOLO_CHECK(hipFree(words));
         delete p;
         HOLO_REJECT("holo_gemv_stream_create: LDS or device memory for the plan");
         return nullptr;
@@ -771,6 +1017,7 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
         (void)hipGetLastError();
         p->slots = nullptr;
         HOLO_CHECK(hipFree(p->dev));
+        HOLO_CHECK(hipFree(words));
         delete p;
         HOLO_REJECT("holo_gemv_stream_create: device memory for the plan");
         return nullptr;
@@ -779,7 +1026,8 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
     p->args.slots = (uint64_t)(uintptr_t)p->slots;
     p->args.table = (uint64_t)(uintptr_t)p->dev;
     p->args.nstages = nstages;
-    p->args.bar = g_stream_bar;
+    p->args.seq = (uint32_t *)words;
+    p->args.flag = g_stream_flag;
     return p;
 }
 
@@ -804,17 +1052,18 @@ void holo_gemv_stream_destroy(void *plan)
     if (!p) return;
     if (p->dev) HOLO_CHECK(hipFree(p->dev));
     if (p->slots) HOLO_CHECK(hipFree(p->slots));
+    if (p->words) HOLO_CHECK(hipFree(p->words));
     delete p;
 }
 
 int holo_gemv_stream_status(void)
 {
-    if (!g_stream_bar) return 0;
+    if (!g_stream_flag) return 0;
     uint32_t flag = 0;
     HOLO_CHECK(hipStreamSynchronize(stream()));
-    HOLO_CHECK(hipMemcpy(&flag, g_stream_bar + kSBarFlag, sizeof(flag), hipMemcpyDeviceToHost));
+    HOLO_CHECK(hipMemcpy(&flag, g_stream_flag, sizeof(flag), hipMemcpyDeviceToHost));
     if (flag == 0) return 0;
-    HOLO_CHECK(hipMemset(g_stream_bar, 0, kSBarBytes));
+    HOLO_CHECK(hipMemset(g_stream_flag, 0, 256));
     HOLO_CHECK(hipDeviceSynchronize());
     return HOLO_ECHAIN;
 }

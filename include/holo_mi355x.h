@@ -109,25 +109,31 @@ int holo_gemv_chain_status(void);
 
 /* ---- a decode step's GEMV stages in one persistent launch ---------------------
  * A plan of dependent GEMV stages (every layer's q/k/v, o, gate/up and down of a
- * decode step), run by holo_gemv_stream_launch as ONE kernel launch with a
- * grid barrier between stages.  Each stage is the GEMV of cuda_matmul_<type>
- * over 1-3 matrices sharing x (gate_up = 0: y[m] = W[m] x), or the fused
- * gate/up (gate_up = 1: y[0] = silu(W[0] x) * (W[1] x)); with norm_w its
- * input is rms_norm(x) * norm_w (cuda_rms_norm's formula, eps), and with r
- * (one plain matrix) its output is y[0] = r + W x (r may alias y[0]).  A
- * stage may read an earlier stage's output as x; y must not overlap the same
- * stage's x.  Results are those of the separate MFMA-path GEMV calls (within
- * fp32 rounding: the norm's summation order differs).  The weight loads of
- * later stages are issued ahead, across the barriers, so a step streams its
- * weights without a ramp or tail per stage.  Q4_0 or Q4_K (HOLO_TYPE_*),
- * in_dim a multiple of 256 up to 18432, 16-byte aligned matrices, vectors and
- * norm weights, at most 16 tiles of rows per CU and stage (16 rows, or 8 for
- * gate/up).  No reference counterpart: it replaces the per-matrix launches
- * of the decode loop (src/ai/llm_cuda.c:604-918).
- * create: copies the stage table to the device (allocates; not under graph
- *   capture); NULL, with the error latched, for anything outside the set.
+ * decode step), run by holo_gemv_stream_launch as ONE kernel launch.  Each
+ * stage is the GEMV of cuda_matmul_<type> over 1-3 matrices sharing x
+ * (gate_up = 0: y[m] = W[m] x), or the fused gate/up (gate_up = 1: y[0] =
+ * silu(W[0] x) * (W[1] x)); with norm_w its input is rms_norm(x) * norm_w
+ * (cuda_rms_norm's formula, eps), and with r (one plain matrix) its output is
+ * y[0] = r + W x (r may alias y[0]).  A stage may read an earlier stage's
+ * output as x or r, when it names that output's address exactly; outputs hand
+ * over to later stages through exchange words (value and a launch/stage tag
+ * in one 64-bit store) that the consumers poll, not a grid barrier.  Rejected:
+ * an input overlapping an earlier output other than exactly, an output
+ * overlapping its own stage's x or another output.  Results are those of the
+ * separate MFMA-path GEMV calls (within fp32 rounding: the norm's summation
+ * order differs).  The weight loads of later stages are issued ahead, across
+ * the stage boundaries.  Q4_0 or Q4_K (HOLO_TYPE_*), in_dim a multiple of 256
+ * up to 18432 (and within the 160 KB of LDS), 16-byte aligned matrices,
+ * vectors and norm weights, at most 16 tiles of rows per CU and stage (16
+ * rows, or 8 for gate/up).  No reference counterpart: it replaces the
+ * per-matrix launches of the decode loop (src/ai/llm_cuda.c:604-918).
+ * create: copies the stage table to the device and allocates the exchange
+ *   buffers (not under graph capture); NULL, with the error latched, for
+ *   anything outside the set.
  * launch: one launch on the library stream (capturable); 0 or HOLO_EINVAL.
- * status: like holo_gemv_chain_status, for the stream kernel's barrier.    */
+ *   Launches of one plan must not overlap (they share its exchange buffers).
+ * status: HOLO_ECHAIN (and clears it) if a launch's exchange wait gave up
+ *   (bounded at ~0.3 s; the results of that launch are then wrong), else 0. */
 typedef struct {
     const void *W[3];
     float *y[3];
