@@ -246,8 +246,9 @@ def test_stream_ragged_rows(holo, synth, oracle):
 
 def test_stream_graph_replays(holo, synth):
     """A plan launch captured in a HIP graph replays bit for bit like the
-    eager launch, with eager launches of the same plan between replays (the
-    barrier counters only grow)."""
+    eager launch, with eager launches of the same plan between replays (each
+    launch advances the plan's launch counter, so every launch's exchange tags
+    differ from the words the previous one left behind)."""
     print("case stream graph replays", flush=True)
     lib = holo.lib()
     t = Q4_0
@@ -302,4 +303,22 @@ def test_stream_rejects_unsupported(holo, synth):
     with pytest.raises(holo.HoloError):  # a residual on a gate/up stage
         holo.StreamPlan([holo.stream_stage([W2.ptr, W2.ptr], [y.ptr], [16], x8.ptr, 512, gate_up=True,
                                            r=y.ptr)], Q4_0)
+    # exchange rules: a later input that overlaps an earlier output other than
+    # exactly, an output over its own stage's input, two outputs of one stage
+    # in one vector
+    W3 = _up(holo, synth.blocks(Q4_0, 512, 512, seed=6))
+    big = holo.DeviceBuffer(4 * 2048)
+    x512 = _up(holo, synth.normal(512, seed=7))
+    first = holo.stream_stage([W3.ptr], [big.ptr], [512], x512.ptr, 512)
+    with pytest.raises(holo.HoloError):  # reads from the middle of stage 0's output
+        holo.StreamPlan([first, holo.stream_stage([W3.ptr], [y.ptr], [16], big.ptr + 256, 512)], Q4_0)
+    with pytest.raises(holo.HoloError):  # reads past what stage 0 wrote
+        W4 = _up(holo, synth.blocks(Q4_0, 16, 1024, seed=8))
+        holo.StreamPlan([first, holo.stream_stage([W4.ptr], [y.ptr], [16], big.ptr, 1024)], Q4_0)
+    with pytest.raises(holo.HoloError):  # an output over its own input
+        holo.StreamPlan([holo.stream_stage([W3.ptr], [x512.ptr], [512], x512.ptr, 512)], Q4_0)
+    with pytest.raises(holo.HoloError):  # two outputs of one stage in one vector
+        holo.StreamPlan([holo.stream_stage([W3.ptr, W3.ptr], [big.ptr, big.ptr], [512, 512], x512.ptr, 512)], Q4_0)
+    ok = holo.StreamPlan([first, holo.stream_stage([W3.ptr], [y.ptr], [16], big.ptr, 512)], Q4_0)
+    ok.close()
     lib.cuda_sync()
