@@ -19,9 +19,9 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxSeg = 3;
 // Activations are held as xi = rint(x * kQmax / amax) per 32-value unit,
-// |xi| <= kQmax, split exactly into three signed bytes xi = 65536 h + 256 m + l
-// (x_convert); each plane's int8 dot is exact in int32.
-constexpr int kQmax = 127 * 65536;
+// |xi| <= kQmax (< 2^22), split exactly into three signed bytes
+// xi = 65536 h + 256 m + l (x_convert); each plane's int8 dot is exact in int32.
+constexpr int kQmax = 63 * 65536;
 
 // ---- wave reduction ----------------------------------------------------------
 
@@ -170,23 +170,29 @@ __device__ __forceinline__ void x_convert(const float4 v, int i, int units, void
         const float amax = octet_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         const float dx = amax * (1.0f / (float)kQmax);
         // kQmax/amax to within an ulp (v_rcp_f32; a correctly rounded divide is
-        // a dozen dependent instructions on the staging path): the clamp below
-        // keeps |xi| <= kQmax, and |x - dx*xi| stays within dx/2 plus an
-        // fp32 rounding of amax
+        // a dozen dependent instructions on the staging path): |x * inv| stays
+        // within kQmax + 1 < 2^22, and |x - dx*xi| within dx/2 plus an fp32
+        // rounding of amax
         const float inv = amax > 0.f ? (float)kQmax * __builtin_amdgcn_rcpf(amax) : 0.f;
-        int xi[4] = {(int)__builtin_rintf(v.x * inv), (int)__builtin_rintf(v.y * inv),
-                     (int)__builtin_rintf(v.z * inv), (int)__builtin_rintf(v.w * inv)};
-        int x1[4], x2[4];
+        // xi = rint(x * inv) in one fma: 1.5 * 2^23 + x * inv lies in
+        // [2^23, 2^24), where floats are the integers, so the fma rounds x * inv
+        // to nearest even and the float's bits are 0x4B400000 + xi.  w = xi +
+        // 0x808080 has bytes B0..B2 with xi = 65536 (B2-128) + 256 (B1-128) +
+        // (B0-128): the signed planes are the bytes of w with the top bit
+        // flipped.
+        uint32_t w[4];
+        const float xv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            xi[k] = min(max(xi[k], -kQmax), kQmax);
-            x1[k] = (xi[k] + 128) >> 8;  // xi = 256*x1 + l,  l = low byte (signed)
-            x2[k] = (x1[k] + 128) >> 8;  // x1 = 256*h  + m,  m = low byte (signed), h = x2
-        }
+        for (int k = 0; k < 4; k++)
+            w[k] = __float_as_uint(__builtin_fmaf(xv[k], inv, 12582912.0f)) - (0x4B400000u - 0x808080u);
+        const uint32_t p01 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);  // w0.b0 w1.b0 w0.b1 w1.b1
+        const uint32_t p23 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);  // w2.b0 w3.b0 w2.b1 w3.b1
+        const uint32_t r01 = __builtin_amdgcn_perm(w[1], w[0], 0x0c0c0602u);  // w0.b2 w1.b2 0 0
+        const uint32_t r23 = __builtin_amdgcn_perm(w[3], w[2], 0x0c0c0602u);  // w2.b2 w3.b2 0 0
         uint32_t *lq = (uint32_t *)((uint4 *)lds + u * 6);
-        lq[c] = pack4(x2[0], x2[1], x2[2], x2[3]);       // h plane
-        lq[8 + c] = pack4(x1[0], x1[1], x1[2], x1[3]);   // m plane
-        lq[16 + c] = pack4(xi[0], xi[1], xi[2], xi[3]);  // l plane
+        lq[c] = __builtin_amdgcn_perm(r23, r01, 0x05040100u) ^ 0x80808080u;       // h plane
+        lq[8 + c] = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;   // m plane
+        lq[16 + c] = __builtin_amdgcn_perm(p23, p01, 0x05040100u) ^ 0x80808080u;  // l plane
         // the MFMA path folds Q4_0's -8 into the stored sum
         const float s2 = (XM == XM_MFMA && FMT == FMT_Q4_0) ? -8.0f * sx : sx;
         if (c == 0) ((float2 *)((uint4 *)lds + units * 6))[u] = make_float2(dx, s2);
