@@ -91,12 +91,21 @@ __device__ __forceinline__ float octet_sum(float v)
     v += dpp_get<0x141>(v);  // row_half_mirror: lane i <- lane 7-i of the octet
     return v;
 }
-__device__ __forceinline__ float octet_max(float v)
+// Maximum of non-negative floats over the octet, compared as their bit
+// patterns (which order like the values): v_max_u32 takes the DPP operand
+// directly, where fmaxf would first canonicalise it.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_get_u(uint32_t v)
 {
-    v = fmaxf(v, dpp_get<0xB1>(v));
-    v = fmaxf(v, dpp_get<0x4E>(v));
-    v = fmaxf(v, dpp_get<0x141>(v));
-    return v;
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float octet_max_nonneg(float f)
+{
+    uint32_t v = __float_as_uint(f);
+    v = max(v, dpp_get_u<0xB1>(v));
+    v = max(v, dpp_get_u<0x4E>(v));
+    v = max(v, dpp_get_u<0x141>(v));
+    return __uint_as_float(v);
 }
 
 // Packs byte 0 of four ints into one dword (little-endian order a, b, c, d).
@@ -167,7 +176,7 @@ __device__ __forceinline__ void x_convert(const float4 v, int i, int units, void
         lx[u * 8 + (c ^ (u & 7))] = v;
         if (c == 0) ((float *)(lx + units * 8))[u] = sx;
     } else {
-        const float amax = octet_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        const float amax = octet_max_nonneg(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         const float dx = amax * (1.0f / (float)kQmax);
         // kQmax/amax to within an ulp (v_rcp_f32; a correctly rounded divide is
         // a dozen dependent instructions on the staging path): |x * inv| stays
