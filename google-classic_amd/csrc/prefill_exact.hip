@@ -280,7 +280,9 @@ __device__ __forceinline__ v16f mfma16(v8h a, v8h b, v16f c)
 // B[8*(l/32)+t][l%32], t = 0..7; D[i][j] lands in lane j + 32*((i/4)%2),
 // register (i%4) + 4*(i/8).  A lane's 16 outputs share one column n, so a
 // block's scale is one value per lane.
-template <int WF, int WM, int WN, int S, int OCC>
+// RD: stages of global loads in flight in registers (a ring), so each
+// stage's loads have RD - 1 stages of products to land behind.
+template <int WF, int WM, int WN, int S, int OCC, int RD>
 __global__ __launch_bounds__(256, OCC) void gemm_exact_k(ExactArgs a)
 {
     using G = XGeo<WM, WN, S>;
@@ -386,15 +388,29 @@ __global__ __launch_bounds__(256, OCC) void gemm_exact_k(ExactArgs a)
         }
     };
 
-    XStage<WF, WM, WN, S> st;
-    st.fetch(a, w, tid, m0, n0, 0);
-    st.stash(lds, tid);
+    // Ring of RD register stages: set d holds stage k with k % RD == d.
+    // Stages past the last block re-read the last one (fetch clamps every
+    // index), so every slot issues the same loads and the loop has one exit,
+    // at its latch, with a trip count known up front: the compiler's wait
+    // before each stash is then exactly that stage's own loads.
+    XStage<WF, WM, WN, S> st[RD];
+#pragma unroll
+    for (int d = 0; d < RD; d++) st[d].fetch(a, w, tid, m0, n0, d * S);
+    st[0].stash(lds, tid);
+    st[0].fetch(a, w, tid, m0, n0, RD * S);
     __syncthreads();
-    for (int k = 0; k < nst; k++) {
-        if (k + 1 < nst) st.fetch(a, w, tid, m0, n0, (k + 1) * S);
-        compute(k & 1, k * S);
-        if (k + 1 < nst) st.stash(lds + ((k + 1) & 1) * G::STAGE, tid);
-        __syncthreads();
+    const int rounds = (nst + RD - 1) / RD;
+    for (int q = 0; q < rounds; q++) {
+#pragma unroll
+        for (int d = 0; d < RD; d++) {
+            const int k = q * RD + d;  // compute(k) skips blocks past nb
+            compute(k & 1, k * S);
+            // stage k + 1 (register set (d + 1) % RD) into the other buffer,
+            // then that set fetches stage k + 1 + RD
+            st[(d + 1) % RD].stash(lds + ((k + 1) & 1) * G::STAGE, tid);
+            st[(d + 1) % RD].fetch(a, w, tid, m0, n0, (k + 1 + RD) * S);
+            __syncthreads();
+        }
     }
 
 #pragma unroll
@@ -494,13 +510,13 @@ __global__ __launch_bounds__(256) void q6_k_int_panel_k(_Float16 *__restrict__ y
     }
 }
 
-template <int WF, int WM, int WN, int S, int OCC>
+template <int WF, int WM, int WN, int S, int OCC, int RD>
 void launch_exact(ExactArgs a)
 {
     using G = XGeo<WM, WN, S>;
     a.ntm = (a.M + G::TM - 1) / G::TM;
     a.tiles = a.ntm * ((a.N + G::TN - 1) / G::TN);
-    auto kern = gemm_exact_k<WF, WM, WN, S, OCC>;
+    auto kern = gemm_exact_k<WF, WM, WN, S, OCC, RD>;
     static bool attr = false;
     if (!attr) {
         HOLO_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS));
@@ -514,6 +530,11 @@ void launch_exact(ExactArgs a)
     HOLO_LAUNCH_CHECK();
 }
 
+// Register stages in flight: two take 512x11008x4096 from 191 to 167 us and
+// 512x4096x11008 from 228 to 182 us; three or four measured the same, and at
+// four the Q8_0, Q4_K and panel variants of the 128 x 128 tile spill.
+constexpr int kExactRing = 2;
+
 // 128 x 128 workgroup tiles (64 x 64 per wave, one block per stage) when there
 // are at least as many as CUs; otherwise 64 x 64 (32 x 32 per wave, two
 // blocks per stage) for four times the workgroups.
@@ -521,8 +542,8 @@ template <int WF>
 void launch_exact_for(const ExactArgs &a)
 {
     const long tiles128 = (long)((a.M + 127) / 128) * ((a.N + 127) / 128);
-    if (tiles128 >= num_cus()) launch_exact<WF, 2, 2, 1, 2>(a);
-    else launch_exact<WF, 1, 1, 2, 2>(a);
+    if (tiles128 >= num_cus()) launch_exact<WF, 2, 2, 1, 2, kExactRing>(a);
+    else launch_exact<WF, 1, 1, 2, 2, kExactRing>(a);
 }
 
 int exact_kind(int type)
