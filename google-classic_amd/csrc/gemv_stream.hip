@@ -4,10 +4,13 @@
 //
 // The reference issues one launch per matrix and token (the decode loop of
 // src/ai/llm_cuda.c:604-918; kernels cuda_ops.cu:618-676, 976-1060); the
-// results here are those of the separate GEMV calls (the MFMA path of
-// gemv.hip: 24-bit activations in three int8 planes, exact int32 block dots,
-// fp32 accumulation), with the rms_norm of the stage's input folded into its
-// staging and the residual add into its stores.
+// results here are those of separate GEMVs (int8 planes of the activations
+// in 22-bit fixed point, exact int32 block dots, fp32 accumulation), with
+// the rms_norm of the stage's input folded into its staging (or into the
+// output scale, below) and the residual add into its stores.  The planes'
+// scale runs per 16 activations (two per 32-weight block, against one in the
+// separate GEMV kernels), so a 16-row tile of outputs owns whole scale
+// groups of the next stage's input.
 //
 // Why one launch: a GEMV launch pays its ramp (dispatch, activation staging,
 // the first HBM round trip of its weights) and its tail (the slowest
@@ -24,7 +27,10 @@
 //                   segment, as the MFMA GEMV), dots on v_mfma_i32_16x16x64_i8,
 //                   one partial per row and tile into LDS; it never stores to
 //                   global memory, so its vector-memory counter holds only
-//                   loads and each item's wait is exact.
+//                   loads and each item's wait is exact.  A tile is 16 output
+//                   rows: 16 rows of the matrices (plain), or 16 gate and the
+//                   same 16 up rows (gate/up: a gate item and an up item per
+//                   segment).
 //   control wave    at a stage's end: sums the 8 partials of each of the
 //                   workgroup's rows (64 rows at a time, one per lane), applies
 //                   the epilogue (silu(g)*u, or r + acc), stores the outputs,
@@ -36,23 +42,28 @@
 // (tag << 32 | value bits) with a single agent-scope store, into the plan's
 // exchange buffer of that output vector.  The tag names the launch and the
 // stage (base + s + 1, base = launch count * (stages + 1)), so a word is
-// either this stage's value or visibly stale.  A consumer copies the words
-// of its whole input into LDS (device-coherent global_load_lds), checks every
-// tag and copies again only the 1 KB pieces that are not yet current, until
-// all are.  Value and tag travel in one single-copy-atomic 64-bit store, so a
-// current tag implies the current value: no fence, no store-completion wait
-// and no arrival counter sit between a producer's epilogue and its
-// consumers.  The launch count advances when the last workgroup of a launch
-// ends (a counter in the plan), so the next launch's tags differ from every
-// word this launch left behind.
+// either this stage's value or visibly stale.  When a later stage is the
+// designated reader of the output (the first stage that reads it as x), the
+// producer also stores, per 16 outputs, a plane record: the 16 values
+// already in the reader's int8 planes (times the reader's norm weight),
+// their scale and sums, 16 exchange words.  The reader then only copies
+// words into place, instead of every CU converting the whole vector.  A
+// consumer copies the words of its whole input into LDS (device-coherent
+// global_load_lds), checks every tag and copies again until all are current.
+// Value and tag travel in one single-copy-atomic 64-bit store, so a current
+// tag implies the current value: no fence, no store-completion wait and no
+// arrival counter sit between a producer's epilogue and its consumers.  The
+// launch count advances when the last workgroup of a launch ends (a counter
+// in the plan), so the next launch's tags differ from every word this launch
+// left behind.
 //
 // Stage boundary (3 workgroup barriers): A  all partials of stage s in LDS;
 // the control wave stores, then gathers the input of stage s+1 (and its norm
 // weight) into LDS, in the space of the compute waves' item stages, which are
-// idle until C; B  the input is in LDS; all waves convert it (rms_norm if
-// asked, then the int8 planes); C  compute resumes.  The compute waves never
-// load activations, so nothing but their own weight items counts against
-// their vector-memory counter.
+// idle until C; B  the input is in LDS; all waves place the plane records (or
+// convert fp32 input: rms_norm if asked, then the int8 planes); C  compute
+// resumes.  The compute waves never load activations, so nothing but their
+// own weight items counts against their vector-memory counter.
 #include "gemv_mfma.h"
 
 #include <hip/hip_ext.h>
@@ -64,11 +75,17 @@ namespace holo {
 
 namespace {
 
-constexpr int kNCW = 8;                     // compute waves
+constexpr int kNCW = 8;                      // compute waves
 constexpr int kStreamThreads = 64 * (kNCW + 1);
-constexpr int kStreamMaxTiles = 16;         // tiles of one stage per workgroup
+constexpr int kStreamMaxTiles = 16;          // tiles (16 output rows) of one stage per workgroup
 constexpr uint32_t kStreamPolls = 1u << 18;  // bounded exchange wait (~0.3 s)
-constexpr int kStreamMaxChunks = 192;        // 1 KB exchange pieces of one input (in_dim <= 24576)
+constexpr int kRecWords = 16;                // exchange words of a plane record (16 values)
+
+// Staged activations of a stage in LDS, per 32-value unit u: the three int8
+// planes (96 bytes at 96 u, as the MFMA GEMV stages them) and, at 96 units +
+// 16 u, the unit's scales {dx of values 0-15, dx of values 16-31, sum of
+// values 0-15, sum of values 16-31}.
+constexpr int kUnitLds = 96 + 16;
 
 // One stage of the plan, in device memory (read with scalar loads).
 struct StreamStage {
@@ -82,13 +99,18 @@ struct StreamStage {
     int mode;             // MODE_PLAIN / MODE_GATEUP
     int units;            // 32-weight units per row
     int G;                // 16-unit segments per row
-    int P;                // item slots per compute wave per tile: ceil(G / kNCW)
-    int total_rows;       // rows of all matrices (plain) or of one (gate/up)
+    int NI;               // items per tile: G (plain), 2 G (gate/up: gate items, then up items)
+    int P;                // item slots per compute wave per tile: ceil(NI / kNCW)
+    int total_rows;       // output rows (plain: of all matrices; gate/up: of h)
     int full_tiles;       // tiles dealt round robin to every workgroup
-    int rem_start;        // first row of the remainder
+    int rem_start;        // first row of the remainder (dealt in 16-row tiles)
     float eps;
+    uint64_t dup;         // gate/up: up base minus gate base
     uint64_t lly[3];      // exchange words of the outputs (gate/up: lly[0])
+    uint64_t llp[3];      // plane records of an output for its designated reader, or 0
+    uint64_t pnw[3];      // that reader's norm weight, or 0
     uint64_t llx;         // exchange words of x when an earlier stage wrote it, else 0
+    uint64_t lpx;         // plane records of x when this stage is their designated reader, else 0
     uint64_t llr;         // exchange words of r when an earlier stage wrote it, else 0
     int xsrc, rsrc;       // the stage that wrote x / r last before this one
 };
@@ -108,9 +130,11 @@ struct StreamArgs {
     uint32_t *flag;       // set when an exchange wait gives up
     uint32_t zero_off;    // LDS: zero region (after the largest stage's planes)
     uint32_t stage_off;   // LDS: the compute waves' item stages
-    uint32_t tpart_off;   // LDS: tile partials [kStreamMaxTiles][kNCW][16]
-    uint32_t red_off;     // LDS: norm reduction [16]
-    uint32_t xbuf_off;    // LDS: x of the next stage as fp32, then its norm weight
+    uint32_t tpart_off;   // LDS: tile partials [kStreamMaxTiles][kNCW][32]
+    uint32_t red_off;     // LDS: reductions, tag base, stale-piece masks [kRedWords]
+    uint32_t pack_off;    // LDS: the control wave's plane bytes [64]
+    uint32_t ss_off;      // LDS: sums of squares of a plane-record input [2 units]
+    uint32_t xbuf_off;    // LDS: x of the next stage (fp32 or words), then its norm weight
 };
 
 __device__ __forceinline__ cstage &stage_at(const StreamArgs &a, int s) { return ((cstage *)(uintptr_t)a.table)[s]; }
@@ -129,25 +153,33 @@ __device__ __forceinline__ float unif(float v)
     return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
+// Remainder rows dealt in 16-row tiles: workgroup b gets remainder tiles
+// [b * nt / W, (b + 1) * nt / W) of the nt = ceil(rem / 16), at most one.
+__host__ __device__ inline void rem_rows(int total, int rem_start, uint32_t W, uint32_t b, int &e0, int &e1)
+{
+    const uint32_t nt = (uint32_t)(total - rem_start + 15) / 16u;
+    e0 = rem_start + 16 * (int)((b * nt) / W);
+    e1 = min(rem_start + 16 * (int)(((b + 1) * nt) / W), total);
+}
+
 // This workgroup's tiles of a stage: F full tiles dealt round robin (tile k
-// = global tile k*W + b), then an even share of the remaining rows as one
-// short tile.
+// = global tile k*W + b), then at most one remainder tile.
 struct Tiles {
-    int F, ex0, ex1, n, TR;
+    int F, ex0, ex1, n;
     __device__ __forceinline__ void init(cstage &s, uint32_t W, uint32_t b)
     {
-        TR = uni(s.mode == MODE_GATEUP ? 8 : 16);
         F = uni(s.full_tiles);
-        const uint32_t rem = (uint32_t)(s.total_rows - s.rem_start);
-        ex0 = uni(s.rem_start + (int)((b * rem) / W));
-        ex1 = uni(s.rem_start + (int)(((b + 1) * rem) / W));
+        int e0, e1;
+        rem_rows(s.total_rows, s.rem_start, W, b, e0, e1);
+        ex0 = uni(e0);
+        ex1 = uni(e1);
         n = uni(F + (ex1 > ex0 ? 1 : 0));
     }
     __device__ __forceinline__ void rows(int k, uint32_t W, uint32_t b, int &row0, int &rend) const
     {
         if (k < F) {
-            row0 = (k * (int)W + (int)b) * TR;
-            rend = row0 + TR;
+            row0 = (k * (int)W + (int)b) * 16;
+            rend = row0 + 16;
         } else {
             row0 = ex0;
             rend = ex1;
@@ -164,21 +196,21 @@ __device__ __forceinline__ void split_row(cstage &s, int v, int &m, int &r)
 }
 
 // A compute wave's walk over its item slots, in order: stage s, tile k of
-// this workgroup's n tiles, slot p < P of the tile (segment cw + kNCW * p).
+// this workgroup's n tiles, slot p < P of the tile (item cw + kNCW * p).
 // Tracked incrementally (no division per slot); the stage constants are
 // read once per stage, into scalar registers.  A stage with no tile for this
 // workgroup is skipped; s = nstages is past the end, where the issue fields
 // are those of the last stage (the dummy loads read its first item).
 struct Walk {
     int s, k, p;
-    int n, P, G, F, TR, units;
+    int n, P, G, NI, F, units;
     int row0, rend, ex0, ex1;
 
     __device__ __forceinline__ void set_tile(uint32_t W, uint32_t b)
     {
         if (k < F) {
-            row0 = uni((k * (int)W + (int)b) * TR);
-            rend = row0 + TR;
+            row0 = uni((k * (int)W + (int)b) * 16);
+            rend = row0 + 16;
         } else {
             row0 = ex0;
             rend = ex1;
@@ -188,19 +220,15 @@ struct Walk {
     {
         // locals, assigned to the members once: a loop over the members
         // themselves keeps the struct in scratch memory
-        int ss = stage, tr = 16, f = 0, e0 = 0, e1 = 0, nn = 0;
+        int ss = stage, f = 0, e0 = 0, e1 = 0, nn = 0;
         for (; ss < a.nstages; ss++) {
             cstage &st = stage_at(a, ss);
-            tr = st.mode == MODE_GATEUP ? 8 : 16;
             f = st.full_tiles;
-            const uint32_t rem = (uint32_t)(st.total_rows - st.rem_start);
-            e0 = st.rem_start + (int)((b * rem) / W);
-            e1 = st.rem_start + (int)(((b + 1) * rem) / W);
+            rem_rows(st.total_rows, st.rem_start, W, b, e0, e1);
             nn = f + (e1 > e0 ? 1 : 0);
             if (nn > 0) break;
         }
         s = uni(ss);
-        TR = uni(tr);
         F = uni(f);
         ex0 = uni(e0);
         ex1 = uni(e1);
@@ -209,6 +237,7 @@ struct Walk {
         p = 0;
         cstage &st = stage_at(a, s < a.nstages ? s : a.nstages - 1);
         G = uni(st.G);
+        NI = uni(st.NI);
         units = uni(st.units);
         if (s >= a.nstages) {
             // past the last stage: the (unused) item 0 of the last stage's row 0
@@ -239,14 +268,13 @@ struct Walk {
 };
 
 // The issue side of a compute wave: every item load is a global load of
-// piece i at rowaddr[i] + col + the 16-unit segment's offset, one code path
-// for every tile and segment.  rowaddr (per tile) is the lane's row: its
-// piece row clamped to the tile's last row (short tiles re-read that row), in
-// the matrix the row falls in (rows of several matrices, or 8 gate + 8 up
-// rows).  The column part is the piece's 16-byte column (colF), or in an
-// 8-unit last segment the column taken modulo half the segment (item_piece's
-// half mapping: the missing half re-reads the first), so no load leaves the
-// row.
+// piece i at rowaddr[i] + col + the segment's offset (+ the up matrix's
+// offset for an up item), one code path for every tile and segment.  rowaddr
+// (per tile) is the lane's row: its piece row clamped to the tile's last row
+// (short tiles re-read that row), in the matrix the row falls in.  The
+// column part is the piece's 16-byte column (colF), or in an 8-unit last
+// segment the column taken modulo half the segment (item_piece's half
+// mapping: the missing half re-reads the first), so no load leaves the row.
 template <int FMT>
 struct Issuer {
     uint32_t colF[Geo<FMT>::NL];
@@ -260,22 +288,16 @@ struct Issuer {
     __device__ __forceinline__ void set_tile(cstage &st, const Walk &c, int lane)
     {
         const uint64_t rb = uni64((uint64_t)st.row_bytes);
-        const bool gu = uni(st.mode) == MODE_GATEUP;
         const uint64_t w0 = uni64(st.W[0]), w1 = uni64(st.W[1]), w2 = uni64(st.W[2]);
         const int re0 = uni(st.row_end[0]), re1 = uni(st.row_end[1]);
         const int row0 = c.row0, last = c.rend - 1;
 #pragma unroll
         for (int i = 0; i < Geo<FMT>::NL; i++) {
             const int pr = item_piece(FMT, 64 * i + lane, false).row;
-            if (gu) {
-                const int v = min(row0 + (pr & 7), last);
-                rowaddr[i] = ((pr >> 3) ? w1 : w0) + (uint64_t)v * rb;
-            } else {
-                const int v = min(row0 + pr, last);
-                const int a1 = v >= re0, a2 = v >= re1;
-                const int r = v - (a2 ? re1 : a1 ? re0 : 0);
-                rowaddr[i] = (a2 ? w2 : a1 ? w1 : w0) + (uint64_t)r * rb;
-            }
+            const int v = min(row0 + pr, last);
+            const int a1 = v >= re0, a2 = v >= re1;  // gate/up: row_end = {INT_MAX, INT_MAX}
+            const int r = v - (a2 ? re1 : a1 ? re0 : 0);
+            rowaddr[i] = (a2 ? w2 : a1 ? w1 : w0) + (uint64_t)r * rb;
         }
     }
 };
@@ -283,20 +305,22 @@ struct Issuer {
 // Item of the issue walk's slot into registers: NL 16-byte loads per lane,
 // the kernel's only weight loads.  Every slot issues exactly NL loads from
 // this one site, so the compiler's vmcnt wait for any slot is exact: a slot
-// with no segment for this wave re-reads the tile's last segment, and a slot
-// past the last stage re-reads item 0 of the last stage.  The data of such
-// slots is never used.
+// with no item for this wave re-reads the tile's last item, and a slot past
+// the last stage re-reads item 0 of the last stage.  The data of such slots
+// is never used.
 template <int FMT>
-__device__ __forceinline__ void stream_issue(Raw2<FMT> &buf, const Walk &c, const Issuer<FMT> &is, int cw)
+__device__ __forceinline__ void stream_issue(Raw2<FMT> &buf, const Walk &c, const Issuer<FMT> &is, cstage &st, int cw)
 {
     using GE = Geo<FMT>;
-    const int seg = uni(min(cw + kNCW * c.p, c.G - 1));
+    const int item = uni(min(cw + kNCW * c.p, c.NI - 1));
+    const bool up = item >= c.G;  // gate/up: items G..2G-1 are the up matrix's
+    const int seg = item - (up ? c.G : 0);
     const bool half = 16 * seg + 16 > c.units;
-    const uint32_t segoff = (uint32_t)seg * GE::SEGB;
+    const uint64_t off = (uint64_t)seg * GE::SEGB + (up ? uni64(st.dup) : 0);
 #pragma unroll
     for (int i = 0; i < GE::NL; i++) {
         const uint32_t col = half && is.colF[i] >= 8u * GE::PR ? is.colF[i] - 8u * GE::PR : is.colF[i];
-        buf.v[i] = __builtin_nontemporal_load((gu32x4a *)(is.rowaddr[i] + (col + segoff)));
+        buf.v[i] = __builtin_nontemporal_load((gu32x4a *)(is.rowaddr[i] + (off + col)));
     }
 }
 
@@ -316,8 +340,141 @@ __device__ __forceinline__ void stream_stage_write(const Raw2<FMT> &b, uint8_t *
     }
 }
 
+// ---- unit dots with two activation scales per 32-weight unit ------------------------
+//
+// As item_unit of the MFMA GEMV, but the unit's weights 0-15 and 16-31 meet
+// activation planes of separate scales: the two MFMAs stay apart and the
+// epilogue is, per unit (d = block scale, S = 65536 Sh + 256 Sm + Sl per half,
+// {dx0, dx1, s0, s1} the unit's staged scales and half sums):
+//   Q4_0  d * (dx0*S0 + dx1*S1 - 8 (s0 + s1))
+//   Q4_K  (d*sc) * (dx0*S0 + dx1*S1) - (dmin*m) * (s0 + s1)
+template <int T, int FMT>
+__device__ __forceinline__ void item_unit2(float &acc, const Chunk<FMT> &c, const uint8_t *ldsb, uint32_t abase,
+                                           uint32_t sbase, int skip, bool tail, float dk, float mk, uint32_t sc,
+                                           uint32_t mn)
+{
+    const v4i a0 = *(const v4i *)(ldsb + abase + 96 * T);
+    const v4i a1 = *(const v4i *)(ldsb + abase + 96 * T + 16);
+    const float4 xs = *(const float4 *)(ldsb + sbase + 16 * T);
+    v4i lo, hi;
+    uint32_t dbits;
+    chunk_unit<T, FMT>(c, lo, hi, dbits);
+    const v4i zero = {0, 0, 0, 0};
+    const v4i s0 = mfma_i8(a0, lo, zero), s1 = mfma_i8(a1, hi, zero);
+    // |Sh| <= 16*128*127, so 256*Sh + Sm is exact in int32
+    const float S0 = fmaf(256.0f, (float)((s0[0] << 8) + s0[1]), (float)s0[2]);
+    const float S1 = fmaf(256.0f, (float)((s1[0] << 8) + s1[1]), (float)s1[2]);
+    const float dS = fmaf(xs.x, S0, xs.y * S1);
+    const float sx = xs.z + xs.w;
+    if constexpr (FMT == FMT_Q4_K) {
+        float dsc = dk * (float)((sc >> (8 * T)) & 0xFFu);
+        float dmn = mk * (float)((mn >> (8 * T)) & 0xFFu);
+        if (tail && T < skip) dsc = dmn = 0.f;
+        acc = fmaf(dsc, dS, fmaf(-dmn, sx, acc));
+    } else {
+        float d = half_bits_to_float(dbits);
+        if (tail && T < skip) d = 0.f;
+        acc = fmaf(d, fmaf(-8.0f, sx, dS), acc);
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ float item_dot2(const Chunk<FMT> &c, const uint8_t *ldsb, uint32_t abase, uint32_t sbase,
+                                           uint32_t cs, int skip, bool tail)
+{
+    float acc = 0.f;
+    float dk = 0.f, mk = 0.f;
+    uint32_t sc = 0, mn = 0;
+    if constexpr (FMT == FMT_Q4_K) {
+        dk = half_bits_to_float(c.h.x);
+        mk = half_bits_to_float(c.h.x >> 16);
+        q4_k_half_scales(c.h, (cs >> 2) & 1u, sc, mn);
+    }
+    item_unit2<0, FMT>(acc, c, ldsb, abase, sbase, skip, tail, dk, mk, sc, mn);
+    item_unit2<1, FMT>(acc, c, ldsb, abase, sbase, skip, tail, dk, mk, sc, mn);
+    item_unit2<2, FMT>(acc, c, ldsb, abase, sbase, skip, tail, dk, mk, sc, mn);
+    item_unit2<3, FMT>(acc, c, ldsb, abase, sbase, skip, tail, dk, mk, sc, mn);
+    return acc;
+}
+
+// ---- activations into planes ------------------------------------------------------------
+
+// Sum / maximum of non-negative floats over the 4 lanes of an aligned quad
+// and over the 16 lanes of a row (all lanes active); every lane gets the result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float quad_sum(float v)
+{
+    v += dpp_f<0xB1>(v);
+    return v + dpp_f<0x4E>(v);
+}
+__device__ __forceinline__ float quad_max_nonneg(float f)
+{
+    uint32_t v = __float_as_uint(f);
+    v = max(v, dpp_u<0xB1>(v));
+    return __uint_as_float(max(v, dpp_u<0x4E>(v)));
+}
+__device__ __forceinline__ float row16_sum(float v)
+{
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    return v + dpp_f<0x140>(v);  // row_mirror
+}
+__device__ __forceinline__ float row16_max_nonneg(float f)
+{
+    uint32_t v = __float_as_uint(f);
+    v = max(v, dpp_u<0xB1>(v));
+    v = max(v, dpp_u<0x4E>(v));
+    v = max(v, dpp_u<0x141>(v));
+    return __uint_as_float(max(v, dpp_u<0x140>(v)));
+}
+
+// xi + 0x808080 for xi = rint(x * inv), |x * inv| < 2^22 (x_convert's rounding
+// identity: the planes are the three low bytes with the top bit flipped).
+__device__ __forceinline__ uint32_t biased_xi(float x, float inv)
+{
+    return __float_as_uint(__builtin_fmaf(x, inv, 12582912.0f)) - (0x4B400000u - 0x808080u);
+}
+
+// Chunk i (4 values: unit i >> 3, chunk c = i & 7) into the planes and the
+// unit's scales.  The 4 chunks of a 16-value half sit in an aligned lane
+// quad (the caller's i = tid + stride*k keeps quads aligned).
+__device__ __forceinline__ void x_convert2(const float4 v, int i, int units, uint8_t *ldsb)
+{
+    const int u = i >> 3, c = i & 7;
+    const float amax = quad_max_nonneg(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    const float sx = quad_sum((v.x + v.y) + (v.z + v.w));
+    const float dx = amax * (1.0f / (float)kQmax);
+    const float inv = amax > 0.f ? (float)kQmax * __builtin_amdgcn_rcpf(amax) : 0.f;
+    const uint32_t w0 = biased_xi(v.x, inv), w1 = biased_xi(v.y, inv), w2 = biased_xi(v.z, inv),
+                   w3 = biased_xi(v.w, inv);
+    const uint32_t p01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);
+    const uint32_t p23 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
+    const uint32_t r01 = __builtin_amdgcn_perm(w1, w0, 0x0c0c0602u);
+    const uint32_t r23 = __builtin_amdgcn_perm(w3, w2, 0x0c0c0602u);
+    uint32_t *lq = (uint32_t *)(ldsb + 96 * u);
+    lq[c] = __builtin_amdgcn_perm(r23, r01, 0x05040100u) ^ 0x80808080u;       // h plane
+    lq[8 + c] = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;   // m plane
+    lq[16 + c] = __builtin_amdgcn_perm(p23, p01, 0x05040100u) ^ 0x80808080u;  // l plane
+    if ((c & 3) == 0) {
+        float *scl = (float *)(ldsb + 96 * units + 16 * u);
+        scl[c >> 2] = dx;
+        scl[2 + (c >> 2)] = sx;
+    }
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void gvoid;
+typedef __attribute__((address_space(1))) uint64_t gword;
 
 // The input of a stage that no earlier stage of the plan wrote (plain fp32,
 // units * 32 floats), by one wave: each global_load_lds_dwordx4 moves 64 lanes
@@ -338,6 +495,21 @@ __device__ __forceinline__ void stream_fetch_norm(cstage &st, uint8_t *wbuf, int
     const float *w = (const float *)uni64(st.nw);
     for (int j = 0; j < n; j++)
         __builtin_amdgcn_global_load_lds((gvoid *)(w + 256 * j + 4 * lane), (lds_void *)(wbuf + 1024 * j), 16, 0, 0);
+}
+
+// Exchange words of a stage input (the fp32 words, or the plane records:
+// either way 8 bytes per input value) into LDS, 1 KB pieces of 128 words,
+// device-coherent (sc1: never answered from a line this XCD's L2 held
+// before another XCD's store).  The tags are checked while the words are put
+// in place (stream_stage_in), which copies again what was not current.
+__device__ __forceinline__ void stream_fetch_words(cstage &st, uint8_t *xbuf, int lane)
+{
+    const int units = uni(st.units), nch = units / 4;  // 128 words = 4 units per piece
+    const uint64_t lp = uni64(st.lpx);
+    const uint8_t *src = (const uint8_t *)(lp ? lp : uni64(st.llx));
+    for (int j = 0; j < nch; j++)
+        __builtin_amdgcn_global_load_lds((gvoid *)(src + 1024 * j + 16 * lane), (lds_void *)(xbuf + 1024 * j), 16, 0,
+                                         kDeviceScope);
 }
 
 // Waits until every workgroup has stored its rows of the stage with tag
@@ -368,20 +540,6 @@ __device__ __forceinline__ void stream_wait_done(const uint32_t *done, uint32_t 
     }
 }
 
-// The input of a stage that an earlier stage wrote: its exchange words
-// (8 bytes per value) into LDS, 1 KB pieces of 128 words, device-coherent
-// (sc1: never answered from a line this XCD's L2 held before another XCD's
-// store).  The tags are checked while the words are converted
-// (stream_convert_x); stream_stage_in copies again what was not current.
-__device__ __forceinline__ void stream_fetch_tagged(cstage &st, uint8_t *xbuf, int lane)
-{
-    const int units = uni(st.units), nch = units / 4;  // 128 words = 4 units per piece
-    const uint8_t *src = (const uint8_t *)uni64(st.llx);
-    for (int j = 0; j < nch; j++)
-        __builtin_amdgcn_global_load_lds((gvoid *)(src + 1024 * j + 16 * lane), (lds_void *)(xbuf + 1024 * j), 16, 0,
-                                         kDeviceScope);
-}
-
 // x value chunk i (4 values) of the staged input: plain fp32, or exchange
 // words (value, tag) pairs, whose tags must all be `tag` (else `bad`).
 __device__ __forceinline__ float4 staged_x4(const uint8_t *xbuf, int i, bool tagged, uint32_t tag, bool &bad)
@@ -394,30 +552,65 @@ __device__ __forceinline__ float4 staged_x4(const uint8_t *xbuf, int i, bool tag
     return *(const float4 *)(xbuf + 16 * i);
 }
 
-constexpr int kRedBad = 15;   // red[15]: a stale exchange word was staged
-constexpr int kRedBase = 14;  // red[14]: this launch's tag base, from the control wave
+constexpr int kRedBase = 14;   // red[14]: this launch's tag base, from the control wave
+constexpr int kRedMask = 16;   // red[16..31]: two stale-piece masks (1 KB pieces of the staged words)
+constexpr int kMaskWords = 8;  // pieces up to 256: in_dim up to 32768
+constexpr int kRedWords = kRedMask + 2 * kMaskWords;
 
-// The staged x in LDS into the int8 planes and {dx, c} pairs, by all threads;
-// with a norm weight, x * (1/sqrt(mean(x^2) + eps)) * w first (cuda_rms_norm's
-// formula, cuda_ops.cu:1479-1504), the 9 waves' sums of squares meeting in red.
-template <int FMT>
-__device__ __forceinline__ void stream_convert_x(cstage &st, uint8_t *ldsb, const uint8_t *xbuf, float *red,
-                                                 uint32_t tag)
+__device__ __forceinline__ bool piece_set(const uint32_t *m, int j) { return (m[j >> 5] >> (j & 31)) & 1u; }
+__device__ __forceinline__ void mark_piece(uint32_t *m, int j)
+{
+    __hip_atomic_fetch_or(m + (j >> 5), 1u << (j & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// The staged input of stage st into the planes and scales, by all threads.
+// A staged word whose tag is not `tag` marks its 1 KB piece in `stale`.
+//   plane records (st.lpx): 4 lanes per record g (16 values: unit g/2, half
+//     g&1), lane j of them takes words 4j..4j+3: for j < 3 the 4 dwords of
+//     plane j (one 16-byte store), for j = 3 the half's dx, its sum and its
+//     sum of squares (ss[g], for the output's norm scale).  With `only`, just
+//     the pieces marked there (the others are in place already).
+//   fp32 (plain or exchange words): converted as x_convert does, with
+//     x * (1/sqrt(mean(x^2) + eps)) * w first when the stage has a norm
+//     weight (cuda_rms_norm's formula, cuda_ops.cu:1479-1504), the 9 waves'
+//     sums of squares meeting in red; always the whole input.
+__device__ __forceinline__ void stream_convert_x(cstage &st, uint8_t *ldsb, const uint8_t *xbuf, float *red, float *ss,
+                                                 uint32_t tag, const uint32_t *only, uint32_t *stale)
 {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int units = uni(st.units), chunks = units * 8;
+    const int units = uni(st.units);
+    if (uni64(st.lpx)) {
+        const int nq = units * 8;
+        for (int q = tid; q < nq; q += kStreamThreads) {
+            if (only && !piece_set(only, q >> 5)) continue;
+            const uint4 a = *(const uint4 *)(xbuf + 32 * q), c = *(const uint4 *)(xbuf + 32 * q + 16);
+            if ((a.y != tag) | (a.w != tag) | (c.y != tag) | (c.w != tag)) mark_piece(stale, q >> 5);
+            const int g = q >> 2, j = q & 3, u = g >> 1, hf = g & 1;
+            if (j < 3) {
+                *(uint4 *)(ldsb + 96 * u + 32 * j + 16 * hf) = make_uint4(a.x, a.z, c.x, c.z);
+            } else {
+                uint32_t *scl = (uint32_t *)(ldsb + 96 * units + 16 * u);
+                scl[hf] = a.x;
+                scl[2 + hf] = a.z;
+                ((uint32_t *)ss)[g] = c.x;
+            }
+        }
+        return;
+    }
+    // (the norm's pass reads the same words as the conversion, which marks them)
+    const int chunks = units * 8;
     const bool norm = uni64(st.nw) != 0;
     const bool tagged = uni64(st.llx) != 0;
-    bool bad = false;
     float scale = 1.f;
+    bool bad = false;
     if (norm) {
-        float ss = 0.f;
+        float s2 = 0.f;
         for (int i = tid; i < chunks; i += kStreamThreads) {
             const float4 v = staged_x4(xbuf, i, tagged, tag, bad);
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            s2 += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
-        ss = wave_sum(ss);
-        if (lane == 0) red[wave] = ss;
+        s2 = wave_sum(s2);
+        if (lane == 0) red[wave] = s2;
         __syncthreads();
         float tot = 0.f;
 #pragma unroll
@@ -426,74 +619,101 @@ __device__ __forceinline__ void stream_convert_x(cstage &st, uint8_t *ldsb, cons
     }
     const float4 *wv = (const float4 *)(xbuf + units * (tagged ? 256 : 128));
     for (int i = tid; i < chunks; i += kStreamThreads) {
-        float4 v = staged_x4(xbuf, i, tagged, tag, bad);
+        bool b1 = false;
+        float4 v = staged_x4(xbuf, i, tagged, tag, b1);
+        if (b1) mark_piece(stale, i >> 5);
         if (norm) {
             const float4 w4 = wv[i];
             v = make_float4(v.x * scale * w4.x, v.y * scale * w4.y, v.z * scale * w4.z, v.w * scale * w4.w);
         }
-        x_convert<FMT, XM_MFMA>(v, i, units, (void *)ldsb);
+        x_convert2(v, i, units, ldsb);
     }
-    if (tagged && __ballot(bad) != 0 && lane == 0) ((uint32_t *)red)[kRedBad] = 1u;
 }
 
-// After the input of stage `st` was staged (B): all waves convert it (C), and
-// while a stale exchange word was among it, the control wave copies the words
-// again and all waves convert again.  Every wave takes the same rounds (each
-// reads the flag after the same barrier), so the barrier counts agree.  After
-// kStreamPolls rounds the wait gives up and sets the plan's flag.
-template <int FMT>
-__device__ __forceinline__ void stream_stage_in(cstage &st, uint8_t *ldsb, uint8_t *xbuf, float *red, uint32_t base,
-                                                uint32_t *flag, bool control, int lane)
+// Copies again the 1 KB pieces of the staged words marked in `m` (control
+// wave).
+__device__ __forceinline__ void stream_refetch(cstage &st, uint8_t *xbuf, const uint32_t *m, int lane)
+{
+    const uint64_t lp = uni64(st.lpx);
+    const uint8_t *src = (const uint8_t *)(lp ? lp : uni64(st.llx));
+    for (int w = 0; w < kMaskWords; w++) {
+        uint32_t bits = (uint32_t)uni((int)m[w]);
+        while (bits) {
+            const int j = 32 * w + __builtin_ctz(bits);
+            bits &= bits - 1u;
+            __builtin_amdgcn_global_load_lds((gvoid *)(src + 1024 * j + 16 * lane), (lds_void *)(xbuf + 1024 * j), 16,
+                                             0, kDeviceScope);
+        }
+    }
+}
+
+// After the input of stage `st` was staged (B): all waves place or convert it
+// (C); while pieces with stale exchange words remain, the control wave copies
+// those pieces again and all waves place them again (plane records: only
+// those pieces; fp32: the whole input, whose norm and planes depend on every
+// word).  Round r reads the marks of mask r&1 and sets those of the next; every
+// wave reads the same mask after the same barrier, so all take the same rounds
+// and the barrier counts agree.  After kStreamPolls rounds the wait gives up
+// and sets the plan's flag.  The control wave cleared mask 0 before B.
+__device__ __forceinline__ void stream_stage_in(cstage &st, uint8_t *ldsb, uint8_t *xbuf, float *red, float *ss,
+                                                uint32_t base, uint32_t *flag, bool control, int lane)
 {
     const uint32_t tag = base + (uint32_t)uni(st.xsrc) + 1u;
-    stream_convert_x<FMT>(st, ldsb, xbuf, red, tag);
+    uint32_t *mask = (uint32_t *)red + kRedMask;
+    stream_convert_x(st, ldsb, xbuf, red, ss, tag, nullptr, mask);
     __syncthreads();  // C
-    if (uni64(st.llx) == 0) return;
-    uint32_t *badp = (uint32_t *)red + kRedBad;
-    for (uint32_t round = 0; uni((int)*badp) != 0; round++) {
-        __syncthreads();  // every wave has read the flag
+    const bool records = uni64(st.lpx) != 0;
+    if (uni64(st.llx) == 0 && !records) return;
+    for (uint32_t round = 0;; round++) {
+        const uint32_t *cur = mask + kMaskWords * (round & 1u);
+        uint32_t *nxt = mask + kMaskWords * ((round + 1u) & 1u);
+        uint32_t any = 0;
+#pragma unroll
+        for (int w = 0; w < kMaskWords; w++) any |= cur[w];
+        if ((uint32_t)uni((int)any) == 0) break;
+        __syncthreads();  // every wave has read the mask
         if (control) {
-            if (lane == 0) *badp = 0u;
+            if (lane < kMaskWords) nxt[lane] = 0u;
             if (round == kStreamPolls) {
                 __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else {
-                __builtin_amdgcn_s_sleep(4);
-                stream_fetch_tagged(st, xbuf, lane);
+                __builtin_amdgcn_s_sleep(2);
+                stream_refetch(st, xbuf, cur, lane);
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             }
         }
         __syncthreads();  // B again
-        if (round < kStreamPolls) stream_convert_x<FMT>(st, ldsb, xbuf, red, tag);
+        if (round < kStreamPolls) stream_convert_x(st, ldsb, xbuf, red, ss, tag, records ? cur : nullptr, nxt);
         __syncthreads();  // C again
     }
 }
 
 // Row v of this workgroup's rows of a stage for lane `lane` in pass q: 64
-// rows a pass, tile k = q * (64 / TR) + lane / TR, row lane % TR of it.
+// rows a pass, tile k = 4 q + lane / 16, row lane % 16 of it.
 __device__ __forceinline__ bool own_row(const Tiles &t, int q, int lane, uint32_t W, uint32_t b, int &k, int &i,
                                         int &v)
 {
-    const int per = 64 / t.TR;
-    k = q * per + lane / t.TR;
-    i = lane % t.TR;
+    k = 4 * q + (lane >> 4);
+    i = lane & 15;
     int row0, rend;
     t.rows(k, W, b, row0, rend);
     v = row0 + i;
     return k < t.n && v < rend;
 }
 
-constexpr int kStreamPasses = kStreamMaxTiles * 16 / 64;  // passes of 64 rows over at most 16 tiles
+constexpr int kStreamPasses = kStreamMaxTiles / 4;  // passes of 64 rows over at most 16 tiles
 
 __device__ __forceinline__ uint64_t exchange_word(float v, uint32_t tag)
 {
     return ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v);
 }
+__device__ __forceinline__ uint64_t exchange_word_u(uint32_t v, uint32_t tag) { return ((uint64_t)tag << 32) | v; }
 
 // The residual rows r[v] of this workgroup's rows of stage s (plain stages
 // with r), one per lane and pass: exchange words when an earlier stage wrote
 // r (waited for like the input), else the caller's fp32 values.
-__device__ __forceinline__ void stream_residual(cstage &st, const Tiles &t, float (&rr)[kStreamPasses], uint32_t base,
-                                                uint32_t *flag, uint32_t W, uint32_t b, int lane)
+__device__ __forceinline__ void stream_prefetch_rr(cstage &st, const Tiles &t, float (&rr)[kStreamPasses],
+                                                   uint32_t base, uint32_t *flag, uint32_t W, uint32_t b, int lane)
 {
 #pragma unroll
     for (int q = 0; q < kStreamPasses; q++) rr[q] = 0.f;
@@ -510,9 +730,7 @@ __device__ __forceinline__ void stream_residual(cstage &st, const Tiles &t, floa
         }
         uint64_t w = 0;
         for (uint32_t polls = 0;; polls++) {
-            if (mine)
-                w = __hip_atomic_load((__attribute__((address_space(1))) uint64_t *)llr + v, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
+            if (mine) w = __hip_atomic_load((gword *)llr + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (__ballot(mine && (uint32_t)(w >> 32) != tag) == 0) break;
             if (polls == kStreamPolls) {
                 __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -524,43 +742,119 @@ __device__ __forceinline__ void stream_residual(cstage &st, const Tiles &t, floa
     }
 }
 
-// The control wave's stores of stage s: each of the workgroup's rows (one per
-// lane and pass), the 8 compute waves' partials summed in wave order; the
-// plain fp32 output and its exchange word.
-__device__ __forceinline__ void stream_epilogue(cstage &st, const Tiles &t, const float *tpart,
-                                                const float (&rr)[kStreamPasses], uint32_t tag, uint32_t W,
+
+// What the control wave's epilogue of stage s reads from global memory, read
+// while the stage still runs, one value per lane and pass:
+//   pw  the norm weight of the designated reader of the row's output, for
+//       the plane records (1 without one);
+//   rr  the residual rows (stream_prefetch_rr).
+// The wave waits for these loads here, so the epilogue issues no load: a
+// load there would wait (vmcnt) for the epilogue's own stores as well.
+__device__ __forceinline__ void stream_prefetch(cstage &st, const Tiles &t, float (&rr)[kStreamPasses],
+                                                float (&pw)[kStreamPasses], uint32_t base, uint32_t *flag, uint32_t W,
                                                 uint32_t b, int lane)
 {
-    typedef __attribute__((address_space(1))) uint64_t gword;
+    stream_prefetch_rr(st, t, rr, base, flag, W, b, lane);
+    const uint64_t p0 = uni64(st.llp[0]), p1 = uni64(st.llp[1]), p2 = uni64(st.llp[2]);
+    const uint64_t n0 = uni64(st.pnw[0]), n1 = uni64(st.pnw[1]), n2 = uni64(st.pnw[2]);
+    const bool gu = uni(st.mode) == MODE_GATEUP;
+#pragma unroll
+    for (int q = 0; q < kStreamPasses; q++) {
+        pw[q] = 1.f;
+        int k, i, v, m = 0, row;
+        const bool mine = own_row(t, q, lane, W, b, k, i, v);
+        row = v;
+        if (mine && !gu) split_row(st, v, m, row);
+        const uint64_t rec = m == 2 ? p2 : m == 1 ? p1 : p0, nw = m == 2 ? n2 : m == 1 ? n1 : n0;
+        if (mine && rec && nw) pw[q] = ((gcfloat *)nw)[row];
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+}
+
+// The plane record of the 16 outputs of lanes 16t..16t+15 (one tile, one
+// scale group of the designated reader's input): each lane holds its value o
+// (its row's output) and nw, the reader's norm weight of that row (1 without
+// a norm): the planes are of o * nw, and word 14 is the group's sum of o^2, from which the reader
+// computes its norm scale.  Lane L stores word L % 16 of group L / 16.
+__device__ __forceinline__ void stream_plane_record(float o, float nw, bool valid, uint64_t rec, uint32_t tag,
+                                                    uint32_t *pack, int lane)
+{
+    const float xw = o * nw;
+    const float amax = row16_max_nonneg(valid ? fabsf(xw) : 0.f);
+    const float sum = row16_sum(valid ? xw : 0.f);
+    const float sq = row16_sum(valid ? o * o : 0.f);
+    const float dx = amax * (1.0f / (float)kQmax);
+    const float inv = amax > 0.f ? (float)kQmax * __builtin_amdgcn_rcpf(amax) : 0.f;
+    pack[lane] = biased_xi(valid ? xw : 0.f, inv);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's pack stores landed (one wave: in order)
+    const int w = lane & 15, base = lane & ~15;
+    uint32_t data = 0u;
+    if (w < 12) {
+        // plane p (h, m, l = bytes 2, 1, 0 of the biased values), values 4j..4j+3
+        const int p = w >> 2, j = w & 3, byte = 2 - p;
+        const uint4 d = *(const uint4 *)(pack + base + 4 * j);
+        const uint32_t sel = (uint32_t)byte | ((uint32_t)(byte + 4) << 8) | 0x0c0c0000u;
+        const uint32_t lo = __builtin_amdgcn_perm(d.y, d.x, sel), hi = __builtin_amdgcn_perm(d.w, d.z, sel);
+        data = (lo | (hi << 16)) ^ 0x80808080u;
+    } else if (w == 12) {
+        data = __float_as_uint(dx);
+    } else if (w == 13) {
+        data = __float_as_uint(sum);
+    } else if (w == 14) {
+        data = __float_as_uint(sq);
+    }
+    if (valid)
+        __hip_atomic_store((gword *)rec + w, exchange_word_u(data, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The control wave's stores of stage s: each of the workgroup's rows (one per
+// lane and pass), the 8 compute waves' partials summed in wave order, times
+// the norm scale cn of a stage whose input came as plane records; the plain
+// fp32 output, its exchange word and, for an output with a designated
+// reader, the plane records.
+__device__ __forceinline__ void stream_epilogue(cstage &st, const Tiles &t, const float *tpart,
+                                                const float (&rr)[kStreamPasses], const float (&pw)[kStreamPasses],
+                                                float cn, uint32_t tag, uint32_t W, uint32_t b, uint32_t *pack,
+                                                int lane)
+{
     const bool gu = uni(st.mode) == MODE_GATEUP;
     const uint64_t y0 = uni64(st.y[0]), y1 = uni64(st.y[1]), y2 = uni64(st.y[2]);
     const uint64_t l0 = uni64(st.lly[0]), l1 = uni64(st.lly[1]), l2 = uni64(st.lly[2]);
+    const uint64_t p0 = uni64(st.llp[0]), p1 = uni64(st.llp[1]), p2 = uni64(st.llp[2]);
     const bool res = uni64(st.r) != 0;
-    const int per = 64 / t.TR;
 #pragma unroll
     for (int q = 0; q < kStreamPasses; q++) {
-        if (q * per >= t.n) break;
+        if (4 * q >= t.n) break;
         int k, i, v;
-        if (own_row(t, q, lane, W, b, k, i, v)) {
-            const float *pt = tpart + k * (kNCW * 16);
+        const bool mine = own_row(t, q, lane, W, b, k, i, v);
+        const float *pt = tpart + (k < kStreamMaxTiles ? k : 0) * (kNCW * 32);
+        float o = 0.f;
+        int m = 0, row = v;
+        if (mine) {
             float s0 = 0.f;
 #pragma unroll
-            for (int w = 0; w < kNCW; w++) s0 += pt[w * 16 + i];
+            for (int w = 0; w < kNCW; w++) s0 += pt[w * 32 + i];
+            s0 *= cn;
             if (gu) {
                 float s1 = 0.f;
 #pragma unroll
-                for (int w = 0; w < kNCW; w++) s1 += pt[w * 16 + 8 + i];
-                const float o = silu(s0) * s1;
-                ((gfloat *)y0)[v] = o;
-                __hip_atomic_store((gword *)l0 + v, exchange_word(o, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int w = 0; w < kNCW; w++) s1 += pt[w * 32 + 16 + i];
+                o = silu(s0) * (s1 * cn);
             } else {
-                int m, row;
                 split_row(st, v, m, row);
-                if (res) s0 = rr[q] + s0;
-                ((gfloat *)(m == 2 ? y2 : m == 1 ? y1 : y0))[row] = s0;
-                __hip_atomic_store((gword *)(m == 2 ? l2 : m == 1 ? l1 : l0) + row, exchange_word(s0, tag),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                o = res ? rr[q] + s0 : s0;
             }
+            ((gfloat *)(m == 2 ? y2 : m == 1 ? y1 : y0))[row] = o;
+            __hip_atomic_store((gword *)(m == 2 ? l2 : m == 1 ? l1 : l0) + row, exchange_word(o, tag),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // plane records: a tile's 16 rows are one group of one output (the
+        // host designates outputs only in stages whose matrices' rows are all
+        // multiples of 16, where every tile is 16 rows of one matrix)
+        const uint64_t rec0 = mine ? (m == 2 ? p2 : m == 1 ? p1 : p0) : 0;
+        if (__ballot(rec0 != 0) != 0) {
+            const int g = (row - i) >> 4;  // the group: the tile's first row / 16
+            stream_plane_record(o, pw[q], rec0 != 0, rec0 + 8ull * kRecWords * (uint64_t)g, tag, pack, lane);
         }
     }
 }
@@ -568,6 +862,19 @@ __device__ __forceinline__ void stream_epilogue(cstage &st, const Tiles &t, cons
 __device__ __forceinline__ void stream_mark_done(uint32_t *done, uint32_t tag, uint32_t b, int lane)
 {
     if (lane == 0) __hip_atomic_store(done + b, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The norm scale of a stage whose input came as plane records with a norm:
+// 1/sqrt(mean(x^2) + eps) from the records' sums of squares, summed in a fixed
+// order (lane l: groups l, l + 64, ..., then the wave reduction).
+__device__ __forceinline__ float stream_norm_scale(cstage &st, const float *ss, int lane)
+{
+    if (!uni64(st.lpx) || !uni64(st.nw)) return 1.f;
+    const int units = uni(st.units), ng = 2 * units;
+    float s = 0.f;
+    for (int g = lane; g < ng; g += 64) s += ss[g];
+    s = wave_sum(s);
+    return 1.0f / sqrtf(s / (float)(units * 32) + unif(st.eps));
 }
 
 template <int FMT, int D>
@@ -581,6 +888,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
     const uint32_t W = gridDim.x, b = blockIdx.x;
     float *tpart = (float *)(ldsb + a.tpart_off);
     float *red = (float *)(ldsb + a.red_off);
+    float *ss = (float *)(ldsb + a.ss_off);
     const int nst = a.nstages;
 
     uint8_t *xbuf = ldsb + a.xbuf_off;
@@ -614,15 +922,15 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
         Raw2<FMT> ring[D];
 #pragma unroll
         for (int d = 0; d < D; d++) {
-            stream_issue<FMT>(ring[d], ci, is, cw);
+            stream_issue<FMT>(ring[d], ci, is, stage_at(a, ci.s < nst ? ci.s : nst - 1), cw);
             advance();
         }
         __syncthreads();  // B of stage 0: x in LDS
         const uint32_t base = (uint32_t)uni((int)((uint32_t *)red)[kRedBase]);
-        stream_convert_x<FMT>(stage_at(a, 0), ldsb, xbuf, red, 0u);
+        stream_convert_x(stage_at(a, 0), ldsb, xbuf, red, ss, 0u, nullptr, (uint32_t *)red + kRedMask);
         __syncthreads();  // C of stage 0
         int s = 0;        // the stage whose boundary comes next
-        float acc = 0.f;
+        float acc0 = 0.f, acc1 = 0.f;  // the tile's gate (or plain) and up partials
         // The loop has one exit, at its latch, and a trip count known up front
         // (the wave's slots, padded to a multiple of D with slots past the last
         // stage).  An exit inside the unrolled body would be merged into the
@@ -640,33 +948,41 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
                 while (s < cp.s) {
                     __syncthreads();  // A
                     __syncthreads();  // B
-                    if (s + 1 < nst) stream_stage_in<FMT>(stage_at(a, s + 1), ldsb, xbuf, red, base, a.flag, false, lane);
+                    if (s + 1 < nst) stream_stage_in(stage_at(a, s + 1), ldsb, xbuf, red, ss, base, a.flag, false, lane);
                     s++;
                 }
                 // a slot past the last stage writes its (unused) item too, so
                 // every slot's wait counts the same loads
                 stream_stage_write<FMT>(ring[d], stage, lane);
-                stream_issue<FMT>(ring[d], ci, is, cw);
+                stream_issue<FMT>(ring[d], ci, is, stage_at(a, ci.s < nst ? ci.s : nst - 1), cw);
                 advance();
                 // the slot's dots against the staged x of stage s
-                const int j = cw + kNCW * cp.p;
-                if (cp.s < nst && j < cp.G) {
+                const int item = cw + kNCW * cp.p;
+                if (cp.s < nst && item < cp.NI) {
                     const int units = cp.units;
+                    const bool up = item >= cp.G;
+                    const int j = item - (up ? cp.G : 0);
                     Chunk<FMT> c;
                     read_chunk<FMT>(c, stage, n, g);
                     const int cs0 = 16 * j + 4 * g;
                     const bool valid = cs0 < units;  // false only in an 8-unit last segment
                     const int cs = valid ? cs0 : units - 4;
                     const uint32_t abase = plane_lane ? (uint32_t)cs * 96u + plane_off : a.zero_off;
-                    acc += item_dot<FMT>(c, ldsb, abase, (uint32_t)units * 96u + (uint32_t)cs * 8u, (uint32_t)cs,
-                                         valid ? 0 : 4, j == cp.G - 1);
+                    const float r = item_dot2<FMT>(c, ldsb, abase, (uint32_t)units * 96u + (uint32_t)cs * 16u,
+                                                   (uint32_t)cs, valid ? 0 : 4, j == cp.G - 1);
+                    if (up) acc1 += r;
+                    else acc0 += r;
                 }
                 if (cp.s < nst && cp.p == cp.P - 1) {
-                    float r = acc;
-                    r += __shfl_xor(r, 16);
-                    r += __shfl_xor(r, 32);
-                    acc = 0.f;
-                    if (lane < 16) tpart[(cp.k * kNCW + cw) * 16 + lane] = r;
+                    float r0 = acc0, r1 = acc1;
+                    r0 += __shfl_xor(r0, 16);
+                    r0 += __shfl_xor(r0, 32);
+                    r1 += __shfl_xor(r1, 16);
+                    r1 += __shfl_xor(r1, 32);
+                    acc0 = acc1 = 0.f;
+                    float *pt = tpart + (cp.k * kNCW + cw) * 32;
+                    if (lane < 16) pt[lane] = r0;
+                    else if (lane < 32) pt[lane] = r1;  // lanes 16-31 hold the same sums
                 }
                 cp.next(a, W, b);
             }
@@ -675,12 +991,13 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
         while (s < nst) {
             __syncthreads();  // A
             __syncthreads();  // B
-            if (s + 1 < nst) stream_stage_in<FMT>(stage_at(a, s + 1), ldsb, xbuf, red, base, a.flag, false, lane);
+            if (s + 1 < nst) stream_stage_in(stage_at(a, s + 1), ldsb, xbuf, red, ss, base, a.flag, false, lane);
             s++;
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the last (dummy) item loads have returned
     } else {
         // ---- control wave ----
+        uint32_t *pack = (uint32_t *)(ldsb + a.pack_off);
         const uint32_t seq0 = __hip_atomic_load(a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const uint32_t base = uni((int)(seq0 * (uint32_t)(nst + 1)));
         {
@@ -691,37 +1008,39 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
         if (lane == 0) ((uint32_t *)red)[kRedBase] = base;
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the LDS-direct loads have landed
         __syncthreads();                     // B of stage 0
-        stream_convert_x<FMT>(stage_at(a, 0), ldsb, xbuf, red, 0u);
+        stream_convert_x(stage_at(a, 0), ldsb, xbuf, red, ss, 0u, nullptr, (uint32_t *)red + kRedMask);
         __syncthreads();  // C of stage 0
+        float cn = 1.f;   // norm scale of the current stage's output
         for (int s = 0; s < nst; s++) {
             cstage &st = stage_at(a, s);
             Tiles t;
             t.init(st, W, b);
-            // residual rows of this stage's rows, gathered while the stage runs
-            float rr[kStreamPasses];
-            stream_residual(st, t, rr, base, a.flag, W, b, lane);
+            // the output scale and the residual rows, while the stage runs
+            if (s > 0) cn = stream_norm_scale(st, ss, lane);
+            float rr[kStreamPasses], pw[kStreamPasses];
+            stream_prefetch(st, t, rr, pw, base, a.flag, W, b, lane);
             __syncthreads();  // A: every partial of stage s is in LDS
-            stream_epilogue(st, t, tpart, rr, base + (uint32_t)s + 1u, W, b, lane);
+            stream_epilogue(st, t, tpart, rr, pw, cn, base + (uint32_t)s + 1u, W, b, pack, lane);
             stream_mark_done(a.seq + 128, base + (uint32_t)s + 1u, b, lane);
             if (s + 1 < nst) {
                 cstage &st1 = stage_at(a, s + 1);
                 const int units1 = uni(st1.units);
-                const bool tagged = uni64(st1.llx) != 0;
+                const bool words = uni64(st1.llx) != 0 || uni64(st1.lpx) != 0;
                 // the partial reads above are done before any copy lands in
                 // their space (xbuf aliases the item stages and partials)
                 __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-                if (uni64(st1.nw)) stream_fetch_norm(st1, xbuf + units1 * (tagged ? 256 : 128), lane);
-                if (tagged) {
-                    if (lane == 0) ((uint32_t *)red)[kRedBad] = 0u;
+                if (uni64(st1.nw) && !uni64(st1.lpx)) stream_fetch_norm(st1, xbuf + units1 * (words ? 256 : 128), lane);
+                if (words) {
+                    if (lane < kMaskWords) ((uint32_t *)red)[kRedMask + lane] = 0u;
                     stream_wait_done(a.seq + 128, base + (uint32_t)uni(st1.xsrc) + 1u, a.flag, lane);
-                    stream_fetch_tagged(st1, xbuf, lane);
-                }
-                else
+                    stream_fetch_words(st1, xbuf, lane);
+                } else {
                     stream_fetch_plain(st1, xbuf, lane);
+                }
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             }
             __syncthreads();  // B
-            if (s + 1 < nst) stream_stage_in<FMT>(stage_at(a, s + 1), ldsb, xbuf, red, base, a.flag, true, lane);
+            if (s + 1 < nst) stream_stage_in(stage_at(a, s + 1), ldsb, xbuf, red, ss, base, a.flag, true, lane);
         }
         // the last workgroup to finish advances the launch count (every
         // workgroup read it at its start, before counting itself done)
@@ -749,23 +1068,23 @@ struct StreamPlan {
     StreamArgs args{};
 };
 
-// LDS: [x planes + {dx, c}][zero region][norm reduction][region], where the
-// region holds the compute waves' item stages and the tile partials during a
-// stage, and the staged input (fp32 or exchange words, then the norm weight)
-// during a boundary.
-size_t stream_lds(int fmt, int max_units, int max_xbuf, uint32_t &zero_off, uint32_t &stage_off,
-                  uint32_t &tpart_off, uint32_t &red_off, uint32_t &xbuf_off)
+// LDS: [x planes + unit scales][zero region][reductions][plane bytes][sums of
+// squares][region], where the region holds the compute waves' item stages and
+// the tile partials during a stage, and the staged input (fp32, exchange
+// words or plane records, then the norm weight) during a boundary.
+size_t stream_lds(int fmt, int max_units, int max_xbuf, StreamArgs &a)
 {
-    const size_t x_lds = ((size_t)max_units * lds_bytes_per_unit<XM_I24>() + 15) & ~(size_t)15;
-    zero_off = zero_region_off((uint32_t)x_lds);
-    red_off = zero_off + kZeroBytes;
-    stage_off = (red_off + 16 * 4 + 15) & ~15u;
-    const int stage = fmt == FMT_Q4_0 ? Geo<FMT_Q4_0>::STAGE : fmt == FMT_Q8_0 ? Geo<FMT_Q8_0>::STAGE
-                                                                                : Geo<FMT_Q4_K>::STAGE;
-    tpart_off = (stage_off + kNCW * stage + 15) & ~15u;
-    xbuf_off = stage_off;
-    const size_t during = tpart_off + (size_t)kStreamMaxTiles * kNCW * 16 * 4;
-    const size_t boundary = xbuf_off + (size_t)max_xbuf;
+    const size_t x_lds = ((size_t)max_units * kUnitLds + 15) & ~(size_t)15;
+    a.zero_off = zero_region_off((uint32_t)x_lds);
+    a.red_off = a.zero_off + kZeroBytes;
+    a.pack_off = a.red_off + kRedWords * 4;
+    a.ss_off = a.pack_off + 64 * 4;
+    a.stage_off = (a.ss_off + 2 * 4 * (uint32_t)max_units + 15) & ~15u;
+    const int stage = fmt == FMT_Q4_0 ? Geo<FMT_Q4_0>::STAGE : Geo<FMT_Q4_K>::STAGE;
+    a.tpart_off = (a.stage_off + kNCW * stage + 15) & ~15u;
+    a.xbuf_off = a.stage_off;
+    const size_t during = a.tpart_off + (size_t)kStreamMaxTiles * kNCW * 32 * 4;
+    const size_t boundary = a.xbuf_off + (size_t)max_xbuf;
     return during > boundary ? during : boundary;
 }
 
@@ -792,7 +1111,7 @@ bool stream_launch_t(StreamPlan &p)
     return true;
 }
 
-constexpr int kStreamD = 4;  // items in flight per compute wave
+constexpr int kStreamD = 3;  // items in flight per compute wave (4 spills at 168 VGPRs)
 
 template <int FMT>
 bool stream_launch_f(StreamPlan &p)
@@ -838,6 +1157,8 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
     const int grid = num_cus();
     StreamStage *host = new StreamStage[nstages];
     int max_units = 0, max_xbuf = 0;
+    bool rows16 = true;  // per stage below: every matrix's rows a multiple of 16
+    std::vector<char> aligned16(nstages, 0);
     for (int s = 0; s < nstages; s++) {
         const holo_stream_stage_t &in = stages[s];
         StreamStage &o = host[s];
@@ -851,6 +1172,7 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
         ok = ok && (!in.norm_w || !((uintptr_t)in.norm_w & 15u));
         ok = ok && (!in.r || (!gu && nmat == 1));
         int total = 0;
+        rows16 = true;
         for (int m = 0; m < 3; m++) {
             if (m < nmat) {
                 const int rows = in.rows[gu ? 0 : m];
@@ -859,7 +1181,8 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
                 o.W[m] = (uint64_t)in.W[m];
                 o.y[m] = (uint64_t)y;
                 total += rows;
-                o.row_end[m] = total;
+                o.row_end[m] = gu ? INT_MAX : total;  // gate/up rows all index W[0] (up: + dup)
+                rows16 = rows16 && rows % 16 == 0;
             } else {
                 o.W[m] = (uint64_t)in.W[0];
                 o.y[m] = (uint64_t)in.y[0];
@@ -878,11 +1201,13 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
         o.eps = in.eps;
         o.r = (uint64_t)in.r;
         o.G = (o.units + 15) / 16;
-        o.P = (o.G + kNCW - 1) / kNCW;
-        const int tr = gu ? 8 : 16;
+        o.NI = gu ? 2 * o.G : o.G;
+        o.P = (o.NI + kNCW - 1) / kNCW;
+        o.dup = gu ? (uint64_t)in.W[1] - (uint64_t)in.W[0] : 0;
         o.total_rows = gu ? in.rows[0] : total;
-        o.full_tiles = o.total_rows / (grid * tr);
-        o.rem_start = o.full_tiles * grid * tr;
+        o.full_tiles = o.total_rows / (grid * 16);
+        o.rem_start = o.full_tiles * grid * 16;
+        aligned16[s] = rows16;
         if (o.full_tiles + 1 > kStreamMaxTiles) {
             delete[] host;
             HOLO_REJECT("holo_gemv_stream_create: a stage with more rows than 16 tiles per CU");
@@ -959,9 +1284,27 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
         v.off = nwords;
         nwords += (size_t)v.rows;
     }
+    // Plane records: each written output (stage s, output m) is designated to
+    // the first later stage that reads exactly that output as its x (its
+    // in_dim = the output's rows) when the 16-row tiles of stage s each fall in
+    // one matrix (every matrix's rows a multiple of 16).  The records of an
+    // output vector share one buffer, as its exchange words do (the tags tell
+    // the writers apart).
+    std::vector<int> lp(nstages, -1), rd(3 * (size_t)nstages, -1);
+    for (int t = 0; t < nstages; t++) {
+        const int s = host[t].xsrc;
+        if (xo[t] < 0 || s < 0 || !aligned16[s]) continue;
+        const int nout = stages[s].gate_up ? 1 : stages[s].nmat;
+        for (int m = 0; m < nout; m++) {
+            if (yo[3 * (size_t)s + m] != xo[t] || rd[3 * (size_t)s + m] >= 0) continue;
+            if (stages[s].rows[m] != stages[t].in_dim) continue;
+            rd[3 * (size_t)s + m] = t;
+            lp[t] = xo[t];
+        }
+    }
     // launch counter line, done counter line, one done word per workgroup
     const size_t kWordsHeader = (512 + 4 * (size_t)grid + 255) & ~(size_t)255;
-    const size_t words_bytes = kWordsHeader + 8 * nwords;
+    const size_t words_bytes = kWordsHeader + 16 * nwords;
     uint8_t *words = nullptr;
     if (hipMalloc((void **)&words, words_bytes) != hipSuccess) {
         (void)hipGetLastError();
@@ -971,22 +1314,29 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
     }
     HOLO_CHECK(hipMemset(words, 0, words_bytes));
     const uint64_t wbase = (uint64_t)(uintptr_t)words + kWordsHeader;
+    const uint64_t rbase = wbase + 8 * nwords;
     for (int s = 0; s < nstages; s++) {
         const holo_stream_stage_t &in = stages[s];
         StreamStage &o = host[s];
         const int nout = in.gate_up ? 1 : in.nmat;
-        for (int m = 0; m < 3; m++) o.lly[m] = wbase + 8 * outs[yo[3 * (size_t)s + (m < nout ? m : 0)]].off;
-        o.llx = xo[s] >= 0 ? wbase + 8 * outs[xo[s]].off : 0;
+        for (int m = 0; m < 3; m++) {
+            const int mm = m < nout ? m : 0;
+            const int i = yo[3 * (size_t)s + mm], t = rd[3 * (size_t)s + mm];
+            o.lly[m] = wbase + 8 * outs[i].off;
+            o.llp[m] = m < nout && t >= 0 ? rbase + 8 * outs[i].off : 0;
+            o.pnw[m] = m < nout && t >= 0 ? (uint64_t)stages[t].norm_w : 0;
+        }
+        o.llx = xo[s] >= 0 && lp[s] < 0 ? wbase + 8 * outs[xo[s]].off : 0;
+        o.lpx = lp[s] >= 0 ? rbase + 8 * outs[lp[s]].off : 0;
         o.llr = ro[s] >= 0 ? wbase + 8 * outs[ro[s]].off : 0;
-        const int xb = o.units * (o.llx ? 256 : 128) + (in.norm_w ? o.units * 128 : 0);
+        const int xb = o.lpx ? o.units * 256 : o.units * (o.llx ? 256 : 128) + (in.norm_w ? o.units * 128 : 0);
         max_xbuf = xb > max_xbuf ? xb : max_xbuf;
     }
     StreamPlan *p = new StreamPlan;
     p->words = words;
     p->nstages = nstages;
     p->fmt = fmt;
-    p->lds = stream_lds(fmt, max_units, max_xbuf, p->args.zero_off, p->args.stage_off, p->args.tpart_off,
-                        p->args.red_off, p->args.xbuf_off);
+    p->lds = stream_lds(fmt, max_units, max_xbuf, p->args);
     if (p->lds > 160 * 1024 || hipMalloc((void **)&p->dev, sizeof(StreamStage) * nstages) != hipSuccess) {
         (void)hipGetLastError();
         delete[] host;
@@ -1004,9 +1354,8 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
         long long n = 0;
         for (int s = 0; s < nstages; s++) {
             const StreamStage &o = host[s];
-            const uint32_t rem = (uint32_t)(o.total_rows - o.rem_start);
-            const int e0 = o.rem_start + (int)(((uint32_t)b * rem) / (uint32_t)grid);
-            const int e1 = o.rem_start + (int)(((uint32_t)(b + 1) * rem) / (uint32_t)grid);
+            int e0, e1;
+            rem_rows(o.total_rows, o.rem_start, (uint32_t)grid, (uint32_t)b, e0, e1);
             n += (long long)(o.full_tiles + (e1 > e0 ? 1 : 0)) * o.P;
         }
         n = (n + kStreamD - 1) / kStreamD * kStreamD;

@@ -97,8 +97,6 @@ Q6_CASES = [(1, 256), (3, 512), (37, 256 * 9), (130, 4096), (4096, 4096), (4096,
 def test_gemv_q6_k_parity(holo, synth, oracle, out_dim, in_dim, x_offset):
     """x_offset 1 shifts the activations by one float, off 16-byte alignment
     (the per-weight kernel); 0 runs the 64-weight task kernel."""
-    if x_offset and out_dim * in_dim > 4096 * 4096:
-        pytest.skip("alignment fallback checked on the smaller shapes")
     print(f"case q6_k {out_dim}x{in_dim} x_offset={x_offset}", flush=True)
     seed = out_dim * 7919 + in_dim
     W = synth.blocks(Q6_K, out_dim, in_dim, seed)

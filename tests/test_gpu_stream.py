@@ -1,17 +1,21 @@
 """GPU tests of the persistent decode-step kernel (holo_gemv_stream_*): a plan
 of dependent GEMV stages run as one launch.
 
-Plain stages are compared bit for bit with the same GEMVs made as separate
-calls (holo_batched_qkv, cuda_matmul_*, holo_batched_ffn_gate_up): the
-stream kernel runs the same item dots, the same per-wave partial order and
-the same activation planes.  Every stage of a multi-layer chain reads an
-earlier stage's output, so a missing or leaky grid barrier, or a weight item
-of one stage consumed as another's, shows up as a mismatch.  Stages with the
-rms_norm folded into their staging and the residual add into their stores
-are compared with the per-launch fused calls (holo_batched_*_norm,
-holo_matmul_add) within 1e-5 (only the norm's summation order differs) and
-with the CPU oracle within the 1e-3 bar.  holo_gemv_stream_status() must
-report no barrier timeout.
+Every stage's output is checked against the CPU oracle run on that stage's
+own input (the stream's output of the stage it reads), within the 1e-3 bar,
+and against the same GEMVs made as separate calls (holo_batched_qkv,
+cuda_matmul_*, holo_batched_ffn_gate_up) within 1e-4 normwise: the stream
+kernel scales its activation planes per 16 values where the separate calls
+scale them per 32, so the two differ by fixed-point rounding only.  Every
+stage of a multi-layer chain reads an earlier stage's output, so a missing
+or leaky hand-over, or a weight item of one stage consumed as another's,
+shows up as a mismatch far above those bounds.  Repeats of one stage and
+graph replays are compared bit for bit.  Stages with the rms_norm folded
+into their input (or into their output scale) and the residual add into
+their stores are compared with the per-launch fused calls
+(holo_batched_*_norm, holo_matmul_add) within 2e-5 and with the CPU oracle
+within the 1e-3 bar.  holo_gemv_stream_status() must report no exchange
+timeout.
 """
 import numpy as np
 import pytest
@@ -73,8 +77,8 @@ def _plain_separate(lib, t, L, x_ptr, out):
                          ids=["q4_0-llama2", "q4_0-small", "q4_k-gqa", "q4_0-768"])
 def test_stream_layers_match_separate_calls(holo, synth, oracle, t, dim, kv, ffn, layers):
     """`layers` decode layers chained (each layer's down output is the next
-    layer's input): 4 * layers stages in one launch, every output bit-equal
-    to the separate calls."""
+    layer's input): 4 * layers stages in one launch, every output against
+    the oracle on its own stage input and against the separate calls."""
     print(f"case stream layers type {t} dim {dim} kv {kv} ffn {ffn} x{layers}", flush=True)
     lib = holo.lib()
     Ls = [Layer(holo, synth, t, dim, kv, ffn, seed=900 + dim + t + 10 * i) for i in range(layers)]
@@ -93,20 +97,31 @@ def test_stream_layers_match_separate_calls(holo, synth, oracle, t, dim, kv, ffn
     holo.check("stream")
     assert lib.holo_gemv_stream_status() == 0
     n = {"q": dim, "k": kv, "v": kv, "o": dim, "h": ffn, "y": dim}
-    for i in range(layers):
-        for name in ("q", "k", "v", "o", "h", "y"):
-            assert np.array_equal(_bits(got[i][name], n[name]), _bits(ref[i][name], n[name])), (i, name)
-    # the first layer's first and last stage against the CPU oracle
-    # (teacher-forced input; later layers of un-normalised random weights
-    # grow without bound, in the separate calls as here)
-    q = got[0]["q"].download(np.float32, dim)
-    want = oracle.matmul(t, Ls[0].host["q"], x, dim, dim)
-    assert normwise_err(q, want) <= 1e-3 and max_rel_err(q, want) <= 1e-3
-    h = got[0]["h"].download(np.float32, ffn)
-    y = got[0]["y"].download(np.float32, dim)
-    assert np.all(np.isfinite(h)) and np.all(np.isfinite(y))
-    want = oracle.matmul(t, Ls[0].host["down"], h, dim, ffn)
-    assert normwise_err(y, want) <= 1e-3 and max_rel_err(y, want) <= 1e-3
+    xin = x
+    for i, L in enumerate(Ls):
+        g = {name: got[i][name].download(np.float32, n[name]) for name in n}
+        r = {name: ref[i][name].download(np.float32, n[name]) for name in n}
+        # each stage against the oracle on the stage's own input (un-normalised
+        # random layers grow without bound: a later layer can overflow, in the
+        # oracle as in the separate calls; such stages are skipped)
+        want = {"q": oracle.matmul(t, L.host["q"], xin, dim, dim), "k": oracle.matmul(t, L.host["k"], xin, kv, dim),
+                "v": oracle.matmul(t, L.host["v"], xin, kv, dim), "o": oracle.matmul(t, L.host["o"], g["v"], dim, kv),
+                "h": oracle.silu_mul(oracle.matmul(t, L.host["gate"], g["o"], ffn, dim),
+                                     oracle.matmul(t, L.host["up"], g["o"], ffn, dim)),
+                "y": oracle.matmul(t, L.host["down"], g["h"], dim, ffn)}
+        for name in n:
+            if i > 0 and not np.all(np.isfinite(want[name])):
+                continue
+            e, m = normwise_err(g[name], want[name]), max_rel_err(g[name], want[name])
+            assert e <= 1e-3 and m <= 1e-3, (i, name, e, m)
+            # the separate calls' chain drifts from this one by the rounding
+            # of each earlier stage (about 1e-5 after four stages): compare
+            # the first layer only
+            if i == 0:
+                e = normwise_err(g[name], r[name])
+                print(f"  layer 0 {name}: vs separate calls {e:.2e}", flush=True)
+                assert e <= 1e-4, (name, e)
+        xin = g["y"]
     plan.close()
 
 
@@ -160,7 +175,7 @@ def test_stream_fused_decode_layers(holo, synth, oracle, t, dim, kv, ffn, layers
     got, ref = xs.download(np.float32, dim), xr.download(np.float32, dim)
     e = normwise_err(got, ref)
     print(f"  vs per-launch fused calls {e:.2e}", flush=True)
-    assert e <= 1e-5
+    assert e <= 2e-5
     # the CPU chain: numpy norms, the oracle's GEMVs, silu_mul
     x = x0.copy()
     for i, L in enumerate(Ls):
@@ -180,8 +195,8 @@ def test_stream_fused_decode_layers(holo, synth, oracle, t, dim, kv, ffn, layers
 def test_stream_long_plan(holo, synth):
     """1040 stages in one launch (the stage table, 150 KB, is read from
     device memory stage by stage).  Each of 260 layers reads the same input
-    and writes outputs of its own, every one bit-equal to the separate
-    calls."""
+    and writes outputs of its own, every one equal to the separate
+    calls within 1e-5 and the repeats of one layer bit-equal to each other."""
     print("case stream 1040 stages", flush=True)
     lib = holo.lib()
     t, dim, kv, ffn, nl = Q4_0, 512, 256, 1280, 260
@@ -200,8 +215,12 @@ def test_stream_long_plan(holo, synth):
     holo.check("stream long plan")
     assert lib.holo_gemv_stream_status() == 0
     n = {"q": dim, "k": kv, "v": kv, "o": dim, "h": ffn, "y": dim}
-    want = [{name: _bits(ref[j][name], n[name]) for name in n} for j in range(4)]
-    for i in range(nl):
+    want = [{name: _bits(got[j][name], n[name]) for name in n} for j in range(4)]
+    for j in range(4):
+        for name in n:
+            e = normwise_err(got[j][name].download(np.float32, n[name]), ref[j][name].download(np.float32, n[name]))
+            assert e <= 1e-5, (j, name, e)
+    for i in range(4, nl):
         for name in n:
             assert np.array_equal(_bits(got[i][name], n[name]), want[i % 4][name]), (i, name)
     plan.close()
