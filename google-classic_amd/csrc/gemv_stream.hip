@@ -96,6 +96,8 @@ struct StreamStage {
     uint64_t r;           // residual: y[0] = r + W x (plain, one matrix), or 0
     int64_t row_bytes;
     int row_end[3];       // prefix sums of the matrices' rows (plain); INT_MAX unused
+    int ystart[3];        // output rows below this are written again by a later stage of the
+                          // plan: no plain store for them (exchange words only)
     int mode;             // MODE_PLAIN / MODE_GATEUP
     int units;            // 32-weight units per row
     int G;                // 16-unit segments per row
@@ -153,8 +155,13 @@ __device__ __forceinline__ float unif(float v)
     return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
-// Remainder rows dealt in 16-row tiles: workgroup b gets remainder tiles
-// [b * nt / W, (b + 1) * nt / W) of the nt = ceil(rem / 16), at most one.
+// The remainder rows of workgroup b (rem = total - rem_start < 16 W): tile
+// [b * nt / W, (b + 1) * nt / W) of the nt = ceil(rem / 16) 16-row tiles, at
+// most one.  Every tile starts at a multiple of 16, so a tile's outputs form
+// whole plane-record groups.  (Splitting the remainder into equal runs of
+// rows balances the HBM bytes better, but a short tile costs the compute
+// waves as much as a full one; measured on the decode chain, the 16-row
+// tiles are faster.)
 __host__ __device__ inline void rem_rows(int total, int rem_start, uint32_t W, uint32_t b, int &e0, int &e1)
 {
     const uint32_t nt = (uint32_t)(total - rem_start + 15) / 16u;
@@ -499,16 +506,22 @@ __device__ __forceinline__ void stream_fetch_norm(cstage &st, uint8_t *wbuf, int
 
 // Exchange words of a stage input (the fp32 words, or the plane records:
 // either way 8 bytes per input value) into LDS, 1 KB pieces of 128 words,
-// device-coherent (sc1: never answered from a line this XCD's L2 held
-// before another XCD's store).  The tags are checked while the words are put
-// in place (stream_stage_in), which copies again what was not current.
+// device-coherent (sc1: never answered from a line this XCD's L2 held before
+// another XCD's store).  The tags are checked while the words are put in
+// place (stream_stage_in), which copies again the pieces that were not
+// current.  One plain loop: the one issuing wave's scalar work per piece
+// bounds the copy (a choice of source per piece made it 2.5x slower).
+__device__ __forceinline__ const uint8_t *words_src(cstage &st)
+{
+    const uint64_t lp = uni64(st.lpx);
+    return (const uint8_t *)(lp ? lp : uni64(st.llx));
+}
 __device__ __forceinline__ void stream_fetch_words(cstage &st, uint8_t *xbuf, int lane)
 {
     const int units = uni(st.units), nch = units / 4;  // 128 words = 4 units per piece
-    const uint64_t lp = uni64(st.lpx);
-    const uint8_t *src = (const uint8_t *)(lp ? lp : uni64(st.llx));
+    const uint8_t *src = words_src(st) + 16 * lane;
     for (int j = 0; j < nch; j++)
-        __builtin_amdgcn_global_load_lds((gvoid *)(src + 1024 * j + 16 * lane), (lds_void *)(xbuf + 1024 * j), 16, 0,
+        __builtin_amdgcn_global_load_lds((gvoid *)(src + 1024 * j), (lds_void *)(xbuf + 1024 * j), 16, 0,
                                          kDeviceScope);
 }
 
@@ -634,15 +647,13 @@ __device__ __forceinline__ void stream_convert_x(cstage &st, uint8_t *ldsb, cons
 // wave).
 __device__ __forceinline__ void stream_refetch(cstage &st, uint8_t *xbuf, const uint32_t *m, int lane)
 {
-    const uint64_t lp = uni64(st.lpx);
-    const uint8_t *src = (const uint8_t *)(lp ? lp : uni64(st.llx));
     for (int w = 0; w < kMaskWords; w++) {
         uint32_t bits = (uint32_t)uni((int)m[w]);
         while (bits) {
             const int j = 32 * w + __builtin_ctz(bits);
             bits &= bits - 1u;
-            __builtin_amdgcn_global_load_lds((gvoid *)(src + 1024 * j + 16 * lane), (lds_void *)(xbuf + 1024 * j), 16,
-                                             0, kDeviceScope);
+            __builtin_amdgcn_global_load_lds((gvoid *)(words_src(st) + 1024 * j + 16 * lane),
+                                             (lds_void *)(xbuf + 1024 * j), 16, 0, kDeviceScope);
         }
     }
 }
@@ -811,7 +822,12 @@ __device__ __forceinline__ void stream_plane_record(float o, float nw, bool vali
 // lane and pass), the 8 compute waves' partials summed in wave order, times
 // the norm scale cn of a stage whose input came as plane records; the plain
 // fp32 output, its exchange word and, for an output with a designated
-// reader, the plane records.
+// reader, the plane records.  The plain store is made only by the last stage
+// of the plan that writes the row: plain stores are cached in the storing
+// XCD's L2 until written back, so two workgroups on different XCDs storing
+// one row in two stages of a launch would race at write-back.  (Exchange
+// words and records are agent-scope stores, written through; each row has
+// one writer per stage.)
 __device__ __forceinline__ void stream_epilogue(cstage &st, const Tiles &t, const float *tpart,
                                                 const float (&rr)[kStreamPasses], const float (&pw)[kStreamPasses],
                                                 float cn, uint32_t tag, uint32_t W, uint32_t b, uint32_t *pack,
@@ -822,6 +838,7 @@ __device__ __forceinline__ void stream_epilogue(cstage &st, const Tiles &t, cons
     const uint64_t l0 = uni64(st.lly[0]), l1 = uni64(st.lly[1]), l2 = uni64(st.lly[2]);
     const uint64_t p0 = uni64(st.llp[0]), p1 = uni64(st.llp[1]), p2 = uni64(st.llp[2]);
     const bool res = uni64(st.r) != 0;
+    const int ys0 = uni(st.ystart[0]), ys1 = uni(st.ystart[1]), ys2 = uni(st.ystart[2]);
 #pragma unroll
     for (int q = 0; q < kStreamPasses; q++) {
         if (4 * q >= t.n) break;
@@ -844,7 +861,7 @@ __device__ __forceinline__ void stream_epilogue(cstage &st, const Tiles &t, cons
                 split_row(st, v, m, row);
                 o = res ? rr[q] + s0 : s0;
             }
-            ((gfloat *)(m == 2 ? y2 : m == 1 ? y1 : y0))[row] = o;
+            if (row >= (m == 2 ? ys2 : m == 1 ? ys1 : ys0)) ((gfloat *)(m == 2 ? y2 : m == 1 ? y1 : y0))[row] = o;
             __hip_atomic_store((gword *)(m == 2 ? l2 : m == 1 ? l1 : l0) + row, exchange_word(o, tag),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -1278,6 +1295,21 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
         HOLO_REJECT("holo_gemv_stream_create: a stage input that overlaps an earlier output other than exactly, or "
                     "an output overlapping its own input or another output");
         return nullptr;
+    }
+    // the plain stores of a row go to its last writer in the plan
+    for (int s = 0; s < nstages; s++) {
+        const int nout = stages[s].gate_up ? 1 : stages[s].nmat;
+        for (int m = 0; m < 3; m++) host[s].ystart[m] = 0;
+        for (int m = 0; m < nout; m++) {
+            int later = 0;
+            for (int s2 = s + 1; s2 < nstages; s2++) {
+                const int n2 = stages[s2].gate_up ? 1 : stages[s2].nmat;
+                for (int m2 = 0; m2 < n2; m2++)
+                    if (yo[3 * (size_t)s2 + m2] == yo[3 * (size_t)s + m] && stages[s2].rows[m2] > later)
+                        later = stages[s2].rows[m2];
+            }
+            host[s].ystart[m] = later;
+        }
     }
     size_t nwords = 0;
     for (OutVec &v : outs) {

@@ -117,16 +117,23 @@ int holo_gemv_chain_status(void);
  * y[0] = r + W x (r may alias y[0]).  A stage may read an earlier stage's
  * output as x or r, when it names that output's address exactly; outputs hand
  * over to later stages through exchange words (value and a launch/stage tag
- * in one 64-bit store) that the consumers poll, not a grid barrier.  Rejected:
- * an input overlapping an earlier output other than exactly, an output
- * overlapping its own stage's x or another output.  Results are those of the
- * separate MFMA-path GEMV calls (within fp32 rounding: the norm's summation
- * order differs).  The weight loads of later stages are issued ahead, across
- * the stage boundaries.  Q4_0 or Q4_K (HOLO_TYPE_*), in_dim a multiple of 256
- * up to 18432 (and within the 160 KB of LDS), 16-byte aligned matrices,
- * vectors and norm weights, at most 16 tiles of rows per CU and stage (16
- * rows, or 8 for gate/up).  No reference counterpart: it replaces the
- * per-matrix launches of the decode loop (src/ai/llm_cuda.c:604-918).
+ * in one 64-bit store) that the consumers poll, not a grid barrier, and the
+ * first later stage that reads an output as x (its in_dim = the output's
+ * rows, all of the producing stage's matrices with rows a multiple of 16)
+ * receives it as plane records: the reader's int8 activation planes, made by
+ * the producer.  Rejected: an input overlapping an earlier output other than
+ * exactly, an output overlapping its own stage's x or another output.  The
+ * activations are 22-bit fixed point per 16 values (the separate GEMV calls:
+ * per 32), so results match the separate MFMA-path calls to about 1e-6
+ * normwise per stage and the CPU reference within the 1e-3 bar.  The weight
+ * loads of later stages are issued ahead, across the stage boundaries.  Q4_0
+ * or Q4_K (HOLO_TYPE_*), in_dim a multiple of 256 up to 18432 (and within the
+ * 160 KB of LDS), 16-byte aligned matrices, vectors and norm weights, at most
+ * 16 tiles of 16 rows per CU and stage.  An output row that a later stage
+ * writes again is stored in plain fp32 only by the last one (the final
+ * contents are those of running the stages in order).  No reference
+ * counterpart: it replaces the per-matrix launches of the decode loop
+ * (src/ai/llm_cuda.c:604-918).
  * create: copies the stage table to the device and allocates the exchange
  *   buffers (not under graph capture); NULL, with the error latched, for
  *   anything outside the set.

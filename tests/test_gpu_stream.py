@@ -263,6 +263,43 @@ def test_stream_ragged_rows(holo, synth, oracle):
     plan.close()
 
 
+def test_stream_rewritten_output(holo, synth, oracle):
+    """An output vector written again by a later stage whose tiles put its
+    rows on other workgroups (the third matrix of a 3-matrix stage, then a
+    single matrix), once over all its rows and once over its first half: the
+    final vector holds the last writer's rows and, past them, the earlier
+    stage's.  Only the last writer of a row stores it in plain fp32; plain
+    stores of one row from two XCDs in one launch would race at L2
+    write-back."""
+    print("case stream rewritten output", flush=True)
+    lib = holo.lib()
+    t, K = Q4_0, 512
+    A1, A2, A3 = (synth.blocks(t, r, K, seed=60 + j) for j, r in enumerate((256, 256, 512)))
+    B, C = synth.blocks(t, 512, K, seed=70), synth.blocks(t, 256, K, seed=71)
+    x0, x1 = synth.normal(K, seed=72), synth.normal(K, seed=73)
+    dA = [_up(holo, a) for a in (A1, A2, A3)]
+    dB, dC, dx0, dx1 = _up(holo, B), _up(holo, C), _up(holo, x0), _up(holo, x1)
+    u1, u2, y, z = (holo.DeviceBuffer(4 * n) for n in (256, 256, 512, 512))
+    for later, rows, W2 in (("full", 512, B), ("half", 256, C)):
+        st = [holo.stream_stage([d.ptr for d in dA], [u1.ptr, u2.ptr, y.ptr], [256, 256, 512], dx0.ptr, K),
+              holo.stream_stage([dB.ptr if later == "full" else dC.ptr], [y.ptr], [rows], dx1.ptr, K),
+              holo.stream_stage([dA[2].ptr], [z.ptr], [512], dx1.ptr, K)]
+        plan = holo.StreamPlan(st, t)
+        assert plan.launch() == 0
+        lib.cuda_sync()
+        holo.check("stream rewritten output")
+        assert lib.holo_gemv_stream_status() == 0
+        first = oracle.matmul(t, A3, x0, 512, K)
+        want = first.copy()
+        want[:rows] = oracle.matmul(t, W2, x1, rows, K)
+        got = y.download(np.float32, 512)
+        for name, g, w in (("y", got, want), ("u1", u1.download(np.float32, 256), oracle.matmul(t, A1, x0, 256, K)),
+                           ("z", z.download(np.float32, 512), oracle.matmul(t, A3, x1, 512, K))):
+            e, m = normwise_err(g, w), max_rel_err(g, w)
+            assert e <= 1e-3 and m <= 1e-3, (later, name, e, m)
+        plan.close()
+
+
 def test_stream_graph_replays(holo, synth):
     """A plan launch captured in a HIP graph replays bit for bit like the
     eager launch, with eager launches of the same plan between replays (each
