@@ -233,9 +233,14 @@ void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, 
  * call's contents and every call on a device shares it: calls that overlap
  * on one device (issued on two streams) race.                              */
 int holo_gemm_q4_0_q8_0_noalloc(float *Y, const void *W, const void *Xq, int M, int N, int K);
-/* Y[M][N] = X[M][K] . W[N][K]^T for W in Q4_0: M >= 64 runs the f16 product
- * below (or, in HOLO_PREFILL_Q8_0 mode, quantises X and runs the Q8_0 product
- * above); M < 64 runs M fp32-activation GEMVs.                               */
+/* Y[M][N] = X[M][K] . W[N][K]^T for W in Q4_0.  M >= 64 runs, by the mode
+ * set below: the exact product (HOLO_PREFILL_EXACT, the default: X split into
+ * two f16 halves, x - xh - xl within 2^-22 |x|, times the block's integers,
+ * exact in f16, on the f16 matrix cores, block scales applied in fp32; fp32
+ * accuracy, within 1e-3 of the CPU path; X 16-byte aligned, |x| < 65504,
+ * else M GEMVs), the f16 product below (HOLO_PREFILL_F16) or the Q8_0
+ * product above (HOLO_PREFILL_Q8_0: X quantised to Q8_0).  M < 64 runs M
+ * GEMVs.                                                                     */
 void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int N, int K,
                             void *scratch_q8);
 /* The same over nmat = 1..3 Q4_0 matrices that multiply the same X in one
@@ -257,9 +262,10 @@ void holo_gemm_q4_0_q8_0_multi(float *const *Y, const void *const *W, const int 
 void holo_gemm_q4_0_f16(float *Y, const void *W, const float *X, int M, int N, int K);
 void holo_gemm_q4_0_f16_multi(float *const *Y, const void *const *W, const int *N, int nmat,
                               const float *X, int M, int K);
-/* Which product holo_matmul_batch_q4_0(_multi) runs for M >= 64: the f16
- * product (default; also taken only when X is 16-byte aligned) or the Q8_0
- * product above.                                                            */
+/* Which product every batched matmul (holo_matmul_batch*, the prompt
+ * forward) runs for M >= 64: HOLO_PREFILL_EXACT (default), HOLO_PREFILL_F16
+ * (Q4_0: the f16 product; other types: their f16 weight panel) or
+ * HOLO_PREFILL_Q8_0 (Q4_0 only: the Q8_0 product; other types as F16).    */
 /* The prompt layer's residual products (no reference counterpart; the batched
  * analogue of holo_matmul_add): Y = R + X . W^T, and Y = R + (silu(G) * U) .
  * W^T with silu(g) * u as cuda_silu_mul computes it -- the add in the
