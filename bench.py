@@ -717,6 +717,52 @@ def cpu_baseline(budget_s: float) -> dict:
 
 # ---- main ----------------------------------------------------------------------------------
 
+def decode_step_config5(lib, layers, A, reps):
+    """Config 5: the full decode step (32 layers + the Q8_0 head) as HIP graphs (unfused, fused, matmuls only)
+    and with its 128 layer GEMVs in one persistent holo_gemv_stream launch.  Returns (result, fused end-to-end
+    ms, head, ones)."""
+    head = holo.DeviceBuffer.from_array(synth.blocks(Q8_0, VOCAB, DIM, synth.tensor_seed(BASE_SEED, 5, 0, 7)))
+    ones = holo.DeviceBuffer.from_array(np.ones(DIM, np.float32))
+    full = capture(lib, lambda: decode_step(lib, layers[:32], head, A, ones, False))
+    mm = capture(lib, lambda: decode_step(lib, layers[:32], head, A, ones, True))
+    fz = capture(lib, lambda: decode_step(lib, layers[:32], head, A, ones, False, True))
+    unfused_ms = time_graphs(lib, [full], reps, 2) / reps
+    mm_ms = time_graphs(lib, [mm], reps, 2) / reps
+    full_ms = time_graphs(lib, [fz], reps, 2) / reps
+    lib.holo_graph_destroy(fz)
+    # the same step with the 128 layer GEMVs in one persistent launch
+    plan_mm, plan_fz = stream_step_plans(layers[:32], A, ones)
+    smm = capture(lib, lambda: decode_step_stream(lib, plan_mm, head, A, ones, False))
+    sfz = capture(lib, lambda: decode_step_stream(lib, plan_fz, head, A, ones, True))
+    smm_ms = time_graphs(lib, [smm], reps, 2) / reps
+    sfz_ms = time_graphs(lib, [sfz], reps, 2) / reps
+    if lib.holo_gemv_stream_status() != 0:
+        raise holo.HoloError("the persistent decode-step launch could not synchronise")
+    for g in (smm, sfz):
+        lib.holo_graph_destroy(g)
+    plan_mm.close()
+    plan_fz.close()
+    step_bytes = 32 * weight_bytes(Q4_0, LAYER) + holo.row_bytes(Q8_0, DIM) * VOCAB
+    best_mm = min(mm_ms, smm_ms)
+    c5 = {
+        "matmuls_ms": round(mm_ms, 4), "end_to_end_ms": round(full_ms, 4),
+        "end_to_end_unfused_ms": round(unfused_ms, 4),
+        "matmuls_stream_ms": round(smm_ms, 4), "end_to_end_stream_ms": round(sfz_ms, 4),
+        "weight_bytes": step_bytes, "matmul_weight_gbs": round(step_bytes / (mm_ms * 1e-3) / 1e9, 1),
+        "matmul_stream_weight_gbs": round(step_bytes / (smm_ms * 1e-3) / 1e9, 1),
+        "end_to_end_weight_gbs": round(step_bytes / (full_ms * 1e-3) / 1e9, 1),
+        "frac": round(step_bytes / (best_mm * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "frac_basis": "weight bytes of the step / the faster matmuls-only variant's ms, over 8 TB/s",
+        "launches": {"matmuls": 32 * 4 + 1, "end_to_end": 32 * 4 + 2, "end_to_end_unfused": 32 * 8 + 2,
+                     "matmuls_stream": 2, "end_to_end_stream": 3}}
+    lib.holo_graph_destroy(full)
+    lib.holo_graph_destroy(mm)
+    log(f"config 5 decode step: matmuls {mm_ms:.3f} ms, end-to-end {full_ms:.3f} ms "
+        f"(unfused {unfused_ms:.3f} ms); one stream launch: matmuls {smm_ms:.3f} ms, "
+        f"end-to-end {sfz_ms:.3f} ms")
+    return c5, full_ms, head, ones
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -735,6 +781,8 @@ def main():
                     help="only run the 512-token prompt forward over 32 layers, print its JSON and exit")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only run the single-GEMV measurements (configs 1 and 3, Q6_K), print their JSON and exit")
+    ap.add_argument("--decode-step-only", action="store_true",
+                    help="only run config 5 (the decode step as graphs and as one stream launch) and exit")
     ap.add_argument("--attention-only", action="store_true",
                     help="only run the decode-attention measurement, print its JSON and exit")
     a = ap.parse_args()
@@ -767,6 +815,12 @@ def main():
         return
     if a.attention_only:
         print(json.dumps({"decode_attention_llama2_7b": decode_attention(lib)}), flush=True)
+        return
+    if a.decode_step_only:
+        s = lib.holo_stream_create()
+        lib.holo_set_stream(s)  # graphs capture a non-null stream
+        c5 = decode_step_config5(lib, [Mats(Q4_0, i, 2, LAYER) for i in range(32)], Acts(), 4)[0]
+        print(json.dumps({"config5_decode_step": c5}), flush=True)
         return
     if a.prompt_only:
         layers = [Mats(Q4_0, i, 2, LAYER) for i in range(32)]
@@ -816,47 +870,10 @@ def main():
 
         # config 5: full decode step (32 layers + Q8_0 head)
         if a.layers >= 32:
-            head = holo.DeviceBuffer.from_array(synth.blocks(Q8_0, VOCAB, DIM, synth.tensor_seed(BASE_SEED, 5, 0, 7)))
-            ones = holo.DeviceBuffer.from_array(np.ones(DIM, np.float32))
-            full = capture(lib, lambda: decode_step(lib, layers[:32], head, A, ones, False))
-            mm = capture(lib, lambda: decode_step(lib, layers[:32], head, A, ones, True))
-            fz = capture(lib, lambda: decode_step(lib, layers[:32], head, A, ones, False, True))
-            reps = max(3, a.steps // 16)
-            unfused_ms = time_graphs(lib, [full], reps, 2) / reps
-            mm_ms = time_graphs(lib, [mm], reps, 2) / reps
-            full_ms = time_graphs(lib, [fz], reps, 2) / reps
-            lib.holo_graph_destroy(fz)
-            # the same step with the 128 layer GEMVs in one persistent launch
-            plan_mm, plan_fz = stream_step_plans(layers[:32], A, ones)
-            smm = capture(lib, lambda: decode_step_stream(lib, plan_mm, head, A, ones, False))
-            sfz = capture(lib, lambda: decode_step_stream(lib, plan_fz, head, A, ones, True))
-            smm_ms = time_graphs(lib, [smm], reps, 2) / reps
-            sfz_ms = time_graphs(lib, [sfz], reps, 2) / reps
-            if lib.holo_gemv_stream_status() != 0:
-                raise holo.HoloError("the persistent decode-step launch could not synchronise")
-            for g in (smm, sfz):
-                lib.holo_graph_destroy(g)
-            plan_mm.close()
-            plan_fz.close()
-            step_bytes = 32 * bytes_step + holo.row_bytes(Q8_0, DIM) * VOCAB
-            best_mm = min(mm_ms, smm_ms)
-            extra["config5_decode_step"] = {
-                "matmuls_ms": round(mm_ms, 4), "end_to_end_ms": round(full_ms, 4),
-                "end_to_end_unfused_ms": round(unfused_ms, 4),
-                "matmuls_stream_ms": round(smm_ms, 4), "end_to_end_stream_ms": round(sfz_ms, 4),
-                "weight_bytes": step_bytes, "matmul_weight_gbs": round(step_bytes / (mm_ms * 1e-3) / 1e9, 1),
-                "end_to_end_weight_gbs": round(step_bytes / (full_ms * 1e-3) / 1e9, 1),
-                "frac": round(step_bytes / (best_mm * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                "frac_basis": "weight bytes of the step / the faster matmuls-only variant's ms, over 8 TB/s",
-                "launches": {"matmuls": 32 * 4 + 1, "end_to_end": 32 * 4 + 2, "end_to_end_unfused": 32 * 8 + 2,
-                             "matmuls_stream": 2, "end_to_end_stream": 3}}
+            c5, full_ms, head, ones = decode_step_config5(lib, layers, A, max(3, a.steps // 16))
+            extra["config5_decode_step"] = c5
             if not a.no_cpu:
                 extra["config5_decode_step"]["cpu_baseline"] = cpu_decode_step(a.cpu_budget / 2)
-            lib.holo_graph_destroy(full)
-            lib.holo_graph_destroy(mm)
-            log(f"config 5 decode step: matmuls {mm_ms:.3f} ms, end-to-end {full_ms:.3f} ms "
-                f"(unfused {unfused_ms:.3f} ms); one stream launch: matmuls {smm_ms:.3f} ms, "
-                f"end-to-end {sfz_ms:.3f} ms")
             extra["config4_prompt_forward_512"] = prompt_forward(lib, layers, head, ones, full_ms)
             log(f"config 4 prompt forward: {extra['config4_prompt_forward_512']}")
             extra["prompt_forward_512_q4_k_m"] = prompt_forward_q4_k_m(lib)
