@@ -1232,28 +1232,33 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
         }
         max_units = o.units > max_units ? o.units : max_units;
     }
-    // Exchange buffers: one per distinct output vector (keyed by its address),
-    // as many words as the most rows any stage writes there.  A stage's x or r
-    // that an earlier stage wrote is read from that buffer (xsrc / rsrc: the
-    // last writer before it); an input that overlaps an earlier output in any
-    // other way, an output that overlaps its own stage's x, two outputs of one
-    // stage in one vector, or outputs that partly overlap are rejected.
+    // Exchange buffers: a word per row of a stage output (stage s, output m),
+    // and for an output with a designated reader a record buffer of the same
+    // size.  A stage's x or r that an earlier stage wrote is read from the
+    // buffers of its last writer (xsrc / rsrc, output xm / rm) and must not
+    // extend past what that writer stored; an input that overlaps an earlier
+    // output in any other way, an output that overlaps its own stage's x, two
+    // outputs of one stage in one vector, or outputs that partly overlap are
+    // rejected (the caller's vectors are keyed by address for these rules).
     struct OutVec {
         uint64_t ptr;
-        int rows, last;
-        size_t off;
+        int rows;        // the most rows any stage wrote there (for the overlap rules)
+        int last, lastm; // the last writer so far and its output index
     };
     std::vector<OutVec> outs;
     std::vector<int> xo(nstages, -1), ro(nstages, -1), yo(3 * (size_t)nstages, -1);
+    std::vector<int> xm(nstages, 0), rm(nstages, 0);
+    auto out_rows = [&](int s, int m) { return stages[s].rows[stages[s].gate_up ? 0 : m]; };
     auto overlap = [](uint64_t a, uint64_t an, uint64_t b, uint64_t bn) { return a < b + bn && b < a + an; };
-    auto source = [&](uint64_t ptr, int n, int &idx, int &src) {
+    auto source = [&](uint64_t ptr, int n, int &idx, int &src, int &srcm) {
         idx = -1;
         src = -1;
         for (size_t i = 0; i < outs.size(); i++) {
             if (outs[i].ptr == ptr) {
-                if (outs[i].rows < n) return false;
+                if (out_rows(outs[i].last, outs[i].lastm) < n) return false;
                 idx = (int)i;
                 src = outs[i].last;
+                srcm = outs[i].lastm;
             } else if (overlap(ptr, 4ull * n, outs[i].ptr, 4ull * outs[i].rows)) {
                 return false;
             }
@@ -1264,8 +1269,8 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
     for (int s = 0; s < nstages && xok; s++) {
         const holo_stream_stage_t &in = stages[s];
         StreamStage &o = host[s];
-        xok = source(o.x, in.in_dim, xo[s], o.xsrc);
-        if (xok && in.r) xok = source(o.r, in.rows[0], ro[s], o.rsrc);
+        xok = source(o.x, in.in_dim, xo[s], o.xsrc, xm[s]);
+        if (xok && in.r) xok = source(o.r, in.rows[0], ro[s], o.rsrc, rm[s]);
         const int nout = in.gate_up ? 1 : in.nmat;
         for (int m = 0; m < nout && xok; m++) {
             const uint64_t y = (uint64_t)in.y[m];
@@ -1278,7 +1283,7 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
             }
             if (!xok) break;
             if (hit < 0) {
-                outs.push_back(OutVec{y, rows, s, 0});
+                outs.push_back(OutVec{y, rows, s, m});
                 hit = (int)outs.size() - 1;
             } else if (outs[hit].last == s) {
                 xok = false;
@@ -1286,14 +1291,16 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
             } else {
                 outs[hit].rows = rows > outs[hit].rows ? rows : outs[hit].rows;
                 outs[hit].last = s;
+                outs[hit].lastm = m;
             }
             yo[3 * (size_t)s + m] = hit;
         }
     }
     if (!xok) {
         delete[] host;
-        HOLO_REJECT("holo_gemv_stream_create: a stage input that overlaps an earlier output other than exactly, or "
-                    "an output overlapping its own input or another output");
+        HOLO_REJECT("holo_gemv_stream_create: a stage input that overlaps an earlier output other than exactly or "
+                    "reads past what its last writer stored, or an output overlapping its own input or another "
+                    "output");
         return nullptr;
     }
     // the plain stores of a row go to its last writer in the plan
@@ -1311,17 +1318,10 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
             host[s].ystart[m] = later;
         }
     }
-    size_t nwords = 0;
-    for (OutVec &v : outs) {
-        v.off = nwords;
-        nwords += (size_t)v.rows;
-    }
     // Plane records: each written output (stage s, output m) is designated to
     // the first later stage that reads exactly that output as its x (its
     // in_dim = the output's rows) when the 16-row tiles of stage s each fall in
-    // one matrix (every matrix's rows a multiple of 16).  The records of an
-    // output vector share one buffer, as its exchange words do (the tags tell
-    // the writers apart).
+    // one matrix (every matrix's rows a multiple of 16).
     std::vector<int> lp(nstages, -1), rd(3 * (size_t)nstages, -1);
     for (int t = 0; t < nstages; t++) {
         const int s = host[t].xsrc;
@@ -1334,9 +1334,65 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
             lp[t] = xo[t];
         }
     }
+    // Which stage outputs share buffers.  A later writer of a vector reuses
+    // the previous writer's buffers only when every stage that reads the
+    // previous version has finished reading it, on every workgroup, before any
+    // workgroup can store the new one: some stage u after the reader t, up to
+    // the new writer, waits for the whole output of a stage p >= t (its x is
+    // an earlier output: its copy checks every word's tag, so every workgroup
+    // has stored p's outputs, after having read t's inputs).  A residual read
+    // by the new writer itself is of its own rows and needs no order.  Else
+    // the new writer gets buffers of its own: a fast workgroup's store would
+    // overwrite words that a slow one still has to read.  (The decode step's
+    // chain shares throughout.)
+    std::vector<int> grp(3 * (size_t)nstages, -1);
+    std::vector<int> grows;  // rows of each buffer group
+    std::vector<char> grec;  // the group holds plane records
+    {
+        std::vector<int> last_k(outs.size(), -1);  // key 3 s + m of the vector's last writer so far
+        for (int s = 0; s < nstages; s++) {
+            const int nout = stages[s].gate_up ? 1 : stages[s].nmat;
+            for (int m = 0; m < nout; m++) {
+                const size_t k = 3 * (size_t)s + m;
+                const int i = yo[k], pk = last_k[i];
+                bool share = pk >= 0;
+                if (share) {
+                    const int ps = pk / 3, pm = pk % 3;
+                    for (int t = ps + 1; t <= s && share; t++) {
+                        const bool rx = xo[t] == i && host[t].xsrc == ps && xm[t] == pm;
+                        const bool rr = ro[t] == i && host[t].rsrc == ps && rm[t] == pm;
+                        if (!rx && !(rr && t < s)) continue;
+                        bool ordered = false;
+                        for (int u = t + 1; u <= s && !ordered; u++) ordered = xo[u] >= 0 && host[u].xsrc >= t;
+                        share = ordered;
+                    }
+                }
+                if (share) {
+                    grp[k] = grp[(size_t)pk];
+                    grows[grp[k]] = out_rows(s, m) > grows[grp[k]] ? out_rows(s, m) : grows[grp[k]];
+                } else {
+                    grp[k] = (int)grows.size();
+                    grows.push_back(out_rows(s, m));
+                    grec.push_back(0);
+                }
+                if (rd[k] >= 0) grec[grp[k]] = 1;
+                last_k[i] = (int)k;
+            }
+        }
+    }
+    std::vector<size_t> gw(grows.size()), gr(grows.size());
+    size_t nwords = 0, nrec = 0;
+    for (size_t g = 0; g < grows.size(); g++) {
+        gw[g] = nwords;
+        nwords += (size_t)grows[g];
+        gr[g] = nrec;
+        if (grec[g]) nrec += (size_t)grows[g];
+    }
+    auto woff = [&](size_t k) { return gw[grp[k]]; };
+    auto roff = [&](size_t k) { return gr[grp[k]]; };
     // launch counter line, done counter line, one done word per workgroup
     const size_t kWordsHeader = (512 + 4 * (size_t)grid + 255) & ~(size_t)255;
-    const size_t words_bytes = kWordsHeader + 16 * nwords;
+    const size_t words_bytes = kWordsHeader + 8 * (nwords + nrec);
     uint8_t *words = nullptr;
     if (hipMalloc((void **)&words, words_bytes) != hipSuccess) {
         (void)hipGetLastError();
@@ -1346,21 +1402,22 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
     }
     HOLO_CHECK(hipMemset(words, 0, words_bytes));
     const uint64_t wbase = (uint64_t)(uintptr_t)words + kWordsHeader;
-    const uint64_t rbase = wbase + 8 * nwords;
+    const uint64_t rbase = wbase + 8 * nwords;  // the record buffers follow the words
     for (int s = 0; s < nstages; s++) {
         const holo_stream_stage_t &in = stages[s];
         StreamStage &o = host[s];
         const int nout = in.gate_up ? 1 : in.nmat;
         for (int m = 0; m < 3; m++) {
-            const int mm = m < nout ? m : 0;
-            const int i = yo[3 * (size_t)s + mm], t = rd[3 * (size_t)s + mm];
-            o.lly[m] = wbase + 8 * outs[i].off;
-            o.llp[m] = m < nout && t >= 0 ? rbase + 8 * outs[i].off : 0;
+            const size_t k = 3 * (size_t)s + (m < nout ? m : 0);
+            const int t = rd[k];
+            o.lly[m] = wbase + 8 * woff(k);
+            o.llp[m] = m < nout && t >= 0 ? rbase + 8 * roff(k) : 0;
             o.pnw[m] = m < nout && t >= 0 ? (uint64_t)stages[t].norm_w : 0;
         }
-        o.llx = xo[s] >= 0 && lp[s] < 0 ? wbase + 8 * outs[xo[s]].off : 0;
-        o.lpx = lp[s] >= 0 ? rbase + 8 * outs[lp[s]].off : 0;
-        o.llr = ro[s] >= 0 ? wbase + 8 * outs[ro[s]].off : 0;
+        const size_t kx = 3 * (size_t)(o.xsrc >= 0 ? o.xsrc : 0) + xm[s];
+        o.llx = xo[s] >= 0 && lp[s] < 0 ? wbase + 8 * woff(kx) : 0;
+        o.lpx = lp[s] >= 0 ? rbase + 8 * roff(kx) : 0;
+        o.llr = ro[s] >= 0 ? wbase + 8 * woff(3 * (size_t)o.rsrc + rm[s]) : 0;
         const int xb = o.lpx ? o.units * 256 : o.units * (o.llx ? 256 : 128) + (in.norm_w ? o.units * 128 : 0);
         max_xbuf = xb > max_xbuf ? xb : max_xbuf;
     }

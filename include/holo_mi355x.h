@@ -121,8 +121,11 @@ int holo_gemv_chain_status(void);
  * first later stage that reads an output as x (its in_dim = the output's
  * rows, all of the producing stage's matrices with rows a multiple of 16)
  * receives it as plane records: the reader's int8 activation planes, made by
- * the producer.  Rejected: an input overlapping an earlier output other than
- * exactly, an output overlapping its own stage's x or another output.  The
+ * the producer.  Every stage output has exchange buffers of its own, so a
+ * later stage may rewrite a vector that earlier stages still read.  Rejected:
+ * an input overlapping an earlier output other than exactly, or reading past
+ * the rows its last writer stored; an output overlapping its own stage's x or
+ * another output.  The
  * activations are 22-bit fixed point per 16 values (the separate GEMV calls:
  * per 32), so results match the separate MFMA-path calls to about 1e-6
  * normwise per stage and the CPU reference within the 1e-3 bar.  The weight

@@ -300,6 +300,35 @@ def test_stream_rewritten_output(holo, synth, oracle):
         plan.close()
 
 
+def test_stream_rewrite_while_read(holo, synth, oracle):
+    """A vector rewritten by a later stage that depends on nothing after the
+    stage still reading the old contents (y = A x; z = B y; y = C x): a fast
+    workgroup may store the new y while a slow one still copies the old one,
+    so every stage output has exchange buffers of its own.  z must be B (A x)
+    and the final y must be C x, over repeated launches."""
+    print("case stream rewrite while read", flush=True)
+    lib = holo.lib()
+    t, K = Q4_0, 1024
+    A, B, Cm = (synth.blocks(t, 1024, K, seed=80 + j) for j in range(3))
+    x = synth.normal(K, seed=83)
+    dA, dB, dC, dx = _up(holo, A), _up(holo, B), _up(holo, Cm), _up(holo, x)
+    y, z = holo.DeviceBuffer(4 * 1024), holo.DeviceBuffer(4 * 1024)
+    plan = holo.StreamPlan([holo.stream_stage([dA.ptr], [y.ptr], [1024], dx.ptr, K),
+                            holo.stream_stage([dB.ptr], [z.ptr], [1024], y.ptr, K),
+                            holo.stream_stage([dC.ptr], [y.ptr], [1024], dx.ptr, K)], t)
+    ya = oracle.matmul(t, A, x, 1024, K)
+    want_z, want_y = oracle.matmul(t, B, ya, 1024, K), oracle.matmul(t, Cm, x, 1024, K)
+    for rep in range(3):
+        assert plan.launch() == 0
+        lib.cuda_sync()
+        holo.check("stream rewrite while read")
+        assert lib.holo_gemv_stream_status() == 0
+        for name, got, want in (("z", z.download(np.float32, 1024), want_z), ("y", y.download(np.float32, 1024), want_y)):
+            e, m = normwise_err(got, want), max_rel_err(got, want)
+            assert e <= 1e-3 and m <= 1e-3, (rep, name, e, m)
+    plan.close()
+
+
 def test_stream_graph_replays(holo, synth):
     """A plan launch captured in a HIP graph replays bit for bit like the
     eager launch, with eager launches of the same plan between replays (each
@@ -375,6 +404,10 @@ def test_stream_rejects_unsupported(holo, synth):
         holo.StreamPlan([holo.stream_stage([W3.ptr], [x512.ptr], [512], x512.ptr, 512)], Q4_0)
     with pytest.raises(holo.HoloError):  # two outputs of one stage in one vector
         holo.StreamPlan([holo.stream_stage([W3.ptr, W3.ptr], [big.ptr, big.ptr], [512, 512], x512.ptr, 512)], Q4_0)
+    W5 = _up(holo, synth.blocks(Q4_0, 256, 512, seed=9))
+    with pytest.raises(holo.HoloError):  # reads past what the last writer (256 rows) stored
+        holo.StreamPlan([first, holo.stream_stage([W5.ptr], [big.ptr], [256], x512.ptr, 512),
+                         holo.stream_stage([W3.ptr], [y.ptr], [16], big.ptr, 512)], Q4_0)
     ok = holo.StreamPlan([first, holo.stream_stage([W3.ptr], [y.ptr], [16], big.ptr, 512)], Q4_0)
     ok.close()
     lib.cuda_sync()
