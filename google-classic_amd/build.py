@@ -77,6 +77,21 @@ def build_synth() -> Path:
     return SYNTH_LIB
 
 
+HARNESS_SRC = ROOT / "tests" / "abi_harness.c"
+HARNESS = ROOT / "tests" / "abi_harness"
+
+
+def build_harness() -> Path:
+    """The C caller of the drop-in boundary (tests/abi_harness.c), linked
+    against the HIP library with an rpath to it; the GPU tests run it."""
+    cc = shutil.which("gcc") or "cc"
+    tmp = HARNESS.with_suffix(".tmp")
+    _run([cc, "-std=c11", "-O2", "-Wall", "-Werror", f"-I{ROOT / 'include'}", str(HARNESS_SRC),
+          f"-L{PKG}", "-lholo_mi355x", "-Wl,-rpath,$ORIGIN/../google-classic_amd", "-o", str(tmp)])
+    os.replace(tmp, HARNESS)
+    return HARNESS
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--hip", action="store_true", help="only the HIP library")
@@ -85,6 +100,7 @@ def main() -> None:
     a = ap.parse_args()
     if not a.synth:
         print("built", build_hip(a.j))
+        print("built", build_harness())
     if not a.hip:
         print("built", build_synth())
 

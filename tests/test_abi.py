@@ -77,3 +77,14 @@ def test_reference_caller_links_against_the_library(tmp_path):
     r = subprocess.run(["gcc", str(main), *objs, "-o", str(exe), f"-L{LIB.parent}", "-lholo_mi355x",
                         f"-Wl,-rpath,{LIB.parent}", "-lm", "-fopenmp"], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_c_harness_is_built_and_linked():
+    """tests/abi_harness (built by build()) links the library through its
+    rpath, and without arguments prints its usage without touching a GPU."""
+    harness = ROOT / "tests" / "abi_harness"
+    assert harness.exists(), "run build()"
+    r = subprocess.run(["ldd", str(harness)], capture_output=True, text=True)
+    assert "libholo_mi355x.so" in r.stdout and "not found" not in r.stdout, r.stdout
+    r = subprocess.run([str(harness)], capture_output=True, text=True, timeout=30)
+    assert r.returncode == 1 and "usage" in r.stderr
