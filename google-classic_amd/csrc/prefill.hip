@@ -803,9 +803,10 @@ void holo_prefill_set_mode(int mode)
 // Exact mode (the default): the exact product (prefill_exact.hip) when every
 // operand fits it; otherwise the callers run fp32-activation GEMVs per row,
 // never a lower-precision product.
-static bool exact_fits(const void *const *W, const int *types, int nmat, const float *X, const float *U, int K)
+static bool exact_fits(const void *const *W, const int *types, int nmat, const float *X, const float *U, int M, int K)
 {
-    if (!X || ((uintptr_t)X & 15u) || ((uintptr_t)U & 15u)) return false;
+    // the product addresses each activation half (M*K f16) with 32-bit byte offsets
+    if (!X || ((uintptr_t)X & 15u) || ((uintptr_t)U & 15u) || (int64_t)M * K > (1LL << 30)) return false;
     for (int i = 0; i < nmat; i++)
         if (!W[i] || !exact_ok(types[i], K, W[i])) return false;
     return true;
@@ -821,7 +822,7 @@ void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int 
 {
     if (M <= 0 || N <= 0) return;
     const int t = HOLO_TYPE_Q4_0;
-    if (M >= 64 && exact_mode() && exact_fits(&W, &t, 1, X, nullptr, K)) {
+    if (M >= 64 && exact_mode() && exact_fits(&W, &t, 1, X, nullptr, M, K)) {
         exact_product(&Y, &W, &t, &N, 1, X, nullptr, nullptr, M, K);
         return;
     }
@@ -849,7 +850,7 @@ void holo_matmul_batch_q4_0_add(float *Y, const void *W, const float *X, const f
         return;
     }
     const int t = HOLO_TYPE_Q4_0;
-    if (M >= 64 && exact_mode() && exact_fits(&W, &t, 1, X, nullptr, K)) {
+    if (M >= 64 && exact_mode() && exact_fits(&W, &t, 1, X, nullptr, M, K)) {
         exact_product(&Y, &W, &t, &N, 1, X, nullptr, R, M, K);
         return;
     }
@@ -879,7 +880,7 @@ void holo_matmul_batch_q4_0_swiglu_add(float *Y, const void *W, float *G, const 
         return;
     }
     const int t = HOLO_TYPE_Q4_0;
-    if (M >= 64 && exact_mode() && exact_fits(&W, &t, 1, G, U, K)) {
+    if (M >= 64 && exact_mode() && exact_fits(&W, &t, 1, G, U, M, K)) {
         exact_product(&Y, &W, &t, &N, 1, G, U, R, M, K);
         return;
     }
@@ -900,7 +901,7 @@ void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const i
         return;
     }
     const int T[3] = {HOLO_TYPE_Q4_0, HOLO_TYPE_Q4_0, HOLO_TYPE_Q4_0};
-    if (M >= 64 && exact_mode() && exact_fits(W, T, nmat, X, nullptr, K)) {
+    if (M >= 64 && exact_mode() && exact_fits(W, T, nmat, X, nullptr, M, K)) {
         exact_product(Y, W, T, N, nmat, X, nullptr, nullptr, M, K);
         return;
     }
@@ -998,7 +999,7 @@ void holo_matmul_batch(float *Y, const void *W, const float *X, int M, int N, in
         HOLO_REJECT("holo_matmul_batch: null pointer");
         return;
     }
-    if (M >= 64 && exact_mode() && exact_fits(&W, &type, 1, X, nullptr, K)) {
+    if (M >= 64 && exact_mode() && exact_fits(&W, &type, 1, X, nullptr, M, K)) {
         exact_product(&Y, &W, &type, &N, 1, X, nullptr, nullptr, M, K);
         return;
     }
@@ -1022,7 +1023,7 @@ void holo_matmul_batch_multi(float *const *Y, const void *const *W, const int *N
         return;
     }
     const int T[3] = {type, type, type};
-    if (M >= 64 && exact_mode() && exact_fits(W, T, nmat, X, nullptr, K)) {
+    if (M >= 64 && exact_mode() && exact_fits(W, T, nmat, X, nullptr, M, K)) {
         exact_product(Y, W, T, N, nmat, X, nullptr, nullptr, M, K);
         return;
     }
@@ -1049,7 +1050,7 @@ void holo_matmul_batch_multi_types(float *const *Y, const void *const *W, const 
         holo_matmul_batch_multi(Y, W, N, nmat, X, M, K, types[0]);
         return;
     }
-    if (M >= 64 && exact_mode() && exact_fits(W, types, nmat, X, nullptr, K)) {
+    if (M >= 64 && exact_mode() && exact_fits(W, types, nmat, X, nullptr, M, K)) {
         exact_product(Y, W, types, N, nmat, X, nullptr, nullptr, M, K);
         return;
     }
@@ -1074,7 +1075,7 @@ void holo_matmul_batch_add(float *Y, const void *W, const float *X, const float 
         HOLO_REJECT("holo_matmul_batch_add: null pointer");
         return;
     }
-    if (M >= 64 && exact_mode() && exact_fits(&W, &type, 1, X, nullptr, K)) {
+    if (M >= 64 && exact_mode() && exact_fits(&W, &type, 1, X, nullptr, M, K)) {
         exact_product(&Y, &W, &type, &N, 1, X, nullptr, R, M, K);  // the add in the GEMM's store
         return;
     }
@@ -1105,7 +1106,7 @@ void holo_matmul_batch_swiglu_add(float *Y, const void *W, float *G, const float
         HOLO_REJECT("holo_matmul_batch_swiglu_add: null pointer");
         return;
     }
-    if (M >= 64 && exact_mode() && exact_fits(&W, &type, 1, G, U, K)) {
+    if (M >= 64 && exact_mode() && exact_fits(&W, &type, 1, G, U, M, K)) {
         exact_product(&Y, &W, &type, &N, 1, G, U, R, M, K);  // silu(G) * U in the activation halves
         return;
     }

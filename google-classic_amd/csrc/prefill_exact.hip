@@ -138,6 +138,53 @@ struct WRaw<EW_Q4_K> {
     uint32_t j;
 };
 
+constexpr uint32_t kXBufWord3 = 0x00020000u;  // raw buffer resource: 32-bit data format
+
+// The per-thread part of every stage load's address, computed once per
+// workgroup: a stage then adds only its block index (a scalar multiple) to a
+// 32-bit offset, where computing each 64-bit address per load and block cost
+// about as many VALU instructions as the block's scale epilogue.  Rows and
+// columns past the last one are clamped here, blocks past the last one per
+// stage (they are re-read, in bounds, and never used).
+template <int WF, int WM, int WN, int S>
+struct XAddr {
+    using G = XGeo<WM, WN, S>;
+    static constexpr bool PANEL = WF == EW_P16 || WF == EW_F16;
+    static constexpr int NWI = PANEL ? G::NWP : G::NB;
+    __amdgpu_buffer_rsrc_t rah, ral;  // the activation halves (M*K f16 each, at most 2 GiB: exact_fits)
+    uint32_t oa[G::NA];               // byte offset of A piece i at block 0
+    int ka[G::NA];                    // its block within the stage
+    int64_t ow[NWI];                  // weights: byte offset of the piece's row (at block 0)
+    int kw[NWI];                      // its block within the stage
+
+    __device__ __forceinline__ XAddr(const ExactArgs &a, const ExactMat &w, int tid, int m0, int n0)
+    {
+        const int nb = a.nb;
+        const uint32_t abytes = (uint32_t)((int64_t)a.M * nb * 64);
+        rah = __builtin_amdgcn_make_buffer_rsrc((void *)a.Ah, (short)0, (int)abytes, kXBufWord3);
+        ral = __builtin_amdgcn_make_buffer_rsrc((void *)a.Al, (short)0, (int)abytes, kXBufWord3);
+#pragma unroll
+        for (int i = 0; i < G::NA; i++) {
+            const int p = tid + G::NT * i, r = p / (4 * S), c = p % (4 * S);
+            oa[i] = (uint32_t)min(m0 + r, a.M - 1) * (uint32_t)(nb * 64) + (uint32_t)(c % 4) * 16u;
+            ka[i] = c / 4;
+        }
+#pragma unroll
+        for (int i = 0; i < NWI; i++) {
+            if constexpr (PANEL) {
+                const int p = min(tid + G::NT * i, G::TN * S * 4 - 1), n = p / (4 * S), c = p % (4 * S);
+                ow[i] = (int64_t)min(n0 + n, w.N - 1) * nb * 64 + (c % 4) * 16;
+                kw[i] = c / 4;
+            } else {
+                const int v = min(tid + G::NT * i, G::TN * S - 1), n = v / S;
+                const int64_t row = min(n0 + n, w.N - 1);
+                ow[i] = WF == EW_Q4_K ? row * (nb / 8) * 144 : row * nb * (WF == EW_Q4_0 ? 18 : 34);
+                kw[i] = v % S;
+            }
+        }
+    }
+};
+
 // Registers of one stage between its global loads and its LDS writes: blocks
 // kb0 .. kb0+S-1 of the workgroup's rows and columns.  Indices past the last
 // row, column or block re-read the last one (in bounds, never used).
@@ -151,16 +198,15 @@ struct XStage {
     v4u rw[PANEL ? G::NWP : 1];
     float rs[WF == EW_P16 ? G::NWS : 1];
 
-    __device__ __forceinline__ void fetch(const ExactArgs &a, const ExactMat &w, int tid, int m0, int n0, int kb0)
+    __device__ __forceinline__ void fetch(const ExactArgs &a, const ExactMat &w, const XAddr<WF, WM, WN, S> &ad,
+                                          int tid, int m0, int n0, int kb0)
     {
         const int nb = a.nb;
-        const int64_t K = (int64_t)nb * 32;
 #pragma unroll
         for (int i = 0; i < G::NA; i++) {
-            const int p = tid + G::NT * i, r = p / (4 * S), c = p % (4 * S);
-            const int64_t o = (int64_t)min(m0 + r, a.M - 1) * K + (int64_t)min(kb0 + c / 4, nb - 1) * 32 + (c % 4) * 8;
-            ah[i] = *(const v4u *)(a.Ah + o);
-            al[i] = *(const v4u *)(a.Al + o);
+            const uint32_t o = ad.oa[i] + (uint32_t)min(kb0 + ad.ka[i], nb - 1) * 64u;
+            ah[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(ad.rah, (int)o, 0, 0));
+            al[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(ad.ral, (int)o, 0, 0));
         }
         if constexpr (WF == EW_Q4_K) {
 #pragma unroll
@@ -170,13 +216,9 @@ struct XStage {
             }
         }
         if constexpr (PANEL) {
-            const _Float16 *wp = (const _Float16 *)w.W;
 #pragma unroll
-            for (int i = 0; i < G::NWP; i++) {
-                const int p = min(tid + G::NT * i, G::TN * S * 4 - 1), n = p / (4 * S), c = p % (4 * S);
-                rw[i] = *(const v4u *)(wp + (int64_t)min(n0 + n, w.N - 1) * K + (int64_t)min(kb0 + c / 4, nb - 1) * 32 +
-                                      (c % 4) * 8);
-            }
+            for (int i = 0; i < G::NWP; i++)
+                rw[i] = *(const v4u *)(w.W + ad.ow[i] + (int64_t)min(kb0 + ad.kw[i], nb - 1) * 64);
             if constexpr (WF == EW_P16) {
 #pragma unroll
                 for (int i = 0; i < G::NWS; i++) {
@@ -188,16 +230,16 @@ struct XStage {
         }
 #pragma unroll
         for (int i = 0; i < G::NB; i++) {
-            const int v = min(tid + G::NT * i, G::TN * S - 1), n = v / S, b = min(kb0 + v % S, nb - 1);
-            const int64_t g = (int64_t)min(n0 + n, w.N - 1) * nb + b;
+            const int b = min(kb0 + ad.kw[i], nb - 1);
             if constexpr (WF == EW_Q4_0) {
-                rb[i].u = load_q4_0(w.W, g, w.w_bytes);
+                rb[i].u = load_q4_0_at(w.W, ad.ow[i] + (int64_t)b * 18, w.w_bytes);
             } else if constexpr (WF == EW_Q8_0) {
-                rb[i].u = load_q8_0(w.W, g, w.w_bytes);
+                rb[i].u = load_q8_0_at(w.W, ad.ow[i] + (int64_t)b * 34, w.w_bytes);
             } else if constexpr (WF == EW_Q4_K) {
-                // unit g: superblock g / 8 (144 bytes, 16-byte aligned), sub-block g % 8
-                const uint8_t *sb = w.W + (g >> 3) * 144;
-                rb[i].j = (uint32_t)(g & 7);
+                // block b of the row: superblock b / 8 (144 bytes, 16-byte
+                // aligned; nb is a multiple of 8), sub-block b % 8
+                const uint8_t *sb = w.W + ad.ow[i] + (int64_t)(b >> 3) * 144;
+                rb[i].j = (uint32_t)(b & 7);
                 rb[i].h = *(const v4u *)sb;
                 rb[i].q = *(const v4u *)(sb + 16 + 16 * rb[i].j);
             }
@@ -393,11 +435,12 @@ __global__ __launch_bounds__(256, OCC) void gemm_exact_k(ExactArgs a)
     // index), so every slot issues the same loads and the loop has one exit,
     // at its latch, with a trip count known up front: the compiler's wait
     // before each stash is then exactly that stage's own loads.
+    const XAddr<WF, WM, WN, S> ad(a, w, tid, m0, n0);
     XStage<WF, WM, WN, S> st[RD];
 #pragma unroll
-    for (int d = 0; d < RD; d++) st[d].fetch(a, w, tid, m0, n0, d * S);
+    for (int d = 0; d < RD; d++) st[d].fetch(a, w, ad, tid, m0, n0, d * S);
     st[0].stash(lds, tid);
-    st[0].fetch(a, w, tid, m0, n0, RD * S);
+    st[0].fetch(a, w, ad, tid, m0, n0, RD * S);
     __syncthreads();
     const int rounds = (nst + RD - 1) / RD;
     for (int q = 0; q < rounds; q++) {
@@ -408,7 +451,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_exact_k(ExactArgs a)
             // stage k + 1 (register set (d + 1) % RD) into the other buffer,
             // then that set fetches stage k + 1 + RD
             st[(d + 1) % RD].stash(lds + ((k + 1) & 1) * G::STAGE, tid);
-            st[(d + 1) % RD].fetch(a, w, tid, m0, n0, (k + 1 + RD) * S);
+            st[(d + 1) % RD].fetch(a, w, ad, tid, m0, n0, (k + 1 + RD) * S);
             __syncthreads();
         }
     }

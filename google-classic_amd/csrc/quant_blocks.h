@@ -63,10 +63,10 @@ struct Q4_0Unit {
     uint32_t dh;    // d as raw f16 bits
 };
 
-// W: matrix base (4-byte aligned); g: block index; total: matrix bytes.
-__device__ __forceinline__ Q4_0Unit load_q4_0(const uint8_t *__restrict__ W, int64_t g, int64_t total)
+// W: matrix base (4-byte aligned); o: the block's byte offset (18 g for block
+// g); total: matrix bytes.
+__device__ __forceinline__ Q4_0Unit load_q4_0_at(const uint8_t *__restrict__ W, int64_t o, int64_t total)
 {
-    int64_t o = g * 18;
     uint32_t s = (uint32_t)(o & 3);
     const uint8_t *p = W + (o - s);
     u32x4 a = *(const u32x4 *)p;
@@ -87,6 +87,11 @@ __device__ __forceinline__ Q4_0Unit load_q4_0(const uint8_t *__restrict__ W, int
     u.d = half_bits_to_float(u.dh);
     return u;
 }
+// g: block index
+__device__ __forceinline__ Q4_0Unit load_q4_0(const uint8_t *__restrict__ W, int64_t g, int64_t total)
+{
+    return load_q4_0_at(W, g * 18, total);
+}
 
 // ---- Q8_0 ------------------------------------------------------------------
 struct Q8_0Unit {
@@ -95,9 +100,8 @@ struct Q8_0Unit {
     uint32_t dh;    // d as raw f16 bits
 };
 
-__device__ __forceinline__ Q8_0Unit load_q8_0(const uint8_t *__restrict__ W, int64_t g, int64_t total)
+__device__ __forceinline__ Q8_0Unit load_q8_0_at(const uint8_t *__restrict__ W, int64_t o, int64_t total)
 {
-    int64_t o = g * 34;
     uint32_t s = (uint32_t)(o & 3);
     const uint8_t *p = W + (o - s);
     u32x4 a = *(const u32x4 *)p;
@@ -120,6 +124,10 @@ __device__ __forceinline__ Q8_0Unit load_q8_0(const uint8_t *__restrict__ W, int
     u.dh = __builtin_amdgcn_alignbyte(a.y, a.x, s) & 0xFFFFu;
     u.d = half_bits_to_float(u.dh);
     return u;
+}
+__device__ __forceinline__ Q8_0Unit load_q8_0(const uint8_t *__restrict__ W, int64_t g, int64_t total)
+{
+    return load_q8_0_at(W, g * 34, total);
 }
 
 // ---- Q4_K ------------------------------------------------------------------
