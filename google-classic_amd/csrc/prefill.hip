@@ -208,6 +208,54 @@ __device__ __forceinline__ void nib_f16(uint32_t x, uint32_t lo[2], uint32_t hi[
     hi[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(c64, t1, 0x04030402u)) + off);
 }
 
+// Per-thread load addresses of a tile, computed once: each piece's row (and
+// its column within a block) at block 0, and its block within the stage.  A
+// stage's fetch then only adds the block offset (clamped to the last block).
+// Rows past the last row or column re-read the last one (in bounds, never used).
+template <int WM, int WN, int S, bool XF16, int WGM = 2, int WGN = 2, bool WP = false>
+struct PAddr {
+    using G = PGeo<WM, WN, S, WGM, WGN>;
+    static constexpr int NWI = WP ? G::NWP : G::NB;
+    const uint8_t *pa[G::NA];            // activation piece i: its row, column (c % 4) * 8
+    int ka[G::NA];                       // its block within the stage
+    const uint16_t *pd[XF16 ? 1 : G::ND];  // activation scales: the row of scale i
+    int kd[XF16 ? 1 : G::ND];
+    int64_t ow[NWI];                     // weights: byte offset of the piece's row (+ column) at block 0
+    int kw[NWI];
+
+    __device__ __forceinline__ PAddr(const PrefillArgs &a, const PrefillMat &w, int tid, int m0, int n0)
+    {
+        const int nb = a.nb;
+        const int64_t K = (int64_t)nb * 32;
+#pragma unroll
+        for (int i = 0; i < G::NA; i++) {
+            const int p = tid + G::NT * i, r = p / (4 * S), c = p % (4 * S);
+            pa[i] = (const uint8_t *)(a.P + (int64_t)min(m0 + r, a.M - 1) * K + (c % 4) * 8);
+            ka[i] = c / 4;
+        }
+        if constexpr (!XF16) {
+#pragma unroll
+            for (int i = 0; i < G::ND; i++) {
+                const int v = min(tid + G::NT * i, G::TM * S - 1);
+                pd[i] = a.D + (int64_t)min(m0 + v / S, a.M - 1) * nb;
+                kd[i] = v % S;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NWI; i++) {
+            if constexpr (WP) {
+                const int p = tid + G::NT * i, n = p / (4 * S), c = p % (4 * S);
+                ow[i] = (int64_t)min(n0 + n, w.N - 1) * K * 2 + (c % 4) * 16;
+                kw[i] = c / 4;
+            } else {
+                const int v = min(tid + G::NT * i, G::TN * S - 1);
+                ow[i] = (int64_t)min(n0 + v / S, w.N - 1) * nb * 18;
+                kw[i] = v % S;
+            }
+        }
+    }
+};
+
 // Registers of one stage in flight between its global loads and its LDS
 // writes: blocks kb0 .. kb0+S-1 of the workgroup's rows and columns; block
 // indices past the row's last block read the last block again (in bounds,
@@ -221,42 +269,30 @@ struct PStage {
     using G = PGeo<WM, WN, S, WGM, WGN>;
     static_assert(!WP || XF16, "a weight panel needs f16 activations");
     v4u ra[G::NA];
-    uint32_t rd[G::ND];
-    Q4_0Unit rb[WP ? 1 : G::NB];
+    uint16_t rd[G::ND];  // as loaded: a widening here would wait for the load
+    Q4_0Raw rb[WP ? 1 : G::NB];
     v4u rw[WP ? G::NWP : 1];
 
-    __device__ __forceinline__ void fetch(const PrefillArgs &a, const PrefillMat &w, int tid, int m0, int n0, int kb0)
+    __device__ __forceinline__ void fetch(const PrefillArgs &a, const PrefillMat &w,
+                                          const PAddr<WM, WN, S, XF16, WGM, WGN, WP> &ad, int kb0)
     {
         const int nb = a.nb;
-        const int64_t K = (int64_t)nb * 32;
 #pragma unroll
-        for (int i = 0; i < G::NA; i++) {
-            const int p = tid + G::NT * i, r = p / (4 * S), c = p % (4 * S);
-            const int m = min(m0 + r, a.M - 1), b = min(kb0 + c / 4, nb - 1);
-            ra[i] = *(const v4u *)(a.P + (int64_t)m * K + (int64_t)b * 32 + (c % 4) * 8);
-        }
+        for (int i = 0; i < G::NA; i++)
+            ra[i] = *(const v4u *)(ad.pa[i] + (int64_t)min(kb0 + ad.ka[i], nb - 1) * 64);
         if constexpr (!XF16) {
 #pragma unroll
-            for (int i = 0; i < G::ND; i++) {
-                const int v = min(tid + G::NT * i, G::TM * S - 1), r = v / S, b = min(kb0 + v % S, nb - 1);
-                rd[i] = a.D[(int64_t)min(m0 + r, a.M - 1) * nb + b];
-            }
+            for (int i = 0; i < G::ND; i++) rd[i] = ad.pd[i][min(kb0 + ad.kd[i], nb - 1)];
         }
         if constexpr (WP) {
-            const _Float16 *wp = (const _Float16 *)w.W;
 #pragma unroll
-            for (int i = 0; i < G::NWP; i++) {
-                const int p = tid + G::NT * i, n = p / (4 * S), c = p % (4 * S);
-                const int b = min(kb0 + c / 4, nb - 1);
-                rw[i] = *(const v4u *)(wp + (int64_t)min(n0 + n, w.N - 1) * K + (int64_t)b * 32 + (c % 4) * 8);
-            }
+            for (int i = 0; i < G::NWP; i++)
+                rw[i] = *(const v4u *)((const uint8_t *)w.W + ad.ow[i] + (int64_t)min(kb0 + ad.kw[i], nb - 1) * 64);
             return;
         }
 #pragma unroll
-        for (int i = 0; i < G::NB; i++) {
-            const int v = min(tid + G::NT * i, G::TN * S - 1), n = v / S, b = min(kb0 + v % S, nb - 1);
-            rb[i] = load_q4_0(w.W, (int64_t)min(n0 + n, w.N - 1) * nb + b, w.w_bytes);
-        }
+        for (int i = 0; i < G::NB; i++)
+            rb[i] = load_q4_0_raw(w.W, ad.ow[i] + (int64_t)min(kb0 + ad.kw[i], nb - 1) * 18, w.w_bytes);
     }
 
     // registers -> one LDS stage buffer (weights unpacked to f16 q-8)
@@ -271,7 +307,7 @@ struct PStage {
 #pragma unroll
             for (int i = 0; i < G::ND; i++) {
                 const int v = tid + G::NT * i;
-                if (v < G::TM * S) ((uint16_t *)(base + G::AD_OFF))[v] = (uint16_t)rd[i];
+                if (v < G::TM * S) ((uint16_t *)(base + G::AD_OFF))[v] = rd[i];
             }
         }
         if constexpr (WP) {
@@ -287,12 +323,13 @@ struct PStage {
         for (int i = 0; i < G::NB; i++) {
             const int v = tid + G::NT * i, n = v / S, s = v % S;
             if (v < G::TN * S) {
+                const Q4_0Unit u = q4_0_unit(rb[i]);
                 uint32_t lo[8], hi[8];
 #pragma unroll
-                for (int j = 0; j < 4; j++) nib_f16(rb[i].q[j], &lo[2 * j], &hi[2 * j]);
+                for (int j = 0; j < 4; j++) nib_f16(u.q[j], &lo[2 * j], &hi[2 * j]);
                 if constexpr (XF16) {
                     // w16 = f16_rne(dw * (q - 8)): one packed f16 multiply per pair
-                    const _Float16 dw = __builtin_bit_cast(_Float16, (uint16_t)rb[i].dh);
+                    const _Float16 dw = __builtin_bit_cast(_Float16, (uint16_t)u.dh);
                     const h2 d2 = {dw, dw};
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
@@ -305,7 +342,7 @@ struct PStage {
                 dst[1] = v4u{lo[4], lo[5], lo[6], lo[7]};  // k = 8..15
                 dst[2] = v4u{hi[0], hi[1], hi[2], hi[3]};  // k = 16..23
                 dst[3] = v4u{hi[4], hi[5], hi[6], hi[7]};  // k = 24..31
-                if constexpr (!XF16) ((uint16_t *)(base + G::BD_OFF))[v] = (uint16_t)rb[i].dh;
+                if constexpr (!XF16) ((uint16_t *)(base + G::BD_OFF))[v] = (uint16_t)u.dh;
             }
         }
     }
@@ -402,38 +439,30 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_q4_0_f16_k(PrefillAr
         }
     };
 
-    PStage<WM, WN, S, XF16, WGM, WGN, WP> pa;
-    pa.fetch(a, w, tid, m0, n0, 0);
-    pa.stash(lds, tid);
-    if constexpr (D == 1) {
-        // stage st+1 loads while stage st is multiplied
-        __syncthreads();
-        for (int st = 0; st < nst; st++) {
-            if (st + 1 < nst) pa.fetch(a, w, tid, m0, n0, (st + 1) * S);
-            compute(st & 1, st * S);
-            if (st + 1 < nst) pa.stash(lds + ((st + 1) & 1) * G::STAGE, tid);
-            __syncthreads();
-        }
-    } else {
-        // two register sets carry stages st+1 and st+2 while stage st is
-        // multiplied, so each stage's loads have two stages of products to land
-        PStage<WM, WN, S, XF16, WGM, WGN, WP> pb;
-        if (nst > 1) pa.fetch(a, w, tid, m0, n0, S);
-        if (nst > 2) pb.fetch(a, w, tid, m0, n0, 2 * S);
-        __syncthreads();
-        for (int st = 0; st < nst; st += 2) {
-            compute(0, st * S);
-            if (st + 1 < nst) {
-                pa.stash(lds + G::STAGE, tid);
-                if (st + 3 < nst) pa.fetch(a, w, tid, m0, n0, (st + 3) * S);
-            }
-            __syncthreads();
-            if (st + 1 >= nst) break;
-            compute(1, (st + 1) * S);
-            if (st + 2 < nst) {
-                pb.stash(lds, tid);
-                if (st + 4 < nst) pb.fetch(a, w, tid, m0, n0, (st + 4) * S);
-            }
+    // Ring of D register stages: set d holds stage k with k % D == d.
+    // Stages past the last block re-read the last one (fetch clamps every
+    // index) and compute skips their blocks, so every slot issues the same
+    // loads and the loop has one exit, at its latch, with a trip count known
+    // up front: the compiler's wait before each stash is then exactly that
+    // stage's own loads (a conditional fetch made it wait for every load in
+    // flight, the other set's too).
+    const PAddr<WM, WN, S, XF16, WGM, WGN, WP> ad(a, w, tid, m0, n0);
+    PStage<WM, WN, S, XF16, WGM, WGN, WP> st[D];
+#pragma unroll
+    for (int d = 0; d < D; d++) st[d].fetch(a, w, ad, d * S);
+    st[0].stash(lds, tid);
+    st[0].fetch(a, w, ad, D * S);
+    __syncthreads();
+    const int rounds = (nst + D - 1) / D;
+    for (int q = 0; q < rounds; q++) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int k = q * D + d;
+            compute(k & 1, k * S);
+            // stage k + 1 (register set (d + 1) % D) into the other buffer,
+            // then that set fetches stage k + 1 + D
+            st[(d + 1) % D].stash(lds + ((k + 1) & 1) * G::STAGE, tid);
+            st[(d + 1) % D].fetch(a, w, ad, (k + 1 + D) * S);
             __syncthreads();
         }
     }

@@ -126,11 +126,11 @@ template <int WF>
 struct WRaw;
 template <>
 struct WRaw<EW_Q4_0> {
-    Q4_0Unit u;
+    Q4_0Raw r;
 };
 template <>
 struct WRaw<EW_Q8_0> {
-    Q8_0Unit u;
+    Q8_0Raw r;
 };
 template <>
 struct WRaw<EW_Q4_K> {
@@ -232,9 +232,9 @@ struct XStage {
         for (int i = 0; i < G::NB; i++) {
             const int b = min(kb0 + ad.kw[i], nb - 1);
             if constexpr (WF == EW_Q4_0) {
-                rb[i].u = load_q4_0_at(w.W, ad.ow[i] + (int64_t)b * 18, w.w_bytes);
+                rb[i].r = load_q4_0_raw(w.W, ad.ow[i] + (int64_t)b * 18, w.w_bytes);
             } else if constexpr (WF == EW_Q8_0) {
-                rb[i].u = load_q8_0_at(w.W, ad.ow[i] + (int64_t)b * 34, w.w_bytes);
+                rb[i].r = load_q8_0_raw(w.W, ad.ow[i] + (int64_t)b * 34, w.w_bytes);
             } else if constexpr (WF == EW_Q4_K) {
                 // block b of the row: superblock b / 8 (144 bytes, 16-byte
                 // aligned; nb is a multiple of 8), sub-block b % 8
@@ -283,16 +283,18 @@ struct XStage {
             uint32_t lo[8], hi[8];
             float scale, mn = 0.f;
             if constexpr (WF == EW_Q4_0) {
+                const Q4_0Unit u = q4_0_unit(rb[i].r);
 #pragma unroll
-                for (int j = 0; j < 4; j++) nibbles_f16(rb[i].u.q[j], (_Float16)-8.0f, &lo[2 * j], &hi[2 * j]);
-                scale = rb[i].u.d;
+                for (int j = 0; j < 4; j++) nibbles_f16(u.q[j], (_Float16)-8.0f, &lo[2 * j], &hi[2 * j]);
+                scale = u.d;
             } else if constexpr (WF == EW_Q8_0) {
+                const Q8_0Unit u = q8_0_unit(rb[i].r);
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    int8s_f16(rb[i].u.q[j], &lo[2 * j]);
-                    int8s_f16(rb[i].u.q[4 + j], &hi[2 * j]);
+                    int8s_f16(u.q[j], &lo[2 * j]);
+                    int8s_f16(u.q[4 + j], &hi[2 * j]);
                 }
-                scale = rb[i].u.d;
+                scale = u.d;
             } else if constexpr (WF == EW_Q4_K) {
                 const v4u q = rb[i].q;
 #pragma unroll

@@ -63,29 +63,49 @@ struct Q4_0Unit {
     uint32_t dh;    // d as raw f16 bits
 };
 
+// The words of one Q4_0 block as loaded, before realignment.  A staging
+// pipeline keeps these in its registers and builds the unit (q4_0_unit) only
+// where it uses it: realigning right after the loads would make the wave wait
+// for them there, one stage early.
+struct Q4_0Raw {
+    u32x4 a;     // the 16 bytes from the block's 4-byte-aligned start
+    uint32_t e;  // the next 4 (2 at the end of the matrix)
+    uint32_t s;  // the block's offset within a (0 or 2)
+};
+
 // W: matrix base (4-byte aligned); o: the block's byte offset (18 g for block
 // g); total: matrix bytes.
-__device__ __forceinline__ Q4_0Unit load_q4_0_at(const uint8_t *__restrict__ W, int64_t o, int64_t total)
+__device__ __forceinline__ Q4_0Raw load_q4_0_raw(const uint8_t *__restrict__ W, int64_t o, int64_t total)
 {
-    uint32_t s = (uint32_t)(o & 3);
-    const uint8_t *p = W + (o - s);
-    u32x4 a = *(const u32x4 *)p;
+    Q4_0Raw r;
+    r.s = (uint32_t)(o & 3);
+    const uint8_t *p = W + (o - r.s);
+    r.a = *(const u32x4 *)p;
     // The 5th dword reaches 2 bytes past the block when s == 0; for the last
     // block of the matrix read only its own 2 bytes.
-    uint32_t e;
-    if (o - s + 20 <= total)
-        e = *(const uint32_t *)(p + 16);
+    if (o - r.s + 20 <= total)
+        r.e = *(const uint32_t *)(p + 16);
     else
-        e = *(const uint16_t *)(p + 16);
-    uint32_t sel = realign_sel(s);
+        r.e = *(const uint16_t *)(p + 16);
+    return r;
+}
+
+__device__ __forceinline__ Q4_0Unit q4_0_unit(const Q4_0Raw &r)
+{
+    const uint32_t sel = realign_sel(r.s);
     Q4_0Unit u;
-    u.q[0] = perm(a.y, a.x, sel);
-    u.q[1] = perm(a.z, a.y, sel);
-    u.q[2] = perm(a.w, a.z, sel);
-    u.q[3] = perm(e, a.w, sel);
-    u.dh = __builtin_amdgcn_alignbyte(a.y, a.x, s) & 0xFFFFu;
+    u.q[0] = perm(r.a.y, r.a.x, sel);
+    u.q[1] = perm(r.a.z, r.a.y, sel);
+    u.q[2] = perm(r.a.w, r.a.z, sel);
+    u.q[3] = perm(r.e, r.a.w, sel);
+    u.dh = __builtin_amdgcn_alignbyte(r.a.y, r.a.x, r.s) & 0xFFFFu;
     u.d = half_bits_to_float(u.dh);
     return u;
+}
+
+__device__ __forceinline__ Q4_0Unit load_q4_0_at(const uint8_t *__restrict__ W, int64_t o, int64_t total)
+{
+    return q4_0_unit(load_q4_0_raw(W, o, total));
 }
 // g: block index
 __device__ __forceinline__ Q4_0Unit load_q4_0(const uint8_t *__restrict__ W, int64_t g, int64_t total)
@@ -100,30 +120,47 @@ struct Q8_0Unit {
     uint32_t dh;    // d as raw f16 bits
 };
 
-__device__ __forceinline__ Q8_0Unit load_q8_0_at(const uint8_t *__restrict__ W, int64_t o, int64_t total)
+// The words of one Q8_0 block as loaded (as Q4_0Raw).
+struct Q8_0Raw {
+    u32x4 a, b;  // the 32 bytes from the block's 4-byte-aligned start
+    uint32_t e;  // the next 4 (2 at the end of the matrix)
+    uint32_t s;  // the block's offset within a (0 or 2)
+};
+
+__device__ __forceinline__ Q8_0Raw load_q8_0_raw(const uint8_t *__restrict__ W, int64_t o, int64_t total)
 {
-    uint32_t s = (uint32_t)(o & 3);
-    const uint8_t *p = W + (o - s);
-    u32x4 a = *(const u32x4 *)p;
-    u32x4 b = *(const u32x4 *)(p + 16);
-    uint32_t e;
-    if (o - s + 36 <= total)
-        e = *(const uint32_t *)(p + 32);
+    Q8_0Raw r;
+    r.s = (uint32_t)(o & 3);
+    const uint8_t *p = W + (o - r.s);
+    r.a = *(const u32x4 *)p;
+    r.b = *(const u32x4 *)(p + 16);
+    if (o - r.s + 36 <= total)
+        r.e = *(const uint32_t *)(p + 32);
     else
-        e = *(const uint16_t *)(p + 32);
-    uint32_t sel = realign_sel(s);
+        r.e = *(const uint16_t *)(p + 32);
+    return r;
+}
+
+__device__ __forceinline__ Q8_0Unit q8_0_unit(const Q8_0Raw &r)
+{
+    const uint32_t sel = realign_sel(r.s);
     Q8_0Unit u;
-    u.q[0] = perm(a.y, a.x, sel);
-    u.q[1] = perm(a.z, a.y, sel);
-    u.q[2] = perm(a.w, a.z, sel);
-    u.q[3] = perm(b.x, a.w, sel);
-    u.q[4] = perm(b.y, b.x, sel);
-    u.q[5] = perm(b.z, b.y, sel);
-    u.q[6] = perm(b.w, b.z, sel);
-    u.q[7] = perm(e, b.w, sel);
-    u.dh = __builtin_amdgcn_alignbyte(a.y, a.x, s) & 0xFFFFu;
+    u.q[0] = perm(r.a.y, r.a.x, sel);
+    u.q[1] = perm(r.a.z, r.a.y, sel);
+    u.q[2] = perm(r.a.w, r.a.z, sel);
+    u.q[3] = perm(r.b.x, r.a.w, sel);
+    u.q[4] = perm(r.b.y, r.b.x, sel);
+    u.q[5] = perm(r.b.z, r.b.y, sel);
+    u.q[6] = perm(r.b.w, r.b.z, sel);
+    u.q[7] = perm(r.e, r.b.w, sel);
+    u.dh = __builtin_amdgcn_alignbyte(r.a.y, r.a.x, r.s) & 0xFFFFu;
     u.d = half_bits_to_float(u.dh);
     return u;
+}
+
+__device__ __forceinline__ Q8_0Unit load_q8_0_at(const uint8_t *__restrict__ W, int64_t o, int64_t total)
+{
+    return q8_0_unit(load_q8_0_raw(W, o, total));
 }
 __device__ __forceinline__ Q8_0Unit load_q8_0(const uint8_t *__restrict__ W, int64_t g, int64_t total)
 {
