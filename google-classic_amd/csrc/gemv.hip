@@ -562,18 +562,31 @@ struct MfmaStage {
     __device__ __forceinline__ gfloat *ybase(int m) const { return (gfloat *)(y0 + (m == 2 ? dy2 : m == 1 ? dy1 : 0)); }
 
     // Slot q: local tile q / P, item (segment) wave + 8 * (q % P).  Slots
-    // past the end issue nothing (a wave cannot end before its loads return).
+    // past the end issue nothing (a wave cannot end before its loads return),
+    // except with ALWAYS, where such a slot re-reads row 0 of the first
+    // matrix (in bounds, never used).  ALWAYS is the first slot, issued while
+    // the activations are staged: with a path that issues no loads, or two
+    // load paths, the compiler could not count the loads in flight and waited
+    // for all of them, this slot's too, before converting the activations.
     // Weights are read once per launch: the loads are non-temporal, so they
     // do not push the activations and other reused lines out of the caches.
+    template <bool ALWAYS = false>
     __device__ __forceinline__ void issue(Raw2<FMT> &b, int q) const
     {
-        if (q >= Q) return;
-        const int k = q / P, p = q - k * P;
+        if (!ALWAYS && q >= Q) return;
+        const bool none = ALWAYS && q >= Q;
+        const int k = none ? F : q / P, p = none ? 0 : q - k * P;
         int row0, rend;
         tile_rows(k, row0, rend);
+        if (none) {
+            row0 = 0;
+            rend = 1;
+        }
         const int seg = min(wave + kWaves * p, G - 1);
         const bool half = 16 * seg + 16 > units;
-        if (kFastIssue && fast && k < F && !half) {
+        // ALWAYS takes the general path alone: one load site, so the loads
+        // in flight can be counted wherever they merge
+        if (!ALWAYS && kFastIssue && fast && k < F && !half) {
             // a full tile in one matrix (GATEUP: 8 rows of each): the
             // uniform item base plus the lane's fixed offsets
             uint64_t base;
@@ -692,32 +705,44 @@ struct MfmaStage {
     {
         constexpr int NPX = 2 * P;
         constexpr int CPOL = XDEV ? kDeviceScope : 0;
-        float4 pre[NPX];
+        constexpr bool NORM = !XDEV && P <= 2;
+        float4 pre[NPX], w4[NORM ? NPX : 1];
         x_preload<NPX, CPOL>(args.x, units, pre);
-        if (issue_first) issue(first, 0);
-        if constexpr (!XDEV && P <= 2) {
-            if (args.nw) rms_norm_pre(pre);
+        // the norm weights before the first slot's loads, and every load
+        // unconditional (a null weight reads as zeros through an empty buffer
+        // range): the conversion then waits for the activations and the
+        // weights only, while the first slot's weights are still in flight
+        if constexpr (NORM) nw_preload(w4);
+        if (issue_first) issue<true>(first, 0);
+        if constexpr (NORM) {
+            if (args.nw) rms_norm_pre(pre, w4);
         }
         x_stage<FMT, XM_MFMA, NPX, CPOL>(args.x, units, (void *)ldsb, pre);
         if (threadIdx.x < kZeroBytes / 16) ((uint4 *)(ldsb + zero_off))[threadIdx.x] = make_uint4(0, 0, 0, 0);
         for (int i = threadIdx.x; i < args.max_tiles; i += kThreads) tcnt[i] = 0;
     }
 
+    // The norm weights of this thread's x chunks (zeros past the row, and all
+    // zeros without a norm).
+    template <int NPX>
+    __device__ __forceinline__ void nw_preload(float4 (&w4)[NPX]) const
+    {
+        const __amdgpu_buffer_rsrc_t rs =
+            args.nw ? x_rsrc((const float *)args.nw, units) : x_rsrc((const float *)args.x, 0);
+#pragma unroll
+        for (int k = 0; k < NPX; k++) {
+            const int i = threadIdx.x + kThreads * k;
+            w4[k] = load_x4<0>(rs, i < units * 8 ? (uint32_t)i * 16u : kOutOfRange);
+        }
+    }
     // x <- x * (1/sqrt(mean(x^2) + eps)) * nw, in registers before staging, as
     // rms_norm_k computes it (cuda_ops.cu:1479-1504): every chunk of x is in
     // pre[] (the host checks in_dim), so each workgroup reduces the whole
     // vector itself; the 8 wave sums meet in the first wave's stage, which is
     // not written before the staging barrier.
     template <int NPX>
-    __device__ __forceinline__ void rms_norm_pre(float4 (&pre)[NPX]) const
+    __device__ __forceinline__ void rms_norm_pre(float4 (&pre)[NPX], const float4 (&w4)[NPX]) const
     {
-        const int tid = threadIdx.x;
-        float4 w4[NPX];
-#pragma unroll
-        for (int k = 0; k < NPX; k++) {
-            const int i = tid + kThreads * k;
-            w4[k] = i < units * 8 ? ((const float4 *)args.nw)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
         float ss = 0.f;
 #pragma unroll
         for (int k = 0; k < NPX; k++)  // chunks past the end were loaded as zeros
