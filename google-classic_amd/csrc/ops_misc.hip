@@ -385,7 +385,9 @@ static void launch_attn_prefill_mfma(float *out, const float *q, const float *kc
 // R rows (4, 2 or 1), which share the activation loads.  Measured on MI355X:
 // 32000x4096 30.3 us (3.5 TB/s), 11008x4096 13.5 us, 4096x11008 14.9 us
 // (2.5 TB/s); issuing the next task's loads ahead of the current task's
-// arithmetic (software pipelining) measured slower at every R.
+// arithmetic (software pipelining) measured slower at every R, and so did
+// loading all 64 activations of a task with its weights (one round trip
+// instead of four, but 159 registers at R = 4: 39 against 30 us at 32000 rows).
 
 __device__ __forceinline__ float q6_ubyte_dot(uint32_t q, const float4 x)
 {
