@@ -47,7 +47,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 // Weight source of one launch.
-enum ExactW { EW_Q4_0 = 0, EW_Q8_0 = 1, EW_Q4_K = 2, EW_P16 = 3, EW_F16 = 4 };
+enum ExactW { EW_Q4_0 = 0, EW_Q8_0 = 1, EW_Q4_K = 2, EW_P16 = 3, EW_F16 = 4, EW_Q6_K = 5 };
 
 constexpr int kExactMats = 3;
 
@@ -117,6 +117,7 @@ struct XGeo {
     static constexpr int NA = TM * S * 4 / NT;           // 16-byte activation pieces per thread and half
     static constexpr int NAS = (TM * S + NT - 1) / NT;   // block sums per thread
     static constexpr int NB = (TN * S + NT - 1) / NT;    // weight blocks per thread
+    static constexpr int NH = (TN * S * 2 + NT - 1) / NT;  // Q6_K: 16-weight half blocks per thread
     static constexpr int NWP = (TN * S * 4 + NT - 1) / NT;  // 16-byte weight-panel pieces per thread
     static constexpr int NWS = (TN * 2 * S + NT - 1) / NT;  // group scales per thread
     static_assert((TM * S * 4) % NT == 0, "activation pieces must split evenly over the threads");
@@ -137,6 +138,21 @@ struct WRaw<EW_Q4_K> {
     v4u h, q;
     uint32_t j;
 };
+// Half p of a 32-weight sub-block of a Q6_K superblock (210 bytes: ql[128],
+// qh[64], int8 scales[16], f16 d; quant.c:241-271): sub-block j of half hf
+// holds, for l = 0..31, q = ((ql[64hf + 32(j&1) + l] >> 4(j>>1)) & 15) |
+// (((qh[32hf + l] >> 2j) & 3) << 4), weight (d * sc[8hf + 2j + l/16]) * (q - 32);
+// half p is l = 16p .. 16p + 15, one scale.  l and h are the dwords around its
+// 16 ql and 16 qh bytes as loaded (the runs start s = 0 or 2 bytes into their
+// first dword), sc its scale byte (bits 0-7 or 8-15 of the pair), d.  Half
+// blocks rather than blocks, so that every thread of the workgroup unpacks
+// (with whole blocks, half of the waves did and the others waited at the
+// barrier).
+template <>
+struct WRaw<EW_Q6_K> {
+    uint32_t l[5], h[5];
+    uint32_t sc, d, s, j;
+};
 
 constexpr uint32_t kXBufWord3 = 0x00020000u;  // raw buffer resource: 32-bit data format
 
@@ -150,7 +166,7 @@ template <int WF, int WM, int WN, int S>
 struct XAddr {
     using G = XGeo<WM, WN, S>;
     static constexpr bool PANEL = WF == EW_P16 || WF == EW_F16;
-    static constexpr int NWI = PANEL ? G::NWP : G::NB;
+    static constexpr int NWI = PANEL ? G::NWP : WF == EW_Q6_K ? G::NH : G::NB;
     __amdgpu_buffer_rsrc_t rah, ral;  // the activation halves (M*K f16 each, at most 2 GiB: exact_fits)
     uint32_t oa[G::NA];               // byte offset of A piece i at block 0
     int ka[G::NA];                    // its block within the stage
@@ -175,6 +191,11 @@ struct XAddr {
                 const int p = min(tid + G::NT * i, G::TN * S * 4 - 1), n = p / (4 * S), c = p % (4 * S);
                 ow[i] = (int64_t)min(n0 + n, w.N - 1) * nb * 64 + (c % 4) * 16;
                 kw[i] = c / 4;
+            } else if constexpr (WF == EW_Q6_K) {
+                // half block v: row v / 2S, block (v % 2S) / 2, half v % 2
+                const int v = min(tid + G::NT * i, G::TN * S * 2 - 1);
+                ow[i] = (int64_t)min(n0 + v / (2 * S), w.N - 1) * (nb / 8) * 210;
+                kw[i] = v % (2 * S);
             } else {
                 const int v = min(tid + G::NT * i, G::TN * S - 1), n = v / S;
                 const int64_t row = min(n0 + n, w.N - 1);
@@ -194,7 +215,8 @@ struct XStage {
     static constexpr bool PANEL = WF == EW_P16 || WF == EW_F16;
     v4u ah[G::NA], al[G::NA];
     float as[WF == EW_Q4_K ? G::NAS : 1];
-    WRaw<WF == EW_Q4_0 || WF == EW_Q8_0 || WF == EW_Q4_K ? WF : EW_Q4_0> rb[PANEL ? 1 : G::NB];
+    WRaw<WF == EW_Q4_0 || WF == EW_Q8_0 || WF == EW_Q4_K || WF == EW_Q6_K ? WF : EW_Q4_0>
+        rb[PANEL ? 1 : WF == EW_Q6_K ? G::NH : G::NB];
     v4u rw[PANEL ? G::NWP : 1];
     float rs[WF == EW_P16 ? G::NWS : 1];
 
@@ -225,6 +247,40 @@ struct XStage {
                     const int v = min(tid + G::NT * i, G::TN * 2 * S - 1), n = v / (2 * S), j = v % (2 * S);
                     rs[i] = w.WS[(int64_t)min(n0 + n, w.N - 1) * (2 * nb) + min(2 * kb0 + j, 2 * nb - 1)];
                 }
+            }
+            return;
+        }
+        if constexpr (WF == EW_Q6_K) {
+            // half p of sub-block b & 7 of superblock b / 8 (nb is a multiple
+            // of 8); superblocks sit at even addresses, the runs at the
+            // superblock's offset within a dword, and the fifth dword of a
+            // run still lies inside the superblock
+            typedef __attribute__((address_space(1))) const uint32_t g32;
+            typedef __attribute__((address_space(1))) const uint16_t g16;
+            typedef __attribute__((address_space(1))) const u32x4 g128;
+#pragma unroll
+            for (int i = 0; i < G::NH; i++) {
+                const int b = min(kb0 + (ad.kw[i] >> 1), nb - 1), p = ad.kw[i] & 1;
+                const uint8_t *sb = w.W + ad.ow[i] + (int64_t)(b >> 3) * 210;
+                const uint32_t sub = (uint32_t)(b & 7), hf = sub >> 2, j = sub & 3;
+                const uint32_t sh = (uint32_t)((uintptr_t)sb & 3u);
+                const uintptr_t pl = (uintptr_t)(sb + 64 * hf + 32 * (j & 1) + 16 * p - sh);
+                const uintptr_t ph = (uintptr_t)(sb + 128 + 32 * hf + 16 * p - sh);
+                const u32x4 l4 = *(const g128 *)pl, h4 = *(const g128 *)ph;
+                rb[i].l[0] = l4.x;
+                rb[i].l[1] = l4.y;
+                rb[i].l[2] = l4.z;
+                rb[i].l[3] = l4.w;
+                rb[i].l[4] = *(const g32 *)(pl + 16);
+                rb[i].h[0] = h4.x;
+                rb[i].h[1] = h4.y;
+                rb[i].h[2] = h4.z;
+                rb[i].h[3] = h4.w;
+                rb[i].h[4] = *(const g32 *)(ph + 16);
+                rb[i].sc = *(const g16 *)(sb + 192 + 8 * hf + 2 * j);
+                rb[i].d = *(const g16 *)(sb + 208);
+                rb[i].s = sh;
+                rb[i].j = j;
             }
             return;
         }
@@ -273,6 +329,31 @@ struct XStage {
                     const int v = tid + G::NT * i;
                     if (v < G::TN * 2 * S) ((float *)(base + G::BS))[v] = rs[i];
                 }
+            }
+            return;
+        }
+        if constexpr (WF == EW_Q6_K) {
+#pragma unroll
+            for (int i = 0; i < G::NH; i++) {
+                const int v = tid + G::NT * i, n = v / (2 * S), sb = (v % (2 * S)) >> 1, p = v & 1;
+                if (v >= G::TN * S * 2) continue;
+                const WRaw<EW_Q6_K> &r = rb[i];
+                const uint32_t shq = 4 * (r.j >> 1), shh = 2 * r.j;
+                uint32_t wv[8];
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const uint32_t l = __builtin_amdgcn_alignbyte(r.l[c + 1], r.l[c], r.s);
+                    const uint32_t hb = __builtin_amdgcn_alignbyte(r.h[c + 1], r.h[c], r.s);
+                    const uint32_t q = ((l >> shq) & 0x0F0F0F0Fu) | (((hb >> shh) & 0x03030303u) << 4);
+                    wv[2 * c] = f16_pair(q, 0x04010400u, (_Float16)-1056.0f);  // 1024 + q - 1056 = q - 32
+                    wv[2 * c + 1] = f16_pair(q, 0x04030402u, (_Float16)-1056.0f);
+                }
+                v4u *dst = (v4u *)(base + G::B + (n * G::ROW + sb * 32 + 16 * p) * 2);
+                dst[0] = v4u{wv[0], wv[1], wv[2], wv[3]};  // k = 16p .. 16p + 7
+                dst[1] = v4u{wv[4], wv[5], wv[6], wv[7]};
+                // exact: 11-bit x 8-bit
+                ((float *)(base + G::BS))[n * 2 * S + 2 * sb + p] =
+                    half_bits_to_float(r.d) * (float)(int8_t)((r.sc >> (8 * p)) & 0xFFu);
             }
             return;
         }
@@ -408,7 +489,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_exact_k(ExactArgs a)
                         acc[mi][ni] = mfma16(ah1[mi], b1[ni], acc[mi][ni]);
                         acc[mi][ni] = mfma16(al0[mi], b0[ni], acc[mi][ni]);
                         acc[mi][ni] = mfma16(al1[mi], b1[ni], acc[mi][ni]);
-                    } else if constexpr (WF == EW_P16) {
+                    } else if constexpr (WF == EW_P16 || WF == EW_Q6_K) {
                         v16f c = mfma16(al0[mi], b0[ni], mfma16(ah0[mi], b0[ni], zero));
 #pragma unroll
                         for (int r = 0; r < 16; r++) acc[mi][ni][r] = __builtin_fmaf(sc0[ni], c[r], acc[mi][ni][r]);
@@ -591,13 +672,21 @@ void launch_exact_for(const ExactArgs &a)
     else launch_exact<WF, 1, 1, 2, 2, kExactRing>(a);
 }
 
+// Q6_K through the integer panel instead of unpacked in the staging
+// (HOLO_EXACT_Q6K_PANEL=1)
+static bool q6_panel()
+{
+    static const bool on = getenv("HOLO_EXACT_Q6K_PANEL") != nullptr;
+    return on;
+}
+
 int exact_kind(int type)
 {
     switch (type) {
     case HOLO_TYPE_Q4_0: return EW_Q4_0;
     case HOLO_TYPE_Q8_0: return EW_Q8_0;
     case HOLO_TYPE_Q4_K: return EW_Q4_K;
-    case HOLO_TYPE_Q6_K: return EW_P16;
+    case HOLO_TYPE_Q6_K: return q6_panel() ? EW_P16 : EW_Q6_K;
     case HOLO_TYPE_F16: return EW_F16;
     default: return -1;
     }
@@ -642,7 +731,7 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
     size_t pbytes = 0;
     for (int i = 0; i < nmat; i++) {
         need_sx = need_sx || types[i] == HOLO_TYPE_Q4_K;
-        if (types[i] == HOLO_TYPE_Q6_K) pbytes += (size_t)N[i] * K * 2 + (size_t)N[i] * (K / 16) * 4;
+        if (types[i] == HOLO_TYPE_Q6_K && q6_panel()) pbytes += (size_t)N[i] * K * 2 + (size_t)N[i] * (K / 16) * 4;
     }
     const int64_t n8 = (int64_t)M * K / 8;
     const unsigned grid = (unsigned)((n8 + 255) / 256);
@@ -665,7 +754,7 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
         if (!pws) return;
         size_t off = 0;
         for (int i = 0; i < nmat; i++) {
-            if (types[i] != HOLO_TYPE_Q6_K) continue;
+            if (types[i] != HOLO_TYPE_Q6_K || !q6_panel()) continue;
             _Float16 *p = (_Float16 *)((uint8_t *)pws + off);
             off += (size_t)N[i] * K * 2;
             float *ps = (float *)((uint8_t *)pws + off);
@@ -713,6 +802,7 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
         case EW_Q8_0: launch_exact_for<EW_Q8_0>(a); break;
         case EW_Q4_K: launch_exact_for<EW_Q4_K>(a); break;
         case EW_P16: launch_exact_for<EW_P16>(a); break;
+        case EW_Q6_K: launch_exact_for<EW_Q6_K>(a); break;
         default: launch_exact_for<EW_F16>(a); break;
         }
     }
