@@ -235,7 +235,7 @@ __global__ __launch_bounds__(256) void mha_k(float *dst, const float *q, const f
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 template <int HD>
-__global__ __launch_bounds__(256) void attn_prefill_mfma_k(float *out, const float *q, const float *kc,
+__global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const float *q, const float *kc,
                                                            const float *vc, int rows, int pos0, int n_heads,
                                                            int n_kv_heads)
 {
@@ -254,12 +254,20 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_k(float *out, const flo
     const int ntiles = last_key / 32 + 1;
     const int qpos = pos0 + q0 + j;  // rows past the prompt: computed, not stored
 
-    float4 qr[NC];
-    {
-        const float *qp = q + (int64_t)min(q0 + j, rows - 1) * q_dim + (int64_t)h * HD + 4 * hh;
-#pragma unroll
-        for (int c = 0; c < NC; c++) qr[c] = *(const float4 *)(qp + 8 * c);
+    // The block's 32 query rows in LDS ([32][HD + 4]: the pad puts the 8 rows a
+    // 16-byte read pass touches on distinct banks), read per step rather than
+    // held in 64 registers: held, the kernel needed more than 256 registers
+    // and ran one wave per SIMD.  The rows alias the merge buffer lo, which is
+    // written only after every wave has left the loop.
+    constexpr int QS = HD + 4;
+    float *qs = amf_lds;
+    for (int e = threadIdx.x; e < 32 * (HD / 4); e += 256) {
+        const int r = e / (HD / 4), c4 = e - r * (HD / 4);
+        *(float4 *)(qs + r * QS + 4 * c4) =
+            *(const float4 *)(q + (int64_t)min(q0 + r, rows - 1) * q_dim + (int64_t)h * HD + 4 * c4);
     }
+    __syncthreads();
+    const float *qrow = qs + j * QS + 4 * hh;
     const float *kb = kc + (int64_t)kvh * HD + 4 * hh;
     const float *vb = vc + (int64_t)kvh * HD + VB * j;
     float m = -INFINITY, l = 0.f;
@@ -278,10 +286,11 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_k(float *out, const flo
         v16f s = v16f{};
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].x, qr[c].x, s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].y, qr[c].y, s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].z, qr[c].z, s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].w, qr[c].w, s, 0, 0, 0);
+            const float4 qc = *(const float4 *)(qrow + 8 * c);
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].x, qc.x, s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].y, qc.y, s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].z, qc.z, s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].w, qc.w, s, 0, 0, 0);
         }
         float tmax = -INFINITY;
 #pragma unroll
@@ -326,6 +335,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_k(float *out, const flo
     }
 
     // merge the 4 waves: O = sum_w e^(m_w - M) O_w, L = sum_w e^(m_w - M) l_w
+    __syncthreads();  // every wave is done with the query rows in lo
 #pragma unroll
     for (int b = 0; b < VB; b++)
 #pragma unroll
