@@ -211,35 +211,47 @@ __global__ __launch_bounds__(256) void mha_k(float *dst, const float *q, const f
                n_kv_heads * hd, lsc, scratch);
 }
 
-// ---- causal prefill attention on the fp32 matrix cores ------------------------------
+// ---- causal prefill attention on the matrix cores ----------------------------------
 //
 // The same result as attention_prefill_k (softmax((q . k_p) / sqrt(hd)) . v,
-// online over key tiles, fp32), for head sizes 32, 64 and 128, with both
-// products on v_mfma_f32_32x32x2_f32.  A workgroup takes one head and 32
-// query rows; its 4 waves take the 32-key tiles in turn (wave w: tiles w,
-// w + 4, ...) and merge their softmax states through LDS at the end.
-//
-// 32x32x2 f32 (wave64): lane l supplies A[l%32][l/32] and B[l/32][l%32];
-// D[i][j] lands in lane j + 32*((i/4)%2), register (i%4) + 4*(i/8).
-//   scores, transposed: S^T = K Q^T.  Half hh of the wave loads 16-byte chunk
-//     2c + hh of its key row (A) and of its query row (B); the 4 elements of a
-//     chunk feed 4 instructions, so A and B agree on the dimension of every
-//     (step, slot).  Lane j + 32hh then holds query j's scores for keys
+// online over key tiles, fp32), for head sizes 32, 64 and 128.  A workgroup
+// takes one head and 32 query rows; its 4 waves take the 32-key tiles in turn
+// (wave w: tiles w, w + 4, ...) and merge their softmax states through LDS at
+// the end.  Both products leave D[i][j] in lane j + 32*((i/4)%2), register
+// (i%4) + 4*(i/8).
+//   scores, transposed: S^T = K Q^T on v_mfma_f32_32x32x16_f16 with K and Q
+//     split into f16 halves (hi*hi + hi*lo + lo*hi, fp32 accumulation): lane
+//     l supplies A[l%32][8*(l/32)+t] and B[8*(l/32)+t][l%32], t = 0..7, i.e.
+//     half hh of the wave dims 16c + 8hh .. + 7 of its key row (A) and of its
+//     query row (B).  Lane j + 32hh then holds query j's scores for keys
 //     (r%4) + 8(r/4) + 4hh, r = 0..15: the row maximum is 15 local steps and
-//     one exchange with lane j ^ 32.
-//   output, transposed: O^T += V^T P^T over 16 steps; step st pairs key
+//     one exchange with lane j ^ 32.  (On v_mfma_f32_32x32x2_f32 the scores
+//     took 64 instructions at head size 128, here 24.)
+//   output, transposed: O^T += V^T P^T over 16 steps of v_mfma_f32_32x32x2_f32
+//     (lane l supplies A[l%32][l/32] and B[l/32][l%32]); step st pairs key
 //     (st%4) + 8(st/4) + 4hh (slot hh) with register st of the probabilities,
 //     which is already the B operand.  A is V: lane i + 32hh reads dims
 //     VB*i .. VB*i + VB - 1 of that key's row, one contiguous row per half;
 //     element b feeds the block of dims VB*i + b.
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 af16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 af16x8 __attribute__((ext_vector_type(8)));
+
+// x = hi + lo exactly to 22 bits: hi = f16(x), lo = f16(x - hi) (x - hi is exact
+// in fp32).  Products of split operands, hi*hi + hi*lo + lo*hi, keep the fp32
+// class of the product (the lo*lo term is below 2^-22 of it).
+__device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo)
+{
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
 
 template <int HD>
 __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const float *q, const float *kc,
                                                            const float *vc, int rows, int pos0, int n_heads,
                                                            int n_kv_heads)
 {
-    constexpr int NC = HD / 8;   // 16-byte chunk pairs of a row
+    constexpr int NQ = HD / 16;  // 16-dim chunks of a row: the K of one f16 score MFMA
     constexpr int VB = HD / 32;  // output blocks: lane i covers dims VB*i .. VB*i + VB - 1
     extern __shared__ float amf_lds[];
     float *lo = amf_lds;                       // [4 waves][HD][32]
@@ -254,21 +266,28 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
     const int ntiles = last_key / 32 + 1;
     const int qpos = pos0 + q0 + j;  // rows past the prompt: computed, not stored
 
-    // The block's 32 query rows in LDS ([32][HD + 4]: the pad puts the 8 rows a
-    // 16-byte read pass touches on distinct banks), read per step rather than
-    // held in 64 registers: held, the kernel needed more than 256 registers
-    // and ran one wave per SIMD.  The rows alias the merge buffer lo, which is
-    // written only after every wave has left the loop.
-    constexpr int QS = HD + 4;
-    float *qs = amf_lds;
+    // The block's 32 query rows in LDS, split into f16 halves ([32][HD + 8]
+    // each: the pad puts the rows a 16-byte read pass touches on distinct
+    // banks), read per step rather than held in registers: held, the kernel
+    // needed more than 256 registers and ran one wave per SIMD.  The rows alias
+    // the merge buffer lo, which is written only after every wave has left the
+    // loop.
+    constexpr int QS = HD + 8;
+    _Float16 *qh = (_Float16 *)amf_lds, *ql = qh + 32 * QS;
     for (int e = threadIdx.x; e < 32 * (HD / 4); e += 256) {
         const int r = e / (HD / 4), c4 = e - r * (HD / 4);
-        *(float4 *)(qs + r * QS + 4 * c4) =
-            *(const float4 *)(q + (int64_t)min(q0 + r, rows - 1) * q_dim + (int64_t)h * HD + 4 * c4);
+        const float4 x = *(const float4 *)(q + (int64_t)min(q0 + r, rows - 1) * q_dim + (int64_t)h * HD + 4 * c4);
+        _Float16 hv[4], lv[4];
+        split_f16(x.x, hv[0], lv[0]);
+        split_f16(x.y, hv[1], lv[1]);
+        split_f16(x.z, hv[2], lv[2]);
+        split_f16(x.w, hv[3], lv[3]);
+        *(af16x4 *)(qh + r * QS + 4 * c4) = af16x4{hv[0], hv[1], hv[2], hv[3]};
+        *(af16x4 *)(ql + r * QS + 4 * c4) = af16x4{lv[0], lv[1], lv[2], lv[3]};
     }
     __syncthreads();
-    const float *qrow = qs + j * QS + 4 * hh;
-    const float *kb = kc + (int64_t)kvh * HD + 4 * hh;
+    const _Float16 *qhr = qh + j * QS + 8 * hh, *qlr = ql + j * QS + 8 * hh;
+    const float *kb = kc + (int64_t)kvh * HD + 8 * hh;
     const float *vb = vc + (int64_t)kvh * HD + VB * j;
     float m = -INFINITY, l = 0.f;
     v16f o[VB];
@@ -277,20 +296,33 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
 
     for (int t = wave; t < ntiles; t += 4) {
         const int key0 = t * 32;
-        float4 kr[NC];
+        // Sᵀ = K Qᵀ on v_mfma_f32_32x32x16_f16 with both operands split:
+        // lane j + 32hh supplies dims 16c + 8hh .. 16c + 8hh + 7 of key j (A) and
+        // of query j (B), as the 32x32x2 f32 layout did for its dims, so the
+        // scores land in the same registers
+        float4 kr[2 * NQ];
         {
             const float *kp = kb + (int64_t)min(key0 + j, last_key) * kv_dim;  // keys past last_key are masked
 #pragma unroll
-            for (int c = 0; c < NC; c++) kr[c] = *(const float4 *)(kp + 8 * c);
+            for (int c = 0; c < NQ; c++) {
+                kr[2 * c] = *(const float4 *)(kp + 16 * c);
+                kr[2 * c + 1] = *(const float4 *)(kp + 16 * c + 4);
+            }
         }
         v16f s = v16f{};
 #pragma unroll
-        for (int c = 0; c < NC; c++) {
-            const float4 qc = *(const float4 *)(qrow + 8 * c);
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].x, qc.x, s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].y, qc.y, s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].z, qc.z, s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[c].w, qc.w, s, 0, 0, 0);
+        for (int c = 0; c < NQ; c++) {
+            const float kv[8] = {kr[2 * c].x,     kr[2 * c].y,     kr[2 * c].z,     kr[2 * c].w,
+                                 kr[2 * c + 1].x, kr[2 * c + 1].y, kr[2 * c + 1].z, kr[2 * c + 1].w};
+            _Float16 h8[8], l8[8];
+#pragma unroll
+            for (int t2 = 0; t2 < 8; t2++) split_f16(kv[t2], h8[t2], l8[t2]);
+            const af16x8 kh = {h8[0], h8[1], h8[2], h8[3], h8[4], h8[5], h8[6], h8[7]};
+            const af16x8 kl = {l8[0], l8[1], l8[2], l8[3], l8[4], l8[5], l8[6], l8[7]};
+            const af16x8 bh = *(const af16x8 *)(qhr + 16 * c), bl = *(const af16x8 *)(qlr + 16 * c);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, bh, s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, bl, s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, bh, s, 0, 0, 0);
         }
         float tmax = -INFINITY;
 #pragma unroll
