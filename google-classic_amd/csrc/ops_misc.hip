@@ -323,6 +323,9 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, bh, s, 0, 0, 0);
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, bl, s, 0, 0, 0);
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, bh, s, 0, 0, 0);
+            // one chunk's split and query reads at a time (hoisting them all
+            // took the kernel past 256 registers)
+            __builtin_amdgcn_sched_barrier(0);
         }
         float tmax = -INFINITY;
 #pragma unroll
