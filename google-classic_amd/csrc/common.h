@@ -43,8 +43,14 @@ void *workspace(int slot, size_t bytes);
 // stream take it, and the product itself (Y[i] = X . W[i]^T, or of silu(X) *
 // U, plus R for one matrix).
 bool exact_ok(int type, int K, const void *W);
+// With NW, the rows of X are RMS-normed first (weight NW, K <= 16384, 16-byte
+// aligned), as holo_rms_norm_rows computes them, inside the activation halves.
 void exact_product(float *const *Y, const void *const *W, const int *types, const int *N, int nmat, const float *X,
-                   const float *U, const float *R, int M, int K);
+                   const float *U, const float *R, int M, int K, const float *NW = nullptr, float eps = 0.f);
+// The exact route for nmat matrices of rows RMS-normed on the way in, when
+// the prefill mode and the shapes take it; false (nothing launched) otherwise.
+bool exact_product_normed(float *const *Y, const void *const *W, const int *types, const int *N, int nmat,
+                          const float *X, const float *NW, float eps, int M, int K);
 // Device address of the fixed scratch array of holo_gemm_q4_0_q8_0_noalloc on
 // the current device (prefill.hip), looked up once per device; nullptr on failure.
 void *noalloc_scratch();

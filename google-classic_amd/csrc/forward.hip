@@ -111,6 +111,22 @@ void matmul_qkv(float *q, float *k, float *v, const holo_llama_layer_t &L, const
     holo_matmul_rows(v, L.wv, xb, n, kv_dim, dim, L.wv_type, exact);
 }
 
+// q, k, v of the rows of x RMS-normed by nw, the norm inside the exact
+// product's activation halves (one launch for the three matrices); false
+// when that route does not take these rows, and nothing ran.
+bool qkv_normed(float *q, float *k, float *v, const holo_llama_layer_t &L, const float *x, const float *nw, float eps,
+                int n, int q_dim, int kv_dim, int dim, int exact)
+{
+    if (!nw || !gemm_rows(L.wq_type, n, dim, exact) || !gemm_rows(L.wk_type, n, dim, exact) ||
+        !gemm_rows(L.wv_type, n, dim, exact))
+        return false;
+    float *Y[3] = {q, k, v};
+    const void *W[3] = {L.wq, L.wk, L.wv};
+    const int T[3] = {L.wq_type, L.wk_type, L.wv_type};
+    const int N[3] = {q_dim, kv_dim, kv_dim};
+    return exact_product_normed(Y, W, T, N, 3, x, nw, eps, n, dim);
+}
+
 // h = silu(W1 xb) * (W3 xb) of n rows (h2: scratch of the same size), by the
 // same three routes; the fused GEMV applies silu * in its epilogue.
 void matmul_gate_up(float *h, float *h2, const holo_llama_layer_t &L, const float *xb, int n, int ffn, int dim,
@@ -216,7 +232,7 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
         if (qkv1) {
             holo_batched_qkv_norm(q, k, v, L.wq, L.wk, L.wv, x, L.attn_norm, m->rms_eps, xb, q_dim, kv_dim, dim,
                                   L.wq_type);
-        } else {
+        } else if (!qkv_normed(q, k, v, L, x, L.attn_norm, m->rms_eps, n, q_dim, kv_dim, dim, exact)) {
             norm_or_copy(xb, x, L.attn_norm, n, dim, m->rms_eps);
             matmul_qkv(q, k, v, L, xb, n, q_dim, kv_dim, dim, exact);
         }
@@ -234,18 +250,23 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
         if (ffn1) {
             holo_batched_ffn_gate_up_norm(hb, L.w1, L.w3, x, L.ffn_norm, m->rms_eps, xb, ffn, dim, L.w1_type);
         } else {
-            norm_or_copy(xb, x, L.ffn_norm, n, dim, m->rms_eps);
             if (L.w3_type == L.w1_type && gemm_rows(L.w1_type, n, dim, exact) && ffn % 128 == 0 &&
                 gemm_rows(L.w2_type, n, ffn, exact)) {
-                // gate and up in one GEMM; the SwiGLU goes into the down GEMM's
-                // activation panel and the residual add into its store
+                // gate and up in one GEMM (the norm in its activation halves
+                // when it takes the exact route); the SwiGLU goes into the down
+                // GEMM's activation panel and the residual add into its store
                 float *Y[2] = {hb, hb2};
                 const void *W[2] = {L.w1, L.w3};
                 const int N[2] = {ffn, ffn};
-                holo_matmul_batch_multi(Y, W, N, 2, xb, n, dim, L.w1_type);
+                const int T[2] = {L.w1_type, L.w3_type};
+                if (!L.ffn_norm || !exact_product_normed(Y, W, T, N, 2, x, L.ffn_norm, m->rms_eps, n, dim)) {
+                    norm_or_copy(xb, x, L.ffn_norm, n, dim, m->rms_eps);
+                    holo_matmul_batch_multi(Y, W, N, 2, xb, n, dim, L.w1_type);
+                }
                 holo_matmul_batch_swiglu_add(x, L.w2, hb, hb2, x, n, dim, ffn, L.w2_type);
                 continue;
             }
+            norm_or_copy(xb, x, L.ffn_norm, n, dim, m->rms_eps);
             matmul_gate_up(hb, hb2, L, xb, n, ffn, dim, exact);
         }
         if (one && fused_gemv_type(L.w2_type)) {

@@ -7,6 +7,7 @@
 // function); where the reference has a quirk, it is kept and said so.
 #include "common.h"
 #include "quant_blocks.h"
+#include "block_reduce.h"
 
 #include "../../include/holo_forward.h"
 
@@ -16,34 +17,7 @@ constexpr int kBlock = 256;
 
 static inline int blocks_for(int n, int per = kBlock) { return (n + per - 1) / per; }
 
-// ---- block-wide reductions (wave64 + LDS) --------------------------------------
-
-__device__ __forceinline__ float wave_reduce_sum(float v)
-{
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-__device__ __forceinline__ float wave_reduce_max(float v)
-{
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-// Sum (or max) over the whole workgroup; every thread gets the result.
-template <bool MAX>
-__device__ float block_reduce(float v, float *scratch)
-{
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nw = (blockDim.x + 63) >> 6;
-    v = MAX ? wave_reduce_max(v) : wave_reduce_sum(v);
-    __syncthreads();
-    if (lane == 0) scratch[wave] = v;
-    __syncthreads();
-    float r = scratch[0];
-    for (int w = 1; w < nw; w++) r = MAX ? fmaxf(r, scratch[w]) : r + scratch[w];
-    return r;
-}
+// ---- block-wide reductions: block_reduce.h ----
 
 // ---- elementwise (cuda_ops.cu:237-314, 1401-1455) ------------------------------------
 

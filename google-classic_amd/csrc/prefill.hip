@@ -843,6 +843,22 @@ static bool exact_fits(const void *const *W, const int *types, int nmat, const f
 
 static bool exact_mode() { return g_prefill_mode == HOLO_PREFILL_EXACT; }
 
+namespace holo {
+
+bool exact_product_normed(float *const *Y, const void *const *W, const int *types, const int *N, int nmat,
+                          const float *X, const float *NW, float eps, int M, int K)
+{
+    if (M < 64 || !exact_mode() || !Y || !W || !types || !N || !NW || ((uintptr_t)NW & 15u) || K > 1024 * 16 ||
+        !multi_fits(N, nmat) || !exact_fits(W, types, nmat, X, nullptr, M, K))
+        return false;
+    for (int i = 0; i < nmat; i++)
+        if (!Y[i]) return false;
+    exact_product(Y, W, types, N, nmat, X, nullptr, nullptr, M, K, NW, eps);
+    return true;
+}
+
+}  // namespace holo
+
 extern "C" {
 
 int holo_prefill_get_mode(void) { return g_prefill_mode; }

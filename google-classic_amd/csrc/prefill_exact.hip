@@ -29,6 +29,7 @@
 // stage's global loads in registers while the current one is multiplied.
 #include "common.h"
 #include "quant_blocks.h"
+#include "block_reduce.h"
 
 #include <hip/hip_ext.h>
 #include <limits.h>
@@ -597,6 +598,56 @@ __global__ __launch_bounds__(256) void xsplit_k(uint4 *__restrict__ Ah, uint4 *_
     if (Sx && (g & 3) == 0) Sx[g >> 2] = s;
 }
 
+// The halves of RMS-normed rows, one workgroup per row: rms_norm_rows4_k's
+// arithmetic (thread t sums the squares of float4s t + 256j, the same
+// workgroup reduction, x * scale * w), so the normed values are the bits the
+// separate norm writes, then xsplit_k's split; the normed rows never reach
+// HBM in fp32.  A 32-block is the 8 float4 of 8 adjacent lanes (K % 32 == 0).
+template <int NV>
+__global__ __launch_bounds__(256) void xsplit_norm_k(uint2 *__restrict__ Ah, uint2 *__restrict__ Al,
+                                                     float *__restrict__ Sx, const float *__restrict__ X,
+                                                     const float *__restrict__ NW, int K, float eps)
+{
+    __shared__ float red[16];
+    const int n4 = K >> 2;
+    const int64_t r4 = (int64_t)blockIdx.x * n4;
+    const float4 *x4 = (const float4 *)X + r4;
+    float4 v[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = threadIdx.x + 256 * j;
+        v[j] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+    }
+    ss = block_reduce<false>(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = threadIdx.x + 256 * j;
+        if (256 * j >= n4) break;  // uniform: no lane of this or a later j is live
+        const float4 w4 = ((const float4 *)NW)[min(i, n4 - 1)];
+        const float y[4] = {v[j].x * scale * w4.x, v[j].y * scale * w4.y, v[j].z * scale * w4.z,
+                            v[j].w * scale * w4.w};
+        _Float16 h[4], l[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            h[e] = (_Float16)y[e];
+            l[e] = (_Float16)(y[e] - (float)h[e]);
+        }
+        // the block's sum over its 8 lanes (octets are wholly live or dead)
+        float s = (y[0] + y[1]) + (y[2] + y[3]);
+        s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+        s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+        s += __shfl_xor(s, 4, 64);
+        if (i < n4) {
+            Ah[r4 + i] = make_uint2(__builtin_bit_cast(uint32_t, h2{h[0], h[1]}), __builtin_bit_cast(uint32_t, h2{h[2], h[3]}));
+            Al[r4 + i] = make_uint2(__builtin_bit_cast(uint32_t, h2{l[0], l[1]}), __builtin_bit_cast(uint32_t, h2{l[2], l[3]}));
+            if (Sx && (i & 7) == 0) Sx[r4 / 8 + (i >> 3)] = s;
+        }
+    }
+}
+
 // ---- Q6_K integer panel: (q - 32) in f16 [N][K] and the group scales d*sc [N][K/16] ----
 // One thread per (superblock, half h, slice s): l = 16s .. 16s + 15 of the
 // half, all four j, the values y[256b + 128h + 32j + l] of
@@ -716,7 +767,7 @@ bool exact_ok(int type, int K, const void *W)
 // with several matrices of one type every N[i] must be a multiple of 128.
 // Matrices of one type share a launch; the activation halves are built once.
 void exact_product(float *const *Y, const void *const *W, const int *types, const int *N, int nmat, const float *X,
-                   const float *U, const float *R, int M, int K)
+                   const float *U, const float *R, int M, int K, const float *NW, float eps)
 {
     const int nb = K / 32;
     const size_t half = ((size_t)M * K * 2 + 255) & ~(size_t)255;
@@ -735,7 +786,13 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
     }
     const int64_t n8 = (int64_t)M * K / 8;
     const unsigned grid = (unsigned)((n8 + 255) / 256);
-    if (U)
+    if (NW && K <= 1024 * 4)
+        hipLaunchKernelGGL(xsplit_norm_k<4>, dim3(M), dim3(256), 0, stream(), (uint2 *)Ah, (uint2 *)Al,
+                           need_sx ? Sx : nullptr, X, NW, K, eps);
+    else if (NW)
+        hipLaunchKernelGGL(xsplit_norm_k<16>, dim3(M), dim3(256), 0, stream(), (uint2 *)Ah, (uint2 *)Al,
+                           need_sx ? Sx : nullptr, X, NW, K, eps);
+    else if (U)
         hipLaunchKernelGGL(xsplit_k<true>, dim3(grid), dim3(256), 0, stream(), (uint4 *)Ah, (uint4 *)Al,
                            need_sx ? Sx : nullptr, X, U, n8);
     else
