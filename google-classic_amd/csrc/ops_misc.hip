@@ -892,12 +892,14 @@ __global__ __launch_bounds__(256) void rms_norm_rows4_k(float *dst, const float 
     const int n4 = n >> 2;
     const float4 *x4 = (const float4 *)(x + (int64_t)blockIdx.x * n);
     float4 *d4 = (float4 *)(dst + (int64_t)blockIdx.x * n);
-    float4 v[NV];
+    float4 v[NV], wv[NV];
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < NV; j++) {
         const int i = threadIdx.x + 256 * j;
         v[j] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        // the weights load with the row, not after the reduction
+        wv[j] = w && i < n4 ? ((const float4 *)w)[i] : make_float4(1.f, 1.f, 1.f, 1.f);
         ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
     }
     ss = block_reduce<false>(ss, scratch);
@@ -906,7 +908,7 @@ __global__ __launch_bounds__(256) void rms_norm_rows4_k(float *dst, const float 
     for (int j = 0; j < NV; j++) {
         const int i = threadIdx.x + 256 * j;
         if (i < n4) {
-            const float4 w4 = w ? ((const float4 *)w)[i] : make_float4(1.f, 1.f, 1.f, 1.f);
+            const float4 w4 = wv[j];
             d4[i] = make_float4(v[j].x * scale * w4.x, v[j].y * scale * w4.y, v[j].z * scale * w4.z,
                                 v[j].w * scale * w4.w);
         }

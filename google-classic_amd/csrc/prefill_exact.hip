@@ -612,12 +612,14 @@ __global__ __launch_bounds__(256) void xsplit_norm_k(uint2 *__restrict__ Ah, uin
     const int n4 = K >> 2;
     const int64_t r4 = (int64_t)blockIdx.x * n4;
     const float4 *x4 = (const float4 *)X + r4;
-    float4 v[NV];
+    float4 v[NV], wv[NV];
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < NV; j++) {
         const int i = threadIdx.x + 256 * j;
         v[j] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        // the weights load with the row, not after the reduction
+        wv[j] = ((const float4 *)NW)[min(i, n4 - 1)];
         ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
     }
     ss = block_reduce<false>(ss, red);
@@ -626,7 +628,7 @@ __global__ __launch_bounds__(256) void xsplit_norm_k(uint2 *__restrict__ Ah, uin
     for (int j = 0; j < NV; j++) {
         const int i = threadIdx.x + 256 * j;
         if (256 * j >= n4) break;  // uniform: no lane of this or a later j is live
-        const float4 w4 = ((const float4 *)NW)[min(i, n4 - 1)];
+        const float4 w4 = wv[j];
         const float y[4] = {v[j].x * scale * w4.x, v[j].y * scale * w4.y, v[j].z * scale * w4.z,
                             v[j].w * scale * w4.w};
         _Float16 h[4], l[4];
