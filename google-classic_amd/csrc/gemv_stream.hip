@@ -39,7 +39,7 @@
 //
 // How a stage's output reaches the next stage (no grid barrier): besides the
 // plain fp32 output, every output value is also stored as one 64-bit word
-// (tag << 32 | value bits) with a single agent-scope store, into the plan's
+// ((tag ^ value bits) << 32 | value bits) with a single agent-scope store, into the plan's
 // exchange buffer of that output vector.  The tag names the launch and the
 // stage (base + s + 1, base = launch count * (stages + 1)), so a word is
 // either this stage's value or visibly stale.  When a later stage is the
@@ -50,9 +50,11 @@
 // words into place, instead of every CU converting the whole vector.  A
 // consumer copies the words of its whole input into LDS (device-coherent
 // global_load_lds), checks every tag and copies again until all are current.
-// Value and tag travel in one single-copy-atomic 64-bit store, so a current
-// tag implies the current value: no fence, no store-completion wait and no
-// arrival counter sit between a producer's epilogue and its consumers.  The
+// Value and tag travel in one single-copy-atomic 64-bit store, and the high
+// half carries the tag XORed with the value, so a word that checks as
+// current holds the current value even if a 16-byte copy paired the halves
+// of two stores: no fence, no store-completion wait and no arrival counter
+// sit between a producer's epilogue and its consumers.  The
 // launch count advances when the last workgroup of a launch ends (a counter
 // in the plan), so the next launch's tags differ from every word this launch
 // left behind.
@@ -525,13 +527,34 @@ __device__ __forceinline__ void stream_fetch_words(cstage &st, uint8_t *xbuf, in
                                          kDeviceScope);
 }
 
+// A wait that reaches kStreamPolls gives up: it sets the library's flag
+// (what holo_gemv_stream_status reports) and records the launch in the
+// plan's give-up word (its tag base + 1).  Every later wait of the same
+// launch sees that record and returns at once, on every workgroup, so a
+// launch whose workgroups are not all resident costs one bounded wait, not
+// one per stage.
+struct StreamFlag {
+    uint32_t *flag;  // the library's sticky flag
+    uint32_t *rec;   // the plan's give-up word (header word 1, zeroed at creation)
+};
+__device__ __forceinline__ bool stream_gave_up(StreamFlag f, uint32_t base)
+{
+    return __hip_atomic_load(f.rec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == base + 1u;
+}
+__device__ __forceinline__ void stream_give_up(StreamFlag f, uint32_t base)
+{
+    __hip_atomic_store(f.flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(f.rec, base + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Waits until every workgroup has stored its rows of the stage with tag
 // `tag` (its done word holds that tag or a later one of this launch).  A done
 // word is stored right after the workgroup's exchange words, without waiting
 // for them to complete, so it only says that the words are on their way: the
 // gather still checks every word's tag.  The wait keeps the polling to 4
 // bytes per workgroup instead of the whole input.
-__device__ __forceinline__ void stream_wait_done(const uint32_t *done, uint32_t tag, uint32_t *flag, int lane)
+__device__ __forceinline__ void stream_wait_done(const uint32_t *done, uint32_t tag, uint32_t base, StreamFlag flag,
+                                                 int lane)
 {
     const int G = (int)gridDim.x;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)done, (short)0, G * 4, kBufferWord3);
@@ -546,26 +569,31 @@ __device__ __forceinline__ void stream_wait_done(const uint32_t *done, uint32_t 
         }
         if (__ballot(late) == 0) return;
         if (polls == kStreamPolls) {
-            __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            stream_give_up(flag, base);
             return;
         }
+        if ((polls & 255u) == 0 && stream_gave_up(flag, base)) return;
         __builtin_amdgcn_s_sleep(2);
     }
 }
 
+// Two exchange words (value, tag ^ value) as a uint4: both current?
+__device__ __forceinline__ bool words_ok(uint4 a, uint32_t tag) { return ((a.y ^ a.x) == tag) & ((a.w ^ a.z) == tag); }
+
 // x value chunk i (4 values) of the staged input: plain fp32, or exchange
-// words (value, tag) pairs, whose tags must all be `tag` (else `bad`).
+// words, which must all carry `tag` (else `bad`).
 __device__ __forceinline__ float4 staged_x4(const uint8_t *xbuf, int i, bool tagged, uint32_t tag, bool &bad)
 {
     if (tagged) {
         const uint4 a = *(const uint4 *)(xbuf + 32 * i), b = *(const uint4 *)(xbuf + 32 * i + 16);
-        bad |= (a.y != tag) | (a.w != tag) | (b.y != tag) | (b.w != tag);
+        bad |= !(words_ok(a, tag) & words_ok(b, tag));
         return make_float4(__uint_as_float(a.x), __uint_as_float(a.z), __uint_as_float(b.x), __uint_as_float(b.z));
     }
     return *(const float4 *)(xbuf + 16 * i);
 }
 
 constexpr int kRedBase = 14;   // red[14]: this launch's tag base, from the control wave
+constexpr int kRedQuit = 15;   // red[15]: the control wave gave the current input's wait up
 constexpr int kRedMask = 16;   // red[16..31]: two stale-piece masks (1 KB pieces of the staged words)
 constexpr int kMaskWords = 8;  // pieces up to 256: in_dim up to 32768
 constexpr int kRedWords = kRedMask + 2 * kMaskWords;
@@ -597,7 +625,7 @@ __device__ __forceinline__ void stream_convert_x(cstage &st, uint8_t *ldsb, cons
         for (int q = tid; q < nq; q += kStreamThreads) {
             if (only && !piece_set(only, q >> 5)) continue;
             const uint4 a = *(const uint4 *)(xbuf + 32 * q), c = *(const uint4 *)(xbuf + 32 * q + 16);
-            if ((a.y != tag) | (a.w != tag) | (c.y != tag) | (c.w != tag)) mark_piece(stale, q >> 5);
+            if (!(words_ok(a, tag) & words_ok(c, tag))) mark_piece(stale, q >> 5);
             const int g = q >> 2, j = q & 3, u = g >> 1, hf = g & 1;
             if (j < 3) {
                 *(uint4 *)(ldsb + 96 * u + 32 * j + 16 * hf) = make_uint4(a.x, a.z, c.x, c.z);
@@ -667,7 +695,7 @@ __device__ __forceinline__ void stream_refetch(cstage &st, uint8_t *xbuf, const 
 // and the barrier counts agree.  After kStreamPolls rounds the wait gives up
 // and sets the plan's flag.  The control wave cleared mask 0 before B.
 __device__ __forceinline__ void stream_stage_in(cstage &st, uint8_t *ldsb, uint8_t *xbuf, float *red, float *ss,
-                                                uint32_t base, uint32_t *flag, bool control, int lane)
+                                                uint32_t base, StreamFlag flag, bool control, int lane)
 {
     const uint32_t tag = base + (uint32_t)uni(st.xsrc) + 1u;
     uint32_t *mask = (uint32_t *)red + kRedMask;
@@ -685,8 +713,10 @@ __device__ __forceinline__ void stream_stage_in(cstage &st, uint8_t *ldsb, uint8
         __syncthreads();  // every wave has read the mask
         if (control) {
             if (lane < kMaskWords) nxt[lane] = 0u;
-            if (round == kStreamPolls) {
-                __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool quit = round == kStreamPolls || stream_gave_up(flag, base);
+            if (lane == 0) ((uint32_t *)red)[kRedQuit] = quit ? 1u : 0u;
+            if (quit) {
+                stream_give_up(flag, base);
             } else {
                 __builtin_amdgcn_s_sleep(2);
                 stream_refetch(st, xbuf, cur, lane);
@@ -694,7 +724,9 @@ __device__ __forceinline__ void stream_stage_in(cstage &st, uint8_t *ldsb, uint8
             }
         }
         __syncthreads();  // B again
-        if (round < kStreamPolls) stream_convert_x(st, ldsb, xbuf, red, ss, tag, records ? cur : nullptr, nxt);
+        // quitting leaves the next mask clear, so every wave leaves the loop
+        if (uni((int)((const uint32_t *)red)[kRedQuit]) == 0)
+            stream_convert_x(st, ldsb, xbuf, red, ss, tag, records ? cur : nullptr, nxt);
         __syncthreads();  // C again
     }
 }
@@ -714,17 +746,26 @@ __device__ __forceinline__ bool own_row(const Tiles &t, int q, int lane, uint32_
 
 constexpr int kStreamPasses = kStreamMaxTiles / 4;  // passes of 64 rows over at most 16 tiles
 
+// An exchange word is (tag ^ v) << 32 | v, stored with one 64-bit agent-scope
+// store, and it is current when its halves XOR to the tag (word_ok).  The
+// copies that read words into LDS are 16-byte loads, not 64-bit atomic
+// loads, so a read could in principle pair the halves of two stores.  Such a
+// pair passes the check only when its low half equals the current store's
+// value: a torn read is either caught or harmless.
+__device__ __forceinline__ uint64_t exchange_word_u(uint32_t v, uint32_t tag)
+{
+    return ((uint64_t)(tag ^ v) << 32) | v;
+}
 __device__ __forceinline__ uint64_t exchange_word(float v, uint32_t tag)
 {
-    return ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v);
+    return exchange_word_u(__float_as_uint(v), tag);
 }
-__device__ __forceinline__ uint64_t exchange_word_u(uint32_t v, uint32_t tag) { return ((uint64_t)tag << 32) | v; }
 
 // The residual rows r[v] of this workgroup's rows of stage s (plain stages
 // with r), one per lane and pass: exchange words when an earlier stage wrote
 // r (waited for like the input), else the caller's fp32 values.
 __device__ __forceinline__ void stream_prefetch_rr(cstage &st, const Tiles &t, float (&rr)[kStreamPasses],
-                                                   uint32_t base, uint32_t *flag, uint32_t W, uint32_t b, int lane)
+                                                   uint32_t base, StreamFlag flag, uint32_t W, uint32_t b, int lane)
 {
 #pragma unroll
     for (int q = 0; q < kStreamPasses; q++) rr[q] = 0.f;
@@ -742,11 +783,12 @@ __device__ __forceinline__ void stream_prefetch_rr(cstage &st, const Tiles &t, f
         uint64_t w = 0;
         for (uint32_t polls = 0;; polls++) {
             if (mine) w = __hip_atomic_load((gword *)llr + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (__ballot(mine && (uint32_t)(w >> 32) != tag) == 0) break;
+            if (__ballot(mine && ((uint32_t)(w >> 32) ^ (uint32_t)w) != tag) == 0) break;
             if (polls == kStreamPolls) {
-                __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                stream_give_up(flag, base);
                 break;
             }
+            if ((polls & 255u) == 0 && stream_gave_up(flag, base)) break;
             __builtin_amdgcn_s_sleep(2);
         }
         rr[q] = __uint_as_float((uint32_t)w);
@@ -762,7 +804,7 @@ __device__ __forceinline__ void stream_prefetch_rr(cstage &st, const Tiles &t, f
 // The wave waits for these loads here, so the epilogue issues no load: a
 // load there would wait (vmcnt) for the epilogue's own stores as well.
 __device__ __forceinline__ void stream_prefetch(cstage &st, const Tiles &t, float (&rr)[kStreamPasses],
-                                                float (&pw)[kStreamPasses], uint32_t base, uint32_t *flag, uint32_t W,
+                                                float (&pw)[kStreamPasses], uint32_t base, StreamFlag flag, uint32_t W,
                                                 uint32_t b, int lane)
 {
     stream_prefetch_rr(st, t, rr, base, flag, W, b, lane);
@@ -944,6 +986,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
         }
         __syncthreads();  // B of stage 0: x in LDS
         const uint32_t base = (uint32_t)uni((int)((uint32_t *)red)[kRedBase]);
+        const StreamFlag fl{a.flag, a.seq + 1};
         stream_convert_x(stage_at(a, 0), ldsb, xbuf, red, ss, 0u, nullptr, (uint32_t *)red + kRedMask);
         __syncthreads();  // C of stage 0
         int s = 0;        // the stage whose boundary comes next
@@ -965,7 +1008,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
                 while (s < cp.s) {
                     __syncthreads();  // A
                     __syncthreads();  // B
-                    if (s + 1 < nst) stream_stage_in(stage_at(a, s + 1), ldsb, xbuf, red, ss, base, a.flag, false, lane);
+                    if (s + 1 < nst) stream_stage_in(stage_at(a, s + 1), ldsb, xbuf, red, ss, base, fl, false, lane);
                     s++;
                 }
                 // a slot past the last stage writes its (unused) item too, so
@@ -1008,7 +1051,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
         while (s < nst) {
             __syncthreads();  // A
             __syncthreads();  // B
-            if (s + 1 < nst) stream_stage_in(stage_at(a, s + 1), ldsb, xbuf, red, ss, base, a.flag, false, lane);
+            if (s + 1 < nst) stream_stage_in(stage_at(a, s + 1), ldsb, xbuf, red, ss, base, fl, false, lane);
             s++;
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the last (dummy) item loads have returned
@@ -1017,6 +1060,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
         uint32_t *pack = (uint32_t *)(ldsb + a.pack_off);
         const uint32_t seq0 = __hip_atomic_load(a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const uint32_t base = uni((int)(seq0 * (uint32_t)(nst + 1)));
+        const StreamFlag fl{a.flag, a.seq + 1};
         {
             cstage &st0 = stage_at(a, 0);
             stream_fetch_plain(st0, xbuf, lane);
@@ -1035,7 +1079,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
             // the output scale and the residual rows, while the stage runs
             if (s > 0) cn = stream_norm_scale(st, ss, lane);
             float rr[kStreamPasses], pw[kStreamPasses];
-            stream_prefetch(st, t, rr, pw, base, a.flag, W, b, lane);
+            stream_prefetch(st, t, rr, pw, base, fl, W, b, lane);
             __syncthreads();  // A: every partial of stage s is in LDS
             stream_epilogue(st, t, tpart, rr, pw, cn, base + (uint32_t)s + 1u, W, b, pack, lane);
             stream_mark_done(a.seq + 128, base + (uint32_t)s + 1u, b, lane);
@@ -1049,7 +1093,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
                 if (uni64(st1.nw) && !uni64(st1.lpx)) stream_fetch_norm(st1, xbuf + units1 * (words ? 256 : 128), lane);
                 if (words) {
                     if (lane < kMaskWords) ((uint32_t *)red)[kRedMask + lane] = 0u;
-                    stream_wait_done(a.seq + 128, base + (uint32_t)uni(st1.xsrc) + 1u, a.flag, lane);
+                    stream_wait_done(a.seq + 128, base + (uint32_t)uni(st1.xsrc) + 1u, base, fl, lane);
                     stream_fetch_words(st1, xbuf, lane);
                 } else {
                     stream_fetch_plain(st1, xbuf, lane);
@@ -1057,7 +1101,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(StreamArgs 
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             }
             __syncthreads();  // B
-            if (s + 1 < nst) stream_stage_in(stage_at(a, s + 1), ldsb, xbuf, red, ss, base, a.flag, true, lane);
+            if (s + 1 < nst) stream_stage_in(stage_at(a, s + 1), ldsb, xbuf, red, ss, base, fl, true, lane);
         }
         // the last workgroup to finish advances the launch count (every
         // workgroup read it at its start, before counting itself done)
@@ -1265,17 +1309,50 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
         }
         return true;
     };
+    // Caller memory that a stage reads with plain loads (an x or r no earlier
+    // stage wrote, and every norm weight).  A workgroup reads it at or before
+    // the reading stage t, so a later stage s may store over it only once
+    // every workgroup is past t: some stage u in (t, s] copies a whole input
+    // whose producer is t or later (the copy waits for every workgroup's done
+    // word of that producer).  Otherwise a fast workgroup's plain stores could
+    // reach memory that a slow one still has to read.  The one exception is a
+    // stage's residual at exactly its own output (y += W x in place): each row
+    // is read and stored by the one workgroup that owns it.
+    struct CallerSpan {
+        uint64_t ptr, bytes;
+        int reader;
+        bool residual;
+    };
+    std::vector<CallerSpan> spans;
+    auto ordered_after = [&](int t, int s) {
+        for (int u = t + 1; u <= s; u++)
+            if (xo[u] >= 0 && host[u].xsrc >= t) return true;
+        return false;
+    };
     bool xok = true;
     for (int s = 0; s < nstages && xok; s++) {
         const holo_stream_stage_t &in = stages[s];
         StreamStage &o = host[s];
         xok = source(o.x, in.in_dim, xo[s], o.xsrc, xm[s]);
         if (xok && in.r) xok = source(o.r, in.rows[0], ro[s], o.rsrc, rm[s]);
+        // a norm weight is plain-loaded: never from memory a stage stores to
+        for (size_t i = 0; i < outs.size() && xok && o.nw; i++)
+            if (overlap(o.nw, 4ull * in.in_dim, outs[i].ptr, 4ull * outs[i].rows)) xok = false;
+        if (!xok) break;
+        if (xo[s] < 0) spans.push_back(CallerSpan{o.x, 4ull * in.in_dim, s, false});
+        if (in.r && ro[s] < 0) spans.push_back(CallerSpan{o.r, 4ull * in.rows[0], s, true});
+        if (o.nw) spans.push_back(CallerSpan{o.nw, 4ull * in.in_dim, s, false});
         const int nout = in.gate_up ? 1 : in.nmat;
         for (int m = 0; m < nout && xok; m++) {
             const uint64_t y = (uint64_t)in.y[m];
             const int rows = in.rows[m];
             if (overlap(y, 4ull * rows, o.x, 4ull * in.in_dim)) xok = false;
+            for (size_t i = 0; i < spans.size() && xok; i++) {
+                const CallerSpan &c = spans[i];
+                if (!overlap(y, 4ull * rows, c.ptr, c.bytes)) continue;
+                if (c.reader == s) xok = c.residual && c.ptr == y && c.bytes == 4ull * rows;
+                else xok = ordered_after(c.reader, s);
+            }
             int hit = -1;
             for (size_t i = 0; i < outs.size() && xok; i++) {
                 if (outs[i].ptr == y) hit = (int)i;
@@ -1299,8 +1376,9 @@ void *holo_gemv_stream_create(const holo_stream_stage_t *stages, int nstages, in
     if (!xok) {
         delete[] host;
         HOLO_REJECT("holo_gemv_stream_create: a stage input that overlaps an earlier output other than exactly or "
-                    "reads past what its last writer stored, or an output overlapping its own input or another "
-                    "output");
+                    "reads past what its last writer stored, a norm weight in stage output memory, an output "
+                    "overlapping its own input or another output, or an output over caller memory that a stage "
+                    "not yet ordered before it reads");
         return nullptr;
     }
     // the plain stores of a row go to its last writer in the plan

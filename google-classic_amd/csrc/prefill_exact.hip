@@ -22,7 +22,9 @@
 //   acc = fmaf(scale[n,b], C, acc)          (Q6_K: once per 16-weight group)
 //   acc = fmaf(-dmin*m[n,b], sum_k x[m,k], acc)    (Q4_K only)
 // so the result carries fp32 accumulation error plus the 2^-22 split, not
-// the 2^-11 of an f16 operand.  f16 range: |x| must stay below 65504.
+// the 2^-11 of an f16 operand.  Each row of x is scaled by a power of two
+// before the split (largest magnitude into [2^14, 2^15)) and the store
+// scales back, so any finite x keeps both halves in f16 range.
 //
 // Workgroup: 4 waves in a 2 x 2 grid, each owning WM x WN 32 x 32 tiles; K
 // advances S blocks per stage through a double-buffered LDS stage, the next
@@ -59,6 +61,7 @@ struct ExactArgs {
     int n_end[kExactMats];         // prefix sums of N_i; unused entries INT_MAX
     const _Float16 *Ah, *Al;       // activation halves [M][K]
     const float *Sx;               // [M][nb] block sums of x (EW_Q4_K)
+    const float *Rs;               // [M] row scales: the halves hold x / Rs
     int M, N, nb;
     int ntm, tiles;
     const float *R;                // one matrix only: Y = R + product (may alias Y)
@@ -550,63 +553,33 @@ __global__ __launch_bounds__(256, OCC) void gemm_exact_k(ExactArgs a)
                 const int m = m0 + wm0 + 32 * mi + (r & 3) + 4 * h + 8 * (r >> 2);
                 if (m < a.M && n < w.N) {
                     const int64_t o = (int64_t)m * w.N + n;
-                    w.Y[o] = a.R ? a.R[o] + acc[mi][ni][r] : acc[mi][ni][r];
+                    const float y = acc[mi][ni][r] * a.Rs[m];  // a power of two: exact
+                    w.Y[o] = a.R ? a.R[o] + y : y;
                 }
             }
         }
 }
 
-// ---- the activation halves: Ah, Al [M][K] f16 and the block sums Sx [M][K/32] ----
-// One thread per 8 values; the 4 threads of a 32-block sit in an aligned
-// lane quad, whose partial sums meet with two DPP steps.  SWIGLU: the
-// activations are silu(g) * u as cuda_silu_mul computes them
-// (cuda_ops.cu:304-314).
+// ---- the activation halves: Ah, Al [M][K] f16, block sums Sx [M][K/32], row scales Rs [M] ----
+// One workgroup per row.  The row's values y (x; silu(g) * u as
+// cuda_silu_mul computes it, cuda_ops.cu:304-314; or the RMS-normed row,
+// rms_norm_rows4_k's arithmetic: thread t sums the squares of float4s
+// t + 256 j, the same workgroup reduction, x * scale * w, so the normed
+// values are the bits the separate norm writes) are scaled by a power of two
+// 2^e chosen from the row's largest magnitude a: a * 2^e lies in
+// [2^14, 2^15).  The halves then never overflow f16 (|y| up to fp32's range
+// is taken) and the low half is a normal f16 for every value above
+// a * 2^-17, so x - xh - xl stays within 2^-22 |x| there and within
+// a * 2^-40 below.  The product's store multiplies by Rs = 2^-e (exact).  A
+// 32-block is the 8 float4 of 8 adjacent lanes (K % 32 == 0); Sx holds the
+// block sums of the scaled values (for the Q4_K min term).
+enum XSplitMode { XS_PLAIN = 0, XS_SWIGLU = 1, XS_NORM = 2 };
 
-template <bool SWIGLU>
-__global__ __launch_bounds__(256) void xsplit_k(uint4 *__restrict__ Ah, uint4 *__restrict__ Al, float *__restrict__ Sx,
-                                                const float *__restrict__ X, const float *__restrict__ U, int64_t n8)
-{
-    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const bool live = g < n8;
-    const int64_t gi = live ? g : n8 - 1;
-    float v[8];
-    *(float4 *)&v[0] = ((const float4 *)X)[2 * gi];
-    *(float4 *)&v[4] = ((const float4 *)X)[2 * gi + 1];
-    if constexpr (SWIGLU) {
-        float u[8];
-        *(float4 *)&u[0] = ((const float4 *)U)[2 * gi];
-        *(float4 *)&u[4] = ((const float4 *)U)[2 * gi + 1];
-#pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = (v[j] / (1.0f + expf(-v[j]))) * u[j];
-    }
-    uint32_t hw[4], lw[4];
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const _Float16 h0 = (_Float16)v[2 * j], h1 = (_Float16)v[2 * j + 1];
-        const _Float16 l0 = (_Float16)(v[2 * j] - (float)h0), l1 = (_Float16)(v[2 * j + 1] - (float)h1);
-        hw[j] = __builtin_bit_cast(uint32_t, h2{h0, h1});
-        lw[j] = __builtin_bit_cast(uint32_t, h2{l0, l1});
-        s += v[2 * j] + v[2 * j + 1];
-    }
-    // sum over the quad (lanes 4q .. 4q+3 = the block's 32 values, in order)
-    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
-    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
-    if (!live) return;
-    Ah[g] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    Al[g] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-    if (Sx && (g & 3) == 0) Sx[g >> 2] = s;
-}
-
-// The halves of RMS-normed rows, one workgroup per row: rms_norm_rows4_k's
-// arithmetic (thread t sums the squares of float4s t + 256j, the same
-// workgroup reduction, x * scale * w), so the normed values are the bits the
-// separate norm writes, then xsplit_k's split; the normed rows never reach
-// HBM in fp32.  A 32-block is the 8 float4 of 8 adjacent lanes (K % 32 == 0).
-template <int NV>
-__global__ __launch_bounds__(256) void xsplit_norm_k(uint2 *__restrict__ Ah, uint2 *__restrict__ Al,
-                                                     float *__restrict__ Sx, const float *__restrict__ X,
-                                                     const float *__restrict__ NW, int K, float eps)
+template <int NV, int MODE>
+__global__ __launch_bounds__(256) void xsplit_row_k(uint2 *__restrict__ Ah, uint2 *__restrict__ Al,
+                                                    float *__restrict__ Sx, float *__restrict__ Rs,
+                                                    const float *__restrict__ X, const float *__restrict__ U,
+                                                    const float *__restrict__ NW, int K, float eps)
 {
     __shared__ float red[16];
     const int n4 = K >> 2;
@@ -618,24 +591,53 @@ __global__ __launch_bounds__(256) void xsplit_norm_k(uint2 *__restrict__ Ah, uin
     for (int j = 0; j < NV; j++) {
         const int i = threadIdx.x + 256 * j;
         v[j] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-        // the weights load with the row, not after the reduction
-        wv[j] = ((const float4 *)NW)[min(i, n4 - 1)];
-        ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+        if constexpr (MODE == XS_SWIGLU) {
+            const float4 u = i < n4 ? ((const float4 *)U + r4)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[j].x = (v[j].x / (1.0f + expf(-v[j].x))) * u.x;
+            v[j].y = (v[j].y / (1.0f + expf(-v[j].y))) * u.y;
+            v[j].z = (v[j].z / (1.0f + expf(-v[j].z))) * u.z;
+            v[j].w = (v[j].w / (1.0f + expf(-v[j].w))) * u.w;
+        }
+        if constexpr (MODE == XS_NORM) {
+            // the weights load with the row, not after the reduction
+            wv[j] = ((const float4 *)NW)[min(i, n4 - 1)];
+            ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+        }
     }
-    ss = block_reduce<false>(ss, red);
-    const float scale = 1.0f / sqrtf(ss / (float)K + eps);
+    float scale = 1.f;
+    if constexpr (MODE == XS_NORM) {
+        ss = block_reduce<false>(ss, red);
+        scale = 1.0f / sqrtf(ss / (float)K + eps);
+    }
+    float am = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        if constexpr (MODE == XS_NORM) {
+            const float4 w4 = wv[j];
+            v[j] = make_float4(v[j].x * scale * w4.x, v[j].y * scale * w4.y, v[j].z * scale * w4.z,
+                               v[j].w * scale * w4.w);
+        }
+        am = fmaxf(am, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    }
+    am = block_reduce<true>(am, red);
+    // 2^e with a * 2^e in [2^14, 2^15); e = 0 for a zero or non-finite row
+    int e = 0;
+    if (am > 0.f && am <= 3.4028235e38f) {
+        int ea;
+        (void)frexpf(am, &ea);  // am = f * 2^ea, f in [0.5, 1)
+        e = 15 - ea;
+    }
+    if (threadIdx.x == 0) Rs[blockIdx.x] = ldexpf(1.0f, -e);
 #pragma unroll
     for (int j = 0; j < NV; j++) {
         const int i = threadIdx.x + 256 * j;
         if (256 * j >= n4) break;  // uniform: no lane of this or a later j is live
-        const float4 w4 = wv[j];
-        const float y[4] = {v[j].x * scale * w4.x, v[j].y * scale * w4.y, v[j].z * scale * w4.z,
-                            v[j].w * scale * w4.w};
+        const float y[4] = {ldexpf(v[j].x, e), ldexpf(v[j].y, e), ldexpf(v[j].z, e), ldexpf(v[j].w, e)};
         _Float16 h[4], l[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            h[e] = (_Float16)y[e];
-            l[e] = (_Float16)(y[e] - (float)h[e]);
+        for (int q = 0; q < 4; q++) {
+            h[q] = (_Float16)y[q];
+            l[q] = (_Float16)(y[q] - (float)h[q]);
         }
         // the block's sum over its 8 lanes (octets are wholly live or dead)
         float s = (y[0] + y[1]) + (y[2] + y[3]);
@@ -748,12 +750,13 @@ int exact_kind(int type)
 }  // namespace
 
 // Takes the exact product: M >= 1, K whole blocks of the type (Q4_K, Q6_K: a
-// multiple of 256), activations 16-byte aligned; the weight stream
+// multiple of 256) up to 16384, activations 16-byte aligned; the weight stream
 // aligned as its loads need (Q4_0/Q8_0: 4 bytes, Q4_K: 16, Q6_K: 2, F16:
 // 16).
 bool exact_ok(int type, int K, const void *W)
 {
     const uintptr_t w = (uintptr_t)W;
+    if (K > 16384) return false;  // the activation split keeps a row in registers
     switch (type) {
     case HOLO_TYPE_Q4_0:
     case HOLO_TYPE_Q8_0: return K % 32 == 0 && K > 0 && (w & 3u) == 0;
@@ -773,33 +776,30 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
 {
     const int nb = K / 32;
     const size_t half = ((size_t)M * K * 2 + 255) & ~(size_t)255;
-    const size_t abytes = 2 * half + (size_t)M * nb * 4;
+    const size_t sxb = ((size_t)M * nb * 4 + 255) & ~(size_t)255;
+    const size_t abytes = 2 * half + sxb + (size_t)M * 4;
     void *aws = workspace(1, abytes);
     const bool own_a = aws == nullptr;
     if (own_a) HOLO_CHECK(hipMallocAsync(&aws, abytes, stream()));
     if (!aws) return;
     _Float16 *Ah = (_Float16 *)aws, *Al = (_Float16 *)((uint8_t *)aws + half);
     float *Sx = (float *)((uint8_t *)aws + 2 * half);
+    float *Rs = (float *)((uint8_t *)aws + 2 * half + sxb);
     bool need_sx = false;
     size_t pbytes = 0;
     for (int i = 0; i < nmat; i++) {
         need_sx = need_sx || types[i] == HOLO_TYPE_Q4_K;
         if (types[i] == HOLO_TYPE_Q6_K && q6_panel()) pbytes += (size_t)N[i] * K * 2 + (size_t)N[i] * (K / 16) * 4;
     }
-    const int64_t n8 = (int64_t)M * K / 8;
-    const unsigned grid = (unsigned)((n8 + 255) / 256);
-    if (NW && K <= 1024 * 4)
-        hipLaunchKernelGGL(xsplit_norm_k<4>, dim3(M), dim3(256), 0, stream(), (uint2 *)Ah, (uint2 *)Al,
-                           need_sx ? Sx : nullptr, X, NW, K, eps);
-    else if (NW)
-        hipLaunchKernelGGL(xsplit_norm_k<16>, dim3(M), dim3(256), 0, stream(), (uint2 *)Ah, (uint2 *)Al,
-                           need_sx ? Sx : nullptr, X, NW, K, eps);
-    else if (U)
-        hipLaunchKernelGGL(xsplit_k<true>, dim3(grid), dim3(256), 0, stream(), (uint4 *)Ah, (uint4 *)Al,
-                           need_sx ? Sx : nullptr, X, U, n8);
-    else
-        hipLaunchKernelGGL(xsplit_k<false>, dim3(grid), dim3(256), 0, stream(), (uint4 *)Ah, (uint4 *)Al,
-                           need_sx ? Sx : nullptr, X, nullptr, n8);
+    // one workgroup per row, K <= 16384 (exact_ok): the row in registers
+    auto split = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(M), dim3(256), 0, stream(), (uint2 *)Ah, (uint2 *)Al, need_sx ? Sx : nullptr,
+                           Rs, X, U, NW, K, eps);
+    };
+    const bool small = K <= 1024 * 4;
+    if (NW) small ? split(xsplit_row_k<4, XS_NORM>) : split(xsplit_row_k<16, XS_NORM>);
+    else if (U) small ? split(xsplit_row_k<4, XS_SWIGLU>) : split(xsplit_row_k<16, XS_SWIGLU>);
+    else small ? split(xsplit_row_k<4, XS_PLAIN>) : split(xsplit_row_k<16, XS_PLAIN>);
     HOLO_LAUNCH_CHECK();
     // Q6_K matrices: their integer panels and group scales
     void *pws = nullptr;
@@ -852,6 +852,7 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
         a.Ah = Ah;
         a.Al = Al;
         a.Sx = Sx;
+        a.Rs = Rs;
         a.M = M;
         a.N = acc;
         a.nb = nb;

@@ -91,7 +91,9 @@ def test_exact_product(holo, synth, oracle, t, M, N, K):
     holo.check("exact product")
     got = down(dY, M * N).reshape(M, N)
     assert np.all(np.isfinite(got))
-    rows = np.arange(M) if M * N * K <= 64 * 4096 * 4096 else np.r_[0:12, M - 4:M]
+    # at the full sizes: the first and last row of every 32-row band, so every
+    # row tile (64 or 128 rows) and the XCD it maps to is checked
+    rows = np.arange(M) if M * N * K <= 64 * 4096 * 4096 else np.unique(np.r_[0:M:32, 31:M:32, 0:4, M - 4:M])
     check_rows(got, X, w, rows, t, K)
     if t in (Q4_0, Q8_0, Q4_K, Q6_K):
         ref = np.stack([oracle.matmul(t, src, X[m], N, K) for m in range(3)])
@@ -170,3 +172,51 @@ def test_exact_multi_types(holo, synth, oracle):
             got = down(dYm[i], M * n).reshape(M, n)
             assert np.array_equal(got.view(np.uint32), down(singles[i], M * n).reshape(M, n).view(np.uint32)), i
             check_rows(got, X, ws[i], np.arange(M), types[i], K)
+
+
+@pytest.mark.parametrize("t", [Q4_0, Q8_0, Q4_K, Q6_K, F16], ids=lambda t: NAMES[t])
+def test_exact_product_row_range(holo, synth, oracle, t):
+    """Rows far from unit scale: the split scales each row by a power of two
+    (largest magnitude into [2^14, 2^15)) and the store scales back, so rows
+    near 1e5 (past f16's 65504), 1e30, 1e-6 and 1e-30 (whose low halves would
+    be f16 subnormals or zero unscaled) keep the same elementwise bound and
+    1e-5 normwise against the float64 truth as unit rows; a zero row gives
+    zeros.  The fused add and SwiGLU forms take the same split."""
+    print(f"case exact product row range {NAMES[t]}", flush=True)
+    M, N, K = 64, 256, 512
+    src, w = weights(synth, oracle, t, N, K, seed=90 + t)
+    X = synth.normal(M * K, seed=91).reshape(M, K)
+    scales = {0: 1e5, 1: 7e4, 2: 1e30, 3: 1e-6, 4: 1e-30, 5: 0.0}
+    for r, f in scales.items():
+        X[r] *= np.float32(f)
+    dW, dX, dY = up(holo, src), up(holo, X), holo.DeviceBuffer(4 * M * N)
+    lib = holo.lib()
+    lib.holo_matmul_batch(dY.ptr, dW.ptr, dX.ptr, M, N, K, t)
+    lib.cuda_sync()
+    holo.check("exact product row range")
+    got = down(dY, M * N).reshape(M, N)
+    assert np.all(np.isfinite(got))
+    assert np.all(got[5] == 0.0)
+    for r in range(M):
+        if r == 5:
+            continue
+        check_rows(got, X, w, np.array([r]), t, K)
+    # SwiGLU in the split with a large up row: silu(g) * u past f16 range
+    G = synth.normal(M * K, seed=92).reshape(M, K)
+    U = synth.normal(M * K, seed=93).reshape(M, K)
+    U[0] *= np.float32(1e6)
+    U[1] *= np.float32(1e-7)
+    dG, dU, dH, dT = up(holo, G), up(holo, U), holo.DeviceBuffer(4 * M * K), holo.DeviceBuffer(4 * M * N)
+    lib.cuda_silu_mul(dH.ptr, dG.ptr, dU.ptr, M * K)
+    lib.holo_matmul_batch(dT.ptr, dW.ptr, dH.ptr, M, N, K, t)
+    Z = np.zeros((M, N), np.float32)
+    dZ = up(holo, Z)
+    lib.holo_matmul_batch_swiglu_add(dZ.ptr, dW.ptr, dG.ptr, dU.ptr, dZ.ptr, M, N, K, t)
+    lib.cuda_sync()
+    holo.check("exact swiglu row range")
+    H = down(dH, M * K).reshape(M, K)
+    T = down(dT, M * N).reshape(M, N)
+    assert np.all(np.isfinite(T))
+    assert np.array_equal(down(dZ, M * N).reshape(M, N), (Z + T).astype(np.float32))
+    for r in (0, 1, 2):
+        check_rows(T, H, w, np.array([r]), t, K)

@@ -176,3 +176,137 @@ def test_decode_step_graph_replays_match_eager(holo, model):
         lib.holo_set_stream(None)
         lib.holo_stream_destroy(s)
     holo.check("graph replays")
+
+
+# ---- the same step as one persistent holo_gemv_stream launch ------------------------------
+
+def stream_plans(holo, dev, B, y11008):
+    """The two 128-stage plans bench.py's stream_step_plans builds, on the same
+    buffer layout: `mm` (the matmuls on xb, o and down writing one shared
+    y11008 buffer) and `fz` (norms in the q/k/v and gate/up staging, residual
+    adds in the o and down stores, in place on x)."""
+    mm, fz = [], []
+    for L in dev:
+        qkv = [L["q"].ptr, L["k"].ptr, L["v"].ptr]
+        gu = [L["gate"].ptr, L["up"].ptr]
+        mm += [holo.stream_stage(qkv, [B.q.ptr, B.k.ptr, B.v.ptr], [DIM] * 3, B.xb.ptr, DIM),
+               holo.stream_stage([L["o"].ptr], [y11008.ptr], [DIM], B.v.ptr, DIM),
+               holo.stream_stage(gu, [B.h.ptr], [FFN], B.xb.ptr, DIM, gate_up=True),
+               holo.stream_stage([L["down"].ptr], [y11008.ptr], [DIM], B.h.ptr, FFN)]
+        fz += [holo.stream_stage(qkv, [B.q.ptr, B.k.ptr, B.v.ptr], [DIM] * 3, B.x.ptr, DIM, norm_w=B.ones.ptr),
+               holo.stream_stage([L["o"].ptr], [B.x.ptr], [DIM], B.v.ptr, DIM, r=B.x.ptr),
+               holo.stream_stage(gu, [B.h.ptr], [FFN], B.x.ptr, DIM, gate_up=True, norm_w=B.ones.ptr),
+               holo.stream_stage([L["down"].ptr], [B.x.ptr], [DIM], B.h.ptr, FFN, r=B.x.ptr)]
+    return holo.StreamPlan(mm, Q4_0), holo.StreamPlan(fz, Q4_0)
+
+
+def oracle_chain(oracle, host, x0):
+    """The decode dataflow of the module docstring on the CPU, untethered."""
+    x = x0.copy()
+    for W in host:
+        xb = rms(x)
+        v = oracle.matmul(Q4_0, W["v"], xb, DIM, DIM)
+        x = (x + oracle.matmul(Q4_0, W["o"], v, DIM, DIM)).astype(np.float32)
+        xb = rms(x)
+        h = oracle.silu_mul(oracle.matmul(Q4_0, W["gate"], xb, FFN, DIM), oracle.matmul(Q4_0, W["up"], xb, FFN, DIM))
+        x = (x + oracle.matmul(Q4_0, W["down"], h, DIM, FFN)).astype(np.float32)
+    return x
+
+
+def test_stream_bench_plans_full_step(holo, oracle, model):
+    """bench.py's two 128-stage stream plans at full size.
+    `mm`: the last layer's q, k, v, h and down output (the values the shared
+    buffers hold after the launch) against the oracle on the GPU's own inputs,
+    and a second launch bit-identical to the first.
+    `fz`: the hidden state after 32 layers against the oracle run untethered
+    through the whole step from the same x, within the 1e-3 bar, and the head
+    logits on it likewise."""
+    lib = holo.lib()
+    host, dev, head_h, head_d, x0 = model
+    B = Bufs(holo)
+    y11008 = holo.DeviceBuffer(4 * FFN)
+    xb = rms(x0)
+    B.xb.upload(xb)
+    mm, fz = stream_plans(holo, dev, B, y11008)
+    try:
+        print("case stream mm plan, 128 stages", flush=True)
+        outs = []
+        for rep in range(2):
+            assert mm.launch() == 0
+            lib.cuda_sync()
+            holo.check("stream mm")
+            assert lib.holo_gemv_stream_status() == 0
+            outs.append({"q": B.q.download(np.float32, DIM), "k": B.k.download(np.float32, DIM),
+                         "v": B.v.download(np.float32, DIM), "h": B.h.download(np.float32, FFN),
+                         "y": y11008.download(np.float32, DIM)})
+        W = host[-1]
+        g = outs[0]
+        worst = 0.0
+        for n in ("q", "k", "v"):
+            worst = max(worst, check(g[n], oracle.matmul(Q4_0, W[n], xb, DIM, DIM), f"mm layer 31 {n}"))
+        worst = max(worst, check(g["h"], oracle.silu_mul(oracle.matmul(Q4_0, W["gate"], xb, FFN, DIM),
+                                                         oracle.matmul(Q4_0, W["up"], xb, FFN, DIM)), "mm gate/up"))
+        worst = max(worst, check(g["y"], oracle.matmul(Q4_0, W["down"], g["h"], DIM, FFN), "mm down"))
+        for n in g:
+            assert np.array_equal(outs[1][n].view(np.uint32), g[n].view(np.uint32)), n
+        print(f"  mm plan: last layer worst error {worst:.2e}, repeat bit-identical", flush=True)
+
+        print("case stream fz plan, 128 stages + head", flush=True)
+        B.x.upload(x0)
+        assert fz.launch() == 0
+        head_launches(lib, B, head_d)
+        lib.cuda_sync()
+        holo.check("stream fz")
+        assert lib.holo_gemv_stream_status() == 0
+        x_end = B.x.download(np.float32, DIM)
+        logits = B.logits.download(np.float32, VOCAB)
+        assert np.all(np.isfinite(x_end)) and np.all(np.isfinite(logits))
+        x_want = oracle_chain(oracle, host, x0)
+        e_x = normwise_err(x_end, x_want)
+        e_l = normwise_err(logits, oracle.matmul(Q8_0, head_h, rms(x_want), VOCAB, DIM))
+        print(f"  fz plan: hidden state {e_x:.2e}, logits {e_l:.2e} normwise vs the oracle chain", flush=True)
+        assert e_x <= TOL and e_l <= TOL
+    finally:
+        mm.close()
+        fz.close()
+
+
+def test_stream_128_stages_every_output(holo, oracle, model):
+    """The mm plan's 128 stages with an output buffer of its own for every
+    stage (q, k, v, gate/up on xb; o on that layer's v; down on that layer's
+    h), so every one of the 224 layer GEMVs is checked against the oracle on
+    the GPU's own input, within the 1e-3 bar."""
+    print("case stream 128 stages, every output", flush=True)
+    lib = holo.lib()
+    host, dev, _, _, x0 = model
+    xb = rms(x0)
+    dxb = holo.DeviceBuffer.from_array(xb)
+    outs, stages = [], []
+    for L in dev:
+        o = {"q": holo.DeviceBuffer(4 * DIM), "k": holo.DeviceBuffer(4 * DIM), "v": holo.DeviceBuffer(4 * DIM),
+             "o": holo.DeviceBuffer(4 * DIM), "h": holo.DeviceBuffer(4 * FFN), "y": holo.DeviceBuffer(4 * DIM)}
+        outs.append(o)
+        stages += [holo.stream_stage([L["q"].ptr, L["k"].ptr, L["v"].ptr], [o["q"].ptr, o["k"].ptr, o["v"].ptr],
+                                     [DIM] * 3, dxb.ptr, DIM),
+                   holo.stream_stage([L["o"].ptr], [o["o"].ptr], [DIM], o["v"].ptr, DIM),
+                   holo.stream_stage([L["gate"].ptr, L["up"].ptr], [o["h"].ptr], [FFN], dxb.ptr, DIM, gate_up=True),
+                   holo.stream_stage([L["down"].ptr], [o["y"].ptr], [DIM], o["h"].ptr, FFN)]
+    plan = holo.StreamPlan(stages, Q4_0)
+    try:
+        assert plan.launch() == 0
+        lib.cuda_sync()
+        holo.check("stream 128")
+        assert lib.holo_gemv_stream_status() == 0
+        worst = 0.0
+        for l, (W, o) in enumerate(zip(host, outs)):
+            g = {n: o[n].download(np.float32, FFN if n == "h" else DIM) for n in o}
+            for n in ("q", "k", "v"):
+                worst = max(worst, check(g[n], oracle.matmul(Q4_0, W[n], xb, DIM, DIM), f"layer {l} {n}"))
+            worst = max(worst, check(g["o"], oracle.matmul(Q4_0, W["o"], g["v"], DIM, DIM), f"layer {l} o"))
+            worst = max(worst, check(g["h"], oracle.silu_mul(oracle.matmul(Q4_0, W["gate"], xb, FFN, DIM),
+                                                             oracle.matmul(Q4_0, W["up"], xb, FFN, DIM)),
+                                     f"layer {l} gate/up"))
+            worst = max(worst, check(g["y"], oracle.matmul(Q4_0, W["down"], g["h"], DIM, FFN), f"layer {l} down"))
+        print(f"  224 GEMVs, worst error {worst:.2e}", flush=True)
+    finally:
+        plan.close()

@@ -111,6 +111,14 @@ def test_quantize_act_bit_exact(holo, synth, oracle, rows, k):
     assert np.array_equal(down(dq, rows * (k // 32) * 34, np.uint8), oracle.quantize_act_q8_0(X))
 
 
+def tile_rows(M):
+    """All rows for small M; otherwise the first and last row of every
+    32-row band (and the last row of M)."""
+    if M <= 96:
+        return np.arange(M)
+    return np.unique(np.r_[0:M:32, 31:M:32, M - 1])
+
+
 @pytest.mark.parametrize("M,N,K", [(16, 16, 32), (64, 64, 256), (77, 150, 4096), (512, 11008, 4096),
                                    (512, 4096, 11008)], ids=str)
 def test_gemm_q4_0_q8_0_bit_exact(holo, synth, oracle, M, N, K):
@@ -122,10 +130,12 @@ def test_gemm_q4_0_q8_0_bit_exact(holo, synth, oracle, M, N, K):
     holo.lib().cuda_sync()
     holo.check("gemm")
     got = down(dY, M * N).reshape(M, N)
-    # the oracle is checked on a row subset at the full sizes (CPU time)
-    rows = slice(0, min(M, 24))
-    want = oracle.gemm_q4_0_q8_0(W, Xq.reshape(M, -1)[rows].copy().reshape(-1), rows.stop, N, K)
-    assert np.array_equal(got[rows].view(np.uint32), want.view(np.uint32))
+    # At the full sizes the oracle runs on a row subset (CPU time) that holds
+    # the first and last row of every 32-row band, so every row tile of every
+    # tile shape (64 and 128 rows), and every XCD the tiles map to, is checked.
+    rows = tile_rows(M)
+    want = oracle.gemm_q4_0_q8_0(W, Xq.reshape(M, -1)[rows].copy().reshape(-1), len(rows), N, K)
+    assert np.array_equal(got[rows].view(np.uint32), want.reshape(len(rows), N).view(np.uint32))
 
 
 def f16_bound(K, A):

@@ -410,4 +410,25 @@ def test_stream_rejects_unsupported(holo, synth):
                          holo.stream_stage([W3.ptr], [y.ptr], [16], big.ptr, 512)], Q4_0)
     ok = holo.StreamPlan([first, holo.stream_stage([W3.ptr], [y.ptr], [16], big.ptr, 512)], Q4_0)
     ok.close()
+    # caller memory read with plain loads: [y = A x; x = C w] stores over the
+    # x that stage 0 may still be reading on a slow workgroup (stage 1 does
+    # not wait for stage 0), so it is rejected; with a stage between them that
+    # copies stage 0's whole output, every workgroup is past stage 0 first
+    w512 = _up(holo, synth.normal(512, seed=10))
+    over_x = holo.stream_stage([W3.ptr], [x512.ptr], [512], w512.ptr, 512)
+    with pytest.raises(holo.HoloError):
+        holo.StreamPlan([first, over_x], Q4_0)
+    mid = holo.DeviceBuffer(4 * 512)
+    ok = holo.StreamPlan([first, holo.stream_stage([W3.ptr], [mid.ptr], [512], big.ptr, 512), over_x], Q4_0)
+    ok.close()
+    with pytest.raises(holo.HoloError):  # a later output over a norm weight read by stage 0
+        holo.StreamPlan([holo.stream_stage([W3.ptr], [big.ptr], [512], x512.ptr, 512, norm_w=w512.ptr),
+                         holo.stream_stage([W3.ptr], [w512.ptr], [512], mid.ptr, 512)], Q4_0)
+    with pytest.raises(holo.HoloError):  # a norm weight in an earlier stage's output
+        holo.StreamPlan([first, holo.stream_stage([W3.ptr], [mid.ptr], [512], x512.ptr, 512, norm_w=big.ptr)],
+                        Q4_0)
+    with pytest.raises(holo.HoloError):  # a residual that overlaps its own output at another offset
+        holo.StreamPlan([holo.stream_stage([W3.ptr], [big.ptr + 64], [512], x512.ptr, 512, r=big.ptr)], Q4_0)
+    ok = holo.StreamPlan([holo.stream_stage([W3.ptr], [big.ptr], [512], x512.ptr, 512, r=big.ptr)], Q4_0)
+    ok.close()
     lib.cuda_sync()
