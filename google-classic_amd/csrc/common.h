@@ -35,7 +35,7 @@ bool attention_scratch_init();
 void attention_scratch_release();
 void panel_workspace_release();  // the batched products' panel buffers (prefill.hip)
 // The batched products' kept workspaces (prefill.hip): slot 0 weight panels,
-// slot 1 activation panels.  A device buffer of at least `bytes`, grown with
+// slot 1 activation panels, slot 2 the exact product's split-K partials.  A device buffer of at least `bytes`, grown with
 // hipMalloc outside graph capture and reused in stream order; nullptr under
 // capture or when growing fails (the caller then allocates stream-ordered).
 void *workspace(int slot, size_t bytes);
@@ -43,6 +43,9 @@ void *workspace(int slot, size_t bytes);
 // stream take it, and the product itself (Y[i] = X . W[i]^T, or of silu(X) *
 // U, plus R for one matrix).
 bool exact_ok(int type, int K, const void *W);
+// The exact product's tile counters (split-K form), allocated once by cuda_init.
+bool exact_init();
+void exact_release();
 // With NW, the rows of X are RMS-normed first (weight NW, K <= 16384, 16-byte
 // aligned), as holo_rms_norm_rows computes them, inside the activation halves.
 void exact_product(float *const *Y, const void *const *W, const int *types, const int *N, int nmat, const float *X,

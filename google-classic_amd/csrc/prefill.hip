@@ -547,8 +547,8 @@ void holo_quantize_act_q8_0(void *dst_blocks, const float *X, int rows, int k)
 // capture, or when growing fails, the call allocates stream-ordered instead.  Calls
 // that overlap on different streams would share a buffer: the library issues
 // on one stream.
-static void *g_ws[2] = {nullptr, nullptr};
-static size_t g_ws_bytes[2] = {0, 0};
+static void *g_ws[3] = {nullptr, nullptr, nullptr};
+static size_t g_ws_bytes[3] = {0, 0, 0};
 
 namespace holo {
 void *workspace(int slot, size_t bytes)
@@ -1023,7 +1023,7 @@ namespace holo {
 void panel_workspace_release()
 {
     (void)hipDeviceSynchronize();
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < 3; i++) {
         if (g_ws[i]) (void)hipFree(g_ws[i]);
         g_ws[i] = nullptr;
         g_ws_bytes[i] = 0;

@@ -48,6 +48,7 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef uint32_t v3u __attribute__((ext_vector_type(3)));
 
 // Weight source of one launch.
 enum ExactW { EW_Q4_0 = 0, EW_Q8_0 = 1, EW_Q4_K = 2, EW_P16 = 3, EW_F16 = 4, EW_Q6_K = 5 };
@@ -691,6 +692,376 @@ __global__ __launch_bounds__(256) void q6_k_int_panel_k(_Float16 *__restrict__ y
     }
 }
 
+// ---- the second tiling: 64 x 256 workgroup tiles, weights straight into registers ----
+//
+// A workgroup takes 64 rows and 256 columns; wave w takes columns 64 w ..
+// 64 w + 63 of them and all 64 rows (2 x 2 tiles of 32 x 32).  The four
+// waves share one copy of the activation halves in LDS, staged S blocks at a
+// time (registers -> LDS, one barrier per stage).  Each lane loads the weight
+// words of its own columns straight into registers, one stage ahead (lane
+// (c, h) of a 32 x 32 tile holds B[k][c] for k = 8h .. 8h + 7 of each
+// 16-column step: Q4_0 / Q4_K the low nibbles of qs[8h .. 8h + 7] for the
+// first step and their high nibbles for the second, Q8_0 qs[8h ..] and
+// qs[16 + 8h ..], F16 the row's own values), so the weights take no LDS
+// traffic and no barrier.  The arithmetic is the first tiling's: per 32-block
+// four MFMAs give C = sum_k (xh + xl) * w, folded in block order by
+// acc = fmaf(scale, C, acc) (Q4_K: then acc = fmaf(-dmin*m, sum x, acc)).
+//
+// With fewer tiles than CUs the K range is split into P parts (P = 2 or 4)
+// of whole stages; each part stores its unscaled accumulators, device-scope,
+// and counts itself on the tile's counter; the last part to arrive adds the
+// parts in part order, scales and stores.  The result then depends on P (a
+// different fp32 summation), which depends on the launch's tile count.
+
+constexpr int kX2Parts = 4;          // the most K parts of a tile
+constexpr int kX2DevScope = 16;      // sc1: device-scope store / device-coherent load
+constexpr int kX2Counters = 16384;   // tile counters of the split form
+
+struct X2Args {
+    float *Y[kExactMats];
+    const uint8_t *W[kExactMats];    // block streams or f16 rows [N_i][K]
+    int n_end[kExactMats];           // prefix sums of N_i; unused entries INT_MAX
+    const _Float16 *Ah, *Al;         // activation halves [M][K]
+    const float *Rs;                 // [M] row scales
+    const float *R;                  // one matrix only: Y = R + product (may alias Y)
+    float *part;                     // [P][tiles][64 x 256] partial accumulators (P > 1)
+    uint32_t *cnt;                   // [tiles] arrival counters, zero between launches (P > 1)
+    int M, N, nb, ntm, tiles, P, spp; // spp: stages per part
+};
+
+template <int S>
+struct X2Geo {
+    static constexpr int RB = S * 64 + 16;         // LDS bytes per row of one half (S blocks of 32 f16 + pad)
+    static constexpr int HALF = 64 * RB;
+    static constexpr int STAGE = (2 * HALF + 255) & ~255;
+    static constexpr int LDS = 2 * STAGE;
+};
+
+// Weight words of one block for one lane and one 32-column tile, as loaded.
+// The weights are read through a buffer resource over the lane's matrix: the
+// lane's row offset (plus 8 h) is the per-lane offset, fixed for the launch,
+// and the block's offset is a wave-uniform scalar.  With an even number of
+// blocks per row every Q4_0 / Q8_0 row starts 4-byte aligned, so block b sits
+// 2 (b & 1) bytes into its first dword: the window starts there rounded down,
+// and its realignment is a constant per unrolled block (none for odd b).
+// The resource's size bounds the reads: a block past the last row's end
+// reads zeros (its scale is then zero anyway).
+template <int WF>
+struct X2Raw;
+template <>
+struct X2Raw<EW_Q4_0> {
+    uint32_t w[3];     // from the block's start rounded down, plus 8 h: qs[8h .. 8h + 7] at byte 2 + 2(b & 1);
+                       // for h = 0 the window also holds d (bytes 0-1 or 2-3)
+};
+template <>
+struct X2Raw<EW_Q8_0> {
+    uint32_t w[3], v[3];  // the two 8-byte runs qs[8h ..] and qs[16 + 8h ..], same windows (h = 0: d too)
+};
+
+// The block scale d of lane (c, 0) in both lanes (c, 0) and (c, 1): the h = 1
+// windows start 8 bytes into the block, so they take it from the h = 0 lane
+// (v_permlane32_swap: lanes 32..63 of the first result are lanes 0..31 of x).
+template <int P>
+__device__ __forceinline__ uint32_t x2_scale_bits(uint32_t w0)
+{
+    const uint32_t x = P ? (w0 >> 16) : (w0 & 0xFFFFu);
+    return __builtin_amdgcn_permlane32_swap(x, x, false, false)[0];
+}
+template <>
+struct X2Raw<EW_F16> {
+    v4u s0, s1;        // k = 8h .. 8h+7 and 16 + 8h .. 16 + 8h + 7
+};
+
+// Block b of the lane's row (vo: the row's byte offset within the matrix,
+// plus 8 h for the block formats, 16 h for F16).  P = b & 1 (block formats).
+template <int WF, int P>
+__device__ __forceinline__ X2Raw<WF> x2_fetch(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t vd, int b)
+{
+    X2Raw<WF> x;
+    if constexpr (WF == EW_Q4_0) {
+        const int so = 18 * b - 2 * P;
+        const v3u t = __builtin_amdgcn_raw_buffer_load_b96(r, (int)vo, so, 0);
+        x.w[0] = t.x;
+        x.w[1] = t.y;
+        x.w[2] = t.z;
+    } else if constexpr (WF == EW_Q8_0) {
+        const int so = 34 * b - 2 * P;
+        const v3u t = __builtin_amdgcn_raw_buffer_load_b96(r, (int)vo, so, 0);
+        x.w[0] = t.x;
+        x.w[1] = t.y;
+        x.w[2] = t.z;
+        const v3u u = __builtin_amdgcn_raw_buffer_load_b96(r, (int)vo, so + 16, 0);
+        x.v[0] = u.x;
+        x.v[1] = u.y;
+        x.v[2] = u.z;
+    } else {
+        x.s0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, 64 * b, 0));
+        x.s1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, 64 * b + 32, 0));
+    }
+    return x;
+}
+
+// The B operands of both 16-k steps and the block's scale; live: the block
+// is inside the part (else the scale is zero).
+template <int WF, int P>
+__device__ __forceinline__ void x2_unpack(const X2Raw<WF> &x, bool live, v8h &b0, v8h &b1, float &sc)
+{
+    uint32_t lo[4], hi[4];
+    if constexpr (WF == EW_Q4_0) {
+        // qs[8h ..] at byte 2 of the window (even b) or 4 (odd b)
+        const uint32_t q0 = P ? x.w[1] : __builtin_amdgcn_alignbyte(x.w[1], x.w[0], 2);
+        const uint32_t q1 = P ? x.w[2] : __builtin_amdgcn_alignbyte(x.w[2], x.w[1], 2);
+        nibbles_f16(q0, (_Float16)-8.0f, &lo[0], &hi[0]);
+        nibbles_f16(q1, (_Float16)-8.0f, &lo[2], &hi[2]);
+        // a mask, not a select: the swap stays outside any branch
+        sc = half_bits_to_float(x2_scale_bits<P>(x.w[0]) & (0u - (uint32_t)live));
+    } else if constexpr (WF == EW_Q8_0) {
+        const uint32_t q0 = P ? x.w[1] : __builtin_amdgcn_alignbyte(x.w[1], x.w[0], 2);
+        const uint32_t q1 = P ? x.w[2] : __builtin_amdgcn_alignbyte(x.w[2], x.w[1], 2);
+        const uint32_t q4 = P ? x.v[1] : __builtin_amdgcn_alignbyte(x.v[1], x.v[0], 2);
+        const uint32_t q5 = P ? x.v[2] : __builtin_amdgcn_alignbyte(x.v[2], x.v[1], 2);
+        int8s_f16(q0, &lo[0]);
+        int8s_f16(q1, &lo[2]);
+        int8s_f16(q4, &hi[0]);
+        int8s_f16(q5, &hi[2]);
+        // a mask, not a select: the swap stays outside any branch
+        sc = half_bits_to_float(x2_scale_bits<P>(x.w[0]) & (0u - (uint32_t)live));
+    } else {
+        b0 = __builtin_bit_cast(v8h, x.s0);
+        b1 = __builtin_bit_cast(v8h, x.s1);
+        sc = 1.f;
+        return;
+    }
+    b0 = __builtin_bit_cast(v8h, v4u{lo[0], lo[1], lo[2], lo[3]});
+    b1 = __builtin_bit_cast(v8h, v4u{hi[0], hi[1], hi[2], hi[3]});
+}
+
+template <int WF, int S>
+__global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
+{
+    static_assert(S % 2 == 0, "blocks of a stage alternate in parity: S even");
+    using G = X2Geo<S>;
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ uint32_t last;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the weight resource stays scalar
+    const int h = lane >> 5, c32 = lane & 31;
+    const int nb = a.nb;
+
+    // workgroup g -> (tile t, part p): the workgroups of XCD x (round-robin
+    // dispatch) take a contiguous run, so the row tiles of a column tile
+    // (which share its weights) run on one XCD together
+    const int g = blockIdx.x, total = a.tiles * a.P;
+    const int L = (total & 7) ? g : (g & 7) * (total >> 3) + (g >> 3);
+    const int t = L % a.tiles, p = L / a.tiles;
+    const int m0 = (t % a.ntm) * 64, n0 = (t / a.ntm) * 256 + 64 * wave;
+    const int kb0 = p * a.spp * S;  // even
+    const int kb1 = min(nb, kb0 + a.spp * S);
+
+    // this wave's 64 columns lie in one matrix (n_end multiples of 64); in
+    // the last column tile a wave may start at or past N: it loads in-bounds
+    // rows of the last matrix and stores nothing
+    const bool live = n0 < a.N;
+    const int nc = min(n0, a.N - 1);
+    const int sel = (nc >= a.n_end[0]) + (nc >= a.n_end[1]);
+    const uint8_t *Wm = sel == 2 ? a.W[2] : sel == 1 ? a.W[1] : a.W[0];
+    float *Ym = sel == 2 ? a.Y[2] : sel == 1 ? a.Y[1] : a.Y[0];
+    const int nbase = sel == 2 ? a.n_end[1] : sel == 1 ? a.n_end[0] : 0;
+    const int Nm = (sel == 2 ? a.n_end[2] : sel == 1 ? a.n_end[1] : a.n_end[0]) - nbase;
+    const int nl = nc - nbase;  // the wave's first column in its matrix (clamped)
+    constexpr uint32_t RBW = WF == EW_Q4_0 ? 18 : WF == EW_Q8_0 ? 34 : 64;
+    const uint32_t rowb = (uint32_t)nb * RBW;
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void *)Wm, (short)0, (int)((uint32_t)Nm * rowb), kXBufWord3);
+    uint32_t vo[2], vd[2];
+#pragma unroll
+    for (int ni = 0; ni < 2; ni++) {
+        vd[ni] = (uint32_t)min(nl + 32 * ni + c32, Nm - 1) * rowb;
+        vo[ni] = vd[ni] + (WF == EW_F16 ? 16u : 8u) * (uint32_t)h;
+    }
+
+    // activation staging: thread tid moves piece tid + 256 i of each half,
+    // row (tid + 256 i) / 4S, 16-byte piece (tid + 256 i) % 4S
+    constexpr int NP = 4 * S;  // pieces per row and half in a stage
+    const uint32_t abytes = (uint32_t)((int64_t)a.M * nb * 64);
+    const __amdgpu_buffer_rsrc_t rah = __builtin_amdgcn_make_buffer_rsrc((void *)a.Ah, (short)0, (int)abytes, kXBufWord3);
+    const __amdgpu_buffer_rsrc_t ral = __builtin_amdgcn_make_buffer_rsrc((void *)a.Al, (short)0, (int)abytes, kXBufWord3);
+    uint32_t aoff[S];
+    int ablk[S];
+    uint32_t lw[S];
+#pragma unroll
+    for (int i = 0; i < S; i++) {
+        const int pc = tid + 256 * i, r = pc / NP, c = pc % NP;
+        aoff[i] = (uint32_t)min(m0 + r, a.M - 1) * (uint32_t)(nb * 64) + (uint32_t)(c & 3) * 16u;
+        ablk[i] = c >> 2;
+        lw[i] = (uint32_t)(r * G::RB + c * 16);
+    }
+    v4u sah[S], sal[S];
+    auto fetch_a = [&](int st) {
+        const int kb = kb0 + st * S;
+#pragma unroll
+        for (int i = 0; i < S; i++) {
+            const uint32_t o = aoff[i] + (uint32_t)min(kb + ablk[i], kb1 - 1) * 64u;
+            sah[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rah, (int)o, 0, 0));
+            sal[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(ral, (int)o, 0, 0));
+        }
+    };
+    auto stash_a = [&](int buf) {
+        uint8_t *base = lds + buf * G::STAGE;
+#pragma unroll
+        for (int i = 0; i < S; i++) {
+            *(v4u *)(base + lw[i]) = sah[i];
+            *(v4u *)(base + G::HALF + lw[i]) = sal[i];
+        }
+    };
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[mi][ni][r] = 0.f;
+
+    // F16 has no scale to zero a block past the part with: its block index
+    // is clamped instead (no alignment depends on it)
+    auto wblk = [&](int b) { return WF == EW_F16 ? min(b, kb1 - 1) : b; };
+    const int nst = (kb1 - kb0 + S - 1) / S;
+    // the weight words of a stage's S blocks, fetched one stage ahead
+    X2Raw<WF> ring[S][2];
+#pragma unroll
+    for (int s = 0; s < S; s++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) {
+            if (s & 1) ring[s][ni] = x2_fetch<WF, 1>(rw, vo[ni], vd[ni], wblk(kb0 + s));
+            else ring[s][ni] = x2_fetch<WF, 0>(rw, vo[ni], vd[ni], wblk(kb0 + s));
+        }
+    fetch_a(0);
+    stash_a(0);
+    fetch_a(1);
+    __syncthreads();
+    for (int st = 0; st < nst; st++) {
+        const uint8_t *base = lds + (st & 1) * G::STAGE;
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const int b = kb0 + st * S + s;
+            // this block's weight operands, then its ring slot fetches block b + S
+            v8h b0[2], b1[2];
+            float sc[2];
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++) {
+                if (s & 1) {
+                    x2_unpack<WF, 1>(ring[s][ni], b < kb1, b0[ni], b1[ni], sc[ni]);
+                    ring[s][ni] = x2_fetch<WF, 1>(rw, vo[ni], vd[ni], wblk(b + S));
+                } else {
+                    x2_unpack<WF, 0>(ring[s][ni], b < kb1, b0[ni], b1[ni], sc[ni]);
+                    ring[s][ni] = x2_fetch<WF, 0>(rw, vo[ni], vd[ni], wblk(b + S));
+                }
+            }
+            const bool bl = b < kb1;  // F16: a block past the part adds nothing
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) {
+                const uint8_t *ra = base + (32 * mi + c32) * G::RB + s * 64 + 16 * h;
+                const v8h ah0 = *(const v8h *)ra, ah1 = *(const v8h *)(ra + 32);
+                const v8h al0 = *(const v8h *)(ra + G::HALF), al1 = *(const v8h *)(ra + G::HALF + 32);
+#pragma unroll
+                for (int ni = 0; ni < 2; ni++) {
+                    if constexpr (WF == EW_F16) {
+                        if (bl) {
+                            acc[mi][ni] = mfma16(ah0, b0[ni], acc[mi][ni]);
+                            acc[mi][ni] = mfma16(ah1, b1[ni], acc[mi][ni]);
+                            acc[mi][ni] = mfma16(al0, b0[ni], acc[mi][ni]);
+                            acc[mi][ni] = mfma16(al1, b1[ni], acc[mi][ni]);
+                        }
+                    } else {
+                        const v16f zero = {};
+                        v16f c = mfma16(ah0, b0[ni], zero);
+                        c = mfma16(ah1, b1[ni], c);
+                        c = mfma16(al0, b0[ni], c);
+                        c = mfma16(al1, b1[ni], c);
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[mi][ni][r] = __builtin_fmaf(sc[ni], c[r], acc[mi][ni][r]);
+                    }
+                }
+            }
+        }
+        // stage st + 1 into the other buffer (free: every wave passed the
+        // barrier after stage st - 1), then fetch stage st + 2
+        stash_a((st + 1) & 1);
+        fetch_a(st + 2);
+        __syncthreads();
+    }
+
+    // lane (c, h) holds rows 4h + 8q + j (register 4q + j) of column c of each tile
+    if (a.P > 1) {
+        // parts: store, count, and the last to arrive adds them in part order
+        const __amdgpu_buffer_rsrc_t rp =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.part, (short)0, -1, kXBufWord3);
+        auto slot = [&](int pp, int mi, int ni, int q) {
+            return (uint32_t)((((((int64_t)pp * a.tiles + t) * 4 + wave) * 4 + 2 * mi + ni) * 4 + q) * 1024 + 16 * lane);
+        };
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 v = {acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2],
+                                      acc[mi][ni][4 * q + 3]};
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), rp, (int)slot(p, mi, ni, q), 0,
+                                                           kX2DevScope);
+                }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores have completed (device scope)
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t old = __hip_atomic_fetch_add(a.cnt + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = old == (uint32_t)(a.P - 1);
+        }
+        __syncthreads();
+        if (!last) return;
+        if (tid == 0) __hip_atomic_store(a.cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float4 sum;
+                    for (int pp = 0; pp < a.P; pp++) {
+                        float4 v;
+                        if (pp == p) {
+                            v = float4{acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2],
+                                       acc[mi][ni][4 * q + 3]};
+                        } else {
+                            v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                               rp, (int)slot(pp, mi, ni, q), 0, kX2DevScope));
+                        }
+                        if (pp == 0) sum = v;
+                        else sum = float4{sum.x + v.x, sum.y + v.y, sum.z + v.z, sum.w + v.w};
+                    }
+                    acc[mi][ni][4 * q] = sum.x;
+                    acc[mi][ni][4 * q + 1] = sum.y;
+                    acc[mi][ni][4 * q + 2] = sum.z;
+                    acc[mi][ni][4 * q + 3] = sum.w;
+                }
+    }
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) {
+            const int n = nl + 32 * ni + c32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + 32 * mi + (r & 3) + 4 * h + 8 * (r >> 2);
+                if (live && m < a.M && n < Nm) {
+                    const int64_t o = (int64_t)m * Nm + n;
+                    const float y = acc[mi][ni][r] * a.Rs[m];  // a power of two: exact
+                    Ym[o] = a.R ? a.R[o] + y : y;
+                }
+            }
+        }
+}
+
 template <int WF, int WM, int WN, int S, int OCC, int RD>
 void launch_exact(ExactArgs a)
 {
@@ -727,6 +1098,52 @@ void launch_exact_for(const ExactArgs &a)
     else launch_exact<WF, 1, 1, 2, 2, kExactRing>(a);
 }
 
+uint32_t *g_x2_cnt = nullptr;  // tile counters of the split form, zero between launches
+
+// The second tiling: P K parts when there are fewer 64 x 256 tiles than CUs
+// (at least 32 blocks a part); the stage count per part is whole.
+template <int WF, int S>
+void launch_exact2(X2Args a)
+{
+    using G = X2Geo<S>;
+    a.ntm = (a.M + 63) / 64;
+    a.tiles = a.ntm * ((a.N + 255) / 256);
+    const int nst = (a.nb + S - 1) / S;
+    int P = 1;
+    while (2 * P <= kX2Parts && a.tiles * P <= num_cus() && a.nb / (2 * P) >= 16 && a.tiles <= kX2Counters &&
+           g_x2_cnt)
+        P *= 2;
+    a.P = P;
+    a.spp = (nst + P - 1) / P;
+    void *pws = nullptr;
+    bool own = false;
+    if (P > 1) {
+        const size_t bytes = (size_t)P * a.tiles * 64 * 256 * 4;
+        pws = workspace(2, bytes);
+        own = pws == nullptr;
+        if (own) HOLO_CHECK(hipMallocAsync(&pws, bytes, stream()));
+        if (!pws) return;
+        a.part = (float *)pws;
+        a.cnt = g_x2_cnt;
+    }
+    auto kern = gemm_exact2_k<WF, S>;
+    static bool attr = false;
+    if (!attr) {
+        HOLO_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS));
+        attr = true;
+    }
+    launch_timed(kern, dim3(a.tiles * P), dim3(256), G::LDS, a);
+    HOLO_LAUNCH_CHECK();
+    if (own) HOLO_CHECK(hipFreeAsync(pws, stream()));
+}
+
+// The first tiling only (HOLO_EXACT_V1=1): for same-box comparisons
+static bool exact_v1()
+{
+    static const bool on = getenv("HOLO_EXACT_V1") != nullptr;
+    return on;
+}
+
 // Q6_K through the integer panel instead of unpacked in the staging
 // (HOLO_EXACT_Q6K_PANEL=1)
 static bool q6_panel()
@@ -748,6 +1165,24 @@ int exact_kind(int type)
 }
 
 }  // namespace
+
+bool exact_init()
+{
+    if (g_x2_cnt) return true;
+    if (hipMalloc((void **)&g_x2_cnt, kX2Counters * sizeof(uint32_t)) != hipSuccess) {
+        (void)hipGetLastError();
+        g_x2_cnt = nullptr;
+        return false;
+    }
+    return hipMemset(g_x2_cnt, 0, kX2Counters * sizeof(uint32_t)) == hipSuccess &&
+           hipDeviceSynchronize() == hipSuccess;
+}
+
+void exact_release()
+{
+    if (g_x2_cnt) (void)hipFree(g_x2_cnt);
+    g_x2_cnt = nullptr;
+}
 
 // Takes the exact product: M >= 1, K whole blocks of the type (Q4_K, Q6_K: a
 // multiple of 256) up to 16384, activations 16-byte aligned; the weight stream
@@ -857,6 +1292,37 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
         a.N = acc;
         a.nb = nb;
         a.R = (nmat == 1) ? R : nullptr;
+        // the second tiling: Q4_0 and Q8_0 rows of an even block count (every
+        // row 4-byte aligned) and F16 rows; with several matrices every N but
+        // the last a multiple of 64 (a wave's 64 columns in one matrix); each
+        // matrix under 2 GiB (32-bit offsets)
+        bool x2 = !exact_v1() && (((kind == EW_Q4_0 || kind == EW_Q8_0) && nb % 2 == 0) || kind == EW_F16);
+        for (int j = 0; j < cnt - 1 && x2; j++) x2 = a.n_end[j] % 64 == 0;
+        for (int j = 0; j < cnt && x2; j++) {
+            const int64_t rows = a.n_end[j] - (j ? a.n_end[j - 1] : 0);
+            x2 = rows * (int64_t)nb * (kind == EW_Q4_0 ? 18 : kind == EW_Q8_0 ? 34 : 64) < (1LL << 31);
+        }
+        if (x2) {
+            X2Args b = {};
+            for (int j = 0; j < kExactMats; j++) {
+                b.Y[j] = a.Y[j];
+                b.W[j] = a.W[j];
+                b.n_end[j] = a.n_end[j];
+            }
+            b.Ah = Ah;
+            b.Al = Al;
+            b.Rs = Rs;
+            b.R = a.R;
+            b.M = M;
+            b.N = acc;
+            b.nb = nb;
+            switch (kind) {
+            case EW_Q4_0: launch_exact2<EW_Q4_0, 2>(b); break;
+            case EW_Q8_0: launch_exact2<EW_Q8_0, 2>(b); break;
+            default: launch_exact2<EW_F16, 2>(b); break;
+            }
+            continue;
+        }
         switch (kind) {
         case EW_Q4_0: launch_exact_for<EW_Q4_0>(a); break;
         case EW_Q8_0: launch_exact_for<EW_Q8_0>(a); break;

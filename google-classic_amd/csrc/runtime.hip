@@ -111,6 +111,10 @@ int cuda_init(void)
         fprintf(stderr, "holo_mi355x: cannot allocate the decode-attention scratch\n");
         return -1;
     }
+    if (!holo::exact_init()) {
+        fprintf(stderr, "holo_mi355x: cannot allocate the batched product's tile counters\n");
+        return -1;
+    }
     if (!holo::noalloc_scratch()) {
         fprintf(stderr, "holo_mi355x: cannot look up the fixed scratch array\n");
         return -1;
@@ -130,6 +134,7 @@ void cuda_cleanup(void)
     holo::gemv_stream_release();
     holo::attention_scratch_release();
     holo::panel_workspace_release();
+    holo::exact_release();
     g_stream = nullptr;
     g_initialized = false;
 }

@@ -74,10 +74,10 @@ def exact_mode(holo):
     lib.holo_prefill_set_mode(EXACT)
 
 
-CASES = [(Q4_0, 64, 128, 256), (Q4_0, 77, 150, 4096), (Q4_0, 512, 11008, 4096), (Q4_0, 512, 4096, 11008),
-         (Q8_0, 100, 256, 512), (Q8_0, 512, 4096, 4096), (Q4_K, 128, 512, 2048), (Q4_K, 512, 14336, 4096),
-         (Q4_K, 512, 4096, 14336), (Q6_K, 96, 384, 1024), (Q6_K, 512, 4096, 11008), (F16, 80, 256, 256),
-         (F16, 512, 1024, 4096), (F32, 70, 200, 128)]
+CASES = [(Q4_0, 64, 128, 256), (Q4_0, 77, 150, 4096), (Q4_0, 66, 256, 1056), (Q4_0, 512, 11008, 4096),
+         (Q4_0, 512, 4096, 11008), (Q8_0, 100, 256, 512), (Q8_0, 70, 192, 1056), (Q8_0, 512, 4096, 4096),
+         (Q4_K, 128, 512, 2048), (Q4_K, 512, 14336, 4096), (Q4_K, 512, 4096, 14336), (Q6_K, 96, 384, 1024),
+         (Q6_K, 512, 4096, 11008), (F16, 80, 256, 256), (F16, 512, 1024, 4096), (F32, 70, 200, 128)]
 
 
 @pytest.mark.parametrize("t,M,N,K", CASES, ids=[f"{NAMES[t]}-{m}x{n}x{k}" for t, m, n, k in CASES])
@@ -220,3 +220,49 @@ def test_exact_product_row_range(holo, synth, oracle, t):
     assert np.array_equal(down(dZ, M * N).reshape(M, N), (Z + T).astype(np.float32))
     for r in (0, 1, 2):
         check_rows(T, H, w, np.array([r]), t, K)
+
+
+@pytest.mark.parametrize("t,M,N,K", [(Q4_0, 512, 4096, 11008), (Q8_0, 200, 512, 8192), (F16, 100, 320, 4096)],
+                         ids=["q4_0-512x4096x11008", "q8_0-200x512x8192", "f16-100x320x4096"])
+def test_exact_split_k_deterministic(holo, synth, oracle, t, M, N, K):
+    """Few column tiles and a long K take the K-split form (parts summed in
+    part order by the last part to arrive, counted on per-tile counters that
+    return to zero): two eager calls and three graph replays (with eager
+    work between them) give the same bits, within the bound of the truth."""
+    print(f"case exact split-K {NAMES[t]} {M}x{N}x{K}", flush=True)
+    lib = holo.lib()
+    src, w = weights(synth, oracle, t, N, K, seed=M + 7 * N + K)
+    X = synth.normal(M * K, seed=K + 9).reshape(M, K)
+    dW, dX = up(holo, src), up(holo, X)
+    outs = []
+    for _ in range(2):
+        dY = holo.DeviceBuffer(4 * M * N)
+        lib.holo_matmul_batch(dY.ptr, dW.ptr, dX.ptr, M, N, K, t)
+        lib.cuda_sync()
+        holo.check("exact split-K eager")
+        outs.append(down(dY, M * N).reshape(M, N))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    check_rows(outs[0], X, w, np.unique(np.r_[0:M:37, M - 1]), t, K)
+    s = lib.holo_stream_create()
+    lib.holo_set_stream(s)
+    try:
+        dG = holo.DeviceBuffer(4 * M * N)
+        assert lib.holo_graph_begin() == 0
+        lib.holo_matmul_batch(dG.ptr, dW.ptr, dX.ptr, M, N, K, t)
+        g = lib.holo_graph_end()
+        holo.check("capture")
+        assert g
+        for rep in range(3):
+            lib.holo_graph_launch(g)
+            lib.cuda_sync()
+            got = down(dG, M * N).reshape(M, N)
+            assert np.array_equal(got.view(np.uint32), outs[0].view(np.uint32)), rep
+            dE = holo.DeviceBuffer(4 * M * N)  # eager work between the replays
+            lib.holo_matmul_batch(dE.ptr, dW.ptr, dX.ptr, M, N, K, t)
+            lib.cuda_sync()
+            assert np.array_equal(down(dE, M * N).reshape(M, N).view(np.uint32), outs[0].view(np.uint32)), rep
+        lib.holo_graph_destroy(g)
+    finally:
+        lib.holo_set_stream(None)
+        lib.holo_stream_destroy(s)
+    holo.check("exact split-K graph")
