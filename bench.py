@@ -30,8 +30,7 @@ The printed JSON line carries
                 compiled from the reference sources into oracle/_ref/ with its
                 release flags; the Q4_0 branch is single-threaded scalar code;
                 a bounded sample of the same layer
-  extra         the unfused drop-in layer (7 cuda_matmul_q4_0 calls), the layer
-                as one multi-stage launch (holo_gemv_chain), configs
+  extra         the unfused drop-in layer (7 cuda_matmul_q4_0 calls), configs
                 1 and 3 (Q8_0 4096x4096; Q4_K Llama-3-8B FFN; per matrix the
                 median kernel time over >= 128 launches and its fraction of
                 HBM peak), the Q6_K GEMV (32000x4096 head and 4096x11008
@@ -143,18 +142,6 @@ def layer_fused(lib, L, A, ev=None, kernel_ev=None):
         c()
         if ev and ev[j][1]:
             lib.holo_event_record(ev[j][1])
-
-
-def layer_chain(lib, L, A):
-    """The same four GEMVs as one holo_gemv_chain launch (grid-wide barriers
-    between the stages, next stage's first weights issued before each)."""
-    b = L.buf
-    st = [holo.gemv_stage([b["q"].ptr, b["k"].ptr, b["v"].ptr], [A["q"], A["k"], A["v"]], [DIM] * 3, A["x4096"], DIM),
-          holo.gemv_stage([b["o"].ptr], [A["y4096"]], [DIM], A["v"], DIM),
-          holo.gemv_stage([b["gate"].ptr, b["up"].ptr], [A["h"]], [FFN], A["x4096"], DIM, gate_up=True),
-          holo.gemv_stage([b["down"].ptr], [A["y4096"]], [DIM], A["h"], FFN)]
-    if holo.gemv_chain(st, Q4_0) != 0:
-        raise holo.HoloError("holo_gemv_chain rejected the layer")
 
 
 def layer_unfused(lib, L, A):
@@ -860,13 +847,6 @@ def main():
                                           "us_per_step": round(ums * 1e3 / a.steps, 2),
                                           "launches_per_step": 7}
         log(f"layer step (7 drop-in launches): {ums * 1e3 / a.steps:.1f} us/step")
-        if a.xmode == "mfma":
-            cms = time_steps(lib, layers, lambda L: layer_chain(lib, L, A), a.steps, a.warmup)
-            if lib.holo_gemv_chain_status() != 0:
-                raise holo.HoloError("multi-stage launch could not synchronise")
-            extra["layer_one_launch_chain"] = {"gbs": round(a.steps * bytes_step / (cms * 1e-3) / 1e9, 1),
-                                               "us_per_step": round(cms * 1e3 / a.steps, 2), "launches_per_step": 1}
-            log(f"layer step (one holo_gemv_chain launch): {cms * 1e3 / a.steps:.1f} us/step")
 
         # config 5: full decode step (32 layers + Q8_0 head)
         if a.layers >= 32:
@@ -901,7 +881,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 x f32 -> f32" if a.xmode == "f32" else "q4_0 x (f32 as 24-bit fixed point) -> f32 (int8 planes, int32 block dots)",
+        "dtype": "q4_0 x f32 -> f32" if a.xmode == "f32" else "q4_0 x (f32 as 22-bit fixed point per 32-block) -> f32 (three int8 planes, int32 block dots on int8 MFMA, fp32 accumulation)",
         "data": "synthetic (seeded GGUF Q4_0 blocks, N(0,1) fp32 activations)",
         "config": {"workload": "Llama-2-7B layer: 7 Q4_0 GEMVs (4x 4096x4096, 2x 11008x4096, 1x 4096x11008) "
                                "as 4 launches (fused q/k/v, o, fused gate/up, down) in a HIP graph, rotating over "

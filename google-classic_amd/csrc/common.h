@@ -22,10 +22,6 @@ void latch_error(int code, const char *what, const char *file, int line);
 // Number of compute units of device 0, read once at init.
 int num_cus();
 
-// Device state of the multi-stage GEMV launch (barrier words), set up by
-// cuda_init so that no allocation happens inside a graph capture.
-bool gemv_chain_init();
-void gemv_chain_release();
 // Barrier words of the persistent decode-step kernel (gemv_stream.hip).
 bool gemv_stream_init();
 void gemv_stream_release();

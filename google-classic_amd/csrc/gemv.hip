@@ -440,11 +440,8 @@ struct MfmaArgs {
 };
 
 // One GEMV launch's work for this workgroup: the per-workgroup constants
-// derived from MfmaArgs and the item pipeline.  Used by gemv_mfma_kernel (one
-// stage) and gemv_chain_kernel (several dependent stages in one launch).
-// XDEV: activations read and outputs written device-coherently (sc1), as the
-// multi-stage launch passes vectors between its stages through memory.
-template <int FMT, int P, int MODE, bool XDEV = false>
+// derived from MfmaArgs and the item pipeline (gemv_mfma_kernel).
+template <int FMT, int P, int MODE>
 struct MfmaStage {
     using GE = Geo<FMT>;
     static constexpr int TR = MODE == MODE_GATEUP ? 8 : 16;  // rows per matrix per tile
@@ -474,9 +471,8 @@ struct MfmaStage {
     // address and piece i of this lane lies loff[i] bytes past it (for GATEUP
     // the offset also picks the gate or up matrix, counted from the lower of
     // the two bases, wlo), so an item costs no per-lane address arithmetic.
-    // fast: every such offset fits 32 bits.  The multi-stage launch keeps
-    // the general path (its registers are taken by the stages it holds).
-    static constexpr bool kFastIssue = !XDEV;
+    // fast: every such offset fits 32 bits.
+    static constexpr bool kFastIssue = true;
     uint32_t loff[kFastIssue ? GE::NL : 1];
     uint64_t wlo;
     bool fast;
@@ -553,11 +549,7 @@ struct MfmaStage {
         m = a1 + a2;
         r = v - (a2 ? re1 : a1 ? re0 : 0);
     }
-    __device__ __forceinline__ static void store_y(gfloat *p, float v)
-    {
-        if constexpr (XDEV) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else *p = v;
-    }
+    __device__ __forceinline__ static void store_y(gfloat *p, float v) { *p = v; }
     __device__ __forceinline__ gbyte *wbase(int m) const { return (gbyte *)(w0 + (m == 2 ? dw2 : m == 1 ? dw1 : 0)); }
     __device__ __forceinline__ gfloat *ybase(int m) const { return (gfloat *)(y0 + (m == 2 ? dy2 : m == 1 ? dy1 : 0)); }
 
@@ -688,7 +680,7 @@ struct MfmaStage {
                 } else if (v < rend) {
                     int m, row;
                     split_row(v, m, row);
-                    if (!XDEV && args.r) s0 = ((gcfloat *)args.r)[row] + s0;
+                    if (args.r) s0 = ((gcfloat *)args.r)[row] + s0;
                     store_y(ybase(m) + row, s0);
                 }
             }
@@ -704,8 +696,8 @@ struct MfmaStage {
     __device__ __forceinline__ void stage_x(Raw2<FMT> &first, bool issue_first) const
     {
         constexpr int NPX = 2 * P;
-        constexpr int CPOL = XDEV ? kDeviceScope : 0;
-        constexpr bool NORM = !XDEV && P <= 2;
+        constexpr int CPOL = 0;
+        constexpr bool NORM = P <= 2;
         float4 pre[NPX], w4[NORM ? NPX : 1];
         x_preload<NPX, CPOL>(args.x, units, pre);
         // the norm weights before the first slot's loads, and every load
@@ -790,134 +782,6 @@ __global__ __launch_bounds__(kThreads) void gemv_mfma_kernel(MfmaArgs args)
     st.stage_x(b0, true);
     __syncthreads();
     st.run(b0, b1);
-}
-
-// ---- several dependent GEMV stages in one launch ----------------------------------
-//
-// A decode layer is a chain of GEMVs whose inputs are earlier outputs.  As
-// separate launches each pays its dispatch, its activation staging and the
-// first HBM round trip of its weights.  gemv_chain_kernel runs the stages in
-// one launch on one workgroup per CU: before the grid-wide barrier that ends
-// a stage, every wave issues the first weight item of the next stage (weights
-// do not depend on the activations), so that item's HBM latency overlaps the
-// barrier and the activation staging.
-//
-// The barrier is a two-level set of counters in device memory that only
-// grow, by a fixed amount per barrier (grid_arrive_wait); every launch leaves
-// them at such a multiple, so the state is valid across launches and graph
-// replays (the grid is the same for every launch).  All
-// workgroups must be resident together: the grid is at most one workgroup per
-// CU and each uses more LDS than half a CU's.  The wait is bounded
-// (kBarrierPolls polls): a workgroup that gives up sets the timeout flag and continues,
-// so no launch can hang; holo_gemv_chain_status() reports and clears it.
-
-constexpr int kMaxStages = 8;
-constexpr uint32_t kBarrierPolls = 1u << 18;  // each poll re-reads and sleeps: ~0.1-0.3 s in all
-
-struct ChainArgs {
-    MfmaArgs st[kMaxStages];
-    int key[kMaxStages];  // 8 * mode + P
-    int nstages;
-    uint32_t *bar;        // barrier words (grid_arrive_wait)
-};
-
-// Barrier words, each on its own 256-byte line: group counters (kBarGroups),
-// the top counter, the timeout flag.
-constexpr int kBarGroups = 8;
-constexpr int kBarStride = 64;  // uint32 words
-constexpr int kBarTop = kBarGroups * kBarStride;
-constexpr int kBarFlag = kBarTop + kBarStride;
-constexpr size_t kBarBytes = (size_t)(kBarFlag + kBarStride) * 4;
-
-// Arrival and wait of one workgroup, by a thread of a wave with no loads
-// outstanding (vmcnt counts loads and stores alike: waiting for the arrival
-// atomic's result also waits for every load the wave issued before it).
-// The caller has made the workgroup's stores complete before.
-__device__ __forceinline__ void grid_arrive_wait(uint32_t *bar)
-{
-    // Two levels, so that no counter takes more than a few dozen atomics:
-    // workgroup b arrives on group counter b % kBarGroups, the last arrival
-    // of a group on the top counter.  Counters only grow, by the group size
-    // (top: by the group count) per barrier, so the barrier number k follows
-    // from the arrival value and the barrier ends when the top counter
-    // reaches k * groups (signed difference: the 32-bit wrap is harmless).
-    const uint32_t G = gridDim.x;
-    const uint32_t ng = G < kBarGroups ? G : kBarGroups;
-    const uint32_t gi = blockIdx.x % ng;
-    const uint32_t size = G / ng + (gi < G % ng ? 1u : 0u);
-    const uint32_t a = __hip_atomic_fetch_add(bar + gi * kBarStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t k = a / size + 1;
-    const uint32_t target = k * ng;
-    if (a + 1 == k * size) {
-        const uint32_t t = __hip_atomic_fetch_add(bar + kBarTop, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (t + 1 == target) return;
-    }
-    for (uint32_t polls = 0;; polls++) {
-        const uint32_t c = __hip_atomic_load(bar + kBarTop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((int32_t)(c - target) >= 0) return;
-        if (polls == kBarrierPolls) {
-            __hip_atomic_store(bar + kBarFlag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-}
-
-// Calls f with the MfmaStage of (mode, P) = key for stage arguments a.
-template <int FMT, class Fn>
-__device__ __forceinline__ void with_stage(int key, const MfmaArgs &a, uint8_t *ldsb, Fn &&f)
-{
-    switch (key) {
-    case 1: { MfmaStage<FMT, 1, MODE_PLAIN, true> st(a, ldsb); f(st); break; }
-    case 2: { MfmaStage<FMT, 2, MODE_PLAIN, true> st(a, ldsb); f(st); break; }
-    case 3: { MfmaStage<FMT, 3, MODE_PLAIN, true> st(a, ldsb); f(st); break; }
-    case 4: { MfmaStage<FMT, 4, MODE_PLAIN, true> st(a, ldsb); f(st); break; }
-    case 9: { MfmaStage<FMT, 1, MODE_GATEUP, true> st(a, ldsb); f(st); break; }
-    case 10: { MfmaStage<FMT, 2, MODE_GATEUP, true> st(a, ldsb); f(st); break; }
-    case 11: { MfmaStage<FMT, 3, MODE_GATEUP, true> st(a, ldsb); f(st); break; }
-    default: { MfmaStage<FMT, 4, MODE_GATEUP, true> st(a, ldsb); f(st); break; }
-    }
-}
-
-template <int FMT>
-__global__ __launch_bounds__(kThreads) void gemv_chain_kernel(ChainArgs ca)
-{
-    extern __shared__ uint4 lds[];
-    uint8_t *ldsb = (uint8_t *)lds;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    Raw2<FMT> b0, b1;
-    for (int s = 0; s < ca.nstages; s++) {
-        // waves 1-7 issued slot 0 of stage s > 0 before the barrier; wave 0
-        // (which waited at the barrier) issues its slot 0 now
-        with_stage<FMT>(ca.key[s], ca.st[s], ldsb, [&](auto &st) {
-            st.stage_x(b0, s == 0 || wave == 0);
-            __syncthreads();
-            st.run(b0, b1);
-        });
-        if (s + 1 < ca.nstages) {
-            // Every wave may have stored outputs of this stage (the last wave
-            // to finish a tile stores it), each one an agent-scope atomic
-            // store (sc1, written through the L2).  Each wave waits for its
-            // own stores to complete (s_waitcnt vmcnt(0)) and only then
-            // reaches the workgroup barrier, so every output store of the
-            // workgroup has completed at agent scope before thread 0 arrives.
-            // The kernel makes no other store that another workgroup reads,
-            // so the L2 write-back of a full agent-scope release fence is not
-            // needed (issued by 8 waves on every CU it cost about 14 us a
-            // stage).  The next stage reads its input with device-coherent
-            // (sc1) loads, which are not answered from a line an L2 cached
-            // before the store.
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // compiler ordering
-            __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0)
-            __syncthreads();
-            if (wave != 0) {
-                with_stage<FMT>(ca.key[s + 1], ca.st[s + 1], ldsb, [&](auto &st) { st.issue(b0, 0); });
-            } else if (threadIdx.x == 0) {
-                grid_arrive_wait(ca.bar);
-            }
-            __syncthreads();
-        }
-    }
 }
 
 // ---- host side ---------------------------------------------------------------------
@@ -1155,97 +1019,6 @@ static void gemv_mfma(int fmt, int mode, int nseg, const void *const *W, float *
     }
 }
 
-// ---- multi-stage launch (host) ----
-
-static uint32_t *g_chain_bar = nullptr;  // barrier words (grid_arrive_wait)
-
-bool gemv_chain_init()
-{
-    if (g_chain_bar) return true;
-    if (hipMalloc((void **)&g_chain_bar, kBarBytes) != hipSuccess) {
-        g_chain_bar = nullptr;
-        return false;
-    }
-    return hipMemset(g_chain_bar, 0, kBarBytes) == hipSuccess && hipDeviceSynchronize() == hipSuccess;
-}
-
-void gemv_chain_release()
-{
-    if (g_chain_bar) hipFree(g_chain_bar);
-    g_chain_bar = nullptr;
-}
-
-// Fills the MFMA arguments of one stage for a grid of `grid` workgroups; false
-// if the stage is outside the MFMA path.
-template <int FMT>
-static bool chain_stage_args(const holo_gemv_stage_t &in, int grid, MfmaArgs &a, int &key, size_t &lds)
-{
-    const bool gu = in.gate_up != 0;
-    const int nmat = gu ? 2 : in.nmat;
-    if (nmat < 1 || nmat > kMaxSeg || !in.x || ((uintptr_t)in.x & 3u)) return false;
-    a = MfmaArgs{};
-    a.units = units_per_row(FMT, in.in_dim);
-    a.row_bytes = row_bytes_of(FMT, in.in_dim);
-    if (a.units < 8 || (a.units & 7) || (a.units + 15) / 16 > 4 * kWaves) return false;
-    a.x = in.x;
-    a.nsegs = (a.units + 15) / 16;
-    a.x_lds_bytes = (a.units * lds_bytes_per_unit<XM_I24>() + 15) & ~15;
-    int total = 0;
-    for (int s = 0; s < kMaxSeg; s++) {
-        if (s < nmat) {
-            if (!in.W[s] || ((uintptr_t)in.W[s] & 15u) || in.rows[gu ? 0 : s] <= 0) return false;
-            if (!in.y[gu ? 0 : s]) return false;
-            a.W[s] = (const uint8_t *)in.W[s];
-            a.y[s] = in.y[gu ? 0 : s];
-            total += in.rows[gu ? 0 : s];
-            a.row_end[s] = total;
-        } else {
-            a.W[s] = a.W[0];
-            a.y[s] = a.y[0];
-            a.row_end[s] = INT_MAX;
-        }
-    }
-    const int tr = gu ? 8 : 16;
-    a.total_rows = gu ? in.rows[0] : total;
-    a.max_tiles = mfma_max_tiles(a.total_rows, tr, grid);
-    a.full_tiles = a.total_rows / (grid * tr);
-    a.rem_start = a.full_tiles * grid * tr;
-    const int P = (a.nsegs + kWaves - 1) / kWaves;
-    key = 8 * (gu ? MODE_GATEUP : MODE_PLAIN) + P;
-    lds = mfma_lds_bytes<FMT>(a.units, a.max_tiles);
-    return true;
-}
-
-template <int FMT>
-static int chain_launch(const holo_gemv_stage_t *stages, int nstages)
-{
-    ChainArgs ca = {};
-    const int grid = num_cus();
-    size_t lds = 0;
-    for (int s = 0; s < nstages; s++) {
-        size_t l = 0;
-        if (!chain_stage_args<FMT>(stages[s], grid, ca.st[s], ca.key[s], l)) return HOLO_EINVAL;
-        lds = l > lds ? l : lds;
-    }
-    if (lds > kMaxMfmaLds) return HOLO_EINVAL;
-    ca.nstages = nstages;
-    ca.bar = g_chain_bar;
-    auto kern = gemv_chain_kernel<FMT>;
-    static bool attr = false;
-    if (!attr) {
-        HOLO_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kMaxMfmaLds));
-        attr = true;
-    }
-    // every workgroup must be resident at once (grid barrier)
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)kern, kThreads, lds) != hipSuccess ||
-        per_cu < 1)
-        return HOLO_EINVAL;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream(), ca);
-    HOLO_LAUNCH_CHECK();
-    return 0;
-}
 
 // One launch over up to three matrices sharing x and in_dim.  nw: stage
 // rms_norm(x) * nw instead of x (the MFMA path with in_dim <= 8192 only;
@@ -1402,28 +1175,6 @@ void holo_gemv_set_xmode(int xmode)
     tuning();
     g_tune.xmode = xmode == 1 ? XM_I24 : (xmode == 2 || xmode == 3) ? XM_MFMA : XM_F32;
     g_tune.mfma_q8 = xmode == 3;
-}
-
-int holo_gemv_chain(const holo_gemv_stage_t *stages, int nstages, int type)
-{
-    if (!stages || nstages < 1 || nstages > kMaxStages || !g_chain_bar) return HOLO_EINVAL;
-    if (tuning().xmode != XM_MFMA) return HOLO_EINVAL;
-    if (type == HOLO_TYPE_Q4_0) return chain_launch<FMT_Q4_0>(stages, nstages);
-    if (type == HOLO_TYPE_Q4_K) return chain_launch<FMT_Q4_K>(stages, nstages);
-    return HOLO_EINVAL;
-}
-
-int holo_gemv_chain_status(void)
-{
-    if (!g_chain_bar) return 0;
-    uint32_t flag = 0;
-    HOLO_CHECK(hipStreamSynchronize(stream()));
-    HOLO_CHECK(hipMemcpy(&flag, g_chain_bar + kBarFlag, sizeof(flag), hipMemcpyDeviceToHost));
-    if (flag == 0) return 0;
-    // a barrier gave up: the counters may be out of step, so start afresh
-    HOLO_CHECK(hipMemset(g_chain_bar, 0, kBarBytes));
-    HOLO_CHECK(hipDeviceSynchronize());
-    return HOLO_ECHAIN;
 }
 
 void holo_time_next_launch(void *start_event, void *stop_event)

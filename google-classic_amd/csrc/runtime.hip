@@ -77,7 +77,7 @@ const char *holo_error_string(int code)
 {
     if (code == 0) return "ok";
     if (code == HOLO_EINVAL) return "invalid argument";
-    if (code == HOLO_ECHAIN) return "multi-stage GEMV launch could not synchronise its workgroups";
+    if (code == HOLO_ECHAIN) return "persistent decode-step launch could not synchronise its workgroups";
     return hipGetErrorString((hipError_t)code);
 }
 
@@ -97,10 +97,6 @@ int cuda_init(void)
     g_cus = g_props.multiProcessorCount > 0 ? g_props.multiProcessorCount : 256;
     if (hipStreamCreateWithFlags(&g_copy_stream, hipStreamNonBlocking) != hipSuccess) {
         fprintf(stderr, "holo_mi355x: cannot create copy stream\n");
-        return -1;
-    }
-    if (!holo::gemv_chain_init()) {
-        fprintf(stderr, "holo_mi355x: cannot allocate the GEMV chain barrier\n");
         return -1;
     }
     if (!holo::gemv_stream_init()) {
@@ -130,7 +126,6 @@ void cuda_cleanup(void)
     hipDeviceSynchronize();
     if (g_copy_stream) hipStreamDestroy(g_copy_stream);
     g_copy_stream = nullptr;
-    holo::gemv_chain_release();
     holo::gemv_stream_release();
     holo::attention_scratch_release();
     holo::panel_workspace_release();

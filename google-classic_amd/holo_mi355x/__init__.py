@@ -127,8 +127,6 @@ _SIGS = {
     "holo_matmul": (None, [_P, _P, _P, _I, _I, _I]),
     "holo_gemv_set_xmode": (None, [_I]),
     "holo_time_next_launch": (None, [_P, _P]),
-    "holo_gemv_chain": (_I, [_P, _I, _I]),
-    "holo_gemv_chain_status": (_I, []),
     "holo_gemv_stream_create": (_P, [_P, _I, _I]),
     "holo_gemv_stream_launch": (_I, [_P]),
     "holo_gemv_stream_destroy": (None, [_P]),
@@ -196,35 +194,6 @@ _lib: C.CDLL | None = None
 EINVAL, ECHAIN = 100001, 100002
 
 
-class GemvStage(C.Structure):
-    """holo_gemv_stage_t (include/holo_mi355x.h): one stage of holo_gemv_chain."""
-    _fields_ = [("W", C.c_void_p * 3), ("y", C.c_void_p * 3), ("rows", C.c_int * 3), ("nmat", C.c_int),
-                ("gate_up", C.c_int), ("x", C.c_void_p), ("in_dim", C.c_int)]
-
-
-def gemv_stage(W, y, rows, x, in_dim, gate_up=False) -> GemvStage:
-    """A chain stage from device pointers: W, y, rows are sequences (gate/up:
-    W = (gate, up), y = (out,), rows = (ffn_dim,))."""
-    s = GemvStage()
-    for i, w in enumerate(W):
-        s.W[i] = w
-    for i, o in enumerate(y):
-        s.y[i] = o
-    for i, r in enumerate(rows):
-        s.rows[i] = r
-    s.nmat = len(W)
-    s.gate_up = 1 if gate_up else 0
-    s.x = x
-    s.in_dim = in_dim
-    return s
-
-
-def gemv_chain(stages, qtype: int) -> int:
-    """holo_gemv_chain over a list of GemvStage; returns its status code."""
-    arr = (GemvStage * len(stages))(*stages)
-    return lib().holo_gemv_chain(C.cast(arr, C.c_void_p), len(stages), qtype)
-
-
 class StreamStage(C.Structure):
     """holo_stream_stage_t (include/holo_mi355x.h): one stage of a
     holo_gemv_stream plan."""
@@ -234,8 +203,9 @@ class StreamStage(C.Structure):
 
 
 def stream_stage(W, y, rows, x, in_dim, gate_up=False, norm_w=None, eps=1e-5, r=None) -> StreamStage:
-    """A stream stage from device pointers (as gemv_stage, plus the optional
-    rms-norm weight of the input and the residual of the output)."""
+    """A stream stage from device pointers: matrices W, outputs y (one for a
+    gate/up pair), their row counts, input x of in_dim values, and the
+    optional rms-norm weight of the input and residual of the output."""
     s = StreamStage()
     for i, w in enumerate(W):
         s.W[i] = w

@@ -27,7 +27,7 @@ extern "C" {
  * 0 = ok, otherwise a hipError_t value, or HOLO_EINVAL for a rejected
  * argument.  holo_last_error() returns and clears the latch.               */
 #define HOLO_EINVAL 100001
-#define HOLO_ECHAIN 100002  /* a multi-stage GEMV launch could not synchronise */
+#define HOLO_ECHAIN 100002  /* a persistent decode-step launch could not synchronise */
 int holo_last_error(void);
 const char *holo_error_string(int code);
 
@@ -78,35 +78,6 @@ void holo_gemv_set_xmode(int xmode);
  * F32/I24 use 1 when the grid has at most 2 tiles per CU, else 2; MFMA
  * uses 1 or 2 by how evenly the rows fill its tiles).  A tuning knob.      */
 void holo_gemv_set_launch(int rows_per_item, int wg_per_cu);
-/* ---- several dependent GEMV stages in one launch ------------------------------
- * Runs stages[0..nstages-1] in order in one kernel launch: each stage is the
- * GEMV of cuda_matmul_<type> over up to three matrices sharing x (gate_up = 0:
- * y[m] = W[m] x, rows[m] rows each), or the fused gate/up of
- * holo_batched_ffn_gate_up (gate_up = 1: y[0] = silu(W[0] x) * (W[1] x),
- * rows[0] rows).  A stage may read an earlier stage's output as its x: a
- * grid-wide barrier separates the stages, and the next stage's first weight
- * loads are issued before it, so a layer's four launches become one.  Same
- * results as the separate calls.  Serves Q4_0 and Q4_K (HOLO_TYPE_*) with
- * in_dim a multiple of 256 up to 16384, 16-byte aligned matrices, up to 8
- * stages, in the default activation mode; returns 0, or HOLO_EINVAL without
- * launching anything for anything else (the caller then makes the separate
- * calls).  The barrier wait is bounded: a launch that could not synchronise
- * (its workgroups not all resident) ends with wrong outputs instead of
- * hanging, and holo_gemv_chain_status() then returns HOLO_ECHAIN.         */
-typedef struct {
-    const void *W[3];
-    float *y[3];
-    int rows[3];
-    int nmat;       /* matrices of a plain stage: 1..3 */
-    int gate_up;    /* 1: W[0] = gate, W[1] = up, output y[0] */
-    const float *x;
-    int in_dim;
-} holo_gemv_stage_t;
-int holo_gemv_chain(const holo_gemv_stage_t *stages, int nstages, int type);
-/* Synchronises the library stream; 0, or HOLO_ECHAIN (and the barrier state
- * reset) if a chain launch since the last call gave up waiting.            */
-int holo_gemv_chain_status(void);
-
 /* ---- a decode step's GEMV stages in one persistent launch ---------------------
  * A plan of dependent GEMV stages (every layer's q/k/v, o, gate/up and down of a
  * decode step), run by holo_gemv_stream_launch as ONE kernel launch.  Each
