@@ -208,11 +208,14 @@ void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, 
  * on one device (issued on two streams) race.                              */
 int holo_gemm_q4_0_q8_0_noalloc(float *Y, const void *W, const void *Xq, int M, int N, int K);
 /* Y[M][N] = X[M][K] . W[N][K]^T for W in Q4_0.  M >= 64 runs, by the mode
- * set below: the exact product (HOLO_PREFILL_EXACT, the default: X split into
- * two f16 halves, x - xh - xl within 2^-22 |x|, times the block's integers,
- * exact in f16, on the f16 matrix cores, block scales applied in fp32; fp32
- * accuracy, within 1e-3 of the CPU path; X 16-byte aligned, |x| < 65504,
- * else M GEMVs), the f16 product below (HOLO_PREFILL_F16) or the Q8_0
+ * set below: the exact product (HOLO_PREFILL_EXACT, the default: each row of
+ * X scaled by a power of two and split into two f16 halves, x - xh - xl
+ * within 2^-22 |x|, times the block's integers, exact in f16, on the f16
+ * matrix cores, block scales applied in fp32 in block order; fp32 accuracy,
+ * within 1e-3 of the CPU path; X 16-byte aligned and K <= 16384, else M
+ * GEMVs; with few column tiles the K range is split in 2 or 4 parts summed
+ * in part order, so the result depends on the launch's tile count but not
+ * on timing), the f16 product below (HOLO_PREFILL_F16) or the Q8_0
  * product above (HOLO_PREFILL_Q8_0: X quantised to Q8_0).  M < 64 runs M
  * GEMVs.                                                                     */
 void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int N, int K,
@@ -259,13 +262,19 @@ void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const i
 /* The batched products for any weight type the GEMVs serve (Q4_0, Q8_0, Q4_K,
  * Q6_K, F16, F32), with the contracts of the Q4_0 calls above.  Q4_0 goes to
  * them.  Every other type, for M >= 64 and K whole blocks (Q4_K, Q6_K: K a
- * multiple of 256), is dequantised into an f16 panel (holo_dequant_f16, N*K*2
- * bytes per matrix) and multiplied on the f16 product: Y = sum_k f16_rne(x) *
- * f16_rne(w), fp32 accumulation.  The panels live in a device buffer the
- * library keeps and grows (hipMalloc, outside graph capture; under capture a
- * stream-ordered allocation per call); calls on one stream reuse it in order.
- * Otherwise one holo_matmul GEMV per row.  No reference counterpart (the reference runs
- * one GEMV per token, llm.c:1049).                                          */
+ * multiple of 256) up to 16384, runs the exact product by default (the block
+ * integers against the two f16 halves of X, block scales in fp32); in
+ * HOLO_PREFILL_F16 mode it is dequantised into an f16 panel
+ * (holo_dequant_f16, N*K*2 bytes per matrix) and multiplied on the f16
+ * product.  Workspaces live in device buffers the library keeps and grows
+ * (hipMalloc, outside graph capture; under capture a stream-ordered
+ * allocation per call); calls on one stream reuse them in order.  Otherwise
+ * one holo_matmul GEMV per row.  The multi forms take up to 3 matrices
+ * sharing X (with several, every N a multiple of 128); an output equals the
+ * single call's bit for bit when both launches split K alike (always when
+ * neither has fewer column tiles than CUs), else within the product's error
+ * bound.  No reference counterpart (the reference runs one GEMV per token,
+ * llm.c:1049).                                                              */
 void holo_matmul_batch(float *Y, const void *W, const float *X, int M, int N, int K, int type);
 void holo_matmul_batch_multi(float *const *Y, const void *const *W, const int *N, int nmat, const float *X,
                              int M, int K, int type);
