@@ -528,10 +528,13 @@ def decode_attention(lib, kv_lens=(512, 2048, 4096), reps=50):
 
 
 def prefill_tops(lib, reps=10):
-    """Config 4 at M = 512, both batched products:
-      q8_0: holo_gemm_q4_0_q8_0 (Q8_0 activations, bit-exact specification),
-      f16:  holo_gemm_q4_0_f16 (f16 activations and dequantised weights; the
-            default of holo_matmul_batch_q4_0 and the prompt forward).
+    """Config 4 at M = 512, the batched products:
+      q8_0: holo_gemm_q4_0_q8_0 (Q8_0 activations, bit-exact specification)
+            on the f16 matrix cores (the default), q8_0_int8_mfma the same on
+            the int8 matrix cores (identical bits);
+      f16:  holo_gemm_q4_0_f16 (f16 activations and dequantised weights);
+      exact: holo_matmul_batch_q4_0 (the default of the batched matmuls and
+            the prompt forward: fp32-accurate).
     gemm_us is the call (the activation panel pass, the GEMM kernel and the
     stream-ordered workspace), kernel_us the GEMM kernel alone
     (holo_time_next_launch).  Both run on v_mfma_f32_32x32x16_f16; useful work
@@ -545,7 +548,12 @@ def prefill_tops(lib, reps=10):
         Y = holo.DeviceBuffer(4 * M * N)
         lib.holo_quantize_act_q8_0(Xq.ptr, X.ptr, M, K)
         ev = holo.Events()
-        calls = {"q8_0": lambda: lib.holo_gemm_q4_0_q8_0(Y.ptr, W.ptr, Xq.ptr, M, N, K),
+        def q8(kind):
+            lib.holo_prefill_set_q8_kernel(kind)
+            lib.holo_gemm_q4_0_q8_0(Y.ptr, W.ptr, Xq.ptr, M, N, K)
+            lib.holo_prefill_set_q8_kernel(0)
+
+        calls = {"q8_0": lambda: q8(0), "q8_0_int8_mfma": lambda: q8(1),
                  "f16": lambda: lib.holo_gemm_q4_0_f16(Y.ptr, W.ptr, X.ptr, M, N, K),
                  "exact": lambda: lib.holo_matmul_batch_q4_0(Y.ptr, W.ptr, X.ptr, M, N, K, None)}
         out[name] = {}

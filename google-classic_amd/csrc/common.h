@@ -50,6 +50,13 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
 // the prefill mode and the shapes take it; false (nothing launched) otherwise.
 bool exact_product_normed(float *const *Y, const void *const *W, const int *types, const int *N, int nmat,
                           const float *X, const float *NW, float eps, int M, int K);
+// The Q8_0 product on the int8 matrix cores (prefill_i8.hip): whether it takes
+// the shapes, its activation panel's bytes (<= the f16 kernel's), and the
+// product into a caller-given panel workspace.
+bool q8i8_fits(const void *const *W, const int *N, int nmat, int M, int K);
+size_t q8i8_panel_bytes(int M, int K);
+void q8i8_product(float *const *Y, const void *const *W, const int *N, int nmat, const void *Xq, int M, int K,
+                  void *ws);
 // Device address of the fixed scratch array of holo_gemm_q4_0_q8_0_noalloc on
 // the current device (prefill.hip), looked up once per device; nullptr on failure.
 void *noalloc_scratch();

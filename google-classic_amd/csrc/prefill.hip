@@ -584,6 +584,12 @@ static size_t act_panel_bytes(int M, int K, bool xf16)
     return (size_t)nblk * 64 + (xf16 ? 0 : (((size_t)nblk * 2 + 255) & ~(size_t)255));
 }
 
+// Which matrix cores the Q8_0 product runs on (holo_prefill_set_q8_kernel):
+// f16 by default, measured faster (config 4: 125 / 131 us against 185 / 285 us
+// on int8, whose extra convert per output and block adds to the epilogue that
+// bounds this specification).
+static int g_q8_kernel = HOLO_Q8_KERNEL_F16;
+
 // ws_given: a caller-provided workspace of at least act_panel_bytes bytes
 // (nothing is allocated); otherwise the library's kept workspace.
 static void gemm_multi(float *const *Y, const void *const *W, const int *N, int nmat, const void *Xq, const float *X,
@@ -600,6 +606,12 @@ static void gemm_multi(float *const *Y, const void *const *W, const int *N, int 
     const bool own = ws == nullptr;
     if (own) HOLO_CHECK(hipMallocAsync(&ws, pbytes + dbytes, stream()));
     if (!ws) return;
+    // the Q8_0 product on the int8 matrix cores (its panel fits the f16 one's space)
+    if (!xf16 && !R && g_q8_kernel == HOLO_Q8_KERNEL_I8 && q8i8_fits(W, N, nmat, M, K)) {
+        q8i8_product(Y, W, N, nmat, Xq, M, K, ws);
+        if (own) HOLO_CHECK(hipFreeAsync(ws, stream()));
+        return;
+    }
     uint4 *P = (uint4 *)ws;
     uint16_t *D = xf16 ? nullptr : (uint16_t *)((uint8_t *)ws + pbytes);
     if (xf16) {
@@ -842,6 +854,21 @@ static bool exact_fits(const void *const *W, const int *types, int nmat, const f
 }
 
 static bool exact_mode() { return g_prefill_mode == HOLO_PREFILL_EXACT; }
+
+extern "C" {
+
+void holo_prefill_set_q8_kernel(int kind)
+{
+    if (kind != HOLO_Q8_KERNEL_F16 && kind != HOLO_Q8_KERNEL_I8) {
+        HOLO_REJECT("holo_prefill_set_q8_kernel: HOLO_Q8_KERNEL_F16 or HOLO_Q8_KERNEL_I8");
+        return;
+    }
+    g_q8_kernel = kind;
+}
+
+int holo_prefill_get_q8_kernel(void) { return g_q8_kernel; }
+
+}  // extern "C"
 
 namespace holo {
 

@@ -145,6 +145,8 @@ _SIGS = {
     "holo_gemm_q4_0_f16": (None, [_P, _P, _P, _I, _I, _I]),
     "holo_gemm_q4_0_f16_multi": (None, [_P, _P, _P, _I, _P, _I, _I]),
     "holo_prefill_set_mode": (None, [_I]),
+    "holo_prefill_set_q8_kernel": (None, [_I]),
+    "holo_prefill_get_q8_kernel": (_I, []),
     "holo_prefill_get_mode": (_I, []),
     "holo_batched_qkv_norm": (None, [_P, _P, _P, _P, _P, _P, _P, _P, C.c_float, _P, _I, _I, _I, _I]),
     "holo_batched_ffn_gate_up_norm": (None, [_P, _P, _P, _P, _P, C.c_float, _P, _I, _I, _I]),

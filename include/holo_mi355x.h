@@ -207,6 +207,19 @@ void holo_gemm_q4_0_q8_0(float *Y, const void *W, const void *Xq, int M, int N, 
  * call's contents and every call on a device shares it: calls that overlap
  * on one device (issued on two streams) race.                              */
 int holo_gemm_q4_0_q8_0_noalloc(float *Y, const void *W, const void *Xq, int M, int N, int K);
+/* The matrix cores the Q8_0 product above (and its multi, no-allocation and
+ * Q8_0-mode batched forms) runs on, with the same specification and bits:
+ * HOLO_Q8_KERNEL_F16 (the default: the integers as f16 on
+ * v_mfma_f32_32x32x16_f16) or HOLO_Q8_KERNEL_I8 (v_mfma_i32_32x32x32_i8 for
+ * each block's integer dot, the -8 of the weights in the accumulator input,
+ * then acc = fmaf((float)I, s, acc); slower, kept for comparison).  The int8
+ * kernel takes K/32 even, 4-byte aligned matrices and, with several
+ * matrices, every N but the last a multiple of 64; other calls run the f16
+ * kernel.  No reference counterpart.                                       */
+#define HOLO_Q8_KERNEL_F16 0
+#define HOLO_Q8_KERNEL_I8 1
+void holo_prefill_set_q8_kernel(int kind);
+int holo_prefill_get_q8_kernel(void);
 /* Y[M][N] = X[M][K] . W[N][K]^T for W in Q4_0.  M >= 64 runs, by the mode
  * set below: the exact product (HOLO_PREFILL_EXACT, the default: each row of
  * X scaled by a power of two and split into two f16 halves, x - xh - xl

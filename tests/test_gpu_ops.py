@@ -521,3 +521,33 @@ def test_embeddings_and_dense_gemv(holo, synth, oracle, t):
         want = rows.astype(np.float64) @ x
         assert normwise_err(down(dy, vocab), want) < 1e-5
     holo.check("embedding")
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 256, 512), (77, 150, 4096), (200, 640, 1056), (512, 11008, 4096),
+                                   (512, 4096, 11008)], ids=str)
+def test_gemm_q4_0_q8_0_int8_and_f16_kernels_agree(holo, synth, oracle, M, N, K):
+    """The Q8_0 product on the f16 matrix cores (the default) and on the int8
+    ones compute the same specification: bit-identical outputs, and equal to
+    the oracle on the first and last row of every 32-row band (1056 = 33
+    blocks: an odd block count, which the int8 kernel hands to the f16 one)."""
+    print(f"case q8 kernels {M}x{N}x{K}", flush=True)
+    lib = holo.lib()
+    assert lib.holo_prefill_get_q8_kernel() == 0
+    W = synth.blocks(Q4_0, N, K, seed=3 * M + N)
+    Xq = oracle.quantize_act_q8_0(synth.normal(M * K, seed=K + 1).reshape(M, K))
+    dW, dXq = up(holo, W), up(holo, Xq)
+    outs = []
+    try:
+        for kind in (1, 0):
+            lib.holo_prefill_set_q8_kernel(kind)
+            dY = holo.DeviceBuffer(4 * M * N)
+            lib.holo_gemm_q4_0_q8_0(dY.ptr, dW.ptr, dXq.ptr, M, N, K)
+            lib.cuda_sync()
+            holo.check("q8 kernel")
+            outs.append(down(dY, M * N).reshape(M, N))
+    finally:
+        lib.holo_prefill_set_q8_kernel(0)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    rows = tile_rows(M)
+    want = oracle.gemm_q4_0_q8_0(W, Xq.reshape(M, -1)[rows].copy().reshape(-1), len(rows), N, K)
+    assert np.array_equal(outs[0][rows].view(np.uint32), want.view(np.uint32))
