@@ -34,6 +34,7 @@
 #include "block_reduce.h"
 
 #include <hip/hip_ext.h>
+#include <algorithm>
 #include <limits.h>
 
 #include <type_traits>
@@ -707,15 +708,27 @@ __global__ __launch_bounds__(256) void q6_k_int_panel_k(_Float16 *__restrict__ y
 // four MFMAs give C = sum_k (xh + xl) * w, folded in block order by
 // acc = fmaf(scale, C, acc) (Q4_K: then acc = fmaf(-dmin*m, sum x, acc)).
 //
-// With fewer tiles than CUs the K range is split into P parts (P = 2 or 4)
-// of whole stages; each part stores its unscaled accumulators, device-scope,
-// and counts itself on the tile's counter; the last part to arrive adds the
-// parts in part order, scales and stores.  The result then depends on P (a
-// different fp32 summation), which depends on the launch's tile count.
+// Work is dealt by stages, not by tiles (a "stream-K" split), one row of
+// tiles at a time: in row tile r, column tile c's stage s is item c * nst + s
+// of the row's U = nct * nst, and of the row's Gr workgroups the i-th takes
+// items [i U / Gr, (i + 1) U / Gr), so every workgroup runs the same number of
+// stages to within one, whatever the tile count.  Workgroup w = i * ntm + r:
+// the ntm workgroups with the same i walk the same column tiles and blocks in
+// step on one XCD, so each weight word is fetched once for all of them, as in
+// a tile-per-workgroup launch.  A range that covers a whole tile stores it
+// directly.  Otherwise the range's share of the tile is a part: the workgroup
+// stores its unscaled accumulators, device-scope, into its own slot (2 w for
+// the first tile of its range, 2 w + 1 for the last), and counts itself on the
+// tile's counter; the last of the tile's workgroups to arrive adds the parts
+// in range order, scales and stores.  The result then depends on where the
+// ranges cut the tiles (a different fp32 summation), which depends on Gr and
+// the launch's shape.
 
-constexpr int kX2Parts = 4;          // the most K parts of a tile
+constexpr int kX2MinStages = 8;      // the fewest stages of a part
+constexpr int kX2MaxSplit = 4;       // workgroups per tile at most (on average)
 constexpr int kX2DevScope = 16;      // sc1: device-scope store / device-coherent load
 constexpr int kX2Counters = 16384;   // tile counters of the split form
+constexpr uint32_t kX2OutOfRange = 0x80000000u;  // a buffer offset past any range: reads zeros
 
 struct X2Args {
     float *Y[kExactMats];
@@ -724,10 +737,15 @@ struct X2Args {
     const _Float16 *Ah, *Al;         // activation halves [M][K]
     const float *Rs;                 // [M] row scales
     const float *R;                  // one matrix only: Y = R + product (may alias Y)
-    float *part;                     // [P][tiles][64 x 256] partial accumulators (P > 1)
-    uint32_t *cnt;                   // [tiles] arrival counters, zero between launches (P > 1)
-    int M, N, nb, ntm, tiles, P, spp; // spp: stages per part
+    float *part;                     // [2 G][64 x 256] part slots (split launches)
+    uint32_t *cnt;                   // [tiles] arrival counters, zero between launches (split launches)
+    int M, N, nb, ntm, tiles, nst;   // nst: stages per tile
+    int gr;                          // workgroups per row of tiles
 };
+
+// First item of the i-th range of a row, and the range that holds item x.
+__device__ __forceinline__ int64_t x2_start(int i, int64_t U, int G) { return (int64_t)i * U / G; }
+__device__ __forceinline__ int x2_owner(int64_t x, int64_t U, int G) { return (int)(((x + 1) * G - 1) / U); }
 
 template <int S>
 struct X2Geo {
@@ -750,12 +768,13 @@ template <int WF>
 struct X2Raw;
 template <>
 struct X2Raw<EW_Q4_0> {
-    uint32_t w[3];     // from the block's start rounded down, plus 8 h: qs[8h .. 8h + 7] at byte 2 + 2(b & 1);
-                       // for h = 0 the window also holds d (bytes 0-1 or 2-3)
+    v4u w;             // from the block's start rounded down, plus 8 h: qs[8h .. 8h + 7] at byte 2 + 2(b & 1);
+                       // for h = 0 the window also holds d (bytes 0-1 or 2-3); the 16-byte load keeps each
+                       // window in one aligned register quad
 };
 template <>
 struct X2Raw<EW_Q8_0> {
-    uint32_t w[3], v[3];  // the two 8-byte runs qs[8h ..] and qs[16 + 8h ..], same windows (h = 0: d too)
+    v4u w, v;          // the two 8-byte runs qs[8h ..] and qs[16 + 8h ..], same windows (h = 0: d too)
 };
 
 // The block scale d of lane (c, 0) in both lanes (c, 0) and (c, 1): the h = 1
@@ -780,20 +799,11 @@ __device__ __forceinline__ X2Raw<WF> x2_fetch(__amdgpu_buffer_rsrc_t r, uint32_t
     X2Raw<WF> x;
     if constexpr (WF == EW_Q4_0) {
         const int so = 18 * b - 2 * P;
-        const v3u t = __builtin_amdgcn_raw_buffer_load_b96(r, (int)vo, so, 0);
-        x.w[0] = t.x;
-        x.w[1] = t.y;
-        x.w[2] = t.z;
+        x.w = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, so, 0));
     } else if constexpr (WF == EW_Q8_0) {
         const int so = 34 * b - 2 * P;
-        const v3u t = __builtin_amdgcn_raw_buffer_load_b96(r, (int)vo, so, 0);
-        x.w[0] = t.x;
-        x.w[1] = t.y;
-        x.w[2] = t.z;
-        const v3u u = __builtin_amdgcn_raw_buffer_load_b96(r, (int)vo, so + 16, 0);
-        x.v[0] = u.x;
-        x.v[1] = u.y;
-        x.v[2] = u.z;
+        x.w = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, so, 0));
+        x.v = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, so + 16, 0));
     } else {
         x.s0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, 64 * b, 0));
         x.s1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, 64 * b + 32, 0));
@@ -807,6 +817,11 @@ template <int WF, int P>
 __device__ __forceinline__ void x2_unpack(const X2Raw<WF> &x, bool live, v8h &b0, v8h &b1, float &sc)
 {
     uint32_t lo[4], hi[4];
+    // the loads' unused last dwords count as read here: otherwise their
+    // registers look free at once and the next write to one of them waits
+    // for the load in flight
+    if constexpr (WF == EW_Q4_0) asm volatile("" ::"v"(x.w[3]));
+    if constexpr (WF == EW_Q8_0) asm volatile("" ::"v"(x.w[3]), "v"(x.v[3]));
     if constexpr (WF == EW_Q4_0) {
         // qs[8h ..] at byte 2 of the window (even b) or 4 (odd b)
         const uint32_t q0 = P ? x.w[1] : __builtin_amdgcn_alignbyte(x.w[1], x.w[0], 2);
@@ -843,20 +858,36 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
     using G = X2Geo<S>;
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ uint32_t last;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the weight resource stays scalar
-    const int h = lane >> 5, c32 = lane & 31;
+    __shared__ __align__(16) float rs_l[64];  // the tile's row scales
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // uniform: the weight resource stays scalar
     const int nb = a.nb;
 
-    // workgroup g -> (tile t, part p): the workgroups of XCD x (round-robin
-    // dispatch) take a contiguous run, so the row tiles of a column tile
-    // (which share its weights) run on one XCD together
-    const int g = blockIdx.x, total = a.tiles * a.P;
-    const int L = (total & 7) ? g : (g & 7) * (total >> 3) + (g >> 3);
-    const int t = L % a.tiles, p = L / a.tiles;
+    // workgroup g -> w = i * ntm + r: the workgroups of XCD x (round-robin
+    // dispatch) take a contiguous run of w, so the row tiles that walk the
+    // same weights in step (same i) run on one XCD together
+    const int NG = (int)gridDim.x, g = blockIdx.x;
+    const int w = (NG & 7) ? g : (g & 7) * (NG >> 3) + (g >> 3);
+    const int nst = a.nst, ntm = a.ntm, Gr = a.gr;
+    const int ri = w / ntm, rt = w - ri * ntm;  // range i of row tile r
+    const int64_t U = (int64_t)(a.tiles / ntm) * nst;
+    const int64_t ibeg = x2_start(ri, U, Gr), iend = x2_start(ri + 1, U, Gr);
+    const int cfirst = (int)(ibeg / nst);  // the first column tile of the range
+
+    // one pass per tile the range touches (uniform)
+    for (int64_t i0 = ibeg; i0 < iend;) {
+    // the thread index as an opaque value of the pass: per-lane addresses are
+    // then computed in each pass, not kept live through every pass's loop
+    int tid_v = (int)threadIdx.x;
+    asm volatile("" : "+v"(tid_v));
+    const int tid = tid_v, lane = tid & 63, h = lane >> 5, c32 = lane & 31;
+    const int ct = (int)(i0 / nst);
+    const int s0 = (int)(i0 - (int64_t)ct * nst);
+    const int s1 = (int)min((int64_t)nst, (int64_t)s0 + (iend - i0));
+    i0 += s1 - s0;
+    const int t = ct * ntm + rt;
     const int m0 = (t % a.ntm) * 64, n0 = (t / a.ntm) * 256 + 64 * wave;
-    const int kb0 = p * a.spp * S;  // even
-    const int kb1 = min(nb, kb0 + a.spp * S);
+    const int kb0 = s0 * S;  // even
+    const int kb1 = min(nb, s1 * S);
 
     // this wave's 64 columns lie in one matrix (n_end multiples of 64); in
     // the last column tile a wave may start at or past N: it loads in-bounds
@@ -926,7 +957,7 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
     // F16 has no scale to zero a block past the part with: its block index
     // is clamped instead (no alignment depends on it)
     auto wblk = [&](int b) { return WF == EW_F16 ? min(b, kb1 - 1) : b; };
-    const int nst = (kb1 - kb0 + S - 1) / S;
+    const int nsg = (kb1 - kb0 + S - 1) / S;  // stages of this pass
     // the weight words of a stage's S blocks, fetched one stage ahead
     X2Raw<WF> ring[S][2];
 #pragma unroll
@@ -936,12 +967,19 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
             if (s & 1) ring[s][ni] = x2_fetch<WF, 1>(rw, vo[ni], vd[ni], wblk(kb0 + s));
             else ring[s][ni] = x2_fetch<WF, 0>(rw, vo[ni], vd[ni], wblk(kb0 + s));
         }
+    __syncthreads();  // the previous pass's readers of rs_l are done
+    if (tid < 64) rs_l[tid] = a.Rs[min(m0 + tid, a.M - 1)];
     fetch_a(0);
     stash_a(0);
     fetch_a(1);
     __syncthreads();
-    for (int st = 0; st < nst; st++) {
+    for (int st = 0; st < nsg; st++) {
         const uint8_t *base = lds + (st & 1) * G::STAGE;
+        // stage st + 1 into the other buffer (free: every wave passed the
+        // barrier after stage st - 1), then fetch stage st + 2: both a whole
+        // stage before their use
+        stash_a((st + 1) & 1);
+        fetch_a(st + 2);
 #pragma unroll
         for (int s = 0; s < S; s++) {
             const int b = kb0 + st * S + s;
@@ -985,21 +1023,22 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
                 }
             }
         }
-        // stage st + 1 into the other buffer (free: every wave passed the
-        // barrier after stage st - 1), then fetch stage st + 2
-        stash_a((st + 1) & 1);
-        fetch_a(st + 2);
         __syncthreads();
     }
 
     // lane (c, h) holds rows 4h + 8q + j (register 4q + j) of column c of each tile
-    if (a.P > 1) {
-        // parts: store, count, and the last to arrive adds them in part order
-        const __amdgpu_buffer_rsrc_t rp =
-            __builtin_amdgcn_make_buffer_rsrc((void *)a.part, (short)0, -1, kXBufWord3);
-        auto slot = [&](int pp, int mi, int ni, int q) {
-            return (uint32_t)((((((int64_t)pp * a.tiles + t) * 4 + wave) * 4 + 2 * mi + ni) * 4 + q) * 1024 + 16 * lane);
+    bool store = s0 == 0 && s1 == nst;
+    if (!store) {
+        // a part: store it in this range's slot, count, and the last of the
+        // tile's ranges to arrive adds the parts in range order.  The slots
+        // (2 G of 64 KB, far below 2^31 bytes) bound the resource, so an
+        // offset of kX2OutOfRange reads zeros.
+        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)a.part, (short)0, (int)((uint32_t)NG * 131072u), kXBufWord3);
+        auto word = [&](int sl, int mi, int ni, int q) {
+            return (uint32_t)sl * 65536u + (uint32_t)((((wave * 4 + 2 * mi + ni) * 4 + q) * 1024) + 16 * lane);
         };
+        const int mine = 2 * w + (ct == cfirst ? 0 : 1);
 #pragma unroll
         for (int mi = 0; mi < 2; mi++)
 #pragma unroll
@@ -1008,58 +1047,147 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
                 for (int q = 0; q < 4; q++) {
                     const float4 v = {acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2],
                                       acc[mi][ni][4 * q + 3]};
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), rp, (int)slot(p, mi, ni, q), 0,
-                                                           kX2DevScope);
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), rp, (int)word(mine, mi, ni, q),
+                                                           0, kX2DevScope);
                 }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores have completed (device scope)
         __syncthreads();
+        const int64_t it = (int64_t)ct * nst;
+        const int jf = x2_owner(it, U, Gr), jl = x2_owner(it + nst - 1, U, Gr);
+        const int nparts = jl - jf + 1;
         if (tid == 0) {
             const uint32_t old = __hip_atomic_fetch_add(a.cnt + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last = old == (uint32_t)(a.P - 1);
+            last = old == (uint32_t)(nparts - 1);
         }
         __syncthreads();
-        if (!last) return;
-        if (tid == 0) __hip_atomic_store(a.cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        store = last;
+        if (store) {
+            if (tid == 0) __hip_atomic_store(a.cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // up to four parts' words of one 32 x 32 tile in one batch of
+            // loads (parts past the last read as zeros and are not added):
+            // one round trip per batch, not one per part and word
 #pragma unroll
-        for (int mi = 0; mi < 2; mi++)
+            for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-            for (int ni = 0; ni < 2; ni++)
+                for (int ni = 0; ni < 2; ni++)
+#pragma unroll 1
+                    for (int jb = 0; jb < nparts; jb += 4) {
+                        v4u wv[4][4];
+#pragma unroll
+                        for (int jj = 0; jj < 4; jj++) {
+                            const int j = jf + jb + jj;
+                            const int sl = 2 * (j * ntm + rt) + ((int)(x2_start(j, U, Gr) / nst) == ct ? 0 : 1);
+#pragma unroll
+                            for (int q = 0; q < 4; q++)
+                                wv[jj][q] = __builtin_bit_cast(
+                                    v4u, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rp, j <= jl ? (int)word(sl, mi, ni, q) : (int)kX2OutOfRange, 0,
+                                             kX2DevScope));
+                        }
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+#pragma unroll
+                            for (int e = 0; e < 4; e++) {
+                                const float p0 = __uint_as_float(wv[0][q][e]);
+                                float v = jb == 0 ? p0 : acc[mi][ni][4 * q + e] + p0;
+#pragma unroll
+                                for (int jj = 1; jj < 4; jj++)
+                                    if (jb + jj < nparts) v = v + __uint_as_float(wv[jj][q][e]);
+                                acc[mi][ni][4 * q + e] = v;
+                            }
+                    }
+        }
+    }
+    if (store) {
+        // the residual of every output first, in one batch of loads (a load
+        // between stores would wait for the stores issued before it as
+        // well), then the stores.  Outputs of under 2^31 bytes go through
+        // buffer resources: the lane's offset for row m0 + 4h (out of range
+        // past the matrix's columns or for a wave without columns) plus a
+        // wave-uniform row offset, no per-element address registers; rows
+        // past M fall outside the resource.
+        float rv[2][2][16];
+        if ((int64_t)a.M * Nm < (1LL << 29)) {
+            const int bytes = a.M * Nm * 4;
+            const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc((void *)Ym, (short)0, bytes, kXBufWord3);
+            const __amdgpu_buffer_rsrc_t rr =
+                __builtin_amdgcn_make_buffer_rsrc((void *)(a.R ? a.R : Ym), (short)0, bytes, kXBufWord3);
+            uint32_t vb[2];
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++) {
+                const int n = nl + 32 * ni + c32;
+                vb[ni] = live && n < Nm ? (uint32_t)(((m0 + 4 * h) * Nm + n) * 4) : kX2OutOfRange;
+            }
+            auto roff = [&](int mi, int q, int j) { return (32 * mi + 8 * q + j) * Nm * 4; };
+            if (a.R) {
+#pragma unroll
+                for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                    for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+#pragma unroll
+                            for (int j = 0; j < 4; j++)
+                                rv[mi][ni][4 * q + j] = __builtin_bit_cast(
+                                    float, __builtin_amdgcn_raw_buffer_load_b32(rr, (int)vb[ni], roff(mi, q, j), 0));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    float4 sum;
-                    for (int pp = 0; pp < a.P; pp++) {
-                        float4 v;
-                        if (pp == p) {
-                            v = float4{acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2],
-                                       acc[mi][ni][4 * q + 3]};
-                        } else {
-                            v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                               rp, (int)slot(pp, mi, ni, q), 0, kX2DevScope));
+                    // rows 32 mi + 8 q + 4 h + j, j = 0..3: one LDS read
+                    const float4 rs = *(const float4 *)(rs_l + 32 * mi + 8 * q + 4 * h);
+                    const float rsj[4] = {rs.x, rs.y, rs.z, rs.w};
+#pragma unroll
+                    for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int r = 4 * q + j;
+                            const float y = acc[mi][ni][r] * rsj[j];  // a power of two: exact
+                            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, a.R ? rv[mi][ni][r] + y : y),
+                                                                  ry, (int)vb[ni], roff(mi, q, j), 0);
                         }
-                        if (pp == 0) sum = v;
-                        else sum = float4{sum.x + v.x, sum.y + v.y, sum.z + v.z, sum.w + v.w};
+                }
+        } else {
+            if (a.R) {
+#pragma unroll
+                for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                    for (int ni = 0; ni < 2; ni++) {
+                        const int n = min(nl + 32 * ni + c32, Nm - 1);
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const int m = min(m0 + 32 * mi + (r & 3) + 4 * h + 8 * (r >> 2), a.M - 1);
+                            rv[mi][ni][r] = a.R[(int64_t)m * Nm + n];
+                        }
                     }
-                    acc[mi][ni][4 * q] = sum.x;
-                    acc[mi][ni][4 * q + 1] = sum.y;
-                    acc[mi][ni][4 * q + 2] = sum.z;
-                    acc[mi][ni][4 * q + 3] = sum.w;
-                }
-    }
-#pragma unroll
-    for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-        for (int ni = 0; ni < 2; ni++) {
-            const int n = nl + 32 * ni + c32;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + 32 * mi + (r & 3) + 4 * h + 8 * (r >> 2);
-                if (live && m < a.M && n < Nm) {
-                    const int64_t o = (int64_t)m * Nm + n;
-                    const float y = acc[mi][ni][r] * a.Rs[m];  // a power of two: exact
-                    Ym[o] = a.R ? a.R[o] + y : y;
-                }
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 rs = *(const float4 *)(rs_l + 32 * mi + 8 * q + 4 * h);
+                    const float rsj[4] = {rs.x, rs.y, rs.z, rs.w};
+#pragma unroll
+                    for (int ni = 0; ni < 2; ni++) {
+                        const int n = nl + 32 * ni + c32;
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int r = 4 * q + j;
+                            const int m = m0 + 32 * mi + j + 4 * h + 8 * q;
+                            if (live && m < a.M && n < Nm) {
+                                const int64_t o = (int64_t)m * Nm + n;
+                                const float y = acc[mi][ni][r] * rsj[j];  // a power of two: exact
+                                Ym[o] = a.R ? rv[mi][ni][r] + y : y;
+                            }
+                        }
+                    }
+                }
         }
+    }
+    }  // passes
 }
 
 template <int WF, int WM, int WN, int S, int OCC, int RD>
@@ -1100,25 +1228,31 @@ void launch_exact_for(const ExactArgs &a)
 
 uint32_t *g_x2_cnt = nullptr;  // tile counters of the split form, zero between launches
 
-// The second tiling: P K parts when there are fewer 64 x 256 tiles than CUs
-// (at least 32 blocks a part); the stage count per part is whole.
+// The second tiling: about 2 workgroups per CU (both resident), the same
+// number per row of tiles, share the stages evenly, with ranges of at least
+// kX2MinStages stages and at most about kX2MaxSplit workgroups per tile; a
+// launch whose ranges all fall on tile boundaries needs no part slots or
+// counters.
 template <int WF, int S>
 void launch_exact2(X2Args a)
 {
     using G = X2Geo<S>;
     a.ntm = (a.M + 63) / 64;
     a.tiles = a.ntm * ((a.N + 255) / 256);
-    const int nst = (a.nb + S - 1) / S;
-    int P = 1;
-    while (2 * P <= kX2Parts && a.tiles * P <= num_cus() && a.nb / (2 * P) >= 16 && a.tiles <= kX2Counters &&
-           g_x2_cnt)
-        P *= 2;
-    a.P = P;
-    a.spp = (nst + P - 1) / P;
+    a.nst = (a.nb + S - 1) / S;
+    const int nct = a.tiles / a.ntm;
+    const int64_t U = (int64_t)nct * a.nst;  // items of a row of tiles
+    int64_t gr = std::max(1, 2 * num_cus() / a.ntm);
+    gr = std::min(gr, U / kX2MinStages);
+    gr = std::max<int64_t>(1, std::min(gr, (int64_t)kX2MaxSplit * nct));
+    if (!g_x2_cnt || a.tiles > kX2Counters) gr = nct;  // whole tiles only
+    a.gr = (int)gr;
+    const int64_t NG = (int64_t)a.ntm * gr;
     void *pws = nullptr;
     bool own = false;
-    if (P > 1) {
-        const size_t bytes = (size_t)P * a.tiles * 64 * 256 * 4;
+    if (U % gr != 0 || (U / gr) % a.nst != 0) {
+        // some range cuts a tile: part slots (two a workgroup) and counters
+        const size_t bytes = (size_t)NG * 2 * 64 * 256 * 4;
         pws = workspace(2, bytes);
         own = pws == nullptr;
         if (own) HOLO_CHECK(hipMallocAsync(&pws, bytes, stream()));
@@ -1132,7 +1266,7 @@ void launch_exact2(X2Args a)
         HOLO_CHECK(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS));
         attr = true;
     }
-    launch_timed(kern, dim3(a.tiles * P), dim3(256), G::LDS, a);
+    launch_timed(kern, dim3((unsigned)NG), dim3(256), G::LDS, a);
     HOLO_LAUNCH_CHECK();
     if (own) HOLO_CHECK(hipFreeAsync(pws, stream()));
 }
