@@ -741,6 +741,7 @@ struct X2Args {
     uint32_t *cnt;                   // [tiles] arrival counters, zero between launches (split launches)
     int M, N, nb, ntm, tiles, nst;   // nst: stages per tile
     int gr;                          // workgroups per row of tiles
+    int xi;                          // ranges are whole parts of tiles: part p's ranges share an XCD
 };
 
 // First item of the i-th range of a row, and the range that holds item x.
@@ -862,12 +863,17 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // uniform: the weight resource stays scalar
     const int nb = a.nb;
 
-    // workgroup g -> w = i * ntm + r: the workgroups of XCD x (round-robin
-    // dispatch) take a contiguous run of w, so the row tiles that walk the
-    // same weights in step (same i) run on one XCD together
+    // workgroup g -> w = i * ntm + r.  The ntm row tiles of one range i
+    // (which walk the same weights in step) run on one XCD (g mod 8 under
+    // round-robin dispatch).  The XCD takes a contiguous run of ranges, or,
+    // when every tile splits into the same whole parts, the ranges i = x
+    // (mod 8): then with a part count dividing 8 an XCD holds one part of
+    // each of its tiles, and reads that part of the activations only.
     const int NG = (int)gridDim.x, g = blockIdx.x;
-    const int w = (NG & 7) ? g : (g & 7) * (NG >> 3) + (g >> 3);
     const int nst = a.nst, ntm = a.ntm, Gr = a.gr;
+    const int w = (NG & 7) ? g
+                  : a.xi   ? ((g & 7) + 8 * ((g >> 3) / ntm)) * ntm + (g >> 3) % ntm
+                           : (g & 7) * (NG >> 3) + (g >> 3);
     const int ri = w / ntm, rt = w - ri * ntm;  // range i of row tile r
     const int64_t U = (int64_t)(a.tiles / ntm) * nst;
     const int64_t ibeg = x2_start(ri, U, Gr), iend = x2_start(ri + 1, U, Gr);
@@ -1248,6 +1254,7 @@ void launch_exact2(X2Args a)
     if (!g_x2_cnt || a.tiles > kX2Counters) gr = nct;  // whole tiles only
     a.gr = (int)gr;
     const int64_t NG = (int64_t)a.ntm * gr;
+    a.xi = gr % 8 == 0 && U % gr == 0 && a.nst % (U / gr) == 0;
     void *pws = nullptr;
     bool own = false;
     if (U % gr != 0 || (U / gr) % a.nst != 0) {
