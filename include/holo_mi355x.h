@@ -226,9 +226,11 @@ int holo_prefill_get_q8_kernel(void);
  * within 2^-22 |x|, times the block's integers, exact in f16, on the f16
  * matrix cores, block scales applied in fp32 in block order; fp32 accuracy,
  * within 1e-3 of the CPU path; X 16-byte aligned and K <= 16384, else M
- * GEMVs; with few column tiles the K range is split in 2 or 4 parts summed
- * in part order, so the result depends on the launch's tile count but not
- * on timing), the f16 product below (HOLO_PREFILL_F16) or the Q8_0
+ * GEMVs; the K blocks of each row of tiles are dealt evenly to about two
+ * workgroups per CU, and a tile whose blocks two or more workgroups share
+ * is the sum of their parts in K order, so the result depends on the
+ * launch's shape and the CU count but not on timing), the f16 product below
+ * (HOLO_PREFILL_F16) or the Q8_0
  * product above (HOLO_PREFILL_Q8_0: X quantised to Q8_0).  M < 64 runs M
  * GEMVs.                                                                     */
 void holo_matmul_batch_q4_0(float *Y, const void *W, const float *X, int M, int N, int K,
@@ -284,9 +286,11 @@ void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const i
  * allocation per call); calls on one stream reuse them in order.  Otherwise
  * one holo_matmul GEMV per row.  The multi forms take up to 3 matrices
  * sharing X (with several, every N a multiple of 128); an output equals the
- * single call's bit for bit when both launches split K alike (always when
- * neither has fewer column tiles than CUs), else within the product's error
- * bound.  No reference counterpart (the reference runs one GEMV per token,
+ * single call's bit for bit when neither launch shares a tile's K blocks
+ * between workgroups (for Q4_0, Q8_0 and F16 that is when the K blocks per
+ * row of tiles split evenly into whole tiles per workgroup), else it is
+ * within the product's error bound.  No reference counterpart (the
+ * reference runs one GEMV per token,
  * llm.c:1049).                                                              */
 void holo_matmul_batch(float *Y, const void *W, const float *X, int M, int N, int K, int type);
 void holo_matmul_batch_multi(float *const *Y, const void *const *W, const int *N, int nmat, const float *X,
