@@ -418,6 +418,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_exact_k(ExactArgs a)
 {
     using G = XGeo<WM, WN, S>;
     extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ __align__(16) float rs_l[G::TM];  // the tile's row scales
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, c32 = lane & 31;
 
@@ -427,6 +428,8 @@ __global__ __launch_bounds__(256, OCC) void gemm_exact_k(ExactArgs a)
     const int g = blockIdx.x;
     const int t = (a.tiles & 7) ? g : (g & 7) * (a.tiles >> 3) + (g >> 3);
     const int m0 = (t % a.ntm) * G::TM, ng = (t / a.ntm) * G::TN;
+    // read in the epilogue, after the stage loop's barriers
+    if (tid < G::TM) rs_l[tid] = a.Rs[min(m0 + tid, a.M - 1)];
     const int sel = (ng >= a.n_end[0]) + (ng >= a.n_end[1]);
     ExactMat w;
     w.W = sel == 2 ? a.W[2] : sel == 1 ? a.W[1] : a.W[0];
@@ -545,18 +548,42 @@ __global__ __launch_bounds__(256, OCC) void gemm_exact_k(ExactArgs a)
         }
     }
 
+    // the residual of every output first, in one batch of loads: a load
+    // between stores would wait for the stores issued before it as well
+    float rv[WM][WN][16];
+    if (a.R) {
+#pragma unroll
+        for (int mi = 0; mi < WM; mi++)
+#pragma unroll
+            for (int ni = 0; ni < WN; ni++) {
+                const int n = min(n0 + wn0 + 32 * ni + c32, w.N - 1);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int m = min(m0 + wm0 + 32 * mi + (r & 3) + 4 * h + 8 * (r >> 2), a.M - 1);
+                    rv[mi][ni][r] = a.R[(int64_t)m * w.N + n];
+                }
+            }
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int mi = 0; mi < WM; mi++)
 #pragma unroll
-        for (int ni = 0; ni < WN; ni++) {
-            const int n = n0 + wn0 + 32 * ni + c32;
+        for (int q = 0; q < 4; q++) {
+            // rows wm0 + 32 mi + 8 q + 4 h + j, j = 0..3: one LDS read
+            const float4 rs = *(const float4 *)(rs_l + wm0 + 32 * mi + 8 * q + 4 * h);
+            const float rsj[4] = {rs.x, rs.y, rs.z, rs.w};
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + wm0 + 32 * mi + (r & 3) + 4 * h + 8 * (r >> 2);
-                if (m < a.M && n < w.N) {
-                    const int64_t o = (int64_t)m * w.N + n;
-                    const float y = acc[mi][ni][r] * a.Rs[m];  // a power of two: exact
-                    w.Y[o] = a.R ? a.R[o] + y : y;
+            for (int ni = 0; ni < WN; ni++) {
+                const int n = n0 + wn0 + 32 * ni + c32;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int r = 4 * q + j;
+                    const int m = m0 + wm0 + 32 * mi + j + 4 * h + 8 * q;
+                    if (m < a.M && n < w.N) {
+                        const int64_t o = (int64_t)m * w.N + n;
+                        const float y = acc[mi][ni][r] * rsj[j];  // a power of two: exact
+                        w.Y[o] = a.R ? rv[mi][ni][r] + y : y;
+                    }
                 }
             }
         }
