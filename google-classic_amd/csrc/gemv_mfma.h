@@ -1,6 +1,6 @@
 // gemv_mfma.h -- device helpers shared by the GEMV kernels (gemv.hip) and
 // the persistent decode-step kernel (gemv_stream.hip): wave reductions, the
-// activation staging (24-bit fixed point in three int8 planes) and the int8
+// activation staging (22-bit fixed point in three int8 planes) and the int8
 // MFMA unit dots over Q4_0 / Q8_0 / Q4_K items.
 #pragma once
 

@@ -56,12 +56,12 @@ void holo_matmul(float *dst, const void *M, const float *v, int out_dim, int in_
 /* ---- GEMV activation mode ------------------------------------------------------
  * All modes hold the dot products to fp32 accuracy and accumulate across
  * blocks in fp32.
- * HOLO_XMODE_MFMA (default): activations are held per 32-block as 24-bit
- * fixed point, xi = rint(x * 127*65536/amax), |x - d*xi| <= amax*2^-23, in
+ * HOLO_XMODE_MFMA (default): activations are held per 32-block as 22-bit
+ * fixed point, xi = rint(x * 63*65536/amax), |x - d*xi| <= amax*2^-23, in
  * three int8 planes, and each block's three exact integer dots run on the
- * int8 matrix cores (v_mfma_i32_16x16x64_i8).  Taken for Q4_0 and Q4_K rows
- * with in_dim a multiple of 256 up to 16384 and 16-byte aligned matrices;
- * other shapes run HOLO_XMODE_F32.
+ * int8 matrix cores (v_mfma_i32_16x16x64_i8).  Taken for Q4_0, Q4_K and Q8_0
+ * rows with in_dim a multiple of 256 up to 16384 and 16-byte aligned
+ * matrices; other shapes run HOLO_XMODE_F32.
  * HOLO_XMODE_F32: every weight is multiplied by the fp32 activation itself
  * (v_cvt_f32_ubyte + FMA).
  * HOLO_XMODE_I24: the MFMA mode's arithmetic on v_dot4_i32_i8.
@@ -70,8 +70,11 @@ void holo_matmul(float *dst, const void *M, const float *v, int out_dim, int in_
  * GEMV entry point.                                                        */
 #define HOLO_XMODE_F32 0
 #define HOLO_XMODE_I24 1
-#define HOLO_XMODE_MFMA 2      /* default; Q8_0 stays on F32, measured faster */
-#define HOLO_XMODE_MFMA_ALL 3  /* MFMA for Q8_0 as well                      */
+#define HOLO_XMODE_MFMA 2      /* default: MFMA for Q4_0, Q4_K and Q8_0      */
+#define HOLO_XMODE_MFMA_ALL 3  /* the same as HOLO_XMODE_MFMA                */
+/* MFMA for Q4_0 and Q4_K, Q8_0 rows up to 8192 on the F32 kernel (the
+ * former default; 4096x4096 Q8_0: 6.2 against 5.9 us on MFMA)              */
+#define HOLO_XMODE_MFMA_Q8F32 4
 void holo_gemv_set_xmode(int xmode);
 /* Launch shape of the GEMV kernels: rows per work item (1, 2 or 4; 0 = the
  * default, 1; F32/I24 modes only) and workgroups per CU (0 = the default:
