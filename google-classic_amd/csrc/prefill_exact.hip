@@ -613,25 +613,37 @@ __global__ __launch_bounds__(256) void xsplit_row_k(uint2 *__restrict__ Ah, uint
     __shared__ float red[16];
     const int n4 = K >> 2;
     const int64_t r4 = (int64_t)blockIdx.x * n4;
-    const float4 *x4 = (const float4 *)X + r4;
+    // every load of the row issued first, through buffer resources over the
+    // row (and the norm weights): a float4 past K reads zeros, so no load
+    // waits behind a branch or behind another's arithmetic
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void *)((const float4 *)X + r4), (short)0, K * 4, kXBufWord3);
+    const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(MODE == XS_SWIGLU ? (const float4 *)U + r4 : (const float4 *)X + r4), (short)0, K * 4, kXBufWord3);
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(MODE == XS_NORM ? NW : X), (short)0, K * 4, kXBufWord3);
     float4 v[NV], wv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int o = (int)(threadIdx.x + 256 * j) * 16;
+        v[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
+        if constexpr (MODE == XS_SWIGLU)
+            wv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ru, o, 0, 0));
+        if constexpr (MODE == XS_NORM)
+            wv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0));
+    }
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int i = threadIdx.x + 256 * j;
-        v[j] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
         if constexpr (MODE == XS_SWIGLU) {
-            const float4 u = i < n4 ? ((const float4 *)U + r4)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 u = wv[j];
             v[j].x = (v[j].x / (1.0f + expf(-v[j].x))) * u.x;
             v[j].y = (v[j].y / (1.0f + expf(-v[j].y))) * u.y;
             v[j].z = (v[j].z / (1.0f + expf(-v[j].z))) * u.z;
             v[j].w = (v[j].w / (1.0f + expf(-v[j].w))) * u.w;
         }
-        if constexpr (MODE == XS_NORM) {
-            // the weights load with the row, not after the reduction
-            wv[j] = ((const float4 *)NW)[min(i, n4 - 1)];
+        if constexpr (MODE == XS_NORM)
             ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
-        }
     }
     float scale = 1.f;
     if constexpr (MODE == XS_NORM) {
