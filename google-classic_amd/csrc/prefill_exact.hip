@@ -774,6 +774,7 @@ struct X2Args {
     const uint8_t *W[kExactMats];    // block streams or f16 rows [N_i][K]
     int n_end[kExactMats];           // prefix sums of N_i; unused entries INT_MAX
     const _Float16 *Ah, *Al;         // activation halves [M][K]
+    const float *Sx;                 // [M][K/32] block sums of the split rows (Q4_K)
     const float *Rs;                 // [M] row scales
     const float *R;                  // one matrix only: Y = R + product (may alias Y)
     float *part;                     // [2 G][64 x 256] part slots (split launches)
@@ -791,7 +792,8 @@ template <int S>
 struct X2Geo {
     static constexpr int RB = S * 64 + 16;         // LDS bytes per row of one half (S blocks of 32 f16 + pad)
     static constexpr int HALF = 64 * RB;
-    static constexpr int STAGE = (2 * HALF + 255) & ~255;
+    static constexpr int SX = 2 * HALF;            // fp32 [S][64]: the rows' block sums (Q4_K)
+    static constexpr int STAGE = (SX + S * 64 * 4 + 255) & ~255;
     static constexpr int LDS = 2 * STAGE;
 };
 
@@ -826,6 +828,17 @@ __device__ __forceinline__ uint32_t x2_scale_bits(uint32_t w0)
     const uint32_t x = P ? (w0 >> 16) : (w0 & 0xFFFFu);
     return __builtin_amdgcn_permlane32_swap(x, x, false, false)[0];
 }
+// Q4_K: a stage (sub-blocks j and j + 1, j even, of a superblock) in three
+// loads: the superblock's 16-byte header (d, dmin, the 12 scale bytes) and,
+// for each sub-block, the lane's 8 qs bytes 8h .. 8h + 7 of its 16 (weights
+// k = 8h .. 8h + 7 in the low nibbles and 16 + 8h .. in the high ones,
+// quant.c's layout, the same as a Q4_0 block's).
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+template <>
+struct X2Raw<EW_Q4_K> {
+    v4u hd;
+    v2u q0, q1;
+};
 template <>
 struct X2Raw<EW_F16> {
     v4u s0, s1;        // k = 8h .. 8h+7 and 16 + 8h .. 16 + 8h + 7
@@ -844,11 +857,36 @@ __device__ __forceinline__ X2Raw<WF> x2_fetch(__amdgpu_buffer_rsrc_t r, uint32_t
         const int so = 34 * b - 2 * P;
         x.w = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, so, 0));
         x.v = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, so + 16, 0));
+    } else if constexpr (WF == EW_Q4_K) {
+        // b even: the stage's first sub-block; vd the row, vo the row + 16 h
+        const int sb = 144 * (b >> 3), qo = sb + 16 + 16 * (b & 7);
+        x.hd = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vd, sb, 0));
+        x.q0 = __builtin_bit_cast(v2u, __builtin_amdgcn_raw_buffer_load_b64(r, (int)vo, qo, 0));
+        x.q1 = __builtin_bit_cast(v2u, __builtin_amdgcn_raw_buffer_load_b64(r, (int)vo, qo + 16, 0));
     } else {
         x.s0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, 64 * b, 0));
         x.s1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, 64 * b + 32, 0));
     }
     return x;
+}
+
+// Sub-block j (the stage's first when e = 0, second when e = 1) of the stage
+// held in x: both 16-k steps' B operands (q, exact in f16), d * sc and
+// dmin * m (exact in fp32: 11-bit times 6-bit), zero past the part.
+__device__ __forceinline__ void x2_unpack_q4_k(const X2Raw<EW_Q4_K> &x, int e, uint32_t j, bool live, v8h &b0,
+                                               v8h &b1, float &dsc, float &dmn)
+{
+    const v2u q = e ? x.q1 : x.q0;
+    uint32_t lo[4], hi[4];
+    nibbles_f16(q.x, (_Float16)0.0f, &lo[0], &hi[0]);
+    nibbles_f16(q.y, (_Float16)0.0f, &lo[2], &hi[2]);
+    b0 = __builtin_bit_cast(v8h, v4u{lo[0], lo[1], lo[2], lo[3]});
+    b1 = __builtin_bit_cast(v8h, v4u{hi[0], hi[1], hi[2], hi[3]});
+    uint32_t sc, mn;
+    q4_k_scale_min(x.hd.y, x.hd.z, x.hd.w, j, sc, mn);
+    const uint32_t dd = x.hd.x & (0u - (uint32_t)live);
+    dsc = half_bits_to_float(dd) * (float)sc;
+    dmn = half_bits_to_float(dd >> 16) * (float)mn;
 }
 
 // The B operands of both 16-k steps and the block's scale; live: the block
@@ -945,8 +983,9 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
     const int nbase = sel == 2 ? a.n_end[1] : sel == 1 ? a.n_end[0] : 0;
     const int Nm = (sel == 2 ? a.n_end[2] : sel == 1 ? a.n_end[1] : a.n_end[0]) - nbase;
     const int nl = nc - nbase;  // the wave's first column in its matrix (clamped)
-    constexpr uint32_t RBW = WF == EW_Q4_0 ? 18 : WF == EW_Q8_0 ? 34 : 64;
-    const uint32_t rowb = (uint32_t)nb * RBW;
+    // bytes of a row: 18 / 34 per Q4_0 / Q8_0 block, 144 per 8 Q4_K sub-blocks, 64 per F16 block
+    const uint32_t rowb = WF == EW_Q4_K ? (uint32_t)(nb >> 3) * 144u
+                                        : (uint32_t)nb * (WF == EW_Q4_0 ? 18u : WF == EW_Q8_0 ? 34u : 64u);
     const __amdgpu_buffer_rsrc_t rw =
         __builtin_amdgcn_make_buffer_rsrc((void *)Wm, (short)0, (int)((uint32_t)Nm * rowb), kXBufWord3);
     uint32_t vo[2], vd[2];
@@ -972,7 +1011,13 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
         ablk[i] = c >> 2;
         lw[i] = (uint32_t)(r * G::RB + c * 16);
     }
+    // Q4_K: the rows' block sums, thread tid < 64 S: row tid % 64, block tid / 64
+    const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a.Sx, (short)0, WF == EW_Q4_K ? (int)((uint32_t)a.M * (uint32_t)nb * 4u) : 0, kXBufWord3);
+    const uint32_t sxo = (uint32_t)min(m0 + (tid & 63), a.M - 1) * (uint32_t)nb;
+    const int sxb = (tid >> 6) & (S - 1);
     v4u sah[S], sal[S];
+    float sxv = 0.f;
     auto fetch_a = [&](int st) {
         const int kb = kb0 + st * S;
 #pragma unroll
@@ -981,6 +1026,9 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
             sah[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rah, (int)o, 0, 0));
             sal[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(ral, (int)o, 0, 0));
         }
+        if constexpr (WF == EW_Q4_K)
+            sxv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                rsx, (int)((sxo + (uint32_t)min(kb + sxb, kb1 - 1)) * 4u), 0, 0));
     };
     auto stash_a = [&](int buf) {
         uint8_t *base = lds + buf * G::STAGE;
@@ -989,6 +1037,8 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
             *(v4u *)(base + lw[i]) = sah[i];
             *(v4u *)(base + G::HALF + lw[i]) = sal[i];
         }
+        if constexpr (WF == EW_Q4_K)
+            if (tid < 64 * S) ((float *)(base + G::SX))[tid] = sxv;  // [block][row]
     };
 
     v16f acc[2][2];
@@ -1004,9 +1054,10 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
     auto wblk = [&](int b) { return WF == EW_F16 ? min(b, kb1 - 1) : b; };
     const int nsg = (kb1 - kb0 + S - 1) / S;  // stages of this pass
     // the weight words of a stage's S blocks, fetched one stage ahead
+    // (Q4_K: one slot per stage, ring[0])
     X2Raw<WF> ring[S][2];
 #pragma unroll
-    for (int s = 0; s < S; s++)
+    for (int s = 0; s < (WF == EW_Q4_K ? 1 : S); s++)
 #pragma unroll
         for (int ni = 0; ni < 2; ni++) {
             if (s & 1) ring[s][ni] = x2_fetch<WF, 1>(rw, vo[ni], vd[ni], wblk(kb0 + s));
@@ -1018,6 +1069,7 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
     stash_a(0);
     fetch_a(1);
     __syncthreads();
+    float mneg[2] = {0.f, 0.f};  // Q4_K: -dmin * m of the lane's column and sub-block (stage start + h)
     for (int st = 0; st < nsg; st++) {
         const uint8_t *base = lds + (st & 1) * G::STAGE;
         // stage st + 1 into the other buffer (free: every wave passed the
@@ -1031,6 +1083,17 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
             // this block's weight operands, then its ring slot fetches block b + S
             v8h b0[2], b1[2];
             float sc[2];
+            if constexpr (WF == EW_Q4_K) {
+                // sub-block b of the stage in ring[0]; its min term goes to
+                // the stage's fp32 MFMA below (lane h: sub-block b - s + h)
+#pragma unroll
+                for (int ni = 0; ni < 2; ni++) {
+                    float dmn;
+                    x2_unpack_q4_k(ring[0][ni], s, (uint32_t)(b & 7), b < kb1, b0[ni], b1[ni], sc[ni], dmn);
+                    if (s == h) mneg[ni] = -dmn;  // a select: h is the lane's half
+                    if (s == S - 1) ring[0][ni] = x2_fetch<WF, 0>(rw, vo[ni], vd[ni], b + 1);
+                }
+            } else {
 #pragma unroll
             for (int ni = 0; ni < 2; ni++) {
                 if (s & 1) {
@@ -1040,6 +1103,7 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
                     x2_unpack<WF, 0>(ring[s][ni], b < kb1, b0[ni], b1[ni], sc[ni]);
                     ring[s][ni] = x2_fetch<WF, 0>(rw, vo[ni], vd[ni], wblk(b + S));
                 }
+            }
             }
             const bool bl = b < kb1;  // F16: a block past the part adds nothing
 #pragma unroll
@@ -1066,6 +1130,20 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
                         for (int r = 0; r < 16; r++) acc[mi][ni][r] = __builtin_fmaf(sc[ni], c[r], acc[mi][ni][r]);
                     }
                 }
+            }
+        }
+        if constexpr (WF == EW_Q4_K) {
+            // the stage's min terms, sum over its two sub-blocks j of
+            // (-dmin m_j)[n] * (sum x)[m][j], on one fp32 MFMA per tile:
+            // A[m][j] = the row's block sum (lane (c, h): row c, sub-block h),
+            // B[j][n] = -dmin m_j of column n (lane (c, h): column c, sub-block h)
+            const float *sxl = (const float *)(base + G::SX);
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) {
+                const float av = sxl[64 * h + 32 * mi + c32];
+#pragma unroll
+                for (int ni = 0; ni < 2; ni++)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, mneg[ni], acc[mi][ni], 0, 0, 0);
             }
         }
         __syncthreads();
@@ -1476,11 +1554,14 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
         // row 4-byte aligned) and F16 rows; with several matrices every N but
         // the last a multiple of 64 (a wave's 64 columns in one matrix); each
         // matrix under 2 GiB (32-bit offsets)
-        bool x2 = !exact_v1() && (((kind == EW_Q4_0 || kind == EW_Q8_0) && nb % 2 == 0) || kind == EW_F16);
+        bool x2 = !exact_v1() &&
+                  (((kind == EW_Q4_0 || kind == EW_Q8_0) && nb % 2 == 0) || kind == EW_F16 || kind == EW_Q4_K);
         for (int j = 0; j < cnt - 1 && x2; j++) x2 = a.n_end[j] % 64 == 0;
         for (int j = 0; j < cnt && x2; j++) {
             const int64_t rows = a.n_end[j] - (j ? a.n_end[j - 1] : 0);
-            x2 = rows * (int64_t)nb * (kind == EW_Q4_0 ? 18 : kind == EW_Q8_0 ? 34 : 64) < (1LL << 31);
+            // bytes per 32-weight block: Q4_0 18, Q4_K 144 / 8, Q8_0 34, F16 64
+            x2 = rows * (int64_t)nb * (kind == EW_Q4_0 || kind == EW_Q4_K ? 18 : kind == EW_Q8_0 ? 34 : 64) <
+                 (1LL << 31);
         }
         if (x2) {
             X2Args b = {};
@@ -1491,6 +1572,7 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
             }
             b.Ah = Ah;
             b.Al = Al;
+            b.Sx = Sx;
             b.Rs = Rs;
             b.R = a.R;
             b.M = M;
@@ -1499,6 +1581,7 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
             switch (kind) {
             case EW_Q4_0: launch_exact2<EW_Q4_0, 2>(b); break;
             case EW_Q8_0: launch_exact2<EW_Q8_0, 2>(b); break;
+            case EW_Q4_K: launch_exact2<EW_Q4_K, 2>(b); break;
             default: launch_exact2<EW_F16, 2>(b); break;
             }
             continue;
