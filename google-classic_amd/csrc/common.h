@@ -11,6 +11,10 @@
 
 namespace holo {
 
+// Word 3 of a raw buffer resource (gfx9: 32-bit data format, no swizzle):
+// loads past its byte range return zeros.
+constexpr uint32_t kRawBufWord3 = 0x00020000u;
+
 // Library stream (null stream unless holo_set_stream was called) and the
 // copy stream of cuda_memcpy_*_async (reference cuda_ops.cu:88-89).
 hipStream_t stream();

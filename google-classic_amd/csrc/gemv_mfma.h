@@ -129,7 +129,7 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d)
 // the buffer unit answers with zeros without touching memory.  Longer rows
 // load their remaining chunks in x_stage.
 constexpr int kPreX = 8;
-constexpr uint32_t kBufferWord3 = 0x00020000u;  // gfx9 raw buffer: 32-bit data format
+constexpr uint32_t kBufferWord3 = kRawBufWord3;
 constexpr uint32_t kOutOfRange = 0x80000000u;
 
 typedef float v4f __attribute__((ext_vector_type(4)));

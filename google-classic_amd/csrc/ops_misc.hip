@@ -201,12 +201,19 @@ __global__ __launch_bounds__(256) void mha_k(float *dst, const float *q, const f
 //     (r%4) + 8(r/4) + 4hh, r = 0..15: the row maximum is 15 local steps and
 //     one exchange with lane j ^ 32.  (On v_mfma_f32_32x32x2_f32 the scores
 //     took 64 instructions at head size 128, here 24.)
-//   output, transposed: O^T += V^T P^T over 16 steps of v_mfma_f32_32x32x2_f32
-//     (lane l supplies A[l%32][l/32] and B[l/32][l%32]); step st pairs key
-//     (st%4) + 8(st/4) + 4hh (slot hh) with register st of the probabilities,
-//     which is already the B operand.  A is V: lane i + 32hh reads dims
-//     VB*i .. VB*i + VB - 1 of that key's row, one contiguous row per half;
-//     element b feeds the block of dims VB*i + b.
+//   output, transposed: O^T += V^T P^T on v_mfma_f32_32x32x16_f16, V and P
+//     split as above.  The contraction runs over the tile's 32 keys in the
+//     order the probabilities sit in registers: k-step ks takes registers
+//     8ks .. 8ks + 7 of lane j + 32hh (keys (r%4) + 8(r/4) + 4hh), which is
+//     its B operand as it stands.  A is V: lane i + 32hh reads dims VB*i ..
+//     VB*i + VB - 1 of each of the same 16 keys' rows, and element b of the
+//     8 keys of step ks is its A operand for the block of dims VB*i + b.
+//     (On v_mfma_f32_32x32x2_f32 this product took 64 instructions of four
+//     times the f16 instruction's cycles at head size 128, here 24.)
+// Workgroup g runs on XCD g mod 8 (round-robin dispatch): with the head count
+// a multiple of 8, XCD x takes heads x H/8 .. (x + 1) H/8 - 1, every query
+// block of each, heaviest (most keys) first, so the XCDs get equal work and
+// each reads its own heads' keys and values.
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 af16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 af16x8 __attribute__((ext_vector_type(8)));
@@ -220,19 +227,59 @@ __device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo)
     lo = (_Float16)(x - (float)hi);
 }
 
+// The same split of 8 values straight into MFMA operands, two at a time: one
+// packed conversion for the two hi, each x - hi by v_fma_mix_f32 reading its
+// hi as f16 (one instruction; exact, x - hi is an fp32), one packed
+// conversion for the two lo.  Written out: the compiler turns the fused
+// form into a conversion and a subtraction.
+typedef _Float16 af16x2 __attribute__((ext_vector_type(2)));
+typedef float af32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split8_f16(const float x[8], af16x8 &hi, af16x8 &lo)
+{
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const af16x2 h = __builtin_convertvector((af32x2){x[2 * i], x[2 * i + 1]}, af16x2);
+        const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+        af32x2 r;
+        asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r.x) : "v"(hb), "v"(x[2 * i]));
+        asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r.y) : "v"(hb), "v"(x[2 * i + 1]));
+        const af16x2 l = __builtin_convertvector(r, af16x2);
+        hi[2 * i] = h.x;
+        hi[2 * i + 1] = h.y;
+        lo[2 * i] = l.x;
+        lo[2 * i + 1] = l.y;
+    }
+}
+
 template <int HD>
 __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const float *q, const float *kc,
                                                            const float *vc, int rows, int pos0, int n_heads,
-                                                           int n_kv_heads)
+                                                           int n_kv_heads, int nqb)
 {
     constexpr int NQ = HD / 16;  // 16-dim chunks of a row: the K of one f16 score MFMA
     constexpr int VB = HD / 32;  // output blocks: lane i covers dims VB*i .. VB*i + VB - 1
     extern __shared__ float amf_lds[];
-    float *lo = amf_lds;                       // [4 waves][HD][32]
-    float *lm = lo + 4 * HD * 32;              // [4][32] running max per query
+    // the waves' outputs [4 waves][32 queries][HD + 1]: the merge pass reads
+    // consecutive dims of a query row (one bank each), the stores from the
+    // MFMA layout put the 32 queries of a register on distinct banks
+    constexpr int OS = HD + 1;
+    float *lo = amf_lds;
+    float *lm = lo + 4 * 32 * OS;              // [4][32] running max per query
     float *ll = lm + 4 * 32;                   // [4][64] running sum per lane
-    const int h = blockIdx.y, q0 = (gridDim.x - 1 - blockIdx.x) * 32;  // heaviest query blocks first
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 31, hh = lane >> 5;
+    // (head, query block) of this workgroup, heaviest query blocks first
+    const int g = blockIdx.x;
+    int h, qb;
+    if (n_heads % 8 == 0) {
+        const int hx = n_heads >> 3, i = g >> 3;  // i: the workgroup's place on its XCD
+        h = (g & 7) * hx + i % hx;
+        qb = nqb - 1 - i / hx;
+    } else {
+        h = g % n_heads;
+        qb = nqb - 1 - g / n_heads;
+    }
+    const int q0 = qb * 32;
+    const int lane = threadIdx.x & 63, j = lane & 31, hh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // uniform: the tiles' resources stay scalar
     const int kvh = h / (n_heads / n_kv_heads);
     const int64_t q_dim = (int64_t)n_heads * HD, kv_dim = (int64_t)n_kv_heads * HD;
     const float scale = 1.0f / sqrtf((float)HD);
@@ -261,8 +308,14 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
     }
     __syncthreads();
     const _Float16 *qhr = qh + j * QS + 8 * hh, *qlr = ql + j * QS + 8 * hh;
-    const float *kb = kc + (int64_t)kvh * HD + 8 * hh;
-    const float *vb = vc + (int64_t)kvh * HD + VB * j;
+    // keys and values through buffer resources based at each tile's first
+    // key: the lane offsets are fixed for the launch, the rows' offsets are
+    // wave-uniform, and rows past last_key fall outside the range and read
+    // zeros (their scores are masked and their probabilities 0)
+    const float *khead = kc + (int64_t)kvh * HD, *vhead = vc + (int64_t)kvh * HD;
+    const uint32_t rowb = (uint32_t)kv_dim * 4u;
+    const uint32_t kvo = (uint32_t)j * rowb + 32u * (uint32_t)hh;          // key j, dims 8hh ..
+    const uint32_t vvo = 4u * (uint32_t)hh * rowb + 4u * VB * (uint32_t)j;  // key 4hh + .., dims VB j ..
     float m = -INFINITY, l = 0.f;
     v16f o[VB];
 #pragma unroll
@@ -274,13 +327,36 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
         // lane j + 32hh supplies dims 16c + 8hh .. 16c + 8hh + 7 of key j (A) and
         // of query j (B), as the 32x32x2 f32 layout did for its dims, so the
         // scores land in the same registers
+        const int nk = min(32, last_key + 1 - key0);  // keys of the tile inside the range
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(khead + (int64_t)key0 * kv_dim), (short)0, (int)((uint32_t)nk * rowb), kRawBufWord3);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(vhead + (int64_t)key0 * kv_dim), (short)0, (int)((uint32_t)nk * rowb), kRawBufWord3);
         float4 kr[2 * NQ];
-        {
-            const float *kp = kb + (int64_t)min(key0 + j, last_key) * kv_dim;  // keys past last_key are masked
 #pragma unroll
-            for (int c = 0; c < NQ; c++) {
-                kr[2 * c] = *(const float4 *)(kp + 16 * c);
-                kr[2 * c + 1] = *(const float4 *)(kp + 16 * c + 4);
+        for (int c = 0; c < NQ; c++) {
+            kr[2 * c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(kvo + 64 * c), 0, 0));
+            kr[2 * c + 1] =
+                __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(kvo + 64 * c + 16), 0, 0));
+        }
+        // the output product's 16 key row pieces, loaded with the keys so that
+        // their round trip runs under the scores
+        float vv[16][VB];
+#pragma unroll
+        for (int st = 0; st < 16; st++) {
+            const int so = (int)((uint32_t)((st & 3) + 8 * (st >> 2)) * rowb);  // wave-uniform
+            if constexpr (VB == 4) {
+                const float4 v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, (int)vvo, so, 0));
+                vv[st][0] = v.x;
+                vv[st][1] = v.y;
+                vv[st][2] = v.z;
+                vv[st][3] = v.w;
+            } else if constexpr (VB == 2) {
+                const float2 v = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)vvo, so, 0));
+                vv[st][0] = v.x;
+                vv[st][1] = v.y;
+            } else {
+                vv[st][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rv, (int)vvo, so, 0));
             }
         }
         v16f s = v16f{};
@@ -288,11 +364,8 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
         for (int c = 0; c < NQ; c++) {
             const float kv[8] = {kr[2 * c].x,     kr[2 * c].y,     kr[2 * c].z,     kr[2 * c].w,
                                  kr[2 * c + 1].x, kr[2 * c + 1].y, kr[2 * c + 1].z, kr[2 * c + 1].w};
-            _Float16 h8[8], l8[8];
-#pragma unroll
-            for (int t2 = 0; t2 < 8; t2++) split_f16(kv[t2], h8[t2], l8[t2]);
-            const af16x8 kh = {h8[0], h8[1], h8[2], h8[3], h8[4], h8[5], h8[6], h8[7]};
-            const af16x8 kl = {l8[0], l8[1], l8[2], l8[3], l8[4], l8[5], l8[6], l8[7]};
+            af16x8 kh, kl;
+            split8_f16(kv, kh, kl);
             const af16x8 bh = *(const af16x8 *)(qhr + 16 * c), bl = *(const af16x8 *)(qlr + 16 * c);
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, bh, s, 0, 0, 0);
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, bl, s, 0, 0, 0);
@@ -324,21 +397,21 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
 #pragma unroll
         for (int b = 0; b < VB; b++) o[b] *= corr;
 #pragma unroll
-        for (int st = 0; st < 16; st++) {
-            const int key = key0 + (st & 3) + 8 * (st >> 2) + 4 * hh;
-            const float *vp = vb + (int64_t)min(key, last_key) * kv_dim;  // masked keys: weight 0
-            if constexpr (VB == 4) {
-                const float4 v = *(const float4 *)vp;
-                o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.x, s[st], o[0], 0, 0, 0);
-                o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.y, s[st], o[1], 0, 0, 0);
-                o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.z, s[st], o[2], 0, 0, 0);
-                o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.w, s[st], o[3], 0, 0, 0);
-            } else if constexpr (VB == 2) {
-                const float2 v = *(const float2 *)vp;
-                o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.x, s[st], o[0], 0, 0, 0);
-                o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.y, s[st], o[1], 0, 0, 0);
-            } else {
-                o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(*vp, s[st], o[0], 0, 0, 0);
+        for (int ks = 0; ks < 2; ks++) {
+            const float pv[8] = {s[8 * ks],     s[8 * ks + 1], s[8 * ks + 2], s[8 * ks + 3],
+                                 s[8 * ks + 4], s[8 * ks + 5], s[8 * ks + 6], s[8 * ks + 7]};
+            af16x8 bh, bl;
+            split8_f16(pv, bh, bl);
+#pragma unroll
+            for (int b = 0; b < VB; b++) {
+                float v8[8];
+#pragma unroll
+                for (int t2 = 0; t2 < 8; t2++) v8[t2] = vv[8 * ks + t2][b];
+                af16x8 ah, al;
+                split8_f16(v8, ah, al);
+                o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, o[b], 0, 0, 0);
+                o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, o[b], 0, 0, 0);
+                o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, o[b], 0, 0, 0);
             }
         }
     }
@@ -350,7 +423,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int i = (r & 3) + 8 * (r >> 2) + 4 * hh;
-            lo[(wave * HD + VB * i + b) * 32 + j] = o[b][r];
+            lo[(wave * 32 + j) * OS + VB * i + b] = o[b][r];
         }
     if (hh == 0) lm[wave * 32 + j] = m;
     ll[wave * 64 + lane] = l;
@@ -367,7 +440,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
             const float mw = lm[w * 32 + qj];
             const float wgt = mw == -INFINITY ? 0.f : expf(mw - M);
             L += wgt * (ll[w * 64 + qj] + ll[w * 64 + 32 + qj]);
-            O += wgt * lo[(w * HD + d) * 32 + qj];
+            O += wgt * lo[(w * 32 + qj) * OS + d];
         }
         out[(int64_t)(q0 + qj) * q_dim + (int64_t)h * HD + d] = O / L;
     }
@@ -377,15 +450,16 @@ template <int HD>
 static void launch_attn_prefill_mfma(float *out, const float *q, const float *kc, const float *vc, int rows, int pos0,
                                      int n_heads, int n_kv_heads)
 {
-    constexpr size_t lds = (size_t)(4 * HD * 32 + 4 * 32 + 4 * 64) * sizeof(float);
+    constexpr size_t lds = (size_t)(4 * 32 * (HD + 1) + 4 * 32 + 4 * 64) * sizeof(float);
     static bool attr = false;
     if (!attr) {
         HOLO_CHECK(hipFuncSetAttribute((const void *)attn_prefill_mfma_k<HD>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr = true;
     }
-    hipLaunchKernelGGL(attn_prefill_mfma_k<HD>, dim3((rows + 31) / 32, n_heads), dim3(256), lds, stream(), out, q, kc,
-                       vc, rows, pos0, n_heads, n_kv_heads);
+    const int nqb = (rows + 31) / 32;
+    hipLaunchKernelGGL(attn_prefill_mfma_k<HD>, dim3((unsigned)(nqb * n_heads)), dim3(256), lds, stream(), out, q, kc,
+                       vc, rows, pos0, n_heads, n_kv_heads, nqb);
     HOLO_LAUNCH_CHECK();
 }
 

@@ -160,7 +160,7 @@ struct WRaw<EW_Q6_K> {
     uint32_t sc, d, s, j;
 };
 
-constexpr uint32_t kXBufWord3 = 0x00020000u;  // raw buffer resource: 32-bit data format
+constexpr uint32_t kXBufWord3 = kRawBufWord3;
 
 // The per-thread part of every stage load's address, computed once per
 // workgroup: a stage then adds only its block index (a scalar multiple) to a

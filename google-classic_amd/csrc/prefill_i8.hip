@@ -40,7 +40,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kI8BufWord3 = 0x00020000u;  // raw buffer resource: 32-bit data format
+constexpr uint32_t kI8BufWord3 = kRawBufWord3;
 constexpr int kI8Mats = 3;
 
 // ---- activation panel: Q8_0 blocks -> int8 rows, d bits, C = -8 sum q ----------
