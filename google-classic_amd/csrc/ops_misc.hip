@@ -266,6 +266,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
     float *lo = amf_lds;
     float *lm = lo + 4 * 32 * OS;              // [4][32] running max per query
     float *ll = lm + 4 * 32;                   // [4][64] running sum per lane
+    float *lw = ll + 4 * 64;                   // [4][32] merge weight of each wave per query
     // (head, query block) of this workgroup, heaviest query blocks first
     const int g = blockIdx.x;
     int h, qb;
@@ -282,7 +283,9 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // uniform: the tiles' resources stay scalar
     const int kvh = h / (n_heads / n_kv_heads);
     const int64_t q_dim = (int64_t)n_heads * HD, kv_dim = (int64_t)n_kv_heads * HD;
-    const float scale = 1.0f / sqrtf((float)HD);
+    // scores in log2 units: (q . k) / sqrt(hd) * log2(e), so that each
+    // probability is one v_exp_f32 (2^x) instead of a full expf
+    const float scale = 1.0f / sqrtf((float)HD) * 1.44269504088896341f;
     const int last_key = pos0 + min(q0 + 32, rows) - 1;  // the furthest position a query here sees
     const int ntiles = last_key / 32 + 1;
     const int qpos = pos0 + q0 + j;  // rows past the prompt: computed, not stored
@@ -385,11 +388,11 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
         const float mnew = fmaxf(m, tmax);
         // a query with no key yet (every key so far past it) keeps m = -inf, l = 0
         const bool none = mnew == -INFINITY;
-        const float corr = none ? 1.0f : expf(m - mnew);
+        const float corr = none ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
         float ps = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            s[r] = none ? 0.f : expf(s[r] - mnew);
+            s[r] = none ? 0.f : __builtin_amdgcn_exp2f(s[r] - mnew);
             ps += s[r];
         }
         l = l * corr + ps;
@@ -416,7 +419,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
         }
     }
 
-    // merge the 4 waves: O = sum_w e^(m_w - M) O_w, L = sum_w e^(m_w - M) l_w
+    // merge the 4 waves: O = sum_w 2^(m_w - M) O_w / L, L = sum_w 2^(m_w - M) l_w
     __syncthreads();  // every wave is done with the query rows in lo
 #pragma unroll
     for (int b = 0; b < VB; b++)
@@ -428,21 +431,31 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
     if (hh == 0) lm[wave * 32 + j] = m;
     ll[wave * 64 + lane] = l;
     __syncthreads();
-    for (int e = threadIdx.x; e < 32 * HD; e += 256) {
-        const int qj = e / HD, d = e - qj * HD;  // consecutive threads: consecutive dims of one row
-        if (q0 + qj >= rows) continue;
+    // each query's four weights 2^(m_w - M) / L, once per query rather than
+    // per output element
+    if (threadIdx.x < 32) {
+        const int qj = threadIdx.x;
         float M = lm[qj];
 #pragma unroll
         for (int w = 1; w < 4; w++) M = fmaxf(M, lm[w * 32 + qj]);
-        float L = 0.f, O = 0.f;
+        float wg[4], L = 0.f;
 #pragma unroll
         for (int w = 0; w < 4; w++) {
             const float mw = lm[w * 32 + qj];
-            const float wgt = mw == -INFINITY ? 0.f : expf(mw - M);
-            L += wgt * (ll[w * 64 + qj] + ll[w * 64 + 32 + qj]);
-            O += wgt * lo[(w * 32 + qj) * OS + d];
+            wg[w] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+            L += wg[w] * (ll[w * 64 + qj] + ll[w * 64 + 32 + qj]);
         }
-        out[(int64_t)(q0 + qj) * q_dim + (int64_t)h * HD + d] = O / L;
+#pragma unroll
+        for (int w = 0; w < 4; w++) lw[w * 32 + qj] = wg[w] / L;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < 32 * HD; e += 256) {
+        const int qj = e / HD, d = e - qj * HD;  // consecutive threads: consecutive dims of one row
+        if (q0 + qj >= rows) continue;
+        float O = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) O += lw[w * 32 + qj] * lo[(w * 32 + qj) * OS + d];
+        out[(int64_t)(q0 + qj) * q_dim + (int64_t)h * HD + d] = O;
     }
 }
 
@@ -450,7 +463,7 @@ template <int HD>
 static void launch_attn_prefill_mfma(float *out, const float *q, const float *kc, const float *vc, int rows, int pos0,
                                      int n_heads, int n_kv_heads)
 {
-    constexpr size_t lds = (size_t)(4 * 32 * (HD + 1) + 4 * 32 + 4 * 64) * sizeof(float);
+    constexpr size_t lds = (size_t)(4 * 32 * (HD + 1) + 4 * 32 + 4 * 64 + 4 * 32) * sizeof(float);
     static bool attr = false;
     if (!attr) {
         HOLO_CHECK(hipFuncSetAttribute((const void *)attn_prefill_mfma_k<HD>,
