@@ -1162,27 +1162,39 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
             return (uint32_t)sl * 65536u + (uint32_t)((((wave * 4 + 2 * mi + ni) * 4 + q) * 1024) + 16 * lane);
         };
         const int mine = 2 * w + (ct == cfirst ? 0 : 1);
-#pragma unroll
-        for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-            for (int ni = 0; ni < 2; ni++)
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const float4 v = {acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2],
-                                      acc[mi][ni][4 * q + 3]};
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), rp, (int)word(mine, mi, ni, q),
-                                                           0, kX2DevScope);
-                }
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores have completed (device scope)
-        __syncthreads();
         const int64_t it = (int64_t)ct * nst;
         const int jf = x2_owner(it, U, Gr), jl = x2_owner(it + nst - 1, U, Gr);
         const int nparts = jl - jf + 1;
-        if (tid == 0) {
-            const uint32_t old = __hip_atomic_fetch_add(a.cnt + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last = old == (uint32_t)(nparts - 1);
-        }
+        // every other range of the tile has already counted itself (at the
+        // end of a range the tile's other parts were usually computed first,
+        // at the start of the next ranges): this one is the last, and adds
+        // its own part from registers instead of storing and reloading it.
+        // Exactly one workgroup can see nparts - 1 before counting itself.
+        if (tid == 0)
+            last = nparts <= 4 &&
+                   __hip_atomic_load(a.cnt + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nparts - 1);
         __syncthreads();
+        const bool early = last;
+        if (!early) {
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 v = {acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2],
+                                          acc[mi][ni][4 * q + 3]};
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), rp,
+                                                               (int)word(mine, mi, ni, q), 0, kX2DevScope);
+                    }
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores have completed (device scope)
+            __syncthreads();
+            if (tid == 0) {
+                const uint32_t old = __hip_atomic_fetch_add(a.cnt + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                last = old == (uint32_t)(nparts - 1);
+            }
+            __syncthreads();
+        }
         store = last;
         if (store) {
             if (tid == 0) __hip_atomic_store(a.cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1200,22 +1212,29 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
                         for (int jj = 0; jj < 4; jj++) {
                             const int j = jf + jb + jj;
                             const int sl = 2 * (j * ntm + rt) + ((int)(x2_start(j, U, Gr) / nst) == ct ? 0 : 1);
+                            // early: this range's own part (j == ri) is in acc, not in its slot
+                            const bool ld = j <= jl && !(early && j == ri);
 #pragma unroll
                             for (int q = 0; q < 4; q++)
                                 wv[jj][q] = __builtin_bit_cast(
                                     v4u, __builtin_amdgcn_raw_buffer_load_b128(
-                                             rp, j <= jl ? (int)word(sl, mi, ni, q) : (int)kX2OutOfRange, 0,
-                                             kX2DevScope));
+                                             rp, ld ? (int)word(sl, mi, ni, q) : (int)kX2OutOfRange, 0, kX2DevScope));
                         }
 #pragma unroll
                         for (int q = 0; q < 4; q++)
 #pragma unroll
                             for (int e = 0; e < 4; e++) {
-                                const float p0 = __uint_as_float(wv[0][q][e]);
-                                float v = jb == 0 ? p0 : acc[mi][ni][4 * q + e] + p0;
+                                // the parts in range order (an early last's own part from
+                                // its accumulators: nparts <= 4, a single batch)
+                                const float own = acc[mi][ni][4 * q + e];
+                                auto part = [&](int jj) {
+                                    return early && jf + jb + jj == ri ? own : __uint_as_float(wv[jj][q][e]);
+                                };
+                                const float p0 = part(0);
+                                float v = jb == 0 ? p0 : own + p0;
 #pragma unroll
                                 for (int jj = 1; jj < 4; jj++)
-                                    if (jb + jj < nparts) v = v + __uint_as_float(wv[jj][q][e]);
+                                    if (jb + jj < nparts) v = v + part(jj);
                                 acc[mi][ni][4 * q + e] = v;
                             }
                     }
