@@ -290,8 +290,8 @@ void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const i
  * one holo_matmul GEMV per row.  The multi forms take up to 3 matrices
  * sharing X (with several, every N a multiple of 128); an output equals the
  * single call's bit for bit when neither launch shares a tile's K blocks
- * between workgroups (for Q4_0, Q8_0 and F16 that is when the K blocks per
- * row of tiles split evenly into whole tiles per workgroup), else it is
+ * between workgroups (for Q4_0, Q8_0, Q4_K and F16 that is when the K blocks
+ * per row of tiles split evenly into whole tiles per workgroup), else it is
  * within the product's error bound.  No reference counterpart (the
  * reference runs one GEMV per token,
  * llm.c:1049).                                                              */
@@ -299,9 +299,12 @@ void holo_matmul_batch(float *Y, const void *W, const float *X, int M, int N, in
 void holo_matmul_batch_multi(float *const *Y, const void *const *W, const int *N, int nmat, const float *X,
                              int M, int K, int type);
 /* The multi form with a type per matrix (q/k/v of a Q4_K_M file: Q4_K, Q4_K,
- * Q6_K): mixed types share one activation panel and one launch, every weight
- * matrix dequantised to its f16 panel (Q4_0 too, to the same f16 values its
- * own kernel unpacks); one type throughout is holo_matmul_batch_multi.      */
+ * Q6_K); one type throughout is holo_matmul_batch_multi.  In the exact
+ * product (the default) the matrices share one activation split and run one
+ * launch per weight type (Q4_K q and k together, Q6_K v on its own); in
+ * HOLO_PREFILL_F16 mode they share one activation panel and one launch,
+ * every weight matrix dequantised to its f16 panel (Q4_0 too, to the same
+ * f16 values its own kernel unpacks).                                       */
 void holo_matmul_batch_multi_types(float *const *Y, const void *const *W, const int *types, const int *N, int nmat,
                                    const float *X, int M, int K);
 void holo_matmul_batch_add(float *Y, const void *W, const float *X, const float *R, int M, int N, int K, int type);
