@@ -222,6 +222,37 @@ def test_exact_product_row_range(holo, synth, oracle, t):
         check_rows(T, H, w, np.array([r]), t, K)
 
 
+PART_CASES = [(Q4_0, 192, 11008, 2048), (Q8_0, 320, 6656, 2048), (Q4_K, 256, 8448, 2048),
+              (Q4_0, 512, 4096, 4096), (Q4_K, 512, 4096, 4096), (Q4_0, 320, 2112, 2048)]
+
+
+@pytest.mark.parametrize("t,M,N,K", PART_CASES, ids=[f"{NAMES[t]}-{m}x{n}x{k}" for t, m, n, k in PART_CASES])
+def test_exact_part_shapes(holo, synth, oracle, t, M, N, K):
+    """Shapes whose stages split tiles unevenly between workgroups: tiles in
+    four and in five parts (192x11008x2048, 320x6656x2048, 256x8448x2048, at
+    the launch's two workgroups per CU on 256 CUs), where the last workgroup
+    of a run either finds every other part counted (and adds them to its own
+    accumulators) or stores its part and counts; the 4096-wide o/v shape, whose
+    parts are mapped to XCDs; a last column tile 64 wide (2112).  Two calls
+    give the same bits, and the first and last row of every 32-row band are
+    within the bound of the float64 truth."""
+    print(f"case exact parts {NAMES[t]} {M}x{N}x{K}", flush=True)
+    lib = holo.lib()
+    src, w = weights(synth, oracle, t, N, K, seed=3 * M + N + K)
+    X = synth.normal(M * K, seed=K + 17).reshape(M, K)
+    dW, dX = up(holo, src), up(holo, X)
+    outs = []
+    for _ in range(2):
+        dY = holo.DeviceBuffer(4 * M * N)
+        lib.holo_matmul_batch(dY.ptr, dW.ptr, dX.ptr, M, N, K, t)
+        lib.cuda_sync()
+        holo.check("exact parts")
+        outs.append(down(dY, M * N).reshape(M, N))
+    assert np.all(np.isfinite(outs[0]))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    check_rows(outs[0], X, w, np.unique(np.r_[0:M:32, 31:M:32, M - 1]), t, K)
+
+
 @pytest.mark.parametrize("t,M,N,K", [(Q4_0, 512, 4096, 11008), (Q8_0, 200, 512, 8192), (F16, 100, 320, 4096)],
                          ids=["q4_0-512x4096x11008", "q8_0-200x512x8192", "f16-100x320x4096"])
 def test_exact_split_k_deterministic(holo, synth, oracle, t, M, N, K):
