@@ -108,7 +108,8 @@ def test_embedding_rows(holo, synth, oracle, t):
 
 
 @pytest.mark.parametrize("hd,nh,nkv,rows,pos0", [(32, 8, 4, 1, 0), (32, 8, 4, 80, 0), (128, 32, 8, 45, 17),
-                                                 (64, 4, 1, 100, 200), (128, 4, 4, 33, 0)])
+                                                 (64, 4, 1, 100, 200), (128, 4, 4, 33, 0),
+                                                 (128, 32, 32, 512, 0), (128, 32, 8, 512, 0), (128, 32, 32, 300, 100)])
 def test_attention_prefill(holo, synth, hd, nh, nkv, rows, pos0):
     print(f"case attention_prefill {hd} {nh} {nkv} {rows} {pos0}", flush=True)
     lib = holo.lib()
