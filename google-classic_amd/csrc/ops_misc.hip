@@ -212,8 +212,11 @@ __global__ __launch_bounds__(256) void mha_k(float *dst, const float *q, const f
 //     times the f16 instruction's cycles at head size 128, here 24.)
 // Workgroup g runs on XCD g mod 8 (round-robin dispatch): with the head count
 // a multiple of 8, XCD x takes heads x H/8 .. (x + 1) H/8 - 1, every query
-// block of each, heaviest (most keys) first, so the XCDs get equal work and
-// each reads its own heads' keys and values.
+// block of each, so the XCDs get equal work and each reads its own heads' keys
+// and values.  Within an XCD the first half of the query-block ranks go out
+// heaviest (most keys) first and the second half lightest first: the second
+// workgroup a CU receives then carries about as many key tiles as the first
+// is short of the heaviest.
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 af16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 af16x8 __attribute__((ext_vector_type(8)));
@@ -267,17 +270,21 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_mfma_k(float *out, const 
     float *lm = lo + 4 * 32 * OS;              // [4][32] running max per query
     float *ll = lm + 4 * 32;                   // [4][64] running sum per lane
     float *lw = ll + 4 * 64;                   // [4][32] merge weight of each wave per query
-    // (head, query block) of this workgroup, heaviest query blocks first
-    const int g = blockIdx.x;
-    int h, qb;
+    // (head, query block) of this workgroup. Query blocks go out by rank k:
+    // the first ceil(nqb/2) ranks heaviest first, the rest lightest first, so
+    // ranks k and k + ceil(nqb/2), which share CUs as the second workgroup
+    // per CU, sum to nqb - 1 blocks and the CUs' key-tile loads come out even
+    const int g = blockIdx.x, H = (nqb + 1) >> 1;
+    int h, k;
     if (n_heads % 8 == 0) {
         const int hx = n_heads >> 3, i = g >> 3;  // i: the workgroup's place on its XCD
         h = (g & 7) * hx + i % hx;
-        qb = nqb - 1 - i / hx;
+        k = i / hx;
     } else {
         h = g % n_heads;
-        qb = nqb - 1 - g / n_heads;
+        k = g / n_heads;
     }
+    const int qb = k < H ? nqb - 1 - k : k - H;
     const int q0 = qb * 32;
     const int lane = threadIdx.x & 63, j = lane & 31, hh = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // uniform: the tiles' resources stay scalar
