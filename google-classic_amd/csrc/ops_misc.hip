@@ -819,12 +819,42 @@ __global__ void rope_k(float *q, float *k, int pos, int hd, int n_heads, int n_k
     rope_head(q, k, pos, hd, n_heads, n_kv_heads, base, blockIdx.x, threadIdx.x);
 }
 
-// Row r of q [rows][n_heads*hd] and k [rows][n_kv_heads*hd] at position pos0 + r.
-__global__ void rope_rows_k(float *q, float *k, int pos0, int hd, int n_heads, int n_kv_heads, float base)
+// Row r = blockIdx.x of q [rows][n_heads*hd] and k [rows][n_kv_heads*hd] at
+// position pos0 + r.  The row's heads, q's then k's, go out in chunks of 4G
+// (blockIdx.y) to G groups of hd/2 threads: thread t takes pair index
+// i = t mod hd/2 of four heads, loads all four pairs before it stores any,
+// and computes the angle of (position, i) once for them.  Same expressions as
+// rope_head: the same bits.
+__global__ __launch_bounds__(1024) void rope_rows_k(float *__restrict__ q, float *__restrict__ k, int pos0, int hd,
+                                                    int n_heads, int n_kv_heads, float base)
 {
-    const int64_t r = blockIdx.y;
-    rope_head(q + r * n_heads * hd, k + r * n_kv_heads * hd, pos0 + (int)r, hd, n_heads, n_kv_heads, base,
-              blockIdx.x, threadIdx.x);
+    const int64_t r = blockIdx.x;
+    const int half = hd / 2, G = blockDim.x / half;
+    const int i = threadIdx.x % half, g = threadIdx.x / half;
+    if (g >= G) return;
+    const float freq = 1.0f / powf(base, (float)(2 * i) / (float)hd);
+    const float th = (float)(pos0 + (int)r) * freq;
+    const float c = cosf(th), s = sinf(th);
+    float *qr = q + r * n_heads * hd, *kr = k + r * n_kv_heads * hd;
+    const int h0 = (int)blockIdx.y * 4 * G + g;
+    float *p[4];
+    float a[4], b[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int h = h0 + u * G;
+        p[u] = h < n_heads ? qr + (int64_t)h * hd
+               : h < n_heads + n_kv_heads ? kr + (int64_t)(h - n_heads) * hd : nullptr;
+        if (p[u]) {
+            a[u] = p[u][i];
+            b[u] = p[u][i + half];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        if (p[u]) {
+            p[u][i] = a[u] * c - b[u] * s;
+            p[u][i + half] = a[u] * s + b[u] * c;
+        }
 }
 
 // ---- embedding lookups (cuda_ops.cu:2147-2300) ---------------------------------------------
@@ -1472,8 +1502,12 @@ void holo_rope_rows(float *q, float *k, int rows, int pos0, int head_dim, int n_
         HOLO_REJECT("holo_rope_rows: null pointer or head_dim > 2048");
         return;
     }
-    hipLaunchKernelGGL(rope_rows_k, dim3(h, rows), dim3(head_dim / 2), 0, stream(), q, k, pos0, head_dim, n_heads,
-                       n_kv_heads, freq_base);
+    // 256 threads (whole head groups of hd/2 pair indices), or one group when hd/2 > 256;
+    // four heads per group
+    const int half = head_dim / 2, threads = half <= 256 ? 256 / half * half : half;
+    const int per_wg = 4 * (threads / half);
+    hipLaunchKernelGGL(rope_rows_k, dim3(rows, (n_heads + n_kv_heads + per_wg - 1) / per_wg), dim3(threads), 0,
+                       stream(), q, k, pos0, head_dim, n_heads, n_kv_heads, freq_base);
     HOLO_LAUNCH_CHECK();
 }
 

@@ -60,12 +60,14 @@ def test_rms_norm_rows(holo, synth, n):
     holo.check("rms_norm_rows")
 
 
-# head size 96: its 48 pairs do not divide a 256-thread row workgroup (the per-head kernel)
-@pytest.mark.parametrize("hd,nh,nkv", [(32, 8, 4), (128, 32, 8), (64, 4, 4), (96, 6, 2)])
-def test_rope_rows(holo, synth, hd, nh, nkv):
-    print(f"case rope_rows {hd} {nh} {nkv}", flush=True)
+# head size 96: its 48 pairs fill 240 of a 256-thread row workgroup (five head
+# groups, the last pass partial); 32 heads of 128 at a late position (large angles)
+@pytest.mark.parametrize("hd,nh,nkv,pos0", [(32, 8, 4, 5), (128, 32, 8, 5), (64, 4, 4, 5), (96, 6, 2, 5),
+                                            (128, 32, 32, 4000)])
+def test_rope_rows(holo, synth, hd, nh, nkv, pos0):
+    print(f"case rope_rows {hd} {nh} {nkv} {pos0}", flush=True)
     lib = holo.lib()
-    rows, pos0 = 19, 5
+    rows = 19
     q = synth.normal(rows * nh * hd, seed=1)
     k = synth.normal(rows * nkv * hd, seed=2)
     dq, dk = up(holo, q), up(holo, k)
