@@ -51,8 +51,8 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef uint32_t v3u __attribute__((ext_vector_type(3)));
 
-// Weight source of one launch.
-enum ExactW { EW_Q4_0 = 0, EW_Q8_0 = 1, EW_Q4_K = 2, EW_P16 = 3, EW_F16 = 4, EW_Q6_K = 5 };
+// Weight source of one launch (EW_Q6R: Q6_K repacked for the second tiling).
+enum ExactW { EW_Q4_0 = 0, EW_Q8_0 = 1, EW_Q4_K = 2, EW_P16 = 3, EW_F16 = 4, EW_Q6_K = 5, EW_Q6R = 6 };
 
 constexpr int kExactMats = 3;
 
@@ -732,6 +732,71 @@ __global__ __launch_bounds__(256) void q6_k_int_panel_k(_Float16 *__restrict__ y
     }
 }
 
+// ---- Q6_K repacked for the second tiling: 64 bytes per row and 64-weight stage ----
+// Record (row n, stage t) holds blocks 2t and 2t + 1 of the row: sub-blocks
+// sub = 2(t mod 4) + s (s = 0, 1) of superblock t / 4, so the stage's two
+// sub-blocks share their half hf = (t mod 4) / 2, their nibble shift
+// 4 (t mod 2) and their qh bytes.  Lane half h of the product reads the two
+// 16-byte pieces at 16 h and 32 + 16 h:
+//   dword 4h + 2s + j  (j = 0, 1): byte u holds the low nibble of weight
+//                      8h + 4j + u of block s (its first k-step) in bits 0-3
+//                      and that of weight 16 + 8h + 4j + u (second k-step)
+//                      in bits 4-7 -- a Q4_0 qs word
+//   dword 8 + 4h + s:  bits 8u + 4j + 2e .. + 1 hold bits 4-5 of weight
+//                      16e + 8h + 4j + u of block s
+//   dword 8 + 4h + 2:  the four int8 group scales, block s group g in byte 2s + g
+//   dword 8 + 4h + 3:  d (f16 bits; the high half zero)
+// with q as dequantize_row_q6_k (quant.c:252-268) takes it:
+// q = ((ql[64hf + 32(j&1) + l] >> 4(j>>1)) & 15) | (((qh[32hf + l] >> 2j) & 3) << 4),
+// j = sub mod 4, scale sc[8hf + 2j + l/16].  The bytes are the superblock's own
+// bits rearranged: the product reads the same integers and scales.
+// One thread per record; superblock k's records are 4k .. 4k + 3.
+__global__ __launch_bounds__(256) void q6r_repack_k(uint4 *__restrict__ out, const uint8_t *__restrict__ W,
+                                                    int64_t nrec)
+{
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nrec) return;
+    const int64_t k = t >> 2;
+    const int q = (int)(t & 3), hf = q >> 1, j0 = 2 * (q & 1);
+    const uint8_t *sb = W + k * 210;
+    uint32_t l0[8], qh[8];  // ql[64hf .. 64hf + 31] (block 0), [.. + 63] (block 1); qh[32hf ..]
+    q6_run16(sb + 64 * hf, *(uint32_t(*)[4])&l0[0]);
+    q6_run16(sb + 64 * hf + 16, *(uint32_t(*)[4])&l0[4]);
+    q6_run16(sb + 128 + 32 * hf, *(uint32_t(*)[4])&qh[0]);
+    q6_run16(sb + 128 + 32 * hf + 16, *(uint32_t(*)[4])&qh[4]);
+    uint32_t l1[8];
+    q6_run16(sb + 64 * hf + 32, *(uint32_t(*)[4])&l1[0]);
+    q6_run16(sb + 64 * hf + 48, *(uint32_t(*)[4])&l1[4]);
+    const uint32_t shq = 4 * (uint32_t)(q & 1);  // nibble of both sub-blocks: j0 / 2
+    const uint16_t *s16 = (const uint16_t *)(sb + 192 + 8 * hf + 2 * j0);
+    const uint32_t sc4 = (uint32_t)s16[0] | ((uint32_t)s16[1] << 16);
+    const uint32_t d = *(const uint16_t *)(sb + 208);
+    uint32_t rec[16];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const uint32_t *ql = s ? l1 : l0;
+            const uint32_t shh = 2 * (uint32_t)(j0 + s);
+            uint32_t hb = 0;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                // dwords of weights 8h + 4j .. (first k-step) and 16 + 8h + 4j .. (second)
+                const uint32_t a = ql[2 * h + j], b = ql[4 + 2 * h + j];
+                rec[4 * h + 2 * s + j] = ((a >> shq) & 0x0F0F0F0Fu) | (((b >> shq) & 0x0F0F0F0Fu) << 4);
+                hb |= ((qh[2 * h + j] >> shh) & 0x03030303u) << (4 * j);
+                hb |= ((qh[4 + 2 * h + j] >> shh) & 0x03030303u) << (4 * j + 2);
+            }
+            rec[8 + 4 * h + s] = hb;
+        }
+        rec[8 + 4 * h + 2] = sc4;
+        rec[8 + 4 * h + 3] = d;
+    }
+    uint4 *o = out + t * 4;
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = make_uint4(rec[4 * i], rec[4 * i + 1], rec[4 * i + 2], rec[4 * i + 3]);
+}
+
 // ---- the second tiling: 64 x 256 workgroup tiles, weights straight into registers ----
 //
 // A workgroup takes 64 rows and 256 columns; wave w takes columns 64 w ..
@@ -742,10 +807,12 @@ __global__ __launch_bounds__(256) void q6_k_int_panel_k(_Float16 *__restrict__ y
 // (c, h) of a 32 x 32 tile holds B[k][c] for k = 8h .. 8h + 7 of each
 // 16-column step: Q4_0 / Q4_K the low nibbles of qs[8h .. 8h + 7] for the
 // first step and their high nibbles for the second, Q8_0 qs[8h ..] and
-// qs[16 + 8h ..], F16 the row's own values), so the weights take no LDS
-// traffic and no barrier.  The arithmetic is the first tiling's: per 32-block
-// four MFMAs give C = sum_k (xh + xl) * w, folded in block order by
-// acc = fmaf(scale, C, acc) (Q4_K: then acc = fmaf(-dmin*m, sum x, acc)).
+// qs[16 + 8h ..], repacked Q6_K the same nibbles with their high bits beside
+// them, F16 the row's own values), so the weights take no LDS traffic and no
+// barrier.  The arithmetic is the first tiling's: per 32-block four MFMAs
+// give C = sum_k (xh + xl) * w, folded in block order by
+// acc = fmaf(scale, C, acc) (Q4_K: then acc = fmaf(-dmin*m, sum x, acc);
+// Q6_K: a C and an fmaf per 16-k step, with its group's scale).
 //
 // Work is dealt by stages, not by tiles (a "stream-K" split), one row of
 // tiles at a time: in row tile r, column tile c's stage s is item c * nst + s
@@ -843,6 +910,12 @@ template <>
 struct X2Raw<EW_F16> {
     v4u s0, s1;        // k = 8h .. 8h+7 and 16 + 8h .. 16 + 8h + 7
 };
+// Q6_K repacked (q6r_repack_k): a stage's record pieces of lane half h,
+// the nibble words at 16h and {high bits of both blocks, scales, d} at 32 + 16h.
+template <>
+struct X2Raw<EW_Q6R> {
+    v4u n, m;
+};
 
 // Block b of the lane's row (vo: the row's byte offset within the matrix,
 // plus 8 h for the block formats, 16 h for F16).  P = b & 1 (block formats).
@@ -857,6 +930,11 @@ __device__ __forceinline__ X2Raw<WF> x2_fetch(__amdgpu_buffer_rsrc_t r, uint32_t
         const int so = 34 * b - 2 * P;
         x.w = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, so, 0));
         x.v = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, so + 16, 0));
+    } else if constexpr (WF == EW_Q6R) {
+        // b even: the stage's record; vo the row's records + 16 h
+        const int so = 32 * b;
+        x.n = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, so, 0));
+        x.m = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, so + 32, 0));
     } else if constexpr (WF == EW_Q4_K) {
         // b even: the stage's first sub-block; vd the row, vo the row + 16 h
         const int sb = 144 * (b >> 3), qo = sb + 16 + 16 * (b & 7);
@@ -887,6 +965,32 @@ __device__ __forceinline__ void x2_unpack_q4_k(const X2Raw<EW_Q4_K> &x, int e, u
     const uint32_t dd = x.hd.x & (0u - (uint32_t)live);
     dsc = half_bits_to_float(dd) * (float)sc;
     dmn = half_bits_to_float(dd >> 16) * (float)mn;
+}
+
+// Block s (0, 1) of the Q6_K stage held in x: both 16-k steps' B operands
+// (q - 32, exact in f16) and their group scales d * sc (exact in fp32:
+// 11-bit times 8-bit, as the first tiling forms them), zero past the part.
+__device__ __forceinline__ void x2_unpack_q6r(const X2Raw<EW_Q6R> &x, int s, bool live, v8h &b0, v8h &b1,
+                                              float &sc0, float &sc1)
+{
+    const uint32_t hb = s ? x.m.y : x.m.x;
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t w = x.n[2 * s + j], hj = hb >> (4 * j);
+        const uint32_t t0 = (w & 0x0F0F0F0Fu) | ((hj & 0x03030303u) << 4);
+        const uint32_t t1 = ((w >> 4) & 0x0F0F0F0Fu) | (((hj >> 2) & 0x03030303u) << 4);
+        lo[2 * j] = f16_pair(t0, 0x04010400u, (_Float16)-1056.0f);  // 1024 + q - 1056 = q - 32
+        lo[2 * j + 1] = f16_pair(t0, 0x04030402u, (_Float16)-1056.0f);
+        hi[2 * j] = f16_pair(t1, 0x04010400u, (_Float16)-1056.0f);
+        hi[2 * j + 1] = f16_pair(t1, 0x04030402u, (_Float16)-1056.0f);
+    }
+    b0 = __builtin_bit_cast(v8h, v4u{lo[0], lo[1], lo[2], lo[3]});
+    b1 = __builtin_bit_cast(v8h, v4u{hi[0], hi[1], hi[2], hi[3]});
+    const float d = half_bits_to_float(x.m.w & (0u - (uint32_t)live));
+    const uint32_t sc = x.m.z >> (16 * s);
+    sc0 = d * (float)(int8_t)(sc & 0xFFu);
+    sc1 = d * (float)(int8_t)((sc >> 8) & 0xFFu);
 }
 
 // The B operands of both 16-k steps and the block's scale; live: the block
@@ -983,16 +1087,20 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
     const int nbase = sel == 2 ? a.n_end[1] : sel == 1 ? a.n_end[0] : 0;
     const int Nm = (sel == 2 ? a.n_end[2] : sel == 1 ? a.n_end[1] : a.n_end[0]) - nbase;
     const int nl = nc - nbase;  // the wave's first column in its matrix (clamped)
-    // bytes of a row: 18 / 34 per Q4_0 / Q8_0 block, 144 per 8 Q4_K sub-blocks, 64 per F16 block
+    // bytes of a row: 18 / 34 per Q4_0 / Q8_0 block, 144 per 8 Q4_K sub-blocks, 64 per F16 block,
+    // 64 per repacked Q6_K stage
     const uint32_t rowb = WF == EW_Q4_K ? (uint32_t)(nb >> 3) * 144u
-                                        : (uint32_t)nb * (WF == EW_Q4_0 ? 18u : WF == EW_Q8_0 ? 34u : 64u);
+                                        : (uint32_t)nb * (WF == EW_Q4_0   ? 18u
+                                                          : WF == EW_Q8_0 ? 34u
+                                                          : WF == EW_Q6R  ? 32u
+                                                                          : 64u);
     const __amdgpu_buffer_rsrc_t rw =
         __builtin_amdgcn_make_buffer_rsrc((void *)Wm, (short)0, (int)((uint32_t)Nm * rowb), kXBufWord3);
     uint32_t vo[2], vd[2];
 #pragma unroll
     for (int ni = 0; ni < 2; ni++) {
         vd[ni] = (uint32_t)min(nl + 32 * ni + c32, Nm - 1) * rowb;
-        vo[ni] = vd[ni] + (WF == EW_F16 ? 16u : 8u) * (uint32_t)h;
+        vo[ni] = vd[ni] + (WF == EW_F16 || WF == EW_Q6R ? 16u : 8u) * (uint32_t)h;
     }
 
     // activation staging: thread tid moves piece tid + 256 i of each half,
@@ -1054,10 +1162,11 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
     auto wblk = [&](int b) { return WF == EW_F16 ? min(b, kb1 - 1) : b; };
     const int nsg = (kb1 - kb0 + S - 1) / S;  // stages of this pass
     // the weight words of a stage's S blocks, fetched one stage ahead
-    // (Q4_K: one slot per stage, ring[0])
+    // (Q4_K, Q6R: one slot per stage, ring[0])
+    constexpr bool kStageSlot = WF == EW_Q4_K || WF == EW_Q6R;
     X2Raw<WF> ring[S][2];
 #pragma unroll
-    for (int s = 0; s < (WF == EW_Q4_K ? 1 : S); s++)
+    for (int s = 0; s < (kStageSlot ? 1 : S); s++)
 #pragma unroll
         for (int ni = 0; ni < 2; ni++) {
             if (s & 1) ring[s][ni] = x2_fetch<WF, 1>(rw, vo[ni], vd[ni], wblk(kb0 + s));
@@ -1082,8 +1191,15 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
             const int b = kb0 + st * S + s;
             // this block's weight operands, then its ring slot fetches block b + S
             v8h b0[2], b1[2];
-            float sc[2];
-            if constexpr (WF == EW_Q4_K) {
+            float sc[2], sc1[2];
+            if constexpr (WF == EW_Q6R) {
+                // block s of the stage's record in ring[0]: a scale per 16-k step
+#pragma unroll
+                for (int ni = 0; ni < 2; ni++) {
+                    x2_unpack_q6r(ring[0][ni], s, b < kb1, b0[ni], b1[ni], sc[ni], sc1[ni]);
+                    if (s == S - 1) ring[0][ni] = x2_fetch<WF, 0>(rw, vo[ni], vd[ni], b + 1);
+                }
+            } else if constexpr (WF == EW_Q4_K) {
                 // sub-block b of the stage in ring[0]; its min term goes to
                 // the stage's fp32 MFMA below (lane h: sub-block b - s + h)
 #pragma unroll
@@ -1120,6 +1236,15 @@ __global__ __launch_bounds__(256, 2) void gemm_exact2_k(X2Args a)
                             acc[mi][ni] = mfma16(al0, b0[ni], acc[mi][ni]);
                             acc[mi][ni] = mfma16(al1, b1[ni], acc[mi][ni]);
                         }
+                    } else if constexpr (WF == EW_Q6R) {
+                        // the first tiling's Q6_K order: each 16-k step's C, then its group scale
+                        const v16f zero = {};
+                        v16f c = mfma16(al0, b0[ni], mfma16(ah0, b0[ni], zero));
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[mi][ni][r] = __builtin_fmaf(sc[ni], c[r], acc[mi][ni][r]);
+                        c = mfma16(al1, b1[ni], mfma16(ah1, b1[ni], zero));
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[mi][ni][r] = __builtin_fmaf(sc1[ni], c[r], acc[mi][ni][r]);
                     } else {
                         const v16f zero = {};
                         v16f c = mfma16(ah0, b0[ni], zero);
@@ -1435,7 +1560,7 @@ int exact_kind(int type)
     case HOLO_TYPE_Q4_0: return EW_Q4_0;
     case HOLO_TYPE_Q8_0: return EW_Q8_0;
     case HOLO_TYPE_Q4_K: return EW_Q4_K;
-    case HOLO_TYPE_Q6_K: return q6_panel() ? EW_P16 : EW_Q6_K;
+    case HOLO_TYPE_Q6_K: return q6_panel() ? EW_P16 : exact_v1() ? EW_Q6_K : EW_Q6R;
     case HOLO_TYPE_F16: return EW_F16;
     default: return -1;
     }
@@ -1499,9 +1624,16 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
     float *Rs = (float *)((uint8_t *)aws + 2 * half + sxb);
     bool need_sx = false;
     size_t pbytes = 0;
+    // each matrix's launch kind: Q6_K repacked for the second tiling unless
+    // a mode asks for another form or the repacked matrix (N*K bytes) would
+    // pass the 32-bit offsets
+    int kinds[kExactMats];
     for (int i = 0; i < nmat; i++) {
         need_sx = need_sx || types[i] == HOLO_TYPE_Q4_K;
-        if (types[i] == HOLO_TYPE_Q6_K && q6_panel()) pbytes += (size_t)N[i] * K * 2 + (size_t)N[i] * (K / 16) * 4;
+        kinds[i] = exact_kind(types[i]);
+        if (kinds[i] == EW_Q6R && (int64_t)N[i] * K >= (1LL << 31)) kinds[i] = EW_Q6_K;
+        if (kinds[i] == EW_P16) pbytes += (size_t)N[i] * K * 2 + (size_t)N[i] * (K / 16) * 4;
+        if (kinds[i] == EW_Q6R) pbytes += ((size_t)N[i] * K + 255) & ~(size_t)255;
     }
     // one workgroup per row, K <= 16384 (exact_ok): the row in registers
     auto split = [&](auto kern) {
@@ -1513,7 +1645,7 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
     else if (U) small ? split(xsplit_row_k<4, XS_SWIGLU>) : split(xsplit_row_k<16, XS_SWIGLU>);
     else small ? split(xsplit_row_k<4, XS_PLAIN>) : split(xsplit_row_k<16, XS_PLAIN>);
     HOLO_LAUNCH_CHECK();
-    // Q6_K matrices: their integer panels and group scales
+    // Q6_K matrices: repacked, or their integer panels and group scales
     void *pws = nullptr;
     bool own_p = false;
     const void *PW[kExactMats] = {nullptr, nullptr, nullptr};
@@ -1525,7 +1657,17 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
         if (!pws) return;
         size_t off = 0;
         for (int i = 0; i < nmat; i++) {
-            if (types[i] != HOLO_TYPE_Q6_K || !q6_panel()) continue;
+            if (kinds[i] == EW_Q6R) {
+                uint4 *p = (uint4 *)((uint8_t *)pws + off);
+                off += ((size_t)N[i] * K + 255) & ~(size_t)255;
+                const int64_t nrec = (int64_t)N[i] * (K / 256) * 4;
+                hipLaunchKernelGGL(q6r_repack_k, dim3((unsigned)((nrec + 255) / 256)), dim3(256), 0, stream(), p,
+                                   (const uint8_t *)W[i], nrec);
+                HOLO_LAUNCH_CHECK();
+                PW[i] = p;
+                continue;
+            }
+            if (kinds[i] != EW_P16) continue;
             _Float16 *p = (_Float16 *)((uint8_t *)pws + off);
             off += (size_t)N[i] * K * 2;
             float *ps = (float *)((uint8_t *)pws + off);
@@ -1542,14 +1684,16 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
     bool done[kExactMats] = {false, false, false};
     for (int i = 0; i < nmat; i++) {
         if (done[i]) continue;
-        const int kind = exact_kind(types[i]);
+        const int kind = kinds[i];
         ExactArgs a = {};
         int cnt = 0, acc = 0;
+        const void *raw[kExactMats] = {W[i], W[i], W[i]};  // the matrices as given (EW_Q6R's fallback)
         for (int j = i; j < nmat; j++) {
-            if (done[j] || exact_kind(types[j]) != kind) continue;
+            if (done[j] || kinds[j] != kind) continue;
             done[j] = true;
             acc += N[j];
             a.Y[cnt] = Y[j];
+            raw[cnt] = W[j];
             a.W[cnt] = (const uint8_t *)(PW[j] ? PW[j] : W[j]);
             a.WS[cnt] = PS[j];
             a.n_end[cnt] = acc;
@@ -1570,16 +1714,17 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
         a.nb = nb;
         a.R = (nmat == 1) ? R : nullptr;
         // the second tiling: Q4_0 and Q8_0 rows of an even block count (every
-        // row 4-byte aligned) and F16 rows; with several matrices every N but
-        // the last a multiple of 64 (a wave's 64 columns in one matrix); each
-        // matrix under 2 GiB (32-bit offsets)
-        bool x2 = !exact_v1() &&
-                  (((kind == EW_Q4_0 || kind == EW_Q8_0) && nb % 2 == 0) || kind == EW_F16 || kind == EW_Q4_K);
+        // row 4-byte aligned), Q4_K, repacked Q6_K and F16 rows; with several
+        // matrices every N but the last a multiple of 64 (a wave's 64 columns
+        // in one matrix); each matrix under 2 GiB (32-bit offsets)
+        bool x2 = !exact_v1() && (((kind == EW_Q4_0 || kind == EW_Q8_0) && nb % 2 == 0) || kind == EW_F16 ||
+                                  kind == EW_Q4_K || kind == EW_Q6R);
         for (int j = 0; j < cnt - 1 && x2; j++) x2 = a.n_end[j] % 64 == 0;
         for (int j = 0; j < cnt && x2; j++) {
             const int64_t rows = a.n_end[j] - (j ? a.n_end[j - 1] : 0);
-            // bytes per 32-weight block: Q4_0 18, Q4_K 144 / 8, Q8_0 34, F16 64
-            x2 = rows * (int64_t)nb * (kind == EW_Q4_0 || kind == EW_Q4_K ? 18 : kind == EW_Q8_0 ? 34 : 64) <
+            // bytes per 32-weight block: Q4_0 18, Q4_K 144 / 8, repacked Q6_K 32, Q8_0 34, F16 64
+            x2 = rows * (int64_t)nb *
+                     (kind == EW_Q4_0 || kind == EW_Q4_K ? 18 : kind == EW_Q6R ? 32 : kind == EW_Q8_0 ? 34 : 64) <
                  (1LL << 31);
         }
         if (x2) {
@@ -1601,8 +1746,15 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
             case EW_Q4_0: launch_exact2<EW_Q4_0, 2>(b); break;
             case EW_Q8_0: launch_exact2<EW_Q8_0, 2>(b); break;
             case EW_Q4_K: launch_exact2<EW_Q4_K, 2>(b); break;
+            case EW_Q6R: launch_exact2<EW_Q6R, 2>(b); break;
             default: launch_exact2<EW_F16, 2>(b); break;
             }
+            continue;
+        }
+        if (kind == EW_Q6R) {
+            // no second tiling for this group: the first, on the matrices as given
+            for (int j = 0; j < kExactMats; j++) a.W[j] = (const uint8_t *)raw[j < cnt ? j : 0];
+            launch_exact_for<EW_Q6_K>(a);
             continue;
         }
         switch (kind) {

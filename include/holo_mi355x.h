@@ -290,8 +290,9 @@ void holo_matmul_batch_q4_0_multi(float *const *Y, const void *const *W, const i
  * one holo_matmul GEMV per row.  The multi forms take up to 3 matrices
  * sharing X (with several, every N a multiple of 128); an output equals the
  * single call's bit for bit when neither launch shares a tile's K blocks
- * between workgroups (for Q4_0, Q8_0, Q4_K and F16 that is when the K blocks
- * per row of tiles split evenly into whole tiles per workgroup), else it is
+ * between workgroups (for Q4_0, Q8_0, Q4_K, Q6_K and F16 that is when the K
+ * blocks per row of tiles split evenly into whole tiles per workgroup; Q6_K
+ * matrices are first repacked into the workspace), else it is
  * within the product's error bound.  No reference counterpart (the
  * reference runs one GEMV per token,
  * llm.c:1049).                                                              */

@@ -223,7 +223,8 @@ def test_exact_product_row_range(holo, synth, oracle, t):
 
 
 PART_CASES = [(Q4_0, 192, 11008, 2048), (Q8_0, 320, 6656, 2048), (Q4_K, 256, 8448, 2048),
-              (Q4_0, 512, 4096, 4096), (Q4_K, 512, 4096, 4096), (Q4_0, 320, 2112, 2048)]
+              (Q4_0, 512, 4096, 4096), (Q4_K, 512, 4096, 4096), (Q4_0, 320, 2112, 2048),
+              (Q6_K, 256, 8448, 2048), (Q6_K, 512, 4096, 4096)]
 
 
 @pytest.mark.parametrize("t,M,N,K", PART_CASES, ids=[f"{NAMES[t]}-{m}x{n}x{k}" for t, m, n, k in PART_CASES])
@@ -253,8 +254,9 @@ def test_exact_part_shapes(holo, synth, oracle, t, M, N, K):
     check_rows(outs[0], X, w, np.unique(np.r_[0:M:32, 31:M:32, M - 1]), t, K)
 
 
-@pytest.mark.parametrize("t,M,N,K", [(Q4_0, 512, 4096, 11008), (Q8_0, 200, 512, 8192), (F16, 100, 320, 4096)],
-                         ids=["q4_0-512x4096x11008", "q8_0-200x512x8192", "f16-100x320x4096"])
+@pytest.mark.parametrize("t,M,N,K", [(Q4_0, 512, 4096, 11008), (Q8_0, 200, 512, 8192), (F16, 100, 320, 4096),
+                                     (Q6_K, 512, 4096, 11008)],
+                         ids=["q4_0-512x4096x11008", "q8_0-200x512x8192", "f16-100x320x4096", "q6_k-512x4096x11008"])
 def test_exact_split_k_deterministic(holo, synth, oracle, t, M, N, K):
     """Few column tiles and a long K take the K-split form (parts summed in
     part order by the last part to arrive, counted on per-tile counters that
