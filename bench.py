@@ -399,9 +399,12 @@ class MixedLayer:
 def prompt_forward_q4_k_m(lib, n_tokens=512):
     """The 512-token prompt of prompt_forward on a Q4_K_M-style Llama-2-7B:
     Q4_K embeddings, q/k/o/gate/up; Q6_K v, down and output head.  Every
-    matrix takes the batched product over an f16 panel dequantised first
-    (holo_matmul_batch); before that path, every non-Q4_0 matrix of a prompt
-    ran one GEMV per token."""
+    matrix takes the exact batched product (holo_matmul_batch's default);
+    its Q6_K matrices are read through a repacked layout, built per call
+    (prompt_ms_q6_k_repacked_per_call) or once by holo_llama_prepare before
+    the timed prompts (prompt_ms, the load-time form; 1 byte per weight of
+    the Q6_K layer matrices, q6_k_prepared_bytes).  Before the batched path,
+    every non-Q4_0 matrix of a prompt ran one GEMV per token."""
     layers = [MixedLayer(i) for i in range(32)]
     emb = holo.DeviceBuffer.from_array(synth.blocks(Q4_K, VOCAB, DIM, synth.tensor_seed(BASE_SEED, 7, 32, 0)))
     head = holo.DeviceBuffer.from_array(synth.blocks(Q6_K, VOCAB, DIM, synth.tensor_seed(BASE_SEED, 7, 32, 1)))
@@ -427,20 +430,34 @@ def prompt_forward_q4_k_m(lib, n_tokens=512):
         if rc != 0:
             raise holo.HoloError(f"holo_llama_forward returned {rc}")
 
-    run()
-    lib.cuda_sync()
-    ev = holo.Events()
-    times = []
-    for _ in range(5):  # each prompt timed alone; the median is reported (single prompts vary by up to 20%)
-        ev.start()
+    def timed():
         run()
-        times.append(ev.stop())
-    ev.close()
-    holo.check("prompt forward q4_k_m")
+        lib.cuda_sync()
+        ev = holo.Events()
+        times = []
+        for _ in range(5):  # each prompt timed alone; the median is reported (single prompts vary by up to 20%)
+            ev.start()
+            run()
+            times.append(ev.stop())
+        ev.close()
+        holo.check("prompt forward q4_k_m")
+        return times
+
+    per_call = timed()
+    rc = lib.holo_llama_prepare(C.byref(m))
+    if rc != 0:
+        raise holo.HoloError(f"holo_llama_prepare returned {rc}")
+    try:
+        times = timed()
+    finally:
+        lib.holo_llama_release(C.byref(m))
     ms = statistics.median(times)
+    q6_bytes = 32 * sum(o * i for name, o, i in LAYER if T[name] == Q6_K)
     return {"prompt_tokens": n_tokens, "prompt_ms": round(ms, 2),
             "prompt_ms_min_max": [round(min(times), 2), round(max(times), 2)],
             "prompt_tokens_per_s": round(n_tokens / (ms * 1e-3), 1),
+            "prompt_ms_q6_k_repacked_per_call": round(statistics.median(per_call), 2),
+            "q6_k_prepared_bytes": q6_bytes,
             "types": "Q4_K q/k/o/gate/up and embeddings; Q6_K v, down and head"}
 
 

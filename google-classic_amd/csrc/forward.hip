@@ -286,6 +286,56 @@ int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0
     return 0;
 }
 
+// Every layer matrix of m with its shape [out][in]: q, k, v, o, gate, down, up.
+static void layer_mats(const holo_llama_t *m, int l, const void *W[7], int T[7], int O[7], int I[7])
+{
+    const holo_llama_layer_t &L = m->layers[l];
+    const int q_dim = m->n_heads * m->head_dim, kv_dim = m->n_kv_heads * m->head_dim, d = m->dim, f = m->ffn_dim;
+    const void *w[7] = {L.wq, L.wk, L.wv, L.wo, L.w1, L.w2, L.w3};
+    const int t[7] = {L.wq_type, L.wk_type, L.wv_type, L.wo_type, L.w1_type, L.w2_type, L.w3_type};
+    const int o[7] = {q_dim, kv_dim, kv_dim, d, f, d, f}, in[7] = {d, d, d, q_dim, d, f, d};
+    for (int i = 0; i < 7; i++) {
+        W[i] = w[i];
+        T[i] = t[i];
+        O[i] = o[i];
+        I[i] = in[i];
+    }
+}
+
+int holo_llama_prepare(const holo_llama_t *m)
+{
+    if (!m || !m->layers || m->n_layers <= 0) {
+        HOLO_REJECT("holo_llama_prepare: null model");
+        return HOLO_EINVAL;
+    }
+    for (int l = 0; l < m->n_layers; l++) {
+        const void *W[7];
+        int T[7], O[7], I[7];
+        layer_mats(m, l, W, T, O, I);
+        for (int i = 0; i < 7; i++) {
+            if (T[i] != HOLO_TYPE_Q6_K || !W[i] || I[i] % 256 != 0 || I[i] > 16384) continue;
+            const int rc = holo_prefill_prepare(W[i], O[i], I[i], T[i]);
+            if (rc != 0) {
+                holo_llama_release(m);
+                return rc;
+            }
+        }
+    }
+    return 0;
+}
+
+void holo_llama_release(const holo_llama_t *m)
+{
+    if (!m || !m->layers) return;
+    for (int l = 0; l < m->n_layers; l++) {
+        const void *W[7];
+        int T[7], O[7], I[7];
+        layer_mats(m, l, W, T, O, I);
+        for (int i = 0; i < 7; i++)
+            if (T[i] == HOLO_TYPE_Q6_K && W[i]) holo_prefill_release(W[i]);
+    }
+}
+
 // This forward is the plain Llama body.  The reference also runs Gemma
 // (embedding scale, post-norms, a 1M RoPE base on global layers) and Qwen
 // (q/k/v biases, QK-norm) variants (llm.c:451-475, 480-485, 516-521,

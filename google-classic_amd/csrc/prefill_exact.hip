@@ -36,6 +36,8 @@
 #include <hip/hip_ext.h>
 #include <algorithm>
 #include <limits.h>
+#include <mutex>
+#include <unordered_map>
 
 #include <type_traits>
 
@@ -1608,6 +1610,34 @@ bool exact_ok(int type, int K, const void *W)
 // nmat matrices sharing the activations; every type must pass exact_ok, and
 // with several matrices of one type every N[i] must be a multiple of 128.
 // Matrices of one type share a launch; the activation halves are built once.
+// ---- Q6_K matrices repacked once (holo_prefill_prepare) ----
+// The repacked copy of each registered matrix, keyed by its device address;
+// the caller keeps the matrix unchanged until it releases it.
+namespace {
+struct PreparedQ6 {
+    int N, K;
+    void *rec;
+};
+std::mutex g_prep_mu;
+std::unordered_map<const void *, PreparedQ6> g_prep;
+
+const void *prepared_q6r(const void *W, int N, int K)
+{
+    std::lock_guard<std::mutex> lk(g_prep_mu);
+    const auto it = g_prep.find(W);
+    return it != g_prep.end() && it->second.N == N && it->second.K == K ? it->second.rec : nullptr;
+}
+
+// W [N][K] Q6_K (K a multiple of 256, W 2-byte aligned) into records [N][K/64][64 B] at out
+void q6r_repack(void *out, const void *W, int N, int K)
+{
+    const int64_t nrec = (int64_t)N * (K / 256) * 4;
+    hipLaunchKernelGGL(q6r_repack_k, dim3((unsigned)((nrec + 255) / 256)), dim3(256), 0, stream(), (uint4 *)out,
+                       (const uint8_t *)W, nrec);
+    HOLO_LAUNCH_CHECK();
+}
+}  // namespace
+
 void exact_product(float *const *Y, const void *const *W, const int *types, const int *N, int nmat, const float *X,
                    const float *U, const float *R, int M, int K, const float *NW, float eps)
 {
@@ -1628,12 +1658,17 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
     // a mode asks for another form or the repacked matrix (N*K bytes) would
     // pass the 32-bit offsets
     int kinds[kExactMats];
+    const void *PW[kExactMats] = {nullptr, nullptr, nullptr};
+    const float *PS[kExactMats] = {nullptr, nullptr, nullptr};
     for (int i = 0; i < nmat; i++) {
         need_sx = need_sx || types[i] == HOLO_TYPE_Q4_K;
         kinds[i] = exact_kind(types[i]);
         if (kinds[i] == EW_Q6R && (int64_t)N[i] * K >= (1LL << 31)) kinds[i] = EW_Q6_K;
         if (kinds[i] == EW_P16) pbytes += (size_t)N[i] * K * 2 + (size_t)N[i] * (K / 16) * 4;
-        if (kinds[i] == EW_Q6R) pbytes += ((size_t)N[i] * K + 255) & ~(size_t)255;
+        if (kinds[i] == EW_Q6R) {
+            PW[i] = prepared_q6r(W[i], N[i], K);  // repacked once by the caller's request
+            if (!PW[i]) pbytes += ((size_t)N[i] * K + 255) & ~(size_t)255;
+        }
     }
     // one workgroup per row, K <= 16384 (exact_ok): the row in registers
     auto split = [&](auto kern) {
@@ -1648,8 +1683,6 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
     // Q6_K matrices: repacked, or their integer panels and group scales
     void *pws = nullptr;
     bool own_p = false;
-    const void *PW[kExactMats] = {nullptr, nullptr, nullptr};
-    const float *PS[kExactMats] = {nullptr, nullptr, nullptr};
     if (pbytes) {
         pws = workspace(0, pbytes);
         own_p = pws == nullptr;
@@ -1658,12 +1691,10 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
         size_t off = 0;
         for (int i = 0; i < nmat; i++) {
             if (kinds[i] == EW_Q6R) {
-                uint4 *p = (uint4 *)((uint8_t *)pws + off);
+                if (PW[i]) continue;  // prepared
+                void *p = (uint8_t *)pws + off;
                 off += ((size_t)N[i] * K + 255) & ~(size_t)255;
-                const int64_t nrec = (int64_t)N[i] * (K / 256) * 4;
-                hipLaunchKernelGGL(q6r_repack_k, dim3((unsigned)((nrec + 255) / 256)), dim3(256), 0, stream(), p,
-                                   (const uint8_t *)W[i], nrec);
-                HOLO_LAUNCH_CHECK();
+                q6r_repack(p, W[i], N[i], K);
                 PW[i] = p;
                 continue;
             }
@@ -1771,3 +1802,61 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
 }
 
 }  // namespace holo
+
+extern "C" {
+
+int holo_prefill_prepare(const void *W, int N, int K, int type)
+{
+    if (!W || N <= 0 || type != HOLO_TYPE_Q6_K || K <= 0 || K % 256 != 0 || K > 16384 || ((uintptr_t)W & 1u) ||
+        (int64_t)N * K >= (1LL << 31)) {
+        HOLO_REJECT("holo_prefill_prepare: not a Q6_K matrix the exact product repacks (K a multiple of 256 up "
+                    "to 16384, 2-byte aligned, N*K under 2^31)");
+        return HOLO_EINVAL;
+    }
+    if (holo::stream_capturing()) {
+        HOLO_REJECT("holo_prefill_prepare: called under graph capture");
+        return HOLO_EINVAL;
+    }
+    {
+        std::lock_guard<std::mutex> lk(holo::g_prep_mu);
+        const auto it = holo::g_prep.find(W);
+        if (it != holo::g_prep.end()) {
+            if (it->second.N == N && it->second.K == K) return 0;
+            HOLO_REJECT("holo_prefill_prepare: W is registered with another shape");
+            return HOLO_EINVAL;
+        }
+    }
+    void *rec = nullptr;
+    const hipError_t e = hipMalloc(&rec, (size_t)N * K);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        HOLO_CHECK(e);
+        return (int)e;
+    }
+    holo::q6r_repack(rec, W, N, K);
+    const hipError_t es = hipStreamSynchronize(holo::stream());
+    if (es != hipSuccess) {
+        HOLO_CHECK(es);
+        (void)hipFree(rec);
+        return (int)es;
+    }
+    std::lock_guard<std::mutex> lk(holo::g_prep_mu);
+    holo::g_prep[W] = holo::PreparedQ6{N, K, rec};
+    return 0;
+}
+
+void holo_prefill_release(const void *W)
+{
+    void *rec = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(holo::g_prep_mu);
+        const auto it = holo::g_prep.find(W);
+        if (it == holo::g_prep.end()) return;
+        rec = it->second.rec;
+        holo::g_prep.erase(it);
+    }
+    HOLO_CHECK(hipStreamSynchronize(holo::stream()));  // no product in flight still reads it
+    HOLO_CHECK(hipFree(rec));
+}
+
+}  // extern "C"

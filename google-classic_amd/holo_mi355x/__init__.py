@@ -158,6 +158,8 @@ _SIGS = {
     "holo_matmul_batch_multi_types": (None, [_P, _P, _P, _P, _I, _P, _I, _I]),
     "holo_matmul_batch_add": (None, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "holo_matmul_batch_swiglu_add": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
+    "holo_prefill_prepare": (_I, [_P, _I, _I, _I]),
+    "holo_prefill_release": (None, [_P]),
     # GGUF files (include/holo_gguf.h)
     "holo_gguf_open": (_P, [C.c_char_p]),
     "holo_gguf_close": (None, [_P]),
@@ -186,6 +188,8 @@ _SIGS = {
     "holo_attention_prefill": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I]),
     "holo_matmul_rows": (None, [_P, _P, _P, _I, _I, _I, _I, _I]),
     "holo_llama_forward": (_I, [_P, _P, _I, _I, _P, _I]),
+    "holo_llama_prepare": (_I, [_P]),
+    "holo_llama_release": (None, [_P]),
     "holo_llama_from_gguf": (_I, [_P, _P, _P, _I]),
     "holo_llama_gguf_check": (_I, [_P]),
 }

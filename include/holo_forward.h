@@ -90,6 +90,15 @@ typedef struct {
  * supported set (nothing launched).  Scratch is stream-ordered.               */
 int holo_llama_forward(const holo_llama_t *m, const int *tokens, int n, int pos0, float *logits, int flags);
 
+/* holo_prefill_prepare for every Q6_K layer matrix of m (q, k, v, o, gate,
+ * down, up; the output head runs the GEMV), and holo_prefill_release for
+ * them: the prompt forward then reads their repacked copies (1 byte per
+ * weight of those matrices) instead of repacking each one per call.  No
+ * reference counterpart.  0, or the first failing holo_prefill_prepare's
+ * code (the matrices prepared before it are released).                      */
+int holo_llama_prepare(const holo_llama_t *m);
+void holo_llama_release(const holo_llama_t *m);
+
 /* Fills m and layers[0..n_layers) from an uploaded GGUF file
  * (holo_gguf_upload), with the reference loader's tensor names and model
  * parameters (llm.c:344-533, 617-660): token_embd, blk.N.{attn_norm,

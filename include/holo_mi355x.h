@@ -311,6 +311,22 @@ void holo_matmul_batch_multi_types(float *const *Y, const void *const *W, const 
 void holo_matmul_batch_add(float *Y, const void *W, const float *X, const float *R, int M, int N, int K, int type);
 void holo_matmul_batch_swiglu_add(float *Y, const void *W, float *G, const float *U, const float *R, int M, int N,
                                   int K, int type);
+/* Q6_K matrices repacked once instead of per call (no reference counterpart;
+ * the load-time step of this library's own exact product).  The exact
+ * product reads Q6_K through a layout of its own (1 byte per weight, the
+ * superblocks' bits rearranged), which every batched call otherwise builds
+ * in its workspace first.  holo_prefill_prepare allocates that copy of W
+ * [N][K] (N*K bytes, hipMalloc), writes it, waits for it, and keeps it until
+ * holo_prefill_release(W): every later exact batched product on W with the
+ * same N and K reads the copy, with the same bits as the per-call form.  W
+ * must not change and must not be freed while registered.  Returns 0 (also
+ * for a W already registered with this shape), or HOLO_EINVAL (not Q6_K, K
+ * not a multiple of 256 up to 16384, W not 2-byte aligned, N*K >= 2^31, a W
+ * registered with another shape, or under graph capture), or the hipError_t
+ * of the allocation.  Release of an unregistered W does nothing; release
+ * waits for the library stream.                                            */
+int holo_prefill_prepare(const void *W, int N, int K, int type);
+void holo_prefill_release(const void *W);
 
 #ifdef __cplusplus
 }

@@ -222,6 +222,63 @@ def test_exact_product_row_range(holo, synth, oracle, t):
         check_rows(T, H, w, np.array([r]), t, K)
 
 
+@pytest.mark.parametrize("M,N,K", [(100, 384, 1024), (512, 4096, 4096)], ids=["whole-tiles", "parts"])
+def test_prepared_q6_k(holo, synth, oracle, M, N, K):
+    """holo_prefill_prepare keeps a repacked copy of a Q6_K matrix: products
+    on it (plain, add form, a captured graph replayed twice) give the bits of
+    the per-call repack, and so does the plain product after release.  It
+    rejects another type, a K that is not a multiple of 256, and a second
+    shape for a registered matrix."""
+    print(f"case prepared q6_k {M}x{N}x{K}", flush=True)
+    lib = holo.lib()
+    src, w = weights(synth, oracle, Q6_K, N, K, seed=M + N + K + 1)
+    X = synth.normal(M * K, seed=K + 23).reshape(M, K)
+    R = synth.normal(M * N, seed=K + 24).reshape(M, N)
+    dW, dX = up(holo, src), up(holo, X)
+
+    def product():
+        dY = holo.DeviceBuffer(4 * M * N)
+        lib.holo_matmul_batch(dY.ptr, dW.ptr, dX.ptr, M, N, K, Q6_K)
+        dS = up(holo, R)
+        lib.holo_matmul_batch_add(dS.ptr, dW.ptr, dX.ptr, dS.ptr, M, N, K, Q6_K)
+        lib.cuda_sync()
+        holo.check("prepared product")
+        return down(dY, M * N).reshape(M, N), down(dS, M * N).reshape(M, N)
+
+    y0, s0 = product()
+    check_rows(y0, X, w, np.unique(np.r_[0:M:32, 31:M:32, M - 1]), Q6_K, K)
+    assert lib.holo_prefill_prepare(dW.ptr, N, K, Q6_K) == 0
+    try:
+        assert lib.holo_prefill_prepare(dW.ptr, N, K, Q6_K) == 0  # registered with this shape: no-op
+        for args in ((dW.ptr, N, K, Q4_0), (dW.ptr, N, 1000, Q6_K), (dW.ptr, N - 32, K, Q6_K)):
+            assert lib.holo_prefill_prepare(*args) == holo.EINVAL
+            assert lib.holo_last_error() == holo.EINVAL
+        y1, s1 = product()
+        assert np.array_equal(y1.view(np.uint32), y0.view(np.uint32))
+        assert np.array_equal(s1.view(np.uint32), s0.view(np.uint32))
+        s = lib.holo_stream_create()
+        lib.holo_set_stream(s)
+        try:
+            dG = holo.DeviceBuffer(4 * M * N)
+            assert lib.holo_graph_begin() == 0
+            lib.holo_matmul_batch(dG.ptr, dW.ptr, dX.ptr, M, N, K, Q6_K)
+            g = lib.holo_graph_end()
+            holo.check("capture")
+            assert g
+            for rep in range(2):
+                lib.holo_graph_launch(g)
+                lib.cuda_sync()
+                got = down(dG, M * N).reshape(M, N)
+                assert np.array_equal(got.view(np.uint32), y0.view(np.uint32)), rep
+            lib.holo_graph_destroy(g)
+        finally:
+            lib.holo_set_stream(None)
+    finally:
+        lib.holo_prefill_release(dW.ptr)
+    y2, _ = product()
+    assert np.array_equal(y2.view(np.uint32), y0.view(np.uint32))
+
+
 PART_CASES = [(Q4_0, 192, 11008, 2048), (Q8_0, 320, 6656, 2048), (Q4_K, 256, 8448, 2048),
               (Q4_0, 512, 4096, 4096), (Q4_K, 512, 4096, 4096), (Q4_0, 320, 2112, 2048),
               (Q6_K, 256, 8448, 2048), (Q6_K, 512, 4096, 4096)]

@@ -243,6 +243,28 @@ def test_prompt_in_one_pass_equals_decode_loop(model):
     assert e <= 5e-5 and ek <= 5e-5 and ev <= 5e-5
 
 
+def test_forward_prepared_equals_per_call(model):
+    """holo_llama_prepare repacks the model's Q6_K matrices (layer 1's down
+    projection here) once; the 80-row prompt then reads the copies and gives
+    the same bits as with the per-call repack, before and after release."""
+    print("case forward prepared", flush=True)
+    lib = model.holo.lib()
+    tokens = np.load(GOLDEN)["tokens"][:80]
+    runs = []
+    for step in ("per-call", "prepared", "released"):
+        if step == "prepared":
+            assert lib.holo_llama_prepare(C.byref(model.m)) == 0
+            assert lib.holo_llama_prepare(C.byref(model.m)) == 0  # already registered: no-op
+        if step == "released":
+            lib.holo_llama_release(C.byref(model.m))
+        model.reset()
+        logits = model.forward(tokens, 0, 0)
+        runs.append((logits, *model.caches(80)))
+    for a, b in ((runs[0], runs[1]), (runs[0], runs[2])):
+        for x, y in zip(a, b):
+            assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
 def test_forward_rejects_bad_input(model):
     print("case forward rejects", flush=True)
     lib = model.holo.lib()
