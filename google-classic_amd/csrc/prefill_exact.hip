@@ -606,8 +606,8 @@ __global__ __launch_bounds__(256, OCC) void gemm_exact_k(ExactArgs a)
 // block sums of the scaled values (for the Q4_K min term).
 enum XSplitMode { XS_PLAIN = 0, XS_SWIGLU = 1, XS_NORM = 2 };
 
-template <int NV, int MODE>
-__global__ __launch_bounds__(256) void xsplit_row_k(uint2 *__restrict__ Ah, uint2 *__restrict__ Al,
+template <int NV, int MODE, int NT = 256>
+__global__ __launch_bounds__(NT) void xsplit_row_k(uint2 *__restrict__ Ah, uint2 *__restrict__ Al,
                                                     float *__restrict__ Sx, float *__restrict__ Rs,
                                                     const float *__restrict__ X, const float *__restrict__ U,
                                                     const float *__restrict__ NW, int K, float eps)
@@ -627,7 +627,7 @@ __global__ __launch_bounds__(256) void xsplit_row_k(uint2 *__restrict__ Ah, uint
     float4 v[NV], wv[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int o = (int)(threadIdx.x + 256 * j) * 16;
+        const int o = (int)(threadIdx.x + NT * j) * 16;
         v[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
         if constexpr (MODE == XS_SWIGLU)
             wv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ru, o, 0, 0));
@@ -673,8 +673,8 @@ __global__ __launch_bounds__(256) void xsplit_row_k(uint2 *__restrict__ Ah, uint
     if (threadIdx.x == 0) Rs[blockIdx.x] = ldexpf(1.0f, -e);
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int i = threadIdx.x + 256 * j;
-        if (256 * j >= n4) break;  // uniform: no lane of this or a later j is live
+        const int i = threadIdx.x + NT * j;
+        if (NT * j >= n4) break;  // uniform: no lane of this or a later j is live
         const float y[4] = {ldexpf(v[j].x, e), ldexpf(v[j].y, e), ldexpf(v[j].z, e), ldexpf(v[j].w, e)};
         _Float16 h[4], l[4];
 #pragma unroll
@@ -1582,10 +1582,47 @@ bool exact_init()
            hipDeviceSynchronize() == hipSuccess;
 }
 
+// ---- Q6_K matrices repacked once (holo_prefill_prepare) ----
+// The repacked copy of each registered matrix, keyed by its device address;
+// the caller keeps the matrix unchanged until it releases it.
+namespace {
+struct PreparedQ6 {
+    int N, K;
+    void *rec;
+};
+std::mutex g_prep_mu;
+std::unordered_map<const void *, PreparedQ6> g_prep;
+
+const void *prepared_q6r(const void *W, int N, int K)
+{
+    std::lock_guard<std::mutex> lk(g_prep_mu);
+    const auto it = g_prep.find(W);
+    return it != g_prep.end() && it->second.N == N && it->second.K == K ? it->second.rec : nullptr;
+}
+
+// Frees every registered copy (cuda_cleanup).
+void prepared_release_all()
+{
+    std::lock_guard<std::mutex> lk(g_prep_mu);
+    for (auto &e : g_prep) (void)hipFree(e.second.rec);
+    g_prep.clear();
+}
+
+// W [N][K] Q6_K (K a multiple of 256, W 2-byte aligned) into records [N][K/64][64 B] at out
+void q6r_repack(void *out, const void *W, int N, int K)
+{
+    const int64_t nrec = (int64_t)N * (K / 256) * 4;
+    hipLaunchKernelGGL(q6r_repack_k, dim3((unsigned)((nrec + 255) / 256)), dim3(256), 0, stream(), (uint4 *)out,
+                       (const uint8_t *)W, nrec);
+    HOLO_LAUNCH_CHECK();
+}
+}  // namespace
+
 void exact_release()
 {
     if (g_x2_cnt) (void)hipFree(g_x2_cnt);
     g_x2_cnt = nullptr;
+    prepared_release_all();
 }
 
 // Takes the exact product: M >= 1, K whole blocks of the type (Q4_K, Q6_K: a
@@ -1610,34 +1647,6 @@ bool exact_ok(int type, int K, const void *W)
 // nmat matrices sharing the activations; every type must pass exact_ok, and
 // with several matrices of one type every N[i] must be a multiple of 128.
 // Matrices of one type share a launch; the activation halves are built once.
-// ---- Q6_K matrices repacked once (holo_prefill_prepare) ----
-// The repacked copy of each registered matrix, keyed by its device address;
-// the caller keeps the matrix unchanged until it releases it.
-namespace {
-struct PreparedQ6 {
-    int N, K;
-    void *rec;
-};
-std::mutex g_prep_mu;
-std::unordered_map<const void *, PreparedQ6> g_prep;
-
-const void *prepared_q6r(const void *W, int N, int K)
-{
-    std::lock_guard<std::mutex> lk(g_prep_mu);
-    const auto it = g_prep.find(W);
-    return it != g_prep.end() && it->second.N == N && it->second.K == K ? it->second.rec : nullptr;
-}
-
-// W [N][K] Q6_K (K a multiple of 256, W 2-byte aligned) into records [N][K/64][64 B] at out
-void q6r_repack(void *out, const void *W, int N, int K)
-{
-    const int64_t nrec = (int64_t)N * (K / 256) * 4;
-    hipLaunchKernelGGL(q6r_repack_k, dim3((unsigned)((nrec + 255) / 256)), dim3(256), 0, stream(), (uint4 *)out,
-                       (const uint8_t *)W, nrec);
-    HOLO_LAUNCH_CHECK();
-}
-}  // namespace
-
 void exact_product(float *const *Y, const void *const *W, const int *types, const int *N, int nmat, const float *X,
                    const float *U, const float *R, int M, int K, const float *NW, float eps)
 {
@@ -1671,14 +1680,19 @@ void exact_product(float *const *Y, const void *const *W, const int *types, cons
         }
     }
     // one workgroup per row, K <= 16384 (exact_ok): the row in registers
-    auto split = [&](auto kern) {
-        hipLaunchKernelGGL(kern, dim3(M), dim3(256), 0, stream(), (uint2 *)Ah, (uint2 *)Al, need_sx ? Sx : nullptr,
+    auto split = [&](auto kern, int nt) {
+        hipLaunchKernelGGL(kern, dim3(M), dim3(nt), 0, stream(), (uint2 *)Ah, (uint2 *)Al, need_sx ? Sx : nullptr,
                            Rs, X, U, NW, K, eps);
     };
+    // the normed form keeps rms_norm_rows4_k's 256 threads (its sum of squares
+    // in the same order); the others reduce only a maximum, so their threads
+    // per row change no bit.  The long SwiGLU rows (g and u in registers) take
+    // 512: 14.9 against 15.8 us at 512 x 11008; 512 or 1024 threads measured
+    // level on the plain 4096-wide rows.
     const bool small = K <= 1024 * 4;
-    if (NW) small ? split(xsplit_row_k<4, XS_NORM>) : split(xsplit_row_k<16, XS_NORM>);
-    else if (U) small ? split(xsplit_row_k<4, XS_SWIGLU>) : split(xsplit_row_k<16, XS_SWIGLU>);
-    else small ? split(xsplit_row_k<4, XS_PLAIN>) : split(xsplit_row_k<16, XS_PLAIN>);
+    if (NW) small ? split(xsplit_row_k<4, XS_NORM>, 256) : split(xsplit_row_k<16, XS_NORM>, 256);
+    else if (U) small ? split(xsplit_row_k<2, XS_SWIGLU, 512>, 512) : split(xsplit_row_k<8, XS_SWIGLU, 512>, 512);
+    else small ? split(xsplit_row_k<4, XS_PLAIN>, 256) : split(xsplit_row_k<16, XS_PLAIN>, 256);
     HOLO_LAUNCH_CHECK();
     // Q6_K matrices: repacked, or their integer panels and group scales
     void *pws = nullptr;

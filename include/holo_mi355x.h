@@ -324,7 +324,7 @@ void holo_matmul_batch_swiglu_add(float *Y, const void *W, float *G, const float
  * not a multiple of 256 up to 16384, W not 2-byte aligned, N*K >= 2^31, a W
  * registered with another shape, or under graph capture), or the hipError_t
  * of the allocation.  Release of an unregistered W does nothing; release
- * waits for the library stream.                                            */
+ * waits for the library stream.  cuda_cleanup releases every copy.         */
 int holo_prefill_prepare(const void *W, int N, int K, int type);
 void holo_prefill_release(const void *W);
 
