@@ -319,7 +319,9 @@ void holo_matmul_batch_swiglu_add(float *Y, const void *W, float *G, const float
  * [N][K] (N*K bytes, hipMalloc), writes it, waits for it, and keeps it until
  * holo_prefill_release(W): every later exact batched product on W with the
  * same N and K reads the copy, with the same bits as the per-call form.  W
- * must not change and must not be freed while registered.  Returns 0 (also
+ * must not change and must not be freed while registered, and a graph
+ * captured while W was registered reads the copy: destroy such graphs
+ * before releasing W.  Returns 0 (also
  * for a W already registered with this shape), or HOLO_EINVAL (not Q6_K, K
  * not a multiple of 256 up to 16384, W not 2-byte aligned, N*K >= 2^31, a W
  * registered with another shape, or under graph capture), or the hipError_t

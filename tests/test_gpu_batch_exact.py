@@ -77,6 +77,7 @@ def exact_mode(holo):
 CASES = [(Q4_0, 64, 128, 256), (Q4_0, 77, 150, 4096), (Q4_0, 66, 256, 1056), (Q4_0, 512, 11008, 4096),
          (Q4_0, 512, 4096, 11008), (Q8_0, 100, 256, 512), (Q8_0, 70, 192, 1056), (Q8_0, 512, 4096, 4096),
          (Q4_K, 128, 512, 2048), (Q4_K, 512, 14336, 4096), (Q4_K, 512, 4096, 14336), (Q6_K, 96, 384, 1024),
+         (Q6_K, 65, 200, 256),
          (Q6_K, 512, 4096, 11008), (F16, 80, 256, 256), (F16, 512, 1024, 4096), (F32, 70, 200, 128)]
 
 
