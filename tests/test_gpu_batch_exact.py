@@ -175,6 +175,34 @@ def test_exact_multi_types(holo, synth, oracle):
             check_rows(got, X, ws[i], np.arange(M), types[i], K)
 
 
+@pytest.mark.parametrize("t,K", [(Q4_0, 11008), (Q6_K, 11008), (Q4_K, 16384)], ids=["q4_0-11008", "q6_k-11008",
+                                                                                      "q4_k-16384"])
+def test_exact_swiglu_long_rows(holo, synth, oracle, t, K):
+    """The SwiGLU split of rows longer than 4096 (the down projection's 11008,
+    and the longest row the split takes): Y = R + (silu(G)*U).W^T equals
+    cuda_silu_mul, the product and an fp32 add bit for bit, within the bound
+    of the float64 truth."""
+    print(f"case exact swiglu long rows {NAMES[t]} K {K}", flush=True)
+    lib = holo.lib()
+    M, N = 72, 128
+    src, w = weights(synth, oracle, t, N, K, seed=K + t)
+    G = synth.normal(M * K, seed=K + 31).reshape(M, K)
+    U = synth.normal(M * K, seed=K + 32).reshape(M, K)
+    R = synth.normal(M * N, seed=K + 33).reshape(M, N)
+    dW, dG, dU, dH = up(holo, src), up(holo, G), up(holo, U), holo.DeviceBuffer(4 * M * K)
+    lib.cuda_silu_mul(dH.ptr, dG.ptr, dU.ptr, M * K)
+    dT = holo.DeviceBuffer(4 * M * N)
+    lib.holo_matmul_batch(dT.ptr, dW.ptr, dH.ptr, M, N, K, t)
+    dZ = up(holo, R)
+    lib.holo_matmul_batch_swiglu_add(dZ.ptr, dW.ptr, dG.ptr, dU.ptr, dZ.ptr, M, N, K, t)
+    lib.cuda_sync()
+    holo.check("exact swiglu long rows")
+    H = down(dH, M * K).reshape(M, K)
+    T = down(dT, M * N).reshape(M, N)
+    assert np.array_equal(down(dZ, M * N).reshape(M, N), (R + T).astype(np.float32))
+    check_rows(T, H, w, np.r_[0:4, M - 4:M], t, K)
+
+
 @pytest.mark.parametrize("t", [Q4_0, Q8_0, Q4_K, Q6_K, F16], ids=lambda t: NAMES[t])
 def test_exact_product_row_range(holo, synth, oracle, t):
     """Rows far from unit scale: the split scales each row by a power of two
