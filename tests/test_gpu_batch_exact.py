@@ -308,6 +308,46 @@ def test_prepared_q6_k(holo, synth, oracle, M, N, K):
     assert np.array_equal(y2.view(np.uint32), y0.view(np.uint32))
 
 
+def _sweep_shapes():
+    """Seeded small shapes per type: M from 64 (the batched path's least) to
+    ragged row tiles, N ragged against the 32-, 64- and 256-column tiles, K
+    from one block (one superblock for Q4_K/Q6_K) to a few hundred."""
+    rng = np.random.default_rng(2024)
+    out = []
+    for t in (Q4_0, Q8_0, Q4_K, Q6_K, F16):
+        step = 256 if t in (Q4_K, Q6_K) else 32
+        for _ in range(6):
+            M = int(rng.choice([64, 65, 96, 127, 130, 200]))
+            N = int(rng.choice([8, 31, 64, 100, 200, 257, 330]))
+            K = step * int(rng.integers(1, 5 if step == 256 else 25))
+            if (t, M, N, K) not in out:
+                out.append((t, M, N, K))
+    return out
+
+
+SWEEP = _sweep_shapes()
+
+
+@pytest.mark.parametrize("t,M,N,K", SWEEP, ids=[f"{NAMES[t]}-{m}x{n}x{k}" for t, m, n, k in SWEEP])
+def test_exact_product_shape_sweep(holo, synth, oracle, t, M, N, K):
+    """Every row of a ragged small product within the elementwise bound of
+    the float64 truth (and 1e-5 normwise), two calls bit-identical."""
+    print(f"case exact sweep {NAMES[t]} {M}x{N}x{K}", flush=True)
+    lib = holo.lib()
+    src, w = weights(synth, oracle, t, N, K, seed=7 * M + 3 * N + K)
+    X = synth.normal(M * K, seed=M + K).reshape(M, K)
+    dW, dX = up(holo, src), up(holo, X)
+    outs = []
+    for _ in range(2):
+        dY = holo.DeviceBuffer(4 * M * N)
+        lib.holo_matmul_batch(dY.ptr, dW.ptr, dX.ptr, M, N, K, t)
+        lib.cuda_sync()
+        holo.check("exact sweep")
+        outs.append(down(dY, M * N).reshape(M, N))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    check_rows(outs[0], X, w, np.arange(M), t, K)
+
+
 PART_CASES = [(Q4_0, 192, 11008, 2048), (Q8_0, 320, 6656, 2048), (Q4_K, 256, 8448, 2048),
               (Q4_0, 512, 4096, 4096), (Q4_K, 512, 4096, 4096), (Q4_0, 320, 2112, 2048),
               (Q6_K, 256, 8448, 2048), (Q6_K, 512, 4096, 4096)]
