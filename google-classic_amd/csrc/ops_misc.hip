@@ -748,6 +748,112 @@ __global__ __launch_bounds__(512) void attn_decode_combine_k(float *out, const f
     if (grp == 0 && d < hd) out[(int64_t)h * hd + d] = (((lg[0][d] + lg[1][d]) + lg[2][d]) + lg[3][d]) * (1.0f / L);
 }
 
+// Short caches in one launch: one workgroup per head, SUB groups of 256
+// threads, group sg taking positions [sg chunk, (sg + 1) chunk) with
+// attn_decode_k's pass (the same loads, scores, online softmax and key-group
+// order), every group looping the same number of passes so the barriers are
+// the workgroup's.  A group whose range is empty keeps (m, l, o) = (-inf, 0,
+// 0) and gets weight 0; the groups merge in group order through LDS, so the
+// result does not depend on timing.  No range partials and no second launch.
+template <int SUB>
+__global__ __launch_bounds__(256 * SUB) void attn_decode_wg_k(float *out, const float *q, const float *kc,
+                                                              const float *vc, int kv_len, int hd, int n_heads,
+                                                              int n_kv_heads, int chunk)
+{
+    __shared__ float4 lq[32];
+    __shared__ float lsc[SUB][kDecKeys];
+    __shared__ float4 lo[SUB][8][32];
+    __shared__ float lm[SUB], ll[SUB];
+    const int h = blockIdx.x;
+    const int kvh = h / (n_heads / n_kv_heads);
+    const int64_t kv_dim = (int64_t)n_kv_heads * hd;
+    const int t = threadIdx.x, sg = __builtin_amdgcn_readfirstlane(t >> 8), u = t & 255;
+    const int lane = u & 63, c = u & 31, g = u >> 5;
+    const int hd4 = hd >> 2;
+    const bool col = c < hd4;
+    const float scale = 1.0f / sqrtf((float)hd);
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < hd4) lq[t] = *(const float4 *)(q + (int64_t)h * hd + 4 * t);
+    __syncthreads();
+    const float4 q4 = col ? lq[c] : zero;
+    const float *kb = kc + (int64_t)kvh * hd + 4 * c;
+    const float *vb = vc + (int64_t)kvh * hd + 4 * c;
+    const int p_begin = sg * chunk, p_end = min(p_begin + chunk, kv_len);
+    float m = -INFINITY, l = 0.f;
+    float4 o4 = zero;
+    for (int i0 = 0; i0 < chunk; i0 += kDecKeys) {
+        const int p0 = p_begin + i0;
+        float4 k4[8], v4[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int p = p0 + g + 8 * j;
+            k4[j] = zero;
+            v4[j] = zero;
+            if (col && p < p_end) {
+                k4[j] = *(const float4 *)(kb + (int64_t)p * kv_dim);
+                v4[j] = *(const float4 *)(vb + (int64_t)p * kv_dim);
+            }
+        }
+        float sj[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            sj[j] = half_wave_sum(q4.x * k4[j].x + q4.y * k4[j].y + q4.z * k4[j].z + q4.w * k4[j].w);
+        if (c == 0) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) lsc[sg][g + 8 * j] = p0 + g + 8 * j < p_end ? sj[j] * scale : -INFINITY;
+        }
+        __syncthreads();
+        if (p0 < p_end) {  // uniform per group: a pass with keys in this group's range
+            const float sl = lsc[sg][lane];
+            const float mnew = fmaxf(m, wave_reduce_max(sl));  // finite: the pass has a key
+            const float corr = expf(m - mnew);
+            const float pl = expf(sl - mnew);
+            l = l * corr + wave_reduce_sum(pl);
+            o4 = make_float4(o4.x * corr, o4.y * corr, o4.z * corr, o4.w * corr);
+            m = mnew;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float w = __shfl(pl, g + 8 * j, 64);
+                o4 = make_float4(fmaf(w, v4[j].x, o4.x), fmaf(w, v4[j].y, o4.y), fmaf(w, v4[j].z, o4.z),
+                                 fmaf(w, v4[j].w, o4.w));
+            }
+        }
+        __syncthreads();  // lsc is rewritten by the next pass
+    }
+    lo[sg][g][c] = o4;
+    if (u == 0) {
+        lm[sg] = m;
+        ll[sg] = l;
+    }
+    __syncthreads();
+    if (t < hd4) {
+        float M = lm[0];
+#pragma unroll
+        for (int k = 1; k < SUB; k++) M = fmaxf(M, lm[k]);  // group 0 always has keys: finite
+        float L = 0.f;
+        float4 r = zero;
+#pragma unroll
+        for (int k = 0; k < SUB; k++) {
+            const float w = lm[k] == -INFINITY ? 0.f : expf(lm[k] - M);
+            float4 rk = lo[k][0][t];
+#pragma unroll
+            for (int gg = 1; gg < 8; gg++)
+                rk = make_float4(rk.x + lo[k][gg][t].x, rk.y + lo[k][gg][t].y, rk.z + lo[k][gg][t].z,
+                                 rk.w + lo[k][gg][t].w);
+            r = make_float4(fmaf(w, rk.x, r.x), fmaf(w, rk.y, r.y), fmaf(w, rk.z, r.z), fmaf(w, rk.w, r.w));
+            L = fmaf(w, ll[k], L);
+        }
+        const float inv = 1.0f / L;
+        *(float4 *)(out + (int64_t)h * hd + 4 * t) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
+    }
+}
+// Up to this many positions (one 64-position pass per group) attn_decode_wg_k:
+// 6.6 against 8.0 us at 128 positions, 32 heads of 128.  With two or more
+// passes its 32 workgroups wait on each pass in turn, and the split kernel's
+// whole-chip read wins (300 / 512 / 1024 positions: 9.8 / 10.8 / 19.4 against
+// 8.3 / 8.5 / 10.1 us).
+constexpr int kDecWgMaxKeys = 4 * kDecKeys;
+
 // Shapes the split kernel takes: head_dim a multiple of 4 up to 128, 16-byte
 // aligned rows.
 static bool decode_attention_fits(const float *q, const float *kc, const float *vc, int hd)
@@ -758,6 +864,14 @@ static bool decode_attention_fits(const float *q, const float *kc, const float *
 static void decode_attention(float *dst, const float *q, const float *kc, const float *vc, int kv_len, int hd,
                              int n_heads, int n_kv_heads)
 {
+    if (kv_len > kDecKeys && kv_len <= kDecWgMaxKeys) {
+        // four groups of whole 64-position passes per head
+        const int chunk = ((kv_len + 3) / 4 + kDecKeys - 1) / kDecKeys * kDecKeys;
+        hipLaunchKernelGGL(attn_decode_wg_k<4>, dim3(n_heads), dim3(1024), 0, stream(), dst, q, kc, vc, kv_len, hd,
+                           n_heads, n_kv_heads, chunk);
+        HOLO_LAUNCH_CHECK();
+        return;
+    }
     int splits = (kv_len + kDecKeys - 1) / kDecKeys;
     if (!g_dec_part) splits = 1;
     splits = min(splits, min(kDecMaxSplits, (int)(kDecPartFloats / ((size_t)n_heads * (hd + 4)))));
