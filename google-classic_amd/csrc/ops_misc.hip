@@ -623,7 +623,7 @@ static int q6_rows_per_wave(int out_dim)
 // (unnormalised output, max, sum) and attn_decode_combine_k merges the ranges
 // of a head in range order, so the result does not depend on timing.
 constexpr int kDecKeys = 64;
-constexpr int kDecMaxSplits = 256;
+constexpr int kDecMaxSplits = 256;  // at most one range per thread of attn_decode_combine_k's 512
 constexpr size_t kDecPartFloats = (size_t)4 << 20;  // 16 MiB of range partials, allocated by cuda_init
 static float *g_dec_part = nullptr;
 
@@ -721,6 +721,7 @@ __global__ __launch_bounds__(256) void attn_decode_k(float *out, float *part, co
 // meet in LDS in group order, so the order is fixed.  (Merging in the split
 // kernel itself, by the last range of a head to arrive, measured slower: the
 // merge becomes a serial tail and every range pays the arrival.)
+static_assert(kDecMaxSplits <= 512, "attn_decode_combine_k: one range per thread");
 __global__ __launch_bounds__(512) void attn_decode_combine_k(float *out, const float *part, int hd, int splits)
 {
     __shared__ float lw[kDecMaxSplits];
@@ -729,19 +730,29 @@ __global__ __launch_bounds__(512) void attn_decode_combine_k(float *out, const f
     const int h = blockIdx.x, t = threadIdx.x, d = t & 127, grp = t >> 7;
     const int stride = hd + 4;
     const float *ph = part + (int64_t)h * splits * stride;
-    float mx = -INFINITY;
-    for (int s = t; s < splits; s += blockDim.x) mx = fmaxf(mx, ph[(int64_t)s * stride + hd]);
-    const float M = block_reduce<true>(mx, scratch);
-    float lsum = 0.f;
-    for (int s = t; s < splits; s += blockDim.x) {
-        const float w = expf(ph[(int64_t)s * stride + hd] - M);
-        lw[s] = w;
-        lsum = fmaf(w, ph[(int64_t)s * stride + hd + 1], lsum);
+    // one round of loads: the partial outputs of ranges grp, grp + 4, ... (the
+    // first kPre of them into registers) together with range t's max and sum,
+    // so the reductions below wait for a single round trip
+    constexpr int kPre = 16;
+    float po[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; i++) {
+        const int s = grp + 4 * i;
+        po[i] = d < hd && s < splits ? ph[(int64_t)s * stride + d] : 0.f;
     }
-    const float L = block_reduce<false>(lsum, scratch);  // its barriers also publish lw
+    const bool mine = t < splits;  // splits <= kDecMaxSplits <= blockDim.x: one range per thread at most
+    const float ms = mine ? ph[(int64_t)t * stride + hd] : -INFINITY;
+    const float ls = mine ? ph[(int64_t)t * stride + hd + 1] : 0.f;
+    const float M = block_reduce<true>(ms, scratch);
+    const float w = mine ? expf(ms - M) : 0.f;
+    if (mine) lw[t] = w;
+    const float L = block_reduce<false>(w * ls, scratch);  // its barriers also publish lw
     if (d < hd) {
         float o = 0.f;
-        for (int s = grp; s < splits; s += 4) o = fmaf(lw[s], ph[(int64_t)s * stride + d], o);
+#pragma unroll
+        for (int i = 0; i < kPre; i++)
+            if (grp + 4 * i < splits) o = fmaf(lw[grp + 4 * i], po[i], o);
+        for (int s = grp + 4 * kPre; s < splits; s += 4) o = fmaf(lw[s], ph[(int64_t)s * stride + d], o);
         lg[grp][d] = o;
     }
     __syncthreads();
