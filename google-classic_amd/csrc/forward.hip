@@ -26,19 +26,6 @@ bool rows_type_ok(int t)
            t == HOLO_TYPE_Q4_K || t == HOLO_TYPE_Q6_K;
 }
 
-// Bytes of one row of a block stream of `type` (whole blocks: in_dim / QK).
-int64_t row_bytes(int type, int in_dim)
-{
-    switch (type) {
-    case HOLO_TYPE_F16: return (int64_t)in_dim * 2;
-    case HOLO_TYPE_Q4_0: return (int64_t)(in_dim / 32) * 18;
-    case HOLO_TYPE_Q8_0: return (int64_t)(in_dim / 32) * 34;
-    case HOLO_TYPE_Q4_K: return (int64_t)(in_dim / 256) * 144;
-    case HOLO_TYPE_Q6_K: return (int64_t)(in_dim / 256) * 210;
-    default: return (int64_t)in_dim * 4;
-    }
-}
-
 bool layer_ok(const holo_llama_layer_t &l)
 {
     return l.wq && l.wk && l.wv && l.wo && l.w1 && l.w2 && l.w3 && rows_type_ok(l.wq_type) && rows_type_ok(l.wk_type) &&
